@@ -1,0 +1,249 @@
+"""Benchmark of the sparse INT4 decode-attention step on one MI355X.
+
+Workload: 28 independent layers' KV caches, batch 1,
+24 query / 8 KV heads, head_dim 128, 32k context = 512 pages of 64 tokens,
+retention 0.25 (top-128 pages per KV head, per-KV-head selection from the
+summed group scores) plus 4 sink and 2 window pages.  K/V are seeded synthetic
+fp16 data (lognormal outlier channels in K, 4 planted pages per KV head),
+quantised by this library to packed INT4 with fp16 metadata, V in 32-channel
+groups.  One step = score + select + sparse attention for all 28 layers, with
+L2 and the 256 MB MALL flushed before every step (outside the timed region).
+
+Prints one JSON line (the driver's contract).  `--gpus N` with N > 1 exits:
+this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
+from flashquest_amd.kernel.kv_quant import quantize_k_int4, quantize_v_int4  # noqa: E402
+
+METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--pages", type=int, default=512)
+    ap.add_argument("--retention", type=float, default=0.25)
+    ap.add_argument("--select", default="per_kv_head_sum", choices=["per_kv_head_sum", "per_q_head"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip control / per-layer / per-q-head lines")
+    ap.add_argument("--cpu-layers", type=int, default=6, help="layers in the CPU baseline sample")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------- data --
+def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda"):
+    """Seeded synthetic INT4 cache, one (sequence, layer) at a time (seed 1000*b + l)."""
+    S = P * page
+    kp = torch.empty(L, B, Hkv, S, D // 2, dtype=torch.uint8, device=dev)
+    vp = torch.empty_like(kp)
+    ks = torch.empty(L, B, Hkv, P, D, dtype=torch.float16, device=dev)
+    km = torch.empty_like(ks)
+    vs = torch.empty(L, B, Hkv, S, D // 32, dtype=torch.float16, device=dev)
+    vm = torch.empty_like(vs)
+    Q = torch.empty(L, B, Hq, 1, D, dtype=torch.float16, device=dev)
+    rep = Hq // Hkv
+    for l in range(L):
+        for b in range(B):
+            g = torch.Generator(device=dev)
+            g.manual_seed(1000 * b + l)
+            K = torch.randn(1, Hkv, S, D, generator=g, device=dev)
+            K *= torch.exp(torch.randn(1, Hkv, 1, D, generator=g, device=dev))      # lognormal(0,1) channels
+            V = torch.randn(1, Hkv, S, D, generator=g, device=dev)
+            q = torch.randn(Hq, D, generator=g, device=dev)
+            qhat = q.view(Hkv, rep, D).mean(1)
+            qhat = qhat / qhat.norm(dim=-1, keepdim=True)
+            rms = K[0].pow(2).mean(dim=(1, 2)).sqrt()
+            for h in range(Hkv):
+                pages = torch.randperm(P - 6, generator=g, device=dev)[:planted] + 4
+                for p in pages.tolist():
+                    noise = torch.randn(page, D, generator=g, device=dev)
+                    K[0, h, p * page:(p + 1) * page] = rms[h] * (0.8 * math.sqrt(D) * qhat[h] + 0.6 * noise)
+            quantize_k_int4(K.half(), page, out=(kp[l, b:b + 1], ks[l, b:b + 1], km[l, b:b + 1]))
+            quantize_v_int4(V.half(), v_group=32, out=(vp[l, b:b + 1], vs[l, b:b + 1], vm[l, b:b + 1]))
+            Q[l, b, :, 0] = q.half()
+    torch.cuda.synchronize()
+    return dict(Q=Q, K_packed=kp, K_scale=ks, K_mn=km, V_packed=vp, V_scale=vs, V_mn=vm)
+
+
+def step_bytes(cache, mask, page=64):
+    """Algorithmic HBM bytes of one step: (scoring, attention) = K metadata of
+    every page; codes + V metadata of the union of selected pages per KV group,
+    plus Q in and O / lse out."""
+    L, B, Hkv, P, D = cache["K_scale"].shape
+    Hq = cache["Q"].shape[2]
+    meta = cache["K_scale"].element_size()
+    G = cache["V_scale"].shape[-1]
+    scoring = L * B * Hkv * P * D * 2 * meta
+    union = mask.view(L, B, Hkv, Hq // Hkv, P).any(3).sum().item()
+    per_page = 2 * page * D // 2 + 2 * page * G * meta
+    qo = L * B * Hq * (D * 2 * 2 + 4)
+    return scoring, union * per_page + qo, union
+
+
+# --------------------------------------------------------------- measurement --
+class Flusher:
+    """Evicts L2 and MALL: a fill kernel over 2 x 256 MB."""
+
+    def __init__(self, dev):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def time_steps(fn_pre, fn_timed, steps, warmup, flush):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for _ in range(warmup):
+        flush()
+        fn_pre()
+        fn_timed()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        flush()
+        fn_pre()
+        ev[i][0].record()
+        fn_timed()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return sum(ms) / len(ms), wall
+
+
+def cpu_baseline(cache, args, n_layers):
+    """Oracle restatement timed on the host (1 thread): fixed-order fp32 scores,
+    top-k selection, fp32 dequant of the selected pages only, fp32 attention."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import fq_oracle as O
+    page = 64
+    host = {k: v[:n_layers, 0].cpu() for k, v in cache.items()}
+    f32 = {k: (t.float().numpy() if t.dtype == torch.float16 else t.numpy()) for k, t in host.items()}
+    Hq, Hkv = f32["Q"].shape[1], f32["K_scale"].shape[1]
+    times = []
+    with threadpool_limits(1):
+        for l in range(n_layers):
+            t0 = time.perf_counter()
+            q = f32["Q"][l][None, :, 0, :]
+            sc = O.page_scores_fixed(q, f32["K_scale"][l][None], f32["K_mn"][l][None], args.select)
+            k = math.ceil(args.retention * sc.shape[-1])
+            m = O.select_pages_vectorized(sc[:, :, None, :], args.retention, 4, 2, k)[:, :, 0, :]
+            if args.select == "per_kv_head_sum":
+                m = np.repeat(m, Hq // Hkv, axis=1)
+            O.sparse_int4_attention_selected(q, f32["K_packed"][l][None], f32["K_scale"][l][None],
+                                             f32["K_mn"][l][None], f32["V_packed"][l][None],
+                                             f32["V_scale"][l][None], f32["V_mn"][l][None], m, page)
+            times.append(time.perf_counter() - t0)
+    per_layer = sorted(times)[len(times) // 2]
+    return {"value": per_layer * args.layers * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"{n_layers} layers of the same workload (batch 1), median layer time x {args.layers}; "
+                      "numpy oracle, BLAS limited to 1 thread"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L, B, P = args.layers, args.batch, args.pages
+    cache = make_cache(L, B, P=P, dev=dev)
+    Hq = cache["Q"].shape[2]
+    flush = Flusher(dev)
+    k = math.ceil(args.retention * P)
+
+    def decoder(retention, kmax, mode, c=cache, mask=None):
+        return QuestDecoder(c["Q"], c["K_packed"], c["K_scale"], c["K_mn"], c["V_packed"], c["V_scale"], c["V_mn"],
+                            retention=retention, num_sinks=4, window_pages=2, k_max_static=kmax,
+                            select_mode=mode, mask_out=mask)
+
+    mask = torch.zeros(L, B, Hq, P, dtype=torch.bool, device=dev)
+    dec = decoder(args.retention, k, args.select, mask=mask)
+    dec()
+    torch.cuda.synchronize()
+    scoring_b, attn_b, union = step_bytes(cache, mask)
+    dec.mask_out = None
+    noop = lambda: None
+    step_ms, wall = time_steps(noop, dec, args.steps, args.warmup, flush)
+    attn_ms, _ = time_steps(dec.select, dec.attend, args.steps, args.warmup, flush)
+    total_b = scoring_b + attn_b
+    extra = {"union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
+             "step_GBps": total_b / (step_ms * 1e-3) / 1e9,
+             "step_roofline_frac": total_b / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+             "attention_kernel_us": attn_ms * 1e3, "select_mode": args.select}
+    if not args.no_extra:
+        ctl = decoder(1.0, P, args.select)
+        ctl_ms, _ = time_steps(noop, ctl, args.steps, args.warmup, flush)
+        full_mask = torch.ones(L, B, Hq, P, dtype=torch.bool, device=dev)
+        sb, ab, _ = step_bytes(cache, full_mask)
+        extra.update({"all_pages_control_us": ctl_ms * 1e3, "sparse_speedup_vs_all_pages": ctl_ms / step_ms,
+                      "all_pages_GBps": (sb + ab) / (ctl_ms * 1e-3) / 1e9})
+        other = "per_q_head" if args.select == "per_kv_head_sum" else "per_kv_head_sum"
+        alt = decoder(args.retention, k, other)
+        alt_ms, _ = time_steps(noop, alt, args.steps, args.warmup, flush)
+        extra[f"{other}_us"] = alt_ms * 1e3
+        # the reference's per-layer call pattern: 28 sequential (select, attend) pairs in one HIP graph
+        per_layer = [decoder(args.retention, k, args.select,
+                             c={key: t[l] for key, t in cache.items()}) for l in range(L)]
+        for d in per_layer:
+            d()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            for d in per_layer:
+                d()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                for d in per_layer:
+                    d()
+        torch.cuda.synchronize()
+        pl_ms, _ = time_steps(noop, graph.replay, args.steps, args.warmup, flush)
+        extra["per_layer_graph_us"] = pl_ms * 1e3
+
+    roof = {"bound": "hbm", "achieved": attn_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": attn_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+            "kernel": "attn_int4_kernel (split-K sparse GQA attention, all 28 layers per launch)",
+            "algorithmic_bytes_per_launch": attn_b}
+    cpu = None
+    if not args.no_cpu_baseline and B == 1:
+        cpu = cpu_baseline(cache, args, min(args.cpu_layers, L))
+    line = {
+        "metric": METRIC, "value": step_ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"BASELINE config 1: {L} independent layers x batch {B}, {Hq}/8 heads, D=128, "
+                               f"{P} pages x 64 tokens, retention {args.retention} ({args.select} top-{k} + 4 sink "
+                               "+ 2 window pages), INT4 K/V with fp16 metadata (V per 32 channels), "
+                               "L2/MALL flushed between steps",
+                   "layers": L, "batch": B, "context": P * 64, "retention": args.retention},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra, "wall_s_timed_region": wall,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

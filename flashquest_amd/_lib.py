@@ -1,0 +1,198 @@
+"""ctypes binding of libfq_hip.so (the C ABI declared in include/fq_hip.h).
+
+The HIP library is the only compute path: every operator in this package
+calls into it, and a missing or unloadable library raises instead of falling
+back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfq_hip.so")
+
+FQ_OK, FQ_ERR_INVALID, FQ_ERR_UNSUPPORTED, FQ_ERR_HIP, FQ_ERR_WORKSPACE = range(5)
+FQ_BF16, FQ_F16, FQ_F32 = 0, 1, 2
+FQ_SELECT_PER_Q_HEAD, FQ_SELECT_PER_KV_HEAD_SUM = 0, 1
+
+SELECT_MODES = {"per_q_head": FQ_SELECT_PER_Q_HEAD, "per_kv_head_sum": FQ_SELECT_PER_KV_HEAD_SUM}
+
+_I64x3 = ctypes.c_int64 * 3
+_I64x4 = ctypes.c_int64 * 4
+_I64x5 = ctypes.c_int64 * 5
+
+
+class Int4Cache(ctypes.Structure):
+    _fields_ = [
+        ("k_packed", ctypes.c_void_p), ("k_strides", _I64x5),
+        ("v_packed", ctypes.c_void_p), ("v_strides", _I64x5),
+        ("k_scale", ctypes.c_void_p), ("ks_strides", _I64x5),
+        ("k_mn", ctypes.c_void_p), ("km_strides", _I64x5),
+        ("v_scale", ctypes.c_void_p), ("vs_strides", _I64x5),
+        ("v_mn", ctypes.c_void_p), ("vm_strides", _I64x5),
+        ("meta_dtype", ctypes.c_int32),
+        ("L", ctypes.c_int32), ("B", ctypes.c_int32), ("H_kv", ctypes.c_int32),
+        ("S", ctypes.c_int32), ("P", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("page_size", ctypes.c_int32), ("v_groups", ctypes.c_int32),
+    ]
+
+
+class Query(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_dtype", ctypes.c_int32), ("q_strides", _I64x4),
+        ("out", ctypes.c_void_p), ("out_dtype", ctypes.c_int32), ("o_strides", _I64x4),
+        ("lse", ctypes.c_void_p), ("lse_strides", _I64x3),
+        ("H_q", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+    ]
+
+
+class TurboCache(ctypes.Structure):
+    _fields_ = [
+        ("k_msb", ctypes.c_void_p), ("kmsb_strides", _I64x5),
+        ("k_lsb", ctypes.c_void_p), ("klsb_strides", _I64x5),
+        ("k_scale", ctypes.c_void_p), ("kst_strides", _I64x5),
+        ("v_msb", ctypes.c_void_p), ("vmsb_strides", _I64x5),
+        ("v_lsb", ctypes.c_void_p), ("vlsb_strides", _I64x5),
+        ("v_scale", ctypes.c_void_p), ("vst_strides", _I64x5),
+        ("L", ctypes.c_int32), ("B", ctypes.c_int32), ("H_kv", ctypes.c_int32),
+        ("S", ctypes.c_int32), ("P", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+_I64P = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); the list every test checks the export table against
+SIGNATURES = {
+    "fq_last_error": (ctypes.c_char_p, []),
+    "fq_abi_version": (ctypes.c_int, []),
+    "fq_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), _I]),
+    "fq_turbo_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TurboCache), _I]),
+    "fq_page_scores_int4": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
+                                           _I, _I, _I, _I, _I, _I, _P]),
+    "fq_select_pages": (ctypes.c_int, [_P, _I64P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I64P, _P]),
+    "fq_compact_ids": (ctypes.c_int, [_P, _I64P, _I, _I, _I, _I, _I, _P, _P]),
+    "fq_sparse_int4_fwd_mask": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I64P,
+                                               _P, ctypes.c_size_t, _P]),
+    "fq_sparse_int4_fwd_ids": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I64P, _I,
+                                              _P, ctypes.c_size_t, _P]),
+    "fq_quest_decode_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
+                                            _P, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quest_select_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
+                                            _P, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quest_attend_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I,
+                                            _P, ctypes.c_size_t, _P]),
+    "fq_merge_attn": (ctypes.c_int, [_P, _P, _P, _P, _I, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, _P,
+                                     _I, _I, _P]),
+    "fq_dense_tail_attn": (ctypes.c_int, [_P, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P, _P,
+                                          _I, _I, _I, _I, _I, _P]),
+    "fq_quantize_k_int4": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
+                                          _I, _P]),
+    "fq_quantize_v_int4": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
+                                          _I, _P]),
+    "fq_wht": (ctypes.c_int, [_P, _I, ctypes.c_int64, _P, _I, ctypes.c_int64, _I, _I, _P, _I, _I, _P]),
+    "fq_quantize_turbo": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P, _P]),
+    "fq_sparse_turbo_fwd_mask": (ctypes.c_int, [ctypes.POINTER(TurboCache), ctypes.POINTER(Query), _P, _I64P,
+                                                _P, ctypes.c_size_t, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libfq_hip.so once; raises RuntimeError when it is missing."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"libfq_hip.so not found at {path}; build it with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'` or `python -m flashquest_amd.build`")
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def lib() -> ctypes.CDLL:
+    return _lib if _lib is not None else load_library()
+
+
+def check(status: int, what: str = "") -> None:
+    """Map an fq_status to the reference's exception types."""
+    if status == FQ_OK:
+        return
+    msg = lib().fq_last_error().decode(errors="replace")
+    msg = f"{what}: {msg}" if what else msg
+    if status == FQ_ERR_INVALID:
+        raise ValueError(msg)
+    if status == FQ_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+_DTYPES = {torch.bfloat16: FQ_BF16, torch.float16: FQ_F16, torch.float32: FQ_F32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise AssertionError(f"unsupported dtype {dt}") from None
+
+
+def i64(values, n: int):
+    vals = list(values)
+    if len(vals) != n:
+        raise ValueError(f"expected {n} strides, got {len(vals)}")
+    return (ctypes.c_int64 * n)(*vals)
+
+
+def strides(t: torch.Tensor, n: int | None = None, lead: int = 0):
+    """Element strides of t, left-padded with `lead` zeros (broadcast axes)."""
+    s = [0] * lead + list(t.stride())
+    return i64(s, n if n is not None else len(s))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise AssertionError("flashquest_amd operators need ROCm device tensors (HIP path only)")
+
+
+# ---------------------------------------------------------------- workspace --
+_ws: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-(device, stream) scratch buffer, zero-initialised when (re)allocated.
+
+    The kernels leave its arrival counters at zero, so the buffer is reused
+    across calls without clearing.  Calls that overlap on one stream are
+    serialised by the stream; distinct streams get distinct buffers.
+    """
+    key = (device.index, stream_handle(device))
+    buf = _ws.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("workspace must be allocated before HIP graph capture (run once eagerly)")
+        buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _ws[key] = buf
+    return buf

@@ -1,0 +1,99 @@
+"""Tensor -> C-ABI descriptor plumbing shared by the operator modules."""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib as L
+
+
+def _ensure_inner_contiguous(t: torch.Tensor, align_elems: int = 1) -> torch.Tensor:
+    """Kernels need a unit-stride innermost axis and aligned rows; copy otherwise."""
+    if t.stride(-1) != 1 or any(s % align_elems for s in t.stride()[:-1]) or \
+            t.data_ptr() % (align_elems * t.element_size()):
+        return t.contiguous()
+    return t
+
+
+def _lead(t: torch.Tensor, want: int) -> int:
+    if t.dim() not in (want - 1, want):
+        raise ValueError(f"expected a {want - 1}D or {want}D tensor, got {tuple(t.shape)}")
+    return want - t.dim()
+
+
+def int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size: int):
+    """Describe a packed INT4 cache view: 4D (B,H,S,X) per layer or 5D (L,B,H,S,X).
+
+    Returns (descriptor, keepalive tensors).
+    """
+    kp = _ensure_inner_contiguous(K_packed, 4)
+    vp = _ensure_inner_contiguous(V_packed, 4)
+    ks = _ensure_inner_contiguous(K_scale, 8)
+    km = _ensure_inner_contiguous(K_mn, 8)
+    vs = _ensure_inner_contiguous(V_scale)
+    vm = _ensure_inner_contiguous(V_mn)
+    if ks.dtype != km.dtype or vs.dtype != ks.dtype or vm.dtype != ks.dtype:
+        raise AssertionError("K_scale, K_mn, V_scale and V_mn must share one dtype")
+    if ks.dtype not in (torch.bfloat16, torch.float16):
+        raise AssertionError(f"metadata dtype must be bf16 or fp16, got {ks.dtype}")
+    lead = _lead(kp, 5)
+    c = L.Int4Cache()
+    c.k_packed, c.k_strides = kp.data_ptr(), L.strides(kp, 5, lead)
+    c.v_packed, c.v_strides = vp.data_ptr(), L.strides(vp, 5, lead)
+    c.k_scale, c.ks_strides = ks.data_ptr(), L.strides(ks, 5, lead)
+    c.k_mn, c.km_strides = km.data_ptr(), L.strides(km, 5, lead)
+    c.v_scale, c.vs_strides = vs.data_ptr(), L.strides(vs, 5, lead)
+    c.v_mn, c.vm_strides = vm.data_ptr(), L.strides(vm, 5, lead)
+    c.meta_dtype = L.dtype_code(ks.dtype)
+    shape = (1,) * lead + tuple(kp.shape)
+    c.L, c.B, c.H_kv, c.S = shape[0], shape[1], shape[2], shape[3]
+    c.D = kp.shape[-1] * 2
+    c.P = ks.shape[-2]
+    c.page_size = int(page_size)
+    c.v_groups = vs.shape[-1]
+    return c, (kp, vp, ks, km, vs, vm)
+
+
+def turbo_cache(K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale, num_pages: int, page_size: int):
+    ts = [_ensure_inner_contiguous(t) for t in (K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale)]
+    lead = _lead(ts[0], 5)
+    c = L.TurboCache()
+    c.k_msb, c.kmsb_strides = ts[0].data_ptr(), L.strides(ts[0], 5, lead)
+    c.k_lsb, c.klsb_strides = ts[1].data_ptr(), L.strides(ts[1], 5, lead)
+    c.k_scale, c.kst_strides = ts[2].data_ptr(), L.strides(ts[2], 5, lead)
+    c.v_msb, c.vmsb_strides = ts[3].data_ptr(), L.strides(ts[3], 5, lead)
+    c.v_lsb, c.vlsb_strides = ts[4].data_ptr(), L.strides(ts[4], 5, lead)
+    c.v_scale, c.vst_strides = ts[5].data_ptr(), L.strides(ts[5], 5, lead)
+    shape = (1,) * lead + tuple(ts[0].shape)
+    c.L, c.B, c.H_kv, c.S = shape[0], shape[1], shape[2], shape[3]
+    c.D = ts[0].shape[-1] * 8
+    c.P = int(num_pages)
+    c.page_size = int(page_size)
+    return c, ts
+
+
+def query(Q3: torch.Tensor, O3: torch.Tensor, lse: torch.Tensor | None, sm_scale: float | None):
+    """Q3/O3: (B, H_q, D) or (L, B, H_q, D); lse: (B, H_q) / (L, B, H_q) or None."""
+    lead = 4 - Q3.dim()
+    q = L.Query()
+    q.q, q.q_dtype, q.q_strides = Q3.data_ptr(), L.dtype_code(Q3.dtype), L.strides(Q3, 4, lead)
+    q.out, q.out_dtype, q.o_strides = O3.data_ptr(), L.dtype_code(O3.dtype), L.strides(O3, 4, lead)
+    if lse is not None:
+        q.lse, q.lse_strides = lse.data_ptr(), L.strides(lse, 3, lead)
+    else:
+        q.lse, q.lse_strides = None, L.i64([0, 0, 0], 3)
+    q.H_q = Q3.shape[-2]
+    q.sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(Q3.shape[-1])
+    return q
+
+
+def retention_tensor(retention, H: int, device) -> torch.Tensor:
+    """selection.py:92-101: scalar in [0, 1] or a (H,) tensor -> device fp32 (H,)."""
+    if isinstance(retention, torch.Tensor):
+        if retention.shape != (H,):
+            raise ValueError(f"per-head retention must be shape ({H},); got {tuple(retention.shape)}")
+        return retention.to(device=device, dtype=torch.float32)
+    if not (0.0 <= float(retention) <= 1.0):
+        raise ValueError(f"scalar retention must be in [0, 1]; got {retention}")
+    return torch.full((H,), float(retention), dtype=torch.float32, device=device)

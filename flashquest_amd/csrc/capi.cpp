@@ -1,0 +1,431 @@
+// C ABI of libfq_hip: argument validation, workspace carving and launches.
+// Declarations and reference citations: include/fq_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "fq_common.h"
+
+namespace fq {
+hipError_t launch_quant_k(const void* k, int in_dtype, const int64_t* k_s, int B, int H, int S, int D,
+                          int page, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
+hipError_t launch_quant_v(const void* v, int in_dtype, const int64_t* v_s, int B, int H, int S, int D,
+                          int group, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
+hipError_t launch_wht(const void* x, int x_dtype, int64_t x_rs, void* out, int out_dtype, int64_t o_rs,
+                      int N, int D, const float* signs, int inverse, int arith, hipStream_t st);
+hipError_t launch_turbo_quant(const void* x, int in_dtype, const int64_t* x_s, int B, int H, int S, int D,
+                              uint8_t* msb, const int64_t* msb_s, uint8_t* lsb, const int64_t* lsb_s,
+                              void* scale, const int64_t* s_s, hipStream_t st);
+hipError_t launch_merge(const void* oa, const float* la, const void* ob, const float* lb, int dtype,
+                        int64_t rs_a, int64_t rs_b, void* out, int64_t rs_o, float* lse_out, int N, int D,
+                        hipStream_t st);
+hipError_t launch_tail(const void* q, const int64_t* q_s, const void* k, const int64_t* k_s, const void* v,
+                       const int64_t* v_s, int kv_dtype, void* out, const int64_t* o_s, float* lse, int B,
+                       int Hq, int Hkv, int T, int D, hipStream_t st);
+hipError_t launch_attn_turbo(const fq_turbo_cache& c, const QueryArgs& q, const Workspace& ws,
+                             const AttnLaunch& al, hipStream_t st);
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+static int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return FQ_OK;
+    return fail(FQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static int s_max_for(int P) { return (P + 3) / 4; }
+
+size_t workspace_bytes(int G, int P, int rows, int nrep, int D) {
+    const size_t sm = (size_t)s_max_for(P);
+    size_t n = 0;
+    n += align256(sizeof(int) * G);                     // n_sel
+    n += align256(sizeof(int) * (size_t)G * P);         // entries
+    n += align256(sizeof(float) * (size_t)G * rows * P);
+    n += align256(sizeof(float) * (size_t)G * sm * nrep * 2);
+    n += align256(sizeof(float) * (size_t)G * sm * nrep * D);
+    return n;
+}
+
+Workspace carve_workspace(void* base, int G, int P, int rows, int nrep, int D) {
+    Workspace w{};
+    char* p = (char*)base;
+    const size_t sm = (size_t)s_max_for(P);
+    w.n_sel = (int*)p;        p += align256(sizeof(int) * G);
+    w.entries = (int*)p;      p += align256(sizeof(int) * (size_t)G * P);
+    w.scores = (float*)p;     p += align256(sizeof(float) * (size_t)G * rows * P);
+    w.part_ml = (float*)p;    p += align256(sizeof(float) * (size_t)G * sm * nrep * 2);
+    w.part_acc = (float*)p;
+    w.s_max = (int)sm;
+    return w;
+}
+
+AttnLaunch choose_split(int G, int max_entries, int s_max) {
+    AttnLaunch al{};
+    if (max_entries < 1) max_entries = 1;
+    // aim for ~1536 workgroups in flight (6 per CU on 256 CUs), >= 1 page per wave
+    const long target = 1536;
+    long pps = ((long)G * max_entries + 4 * target - 1) / (4 * target) * 4;
+    if (pps < 4) pps = 4;
+    long splits = (max_entries + pps - 1) / pps;
+    if (splits > s_max) {
+        pps = ((max_entries + s_max - 1) / s_max + 3) / 4 * 4;
+        splits = (max_entries + pps - 1) / pps;
+    }
+    al.pages_per_split = (int)pps;
+    al.splits = (int)(splits < 1 ? 1 : splits);
+    return al;
+}
+
+static bool is_half(int dt) { return dt == FQ_BF16 || dt == FQ_F16; }
+static bool is_float_dtype(int dt) { return dt == FQ_BF16 || dt == FQ_F16 || dt == FQ_F32; }
+
+static int check_cache(const fq_int4_cache* c, Int4Cache* out) {
+    if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
+    if (!is_half(c->meta_dtype)) return fail(FQ_ERR_UNSUPPORTED, "metadata dtype must be bf16 or fp16");
+    if (c->L < 1 || c->B < 1 || c->H_kv < 1) return fail(FQ_ERR_INVALID, "empty L/B/H_kv");
+    if (c->P < 1 || c->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d outside [1, %d]", c->P, kMaxPages);
+    if (c->page_size < 1 || c->page_size > 4096) return fail(FQ_ERR_INVALID, "page_size=%d", c->page_size);
+    if (c->S < 0) return fail(FQ_ERR_INVALID, "negative S");
+    if (c->v_groups != 1 && c->v_groups != c->D / 32)
+        return fail(FQ_ERR_UNSUPPORTED, "V groups=%d must be 1 or D/32", c->v_groups);
+    if (!c->k_packed || !c->v_packed || !c->k_scale || !c->k_mn || !c->v_scale || !c->v_mn)
+        return fail(FQ_ERR_INVALID, "NULL cache tensor");
+    for (int i = 0; i < 4; ++i) {
+        if (c->k_strides[i] % 4 || c->v_strides[i] % 4)
+            return fail(FQ_ERR_UNSUPPORTED, "packed K/V strides must be multiples of 4 bytes");
+        if (c->ks_strides[i] % 8 || c->km_strides[i] % 8)
+            return fail(FQ_ERR_UNSUPPORTED, "K metadata strides must be multiples of 8 elements");
+    }
+    if (c->k_strides[4] != 1 || c->v_strides[4] != 1 || c->ks_strides[4] != 1 || c->km_strides[4] != 1 ||
+        c->vs_strides[4] != 1 || c->vm_strides[4] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "innermost cache axis must be contiguous");
+    if (((uintptr_t)c->k_packed | (uintptr_t)c->v_packed) & 3)
+        return fail(FQ_ERR_UNSUPPORTED, "packed K/V must be 4-byte aligned");
+    if (((uintptr_t)c->k_scale | (uintptr_t)c->k_mn) & 15)
+        return fail(FQ_ERR_UNSUPPORTED, "K metadata must be 16-byte aligned");
+    Int4Cache& o = *out;
+    o.kp = c->k_packed; o.vp = c->v_packed; o.ksc = c->k_scale; o.kmn = c->k_mn;
+    o.vsc = c->v_scale; o.vmn = c->v_mn;
+    for (int i = 0; i < 4; ++i) {
+        o.kp_s[i] = c->k_strides[i]; o.vp_s[i] = c->v_strides[i];
+        o.ksc_s[i] = c->ks_strides[i]; o.kmn_s[i] = c->km_strides[i];
+        o.vsc_s[i] = c->vs_strides[i]; o.vmn_s[i] = c->vm_strides[i];
+    }
+    o.L = c->L; o.B = c->B; o.Hkv = c->H_kv; o.S = c->S; o.P = c->P; o.D = c->D;
+    o.page = c->page_size; o.G = c->v_groups; o.meta_dtype = c->meta_dtype;
+    return FQ_OK;
+}
+
+static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
+    if (!q || !q->q || !q->out) return fail(FQ_ERR_INVALID, "query/output is NULL");
+    if (!is_float_dtype(q->q_dtype) || !is_float_dtype(q->out_dtype))
+        return fail(FQ_ERR_INVALID, "query/output dtype must be bf16, fp16 or fp32");
+    if (q->H_q < 1 || q->H_q % Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, Hkv);
+    const int nrep = q->H_q / Hkv;
+    if (nrep != 1 && nrep != 2 && nrep != 3 && nrep != 4 && nrep != 8)
+        return fail(FQ_ERR_UNSUPPORTED, "GQA ratio %d not in (1, 2, 3, 4, 8)", nrep);
+    QueryArgs& o = *out;
+    o.q = q->q; o.q_dtype = q->q_dtype; o.out = q->out; o.out_dtype = q->out_dtype; o.lse = q->lse;
+    for (int i = 0; i < 4; ++i) { o.q_s[i] = q->q_strides[i]; o.o_s[i] = q->o_strides[i]; }
+    for (int i = 0; i < 3; ++i) o.lse_s[i] = q->lse_strides[i];
+    o.Hq = q->H_q; o.nrep = nrep;
+    const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)D);
+    o.qk_scale = sm * kLog2e;
+    return FQ_OK;
+}
+
+}  // namespace fq
+
+using namespace fq;
+
+extern "C" {
+
+const char* fq_last_error(void) { return g_err.c_str(); }
+int fq_abi_version(void) { return 1; }
+
+size_t fq_workspace_bytes(const fq_int4_cache* cache, int32_t H_q) {
+    if (!cache || cache->H_kv < 1 || H_q % cache->H_kv) return 0;
+    const int G = cache->L * cache->B * cache->H_kv;
+    const int nrep = H_q / cache->H_kv;
+    return workspace_bytes(G, cache->P, nrep, nrep, cache->D);
+}
+
+int fq_page_scores_int4(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* k_scale,
+                        const int64_t ks_strides[4], const void* k_mn, const int64_t km_strides[4],
+                        int32_t meta_dtype, float* scores, const int64_t sc_strides[4], int32_t B,
+                        int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D, fq_stream_t stream) {
+    if (H_kv < 1 || H_q % H_kv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, H_kv);
+    if (D != 64 && D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", D);
+    if (!is_half(meta_dtype) || !is_float_dtype(q_dtype)) return fail(FQ_ERR_UNSUPPORTED, "dtype");
+    if (P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d > %d", P, kMaxPages);
+    if ((H_q / H_kv) * S_q > kMaxRows) return fail(FQ_ERR_UNSUPPORTED, "n_rep * S_q > %d", kMaxRows);
+    if (B == 0 || P == 0 || S_q == 0) return FQ_OK;
+    if (ks_strides[3] != 1 || km_strides[3] != 1 || ks_strides[2] % 8 || km_strides[2] % 8 ||
+        ks_strides[1] % 8 || km_strides[1] % 8 || ks_strides[0] % 8 || km_strides[0] % 8 ||
+        (((uintptr_t)k_scale | (uintptr_t)k_mn) & 15))
+        return fail(FQ_ERR_UNSUPPORTED, "K metadata must be 16-byte aligned with a contiguous channel axis");
+    Int4Cache c{};
+    c.ksc = k_scale; c.kmn = k_mn;
+    c.ksc_s[0] = 0; c.kmn_s[0] = 0;
+    for (int i = 0; i < 3; ++i) { c.ksc_s[i + 1] = ks_strides[i]; c.kmn_s[i + 1] = km_strides[i]; }
+    c.L = 1; c.B = B; c.Hkv = H_kv; c.P = P; c.D = D; c.meta_dtype = meta_dtype;
+    QueryArgs qa{};
+    qa.q = q; qa.q_dtype = q_dtype; qa.q_s[0] = 0; qa.Hq = H_q; qa.nrep = H_q / H_kv;
+    return hip_status(launch_score(c, qa, S_q, q_strides, scores, sc_strides, nullptr, 0, nullptr, 0, 0, -1,
+                                   nullptr, (hipStream_t)stream),
+                      "page scores");
+}
+
+int fq_select_pages(const float* scores, const int64_t sc_strides[4], int32_t B, int32_t H, int32_t S_q,
+                    int32_t P, const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                    uint8_t* mask, const int64_t mask_strides[4], fq_stream_t stream) {
+    if (P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d > %d", P, kMaxPages);
+    if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
+    if (B * H * S_q == 0 || P == 0) return FQ_OK;
+    return hip_status(launch_select_rows(scores, sc_strides, B, H, S_q, P, retention, num_sinks < 0 ? 0 : num_sinks,
+                                         window_pages < 0 ? 0 : window_pages, k_max, mask, mask_strides,
+                                         (hipStream_t)stream),
+                      "select pages");
+}
+
+int fq_compact_ids(const uint8_t* mask, const int64_t mask_strides[4], int32_t B, int32_t H, int32_t S_q,
+                   int32_t P, int32_t bucket_max, int32_t* ids, fq_stream_t stream) {
+    if (bucket_max < 1) return fail(FQ_ERR_INVALID, "BUCKET_MAX must be >= 1, got %d", bucket_max);
+    if (B * H * S_q == 0) return FQ_OK;
+    return hip_status(launch_compact_ids(mask, mask_strides, B, H, S_q, P, bucket_max, ids, (hipStream_t)stream),
+                      "compact ids");
+}
+
+static int attn_common(const fq_int4_cache* cache, const fq_query* query, void* workspace,
+                       size_t workspace_bytes_, Int4Cache* c, QueryArgs* q, Workspace* ws) {
+    int st = check_cache(cache, c);
+    if (st) return st;
+    st = check_query(query, c->D, c->Hkv, q);
+    if (st) return st;
+    if (((uintptr_t)q->q) & 1) return fail(FQ_ERR_UNSUPPORTED, "query must be 2-byte aligned");
+    const int G = c->L * c->B * c->Hkv;
+    const size_t need = workspace_bytes(G, c->P, q->nrep, q->nrep, c->D);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
+    if ((uintptr_t)workspace & 255) return fail(FQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    *ws = carve_workspace(workspace, G, c->P, q->nrep, q->nrep, c->D);
+    return FQ_OK;
+}
+
+int fq_sparse_int4_fwd_mask(const fq_int4_cache* cache, const fq_query* query, const uint8_t* mask,
+                            const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
+                            fq_stream_t stream) {
+    Int4Cache c{};
+    QueryArgs q{};
+    Workspace ws{};
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    if (st) return st;
+    if (!mask) return fail(FQ_ERR_INVALID, "selection mask is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    st = hip_status(launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, q.nrep, c.P, ws, s), "page union");
+    if (st) return st;
+    const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, c.P, ws.s_max);
+    return hip_status(launch_attn_int4(c, q, ws, al, s), "sparse int4 attention");
+}
+
+int fq_sparse_int4_fwd_ids(const fq_int4_cache* cache, const fq_query* query, const int32_t* ids,
+                           const int64_t id_strides[4], int32_t bucket, void* workspace, size_t workspace_bytes_,
+                           fq_stream_t stream) {
+    Int4Cache c{};
+    QueryArgs q{};
+    Workspace ws{};
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    if (st) return st;
+    if (!ids || bucket < 1) return fail(FQ_ERR_INVALID, "page id list is NULL or empty");
+    hipStream_t s = (hipStream_t)stream;
+    st = hip_status(launch_union_from_ids(ids, id_strides, bucket, c.L, c.B, c.Hkv, q.nrep, c.P, ws, s),
+                    "page union");
+    if (st) return st;
+    long bound = (long)q.nrep * bucket;
+    if (bound > c.P) bound = c.P;
+    const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, (int)bound, ws.s_max);
+    return hip_status(launch_attn_int4(c, q, ws, al, s), "sparse int4 attention");
+}
+
+static int quest_bound(const Int4Cache& c, const QueryArgs& q, int num_sinks, int window_pages, int k_max,
+                       int select_mode) {
+    long bound = c.P;
+    if (k_max >= 0) {
+        const long per = (long)k_max + num_sinks + window_pages;
+        bound = select_mode == FQ_SELECT_PER_Q_HEAD ? per * q.nrep : per;
+        if (bound > c.P) bound = c.P;
+    }
+    return (int)bound;
+}
+
+int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                         fq_stream_t stream) {
+    Int4Cache c{};
+    QueryArgs q{};
+    Workspace ws{};
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    if (st) return st;
+    if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
+    if (select_mode != FQ_SELECT_PER_Q_HEAD && select_mode != FQ_SELECT_PER_KV_HEAD_SUM)
+        return fail(FQ_ERR_INVALID, "select_mode=%d", select_mode);
+    if (num_sinks < 0) num_sinks = 0;
+    if (window_pages < 0) window_pages = 0;
+    if (k_max > c.P) k_max = c.P;
+    const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
+    int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};   // (L*B, H_q, 1, P) contiguous
+    float* sc_user = (scores_out && select_mode == FQ_SELECT_PER_Q_HEAD) ? scores_out : nullptr;
+    return hip_status(launch_score(c, q, 1, q4, sc_user, sc4, &ws, select_mode, retention, num_sinks, window_pages,
+                                   k_max, mask_out, (hipStream_t)stream),
+                      "score+select");
+}
+
+int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks,
+                         int32_t window_pages, int32_t k_max, int32_t select_mode, void* workspace,
+                         size_t workspace_bytes_, fq_stream_t stream) {
+    Int4Cache c{};
+    QueryArgs q{};
+    Workspace ws{};
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    if (st) return st;
+    if (num_sinks < 0) num_sinks = 0;
+    if (window_pages < 0) window_pages = 0;
+    if (k_max > c.P) k_max = c.P;
+    const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
+                                                                      select_mode), ws.s_max);
+    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream), "sparse int4 attention");
+}
+
+int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                         fq_stream_t stream) {
+    int st = fq_quest_select_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out,
+                                  mask_out, workspace, workspace_bytes_, stream);
+    if (st) return st;
+    return fq_quest_attend_int4(cache, query, num_sinks, window_pages, k_max, select_mode, workspace,
+                                workspace_bytes_, stream);
+}
+
+int fq_merge_attn(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b, int32_t dtype,
+                  int64_t o_row_stride_a, int64_t o_row_stride_b, void* out, int64_t out_row_stride,
+                  float* lse_out, int32_t N, int32_t D, fq_stream_t stream) {
+    if (!is_float_dtype(dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_merge(o_a, lse_a, o_b, lse_b, dtype, o_row_stride_a, o_row_stride_b, out,
+                                   out_row_stride, lse_out, N, D, (hipStream_t)stream),
+                      "merge");
+}
+
+int fq_dense_tail_attn(const void* q, const int64_t q_strides[3], const void* k, const int64_t k_strides[4],
+                       const void* v, const int64_t v_strides[4], int32_t kv_dtype, void* out,
+                       const int64_t o_strides[3], float* lse, int32_t B, int32_t H_q, int32_t H_kv, int32_t T,
+                       int32_t D, fq_stream_t stream) {
+    if (T < 1 || T > 1024) return fail(FQ_ERR_UNSUPPORTED, "tail length %d outside [1, 1024]", T);
+    if (D > 256) return fail(FQ_ERR_UNSUPPORTED, "head_dim %d > 256", D);
+    if (H_kv < 1 || H_q % H_kv) return fail(FQ_ERR_INVALID, "H_q must be divisible by H_kv");
+    if (!is_float_dtype(kv_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    if (B * H_q == 0) return FQ_OK;
+    return hip_status(launch_tail(q, q_strides, k, k_strides, v, v_strides, kv_dtype, out, o_strides, lse, B, H_q,
+                                  H_kv, T, D, (hipStream_t)stream),
+                      "tail attention");
+}
+
+int fq_quantize_k_int4(const void* k, int32_t in_dtype, const int64_t k_strides[4], int32_t B, int32_t H,
+                       int32_t S, int32_t D, int32_t page_size, uint8_t* packed, const int64_t p_strides[4],
+                       void* scale, const int64_t s_strides[4], void* mn, const int64_t m_strides[4],
+                       int32_t meta_dtype, fq_stream_t stream) {
+    if (D % 2) return fail(FQ_ERR_INVALID, "quantize_k_int4 requires even head_dim; got %d", D);
+    if (page_size < 1) return fail(FQ_ERR_INVALID, "page_size must be >= 1");
+    if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_quant_k(k, in_dtype, k_strides, B, H, S, D, page_size, packed, p_strides, scale,
+                                     s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream),
+                      "quantize k");
+}
+
+int fq_quantize_v_int4(const void* v, int32_t in_dtype, const int64_t v_strides[4], int32_t B, int32_t H,
+                       int32_t S, int32_t D, int32_t group, uint8_t* packed, const int64_t p_strides[4],
+                       void* scale, const int64_t s_strides[4], void* mn, const int64_t m_strides[4],
+                       int32_t meta_dtype, fq_stream_t stream) {
+    if (D % 2) return fail(FQ_ERR_INVALID, "quantize_v_int4 requires even head_dim; got %d", D);
+    if (group < 2 || group % 2 || D % group) return fail(FQ_ERR_INVALID, "bad V group %d for D=%d", group, D);
+    if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_quant_v(v, in_dtype, v_strides, B, H, S, D, group, packed, p_strides, scale,
+                                     s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream),
+                      "quantize v");
+}
+
+int fq_wht(const void* x, int32_t x_dtype, int64_t x_row_stride, void* out, int32_t out_dtype,
+           int64_t out_row_stride, int32_t N, int32_t D, const float* signs, int32_t inverse, int32_t arith_dtype,
+           fq_stream_t stream) {
+    if (D < 8 || D > 128 || (D & (D - 1)))
+        return fail(FQ_ERR_INVALID, "head_dim must be a positive power of 2 in [8, 128], got %d", D);
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(out_dtype) || !is_float_dtype(arith_dtype))
+        return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_wht(x, x_dtype, x_row_stride, out, out_dtype, out_row_stride, N, D, signs, inverse,
+                                 arith_dtype, (hipStream_t)stream),
+                      "wht");
+}
+
+int fq_quantize_turbo(const void* x, int32_t in_dtype, const int64_t x_strides[4], int32_t B, int32_t H,
+                      int32_t S, int32_t D, uint8_t* msb, const int64_t msb_strides[4], uint8_t* lsb,
+                      const int64_t lsb_strides[4], void* scale, const int64_t s_strides[4], fq_stream_t stream) {
+    if (D != 64 && D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", D);
+    if (!is_float_dtype(in_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_turbo_quant(x, in_dtype, x_strides, B, H, S, D, msb, msb_strides, lsb, lsb_strides,
+                                         scale, s_strides, (hipStream_t)stream),
+                      "quantize turbo");
+}
+
+size_t fq_turbo_workspace_bytes(const fq_turbo_cache* cache, int32_t H_q) {
+    if (!cache || cache->H_kv < 1 || H_q % cache->H_kv) return 0;
+    const int G = cache->L * cache->B * cache->H_kv;
+    const int nrep = H_q / cache->H_kv;
+    return workspace_bytes(G, cache->P, nrep, nrep, cache->D);
+}
+
+int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query, const uint8_t* mask,
+                             const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
+                             fq_stream_t stream) {
+    if (!cache) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    if (cache->D != 64 && cache->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", cache->D);
+    if (cache->P < 1 || cache->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", cache->P);
+    if (cache->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
+    for (int i = 0; i < 5; ++i)
+        if ((i == 4) != 0 && (cache->kmsb_strides[4] != 1 || cache->klsb_strides[4] != 1 ||
+                              cache->vmsb_strides[4] != 1 || cache->vlsb_strides[4] != 1))
+            return fail(FQ_ERR_UNSUPPORTED, "innermost turbo plane axis must be contiguous");
+    QueryArgs q{};
+    int st = check_query(query, cache->D, cache->H_kv, &q);
+    if (st) return st;
+    const int G = cache->L * cache->B * cache->H_kv;
+    const size_t need = workspace_bytes(G, cache->P, q.nrep, q.nrep, cache->D);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
+    Workspace ws = carve_workspace(workspace, G, cache->P, q.nrep, q.nrep, cache->D);
+    hipStream_t s = (hipStream_t)stream;
+    st = hip_status(launch_union_from_mask(mask, mask_strides, cache->L, cache->B, cache->H_kv, q.nrep, cache->P,
+                                           ws, s),
+                    "page union");
+    if (st) return st;
+    const AttnLaunch al = choose_split(G, cache->P, ws.s_max);
+    return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "sparse turbo attention");
+}
+
+}  // extern "C"

@@ -1,0 +1,386 @@
+// Quest page scoring from INT4 K metadata, top-k page selection and the
+// page-list builders that feed the attention kernel (gfx950).
+//
+// Reference semantics:
+//   scoring   src/flashquest/eager/criticality.py:128-163
+//   selection src/flashquest/eager/selection.py:65-126
+//   compact   src/flashquest/eager/selection.py:129-164
+#include "fq_common.h"
+
+namespace fq {
+namespace {
+
+// Per-group selection state shared by the fused scoring kernel and the
+// standalone selection kernel.
+struct SelectLds {
+    uint32_t keys[kMaxPages];
+    uint8_t qmask[kMaxPages];
+    int hist[256];
+    int tmp[8];
+};
+
+// Marks the top-k of keys[0..P) into qmask (|= bit), ties to the lower index.
+FQ_DEV void topk_into_qmask(SelectLds& s, int P, int k, uint8_t bit) {
+    const int tid = threadIdx.x;
+    if (k <= 0) return;
+    if (k >= P) {
+        for (int i = tid; i < P; i += kThreads) s.qmask[i] |= bit;
+        __syncthreads();
+        return;
+    }
+    int take_eq = 0;
+    const uint32_t T = block_radix_select(s.keys, P, k, s.hist, s.tmp, &take_eq);
+    // count of keys equal to T (all of them match the final prefix)
+    const int n_eq = s.hist[T & 255u];
+    if (take_eq >= n_eq) {
+        for (int i = tid; i < P; i += kThreads)
+            if (s.keys[i] >= T) s.qmask[i] |= bit;
+        __syncthreads();
+    } else {
+        for (int i = tid; i < P; i += kThreads)
+            if (s.keys[i] > T) s.qmask[i] |= bit;
+        block_compact(P, [&](int i) { return s.keys[i] == T; },
+                      [&](int i, int rank) { if (rank < take_eq) s.qmask[i] |= bit; }, s.tmp);
+    }
+}
+
+FQ_DEV int k_for(float r, int P, int k_max) {
+    // selection.py:103: ceil(fp32(r) * fp32(P)) clamped to [0, P]
+    float kf = ceilf(__fmul_rn(r, (float)P));
+    int k = kf <= 0.f ? 0 : (kf >= (float)P ? P : (int)kf);
+    if (k_max >= 0 && k > k_max) k = k_max;
+    return k;
+}
+
+FQ_DEV void force_pages(SelectLds& s, int P, int num_sinks, int window, uint8_t bits) {
+    const int ns = num_sinks < P ? num_sinks : P;
+    const int w = window < P ? window : P;
+    for (int i = threadIdx.x; i < P; i += kThreads)
+        if (i < ns || (w > 0 && i >= P - w)) s.qmask[i] |= bits;
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Scoring.  One workgroup scores `ppc` pages of one KV group for all of its
+// query rows; NL = D/8 lanes cooperate on a page, each owning 8 channels.
+// Order (matched by the CPU oracle): lane sums its 8 products left to right
+// (products rounded, no FMA), lanes combine by the 16-lane DPP butterfly;
+// score = t1 + t2 * 15.
+// ---------------------------------------------------------------------------
+struct ScoreParams {
+    Int4Cache c;
+    const void* q; int q_dtype; int64_t q_s[5];   // l, b, h_q, s_q, d
+    int Hq, nrep, Sq, rows;                       // rows = nrep * Sq
+    float* scores; int64_t sc_s[4];              // user output (l*B+b, h_q, s_q, p) or null
+    int ppc, nchunks;
+    float* ws_scores;                             // [G][nrep][P] (per-q) or [G][1][P] (summed), or null
+    int mode;
+};
+
+template <int D, typename MT>
+__global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
+    constexpr int NL = D / 8;
+    constexpr int PPP = kThreads / NL;           // pages per pass
+    __shared__ float s_q[kMaxRows][D];
+    __shared__ float s_qp[kMaxRows][D];
+
+    const Int4Cache& c = a.c;
+    const int g = blockIdx.y;
+    const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
+    const int tid = threadIdx.x;
+
+    for (int i = tid; i < a.rows * D; i += kThreads) {
+        const int r = i / D, d = i % D;
+        const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
+        const float v = load_any(a.q, a.q_dtype,
+                                 l * a.q_s[0] + b * a.q_s[1] + hq * a.q_s[2] + sq * a.q_s[3] + d * a.q_s[4]);
+        s_q[r][d] = v;
+        s_qp[r][d] = v > 0.f ? v : 0.f;
+    }
+    __syncthreads();
+
+    const int lane_in_page = tid % NL;
+    const int page_in_pass = tid / NL;
+    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
+    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
+    float* ws_scores = a.ws_scores ? a.ws_scores + (int64_t)g * a.rows * c.P : nullptr;
+
+    const int p_begin = blockIdx.x * a.ppc;
+    const int p_end = min(c.P, p_begin + a.ppc);
+    for (int p0 = p_begin; p0 < p_end; p0 += PPP) {
+        const int p = p0 + page_in_pass;
+        if (p < p_end) {
+            const uint4 sv = *(const uint4*)(ksc + p * c.ksc_s[3] + lane_in_page * 8);
+            const uint4 mv = *(const uint4*)(kmn + p * c.kmn_s[3] + lane_in_page * 8);
+            float sf[8], mf[8];
+            const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+            const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sf[2 * j] = half_to_f<MT>(sw[j]);
+                sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
+                mf[2 * j] = half_to_f<MT>(mw[j]);
+                mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
+            }
+            float acc_kv = 0.f;
+            for (int r = 0; r < a.rows; ++r) {
+                const float* qr = &s_q[r][lane_in_page * 8];
+                const float* qp = &s_qp[r][lane_in_page * 8];
+                float t1 = __fmul_rn(qr[0], mf[0]);
+                float t2 = __fmul_rn(qp[0], sf[0]);
+#pragma unroll
+                for (int j = 1; j < 8; ++j) {
+                    t1 = __fadd_rn(t1, __fmul_rn(qr[j], mf[j]));
+                    t2 = __fadd_rn(t2, __fmul_rn(qp[j], sf[j]));
+                }
+                t1 = row_sum<NL>(t1);
+                t2 = row_sum<NL>(t2);
+                const float sc = __fadd_rn(t1, __fmul_rn(t2, 15.0f));
+                if (lane_in_page == 0) {
+                    const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
+                    if (a.scores)
+                        a.scores[(l * c.B + b) * a.sc_s[0] + hq * a.sc_s[1] + sq * a.sc_s[2] + p * a.sc_s[3]] = sc;
+                    if (ws_scores && a.mode == FQ_SELECT_PER_Q_HEAD) ws_scores[r * c.P + p] = sc;
+                }
+                acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
+            }
+            if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
+                ws_scores[p] = acc_kv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-group selection for the fused decode: one workgroup per KV group reads
+// the group's scores (written by score_kernel), selects pages per query head
+// (or once per KV head), adds the forced pages and writes the ascending union
+// page list (page | selecting-heads mask << 16) and its length.
+// ---------------------------------------------------------------------------
+struct GroupSelectParams {
+    Workspace ws; int mode, nrep, Hkv, P;
+    const float* retention; int num_sinks, window, k_max;
+    uint8_t* mask_out;                            // (l, b, h_q, p) contiguous or null
+};
+
+__global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectParams a) {
+    __shared__ SelectLds s;
+    const int g = blockIdx.x, h = g % a.Hkv, tid = threadIdx.x, P = a.P;
+    const int rows = a.mode == FQ_SELECT_PER_Q_HEAD ? a.nrep : 1;
+    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
+    for (int i = tid; i < P; i += kThreads) s.qmask[i] = 0;
+    __syncthreads();
+    const uint8_t all_bits = (uint8_t)((1u << a.nrep) - 1u);
+    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
+        for (int r = 0; r < rows; ++r) {
+            for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[r * P + i]);
+            __syncthreads();
+            topk_into_qmask(s, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
+        }
+    } else {
+        float rmax = 0.f;
+        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, a.retention[h * a.nrep + r]);
+        for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[i]);
+        __syncthreads();
+        topk_into_qmask(s, P, k_for(rmax, P, a.k_max), all_bits);
+    }
+    force_pages(s, P, a.num_sinks, a.window, all_bits);
+    int* entries = a.ws.entries + (int64_t)g * P;
+    const int n = block_compact(P, [&](int i) { return s.qmask[i] != 0; },
+                                [&](int i, int rank) { entries[rank] = i | ((int)s.qmask[i] << 16); }, s.tmp);
+    if (a.mask_out) {
+        uint8_t* mo = a.mask_out + ((int64_t)g * a.nrep) * P;
+        for (int i = tid; i < a.nrep * P; i += kThreads) {
+            const int r = i / P, p = i % P;
+            mo[(int64_t)r * P + p] = (s.qmask[p] >> r) & 1;
+        }
+    }
+    if (tid == 0) a.ws.n_sel[g] = n;
+}
+
+// ---------------------------------------------------------------------------
+// Standalone selection: one workgroup per (b, h, s_q) score row.
+// ---------------------------------------------------------------------------
+struct SelectParams {
+    const float* scores; int64_t sc_s[4];
+    int B, H, Sq, P;
+    const float* retention; int num_sinks, window, k_max;
+    uint8_t* mask; int64_t m_s[4];
+};
+
+__global__ __launch_bounds__(kThreads) void select_rows_kernel(SelectParams a) {
+    __shared__ SelectLds s;
+    const int row = blockIdx.x;
+    const int sq = row % a.Sq, h = (row / a.Sq) % a.H, b = row / (a.Sq * a.H);
+    const int tid = threadIdx.x, P = a.P;
+    const float* src = a.scores + b * a.sc_s[0] + h * a.sc_s[1] + sq * a.sc_s[2];
+    for (int i = tid; i < P; i += kThreads) {
+        s.keys[i] = sortable_key(src[i * a.sc_s[3]]);
+        s.qmask[i] = 0;
+    }
+    __syncthreads();
+    topk_into_qmask(s, P, k_for(a.retention[h], P, a.k_max), 1);
+    force_pages(s, P, a.num_sinks, a.window, 1);
+    uint8_t* dst = a.mask + b * a.m_s[0] + h * a.m_s[1] + sq * a.m_s[2];
+    for (int i = tid; i < P; i += kThreads) dst[i * a.m_s[3]] = s.qmask[i];
+}
+
+// mask row -> descending ids, -1 padded (selection.py:153-163)
+struct CompactParams {
+    const uint8_t* mask; int64_t m_s[4];
+    int B, H, Sq, P, bucket;
+    int32_t* ids;
+};
+
+__global__ __launch_bounds__(kThreads) void compact_ids_kernel(CompactParams a) {
+    __shared__ int s_tmp[8];
+    const int row = blockIdx.x;
+    const int sq = row % a.Sq, h = (row / a.Sq) % a.H, b = row / (a.Sq * a.H);
+    const uint8_t* src = a.mask + b * a.m_s[0] + h * a.m_s[1] + sq * a.m_s[2];
+    int32_t* dst = a.ids + (int64_t)row * a.bucket;
+    const int P = a.P, bucket = a.bucket;
+    const int n = block_compact(P, [&](int i) { return src[(int64_t)(P - 1 - i) * a.m_s[3]] != 0; },
+                                [&](int i, int rank) { if (rank < bucket) dst[rank] = P - 1 - i; },
+                                s_tmp);
+    for (int i = n + threadIdx.x; i < bucket; i += kThreads) dst[i] = -1;
+}
+
+// bool mask (l, b, h_q, p) -> per-group union list
+struct UnionParams {
+    const uint8_t* mask; int64_t m_s[4];
+    const int32_t* ids; int64_t id_s[4]; int bucket;
+    int L, B, Hkv, nrep, P;
+    Workspace ws;
+};
+
+__global__ __launch_bounds__(kThreads) void union_from_mask_kernel(UnionParams a) {
+    __shared__ uint8_t qm[kMaxPages];
+    __shared__ int s_tmp[8];
+    const int g = blockIdx.x;
+    const int h = g % a.Hkv, b = (g / a.Hkv) % a.B, l = g / (a.Hkv * a.B);
+    const int P = a.P;
+    for (int i = threadIdx.x; i < P; i += kThreads) {
+        uint32_t bits = 0;
+        for (int r = 0; r < a.nrep; ++r) {
+            const int hq = h * a.nrep + r;
+            bits |= (a.mask[l * a.m_s[0] + b * a.m_s[1] + hq * a.m_s[2] + i * a.m_s[3]] != 0) << r;
+        }
+        qm[i] = (uint8_t)bits;
+    }
+    __syncthreads();
+    int* entries = a.ws.entries + (int64_t)g * P;
+    const int n = block_compact(P, [&](int i) { return qm[i] != 0; },
+                                [&](int i, int rank) { entries[rank] = i | ((int)qm[i] << 16); }, s_tmp);
+    if (threadIdx.x == 0) a.ws.n_sel[g] = n;
+}
+
+__global__ __launch_bounds__(kThreads) void union_from_ids_kernel(UnionParams a) {
+    __shared__ uint32_t qm[kMaxPages];
+    __shared__ int s_tmp[8];
+    const int g = blockIdx.x;
+    const int h = g % a.Hkv, b = (g / a.Hkv) % a.B, l = g / (a.Hkv * a.B);
+    const int P = a.P;
+    for (int i = threadIdx.x; i < P; i += kThreads) qm[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.nrep * a.bucket; i += kThreads) {
+        const int r = i / a.bucket, j = i % a.bucket;
+        const int hq = h * a.nrep + r;
+        const int id = a.ids[l * a.id_s[0] + b * a.id_s[1] + hq * a.id_s[2] + j * a.id_s[3]];
+        if (id >= 0 && id < P) atomicOr(&qm[id], 1u << r);
+    }
+    __syncthreads();
+    int* entries = a.ws.entries + (int64_t)g * P;
+    const int n = block_compact(P, [&](int i) { return qm[i] != 0; },
+                                [&](int i, int rank) { entries[rank] = i | ((int)qm[i] << 16); }, s_tmp);
+    if (threadIdx.x == 0) a.ws.n_sel[g] = n;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const int64_t* q4_s,
+                        float* scores, const int64_t* sc4_s, const Workspace* ws, int select_mode,
+                        const float* retention, int num_sinks, int window, int k_max,
+                        uint8_t* mask_out, hipStream_t st) {
+    ScoreParams a{};
+    a.c = c;
+    a.q = q.q; a.q_dtype = q.q_dtype;
+    // q strides: (l, b, h_q, s_q, d)
+    a.q_s[0] = q.q_s[0]; a.q_s[1] = q4_s[0]; a.q_s[2] = q4_s[1]; a.q_s[3] = q4_s[2]; a.q_s[4] = q4_s[3];
+    a.Hq = q.Hq; a.nrep = q.nrep; a.Sq = S_q; a.rows = q.nrep * S_q;
+    a.scores = scores;
+    if (sc4_s) for (int i = 0; i < 4; ++i) a.sc_s[i] = sc4_s[i];
+    const int G = c.L * c.B * c.Hkv;
+    // pages per chunk: aim for >= ~2 waves of workgroups over 256 CUs
+    const int ppp = kThreads / (c.D / 8);
+    int target_chunks = (2048 + G - 1) / G;
+    int ppc = (c.P + target_chunks - 1) / target_chunks;
+    ppc = ((ppc + ppp - 1) / ppp) * ppp;
+    if (ppc < ppp) ppc = ppp;
+    a.ppc = ppc;
+    a.nchunks = (c.P + ppc - 1) / ppc;
+    a.ws_scores = ws ? ws->scores : nullptr;
+    a.mode = select_mode;
+    if (a.rows > kMaxRows || c.P > kMaxPages) return hipErrorInvalidValue;
+    dim3 grid(a.nchunks, G);
+#define FQ_SCORE(D_, MT_) hipLaunchKernelGGL((score_kernel<D_, MT_>), grid, dim3(kThreads), 0, st, a)
+    if (c.D == 128) {
+        if (c.meta_dtype == FQ_BF16) FQ_SCORE(128, bf16); else FQ_SCORE(128, f16);
+    } else {
+        if (c.meta_dtype == FQ_BF16) FQ_SCORE(64, bf16); else FQ_SCORE(64, f16);
+    }
+#undef FQ_SCORE
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !ws) return e;
+    GroupSelectParams sp{};
+    sp.ws = *ws; sp.mode = select_mode; sp.nrep = q.nrep; sp.Hkv = c.Hkv; sp.P = c.P;
+    sp.retention = retention; sp.num_sinks = num_sinks; sp.window = window; sp.k_max = k_max;
+    sp.mask_out = mask_out;
+    hipLaunchKernelGGL(select_groups_kernel, dim3(G), dim3(kThreads), 0, st, sp);
+    return hipGetLastError();
+}
+
+hipError_t launch_select_rows(const float* scores, const int64_t* sc_s, int B, int H, int S_q, int P,
+                              const float* retention, int num_sinks, int window, int k_max,
+                              uint8_t* mask, const int64_t* m_s, hipStream_t st) {
+    SelectParams a{};
+    a.scores = scores;
+    for (int i = 0; i < 4; ++i) { a.sc_s[i] = sc_s[i]; a.m_s[i] = m_s[i]; }
+    a.B = B; a.H = H; a.Sq = S_q; a.P = P;
+    a.retention = retention; a.num_sinks = num_sinks; a.window = window; a.k_max = k_max;
+    a.mask = mask;
+    hipLaunchKernelGGL(select_rows_kernel, dim3(B * H * S_q), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_compact_ids(const uint8_t* mask, const int64_t* m_s, int B, int H, int S_q, int P,
+                              int bucket, int32_t* ids, hipStream_t st) {
+    CompactParams a{};
+    a.mask = mask;
+    for (int i = 0; i < 4; ++i) a.m_s[i] = m_s[i];
+    a.B = B; a.H = H; a.Sq = S_q; a.P = P; a.bucket = bucket; a.ids = ids;
+    hipLaunchKernelGGL(compact_ids_kernel, dim3(B * H * S_q), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_union_from_mask(const uint8_t* mask, const int64_t* m_s, int L, int B, int Hkv,
+                                  int nrep, int P, const Workspace& ws, hipStream_t st) {
+    UnionParams a{};
+    a.mask = mask;
+    for (int i = 0; i < 4; ++i) a.m_s[i] = m_s[i];
+    a.L = L; a.B = B; a.Hkv = Hkv; a.nrep = nrep; a.P = P; a.ws = ws;
+    hipLaunchKernelGGL(union_from_mask_kernel, dim3(L * B * Hkv), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bucket, int L, int B,
+                                 int Hkv, int nrep, int P, const Workspace& ws, hipStream_t st) {
+    UnionParams a{};
+    a.ids = ids;
+    for (int i = 0; i < 4; ++i) a.id_s[i] = id_s[i];
+    a.bucket = bucket;
+    a.L = L; a.B = B; a.Hkv = Hkv; a.nrep = nrep; a.P = P; a.ws = ws;
+    hipLaunchKernelGGL(union_from_ids_kernel, dim3(L * B * Hkv), dim3(kThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace fq

@@ -1,0 +1,190 @@
+"""The decode step of the reference's attention patch, on HIP.
+
+Mirrors the S_q == 1 branch of make_quest_persistent_forward
+(src/flashquest/eager/llama_persistent_patch.py:202-245): score the completed
+pages from their K metadata, select pages, run sparse attention over the
+packed cache, and merge with dense attention over the partial-page tail
+(_bf16_dense_attn_with_lse 30-47, _merge_two_attentions 50-61).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib as L
+from .. import _ops
+
+
+def bf16_dense_attn_with_lse(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor):
+    """llama_persistent_patch.py:30-47.  Q (B,H_q,1,D); K, V (B,H_kv,T,D).
+    Returns (O (B,H_q,1,D) bf16, lse (B,H_q,1) fp32, natural log)."""
+    L.require_device(Q, K, V)
+    B, H_q, _, D = Q.shape
+    H_kv, T = K.shape[1], K.shape[2]
+    if K.dtype != V.dtype or Q.dtype != K.dtype:
+        raise AssertionError("Q, K and V must share a dtype")
+    Q3 = Q[:, :, 0, :]
+    O = torch.empty(B, H_q, D, dtype=torch.bfloat16, device=Q.device)
+    lse = torch.empty(B, H_q, dtype=torch.float32, device=Q.device)
+    L.check(L.lib().fq_dense_tail_attn(Q3.data_ptr(), L.strides(Q3, 3), K.data_ptr(), L.strides(K, 4),
+                                       V.data_ptr(), L.strides(V, 4), L.dtype_code(K.dtype), O.data_ptr(),
+                                       L.strides(O, 3), lse.data_ptr(), B, H_q, H_kv, T, D,
+                                       L.stream_handle(Q.device)), "bf16_dense_attn_with_lse")
+    return O.unsqueeze(2), lse.unsqueeze(2)
+
+
+def merge_two_attentions(O_a, lse_a, O_b, lse_b) -> torch.Tensor:
+    """llama_persistent_patch.py:50-61: LSE-weighted merge, output in O_a's dtype."""
+    L.require_device(O_a, O_b)
+    D = O_a.shape[-1]
+    oa = O_a.reshape(-1, D)
+    ob = O_b.to(O_a.dtype).reshape(-1, D)
+    la = lse_a.reshape(-1).float().contiguous()
+    lb = lse_b.reshape(-1).float().contiguous()
+    out = torch.empty_like(oa)
+    N = oa.shape[0]
+    L.check(L.lib().fq_merge_attn(oa.data_ptr(), la.data_ptr(), ob.data_ptr(), lb.data_ptr(),
+                                  L.dtype_code(oa.dtype), oa.stride(0), ob.stride(0), out.data_ptr(),
+                                  out.stride(0), None, N, D, L.stream_handle(O_a.device)),
+            "merge_two_attentions")
+    return out.view(O_a.shape)
+
+
+def quest_decode_int4(
+    Q: torch.Tensor,
+    K_packed: torch.Tensor,
+    K_scale: torch.Tensor,
+    K_mn: torch.Tensor,
+    V_packed: torch.Tensor,
+    V_scale: torch.Tensor,
+    V_mn: torch.Tensor,
+    *,
+    retention: float | torch.Tensor,
+    num_sinks: int = 4,
+    window_pages: int = 2,
+    k_max_static: int | None = None,
+    page_size: int = 64,
+    select_mode: str = "per_q_head",
+    sm_scale: float | None = None,
+    return_lse: bool = True,
+    return_selection: bool = False,
+    out: torch.Tensor | None = None,
+):
+    """Fused score -> select -> sparse attention over completed pages.
+
+    One layer: Q (B,H_q,1,D), cache tensors 4D (B,H_kv,...).  L layers at once:
+    Q (L,B,H_q,1,D), cache tensors 5D (L,B,H_kv,...), every layer independent.
+    ``select_mode`` "per_q_head" is the reference's selection
+    (selection.py:103-117); "per_kv_head_sum" selects once per KV head from
+    the fp32 sum of its query heads' scores.
+    Returns (O like Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
+    """
+    if select_mode not in L.SELECT_MODES:
+        raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
+    L.require_device(Q, K_packed, K_scale)
+    if Q.shape[-2] != 1:
+        raise NotImplementedError(f"quest_decode_int4: decode-only (S_q={Q.shape[-2]})")
+    D = Q.shape[-1]
+    if D not in (64, 128):
+        raise NotImplementedError(f"head_dim={D} not in (64, 128)")
+    layered = Q.dim() == 5
+    Q3 = Q[..., 0, :]
+    H_q = Q3.shape[-2]
+    P = K_scale.shape[-2]
+    O3 = torch.empty_like(Q3) if out is None else out[..., 0, :]
+    lse = torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device) if return_lse else None
+    cache, keep = _ops.int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size)
+    if H_q % cache.H_kv:
+        raise ValueError(f"H_q={H_q} must be divisible by H_kv={cache.H_kv}")
+    query = _ops.query(Q3, O3, lse, sm_scale)
+    r = _ops.retention_tensor(retention, H_q, Q.device)
+    k_max = -1 if k_max_static is None else min(int(k_max_static), P)
+    mask = None
+    if return_selection:
+        mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
+    ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q))
+    L.check(L.lib().fq_quest_decode_int4(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
+                                         L.SELECT_MODES[select_mode], None,
+                                         None if mask is None else mask.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+            "quest_decode_int4")
+    O = O3.unsqueeze(-2)
+    lse_out = lse.unsqueeze(-1) if lse is not None else None
+    if return_selection:
+        return O, lse_out, mask
+    return O, lse_out
+
+
+class QuestDecoder:
+    """A reusable fused decode over fixed cache tensors (the bench's timed unit).
+
+    Builds the C descriptors once; ``select()`` and ``attend()`` launch the two
+    kernels of fq_quest_decode_int4 separately, ``__call__`` launches both.
+    Every launch goes to torch's current stream, so the calls can be captured
+    in a HIP graph after one eager call has sized the workspace.
+    """
+
+    def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
+                 window_pages=2, k_max_static=None, page_size=64, select_mode="per_q_head", sm_scale=None,
+                 out=None, lse=None, mask_out=None):
+        if select_mode not in L.SELECT_MODES:
+            raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
+        self.Q3 = Q[..., 0, :]
+        self.O3 = torch.empty_like(self.Q3) if out is None else out[..., 0, :]
+        self.lse = lse
+        self.cache, self._keep = _ops.int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size)
+        self.query = _ops.query(self.Q3, self.O3, lse, sm_scale)
+        H_q = self.Q3.shape[-2]
+        P = K_scale.shape[-2]
+        self.r = _ops.retention_tensor(retention, H_q, Q.device)
+        self.k_max = -1 if k_max_static is None else min(int(k_max_static), P)
+        self.sinks, self.window = int(num_sinks), int(window_pages)
+        self.mode = L.SELECT_MODES[select_mode]
+        self.mask_out = mask_out
+        self.device = Q.device
+        self.ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(self.cache, H_q))
+
+    def select(self):
+        L.check(L.lib().fq_quest_select_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
+                                             self.k_max, self.mode, None, L.ptr(self.mask_out), self.ws.data_ptr(),
+                                             self.ws.numel(), L.stream_handle(self.device)), "quest select")
+
+    def attend(self):
+        L.check(L.lib().fq_quest_attend_int4(self.cache, self.query, self.sinks, self.window, self.k_max,
+                                             self.mode, self.ws.data_ptr(), self.ws.numel(),
+                                             L.stream_handle(self.device)), "quest attend")
+
+    def __call__(self):
+        self.select()
+        self.attend()
+        return self.O3.unsqueeze(-2)
+
+
+def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: int, window_pages: int,
+                        page_size: int, k_max_static: int | None = None, select_mode: str = "per_q_head"):
+    """The decode branch of llama_persistent_patch.py:202-245 for one layer.
+
+    ``views`` is PersistentInt4KVCache.get_views(layer) (persistent_int4.py:134-159).
+    Returns attention output (B, H_q, 1, D) in q's dtype.
+    """
+    completed = views["completed_len"]
+    partial = views["partial_len"]
+    if completed == 0:
+        o, _ = bf16_dense_attn_with_lse(q, views["K_partial"], views["V_partial"])
+        return o.to(q.dtype)
+    o_sparse, lse_sparse = quest_decode_int4(
+        q, views["K_packed"], views["K_scale"], views["K_mn"], views["V_packed"], views["V_scale"],
+        views["V_mn"], retention=retention, num_sinks=num_sinks, window_pages=window_pages,
+        k_max_static=k_max_static, page_size=page_size, select_mode=select_mode)
+    if partial == 0:
+        return o_sparse
+    o_tail, lse_tail = bf16_dense_attn_with_lse(q.to(views["K_partial"].dtype), views["K_partial"],
+                                                views["V_partial"])
+    return merge_two_attentions(o_sparse, lse_sparse, o_tail, lse_tail)
+
+
+def static_bucket(retention_max: float, max_seq_len: int, page_size: int, num_sinks: int, window_pages: int):
+    """llama_persistent_patch.py:81-85: (k_max_static, bucket_max_static)."""
+    k = math.ceil(retention_max * (max_seq_len // page_size))
+    return k, k + num_sinks + window_pages

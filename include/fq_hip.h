@@ -1,0 +1,232 @@
+/*
+ * fq_hip.h — C ABI of the MI355X (gfx950) sparse INT4 / turbo decode-attention
+ * library (libfq_hip.so).
+ *
+ * Every entry point takes raw device pointers, int64 element strides, plain
+ * sizes and an explicit hipStream_t; nothing allocates device memory (callers
+ * pass a workspace sized by fq_workspace_bytes) and nothing synchronises.
+ * Every function returns an fq_status; fq_last_error() returns a message for
+ * the calling thread's most recent failure.
+ *
+ * The reference (Dialovos/flashquest) is Python + Triton with no FFI; each
+ * entry below replaces one Python operator of its decode path, cited as
+ * path:line relative to the reference root.  A caller maps tensors to
+ * (pointer, strides) exactly as the reference's Triton launch does
+ * (src/flashquest/kernel/sparse_int4_fwd.py:221-244).
+ *
+ * Layout contract (matches the reference's persistent caches,
+ * src/flashquest/cache/persistent_int4.py:46-59):
+ *   K_packed, V_packed : (L, B, H_kv, S, D/2) u8, byte k = code[2k] | code[2k+1] << 4
+ *   K_scale, K_mn      : (L, B, H_kv, P, D)    bf16 or fp16, per page and channel
+ *   V_scale, V_mn      : (L, B, H_kv, S, G)    bf16 or fp16, per token (G = 1, the
+ *                        reference) or per token and 32-channel group (G = D/32)
+ * The innermost axis of every cache tensor must have stride 1; the packed
+ * rows must be 4-byte aligned.  L (layers) is an extra batch axis: the
+ * reference calls the operators once per layer (L = 1, layer stride 0).
+ */
+#ifndef FQ_HIP_H
+#define FQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* fq_stream_t; /* == hipStream_t */
+
+/* Status codes.  The Python layer maps them to the reference's exception
+ * types (sparse_int4_fwd.py:187-204, selection.py:92-101, 147-150). */
+enum fq_status {
+    FQ_OK = 0,
+    FQ_ERR_INVALID = 1,     /* bad shape / stride / argument  -> ValueError / AssertionError */
+    FQ_ERR_UNSUPPORTED = 2, /* shape or dtype outside the kernels -> NotImplementedError   */
+    FQ_ERR_HIP = 3,         /* HIP runtime error (launch failure)  -> RuntimeError          */
+    FQ_ERR_WORKSPACE = 4    /* workspace missing or too small      -> RuntimeError          */
+};
+
+enum fq_dtype { FQ_BF16 = 0, FQ_F16 = 1, FQ_F32 = 2 };
+
+/* Page selection policy for the fused decode entry.
+ * FQ_SELECT_PER_Q_HEAD: top-k per query head (selection.py:103-117), the
+ *   reference's behaviour; the kernel reads the union over the GQA group.
+ * FQ_SELECT_PER_KV_HEAD_SUM: one top-k per KV head over the fp32 sum of the
+ *   group's query-head scores, applied to every query head of the group. */
+enum fq_select_mode { FQ_SELECT_PER_Q_HEAD = 0, FQ_SELECT_PER_KV_HEAD_SUM = 1 };
+
+/* Packed INT4 cache view (see the layout contract above). */
+typedef struct fq_int4_cache {
+    const uint8_t* k_packed; int64_t k_strides[5];
+    const uint8_t* v_packed; int64_t v_strides[5];
+    const void* k_scale;     int64_t ks_strides[5];
+    const void* k_mn;        int64_t km_strides[5];
+    const void* v_scale;     int64_t vs_strides[5];
+    const void* v_mn;        int64_t vm_strides[5];
+    int32_t meta_dtype;      /* FQ_BF16 or FQ_F16 */
+    int32_t L, B, H_kv;
+    int32_t S;               /* tokens in the view (completed_len); tokens >= S are masked */
+    int32_t P;               /* pages (K_scale.shape[-2]) */
+    int32_t D;               /* head dim: 64 or 128 */
+    int32_t page_size;       /* tokens per page, multiple of 4 (reference default 64) */
+    int32_t v_groups;        /* G: 1 (reference) or D/32 */
+} fq_int4_cache;
+
+/* Decode query and outputs: Q (L, B, H_q, D), O (L, B, H_q, D), lse (L, B, H_q). */
+typedef struct fq_query {
+    const void* q;   int32_t q_dtype;   int64_t q_strides[4];
+    void* out;       int32_t out_dtype; int64_t o_strides[4];
+    float* lse;      int64_t lse_strides[3];  /* may be NULL (return_lse=False) */
+    int32_t H_q;
+    float sm_scale;  /* <= 0 selects 1/sqrt(D) (sparse_int4_fwd.py:206-207) */
+} fq_query;
+
+/* TurboQuant K3-V3 cache (persistent_turbo.py:55-73):
+ * msb (L,B,H_kv,S,D/8), lsb (L,B,H_kv,S,D/4) u8; per-token scale (L,B,H_kv,S,1) bf16. */
+typedef struct fq_turbo_cache {
+    const uint8_t* k_msb; int64_t kmsb_strides[5];
+    const uint8_t* k_lsb; int64_t klsb_strides[5];
+    const void* k_scale;  int64_t kst_strides[5];
+    const uint8_t* v_msb; int64_t vmsb_strides[5];
+    const uint8_t* v_lsb; int64_t vlsb_strides[5];
+    const void* v_scale;  int64_t vst_strides[5];
+    int32_t L, B, H_kv, S, P, D, page_size;
+} fq_turbo_cache;
+
+const char* fq_last_error(void);
+int fq_abi_version(void);
+
+/* Bytes of workspace the attention / decode entries need for this cache and
+ * H_q (page lists, scores and split partials; no initialisation needed).
+ * Calls that share a workspace must be ordered (same stream). */
+size_t fq_workspace_bytes(const fq_int4_cache* cache, int32_t H_q);
+
+/* page_scores_int4_fast (src/flashquest/eager/criticality.py:128-163).
+ * Q (B, H_q, S_q, D) any dtype; meta (B, H_kv, P, D); scores (B, H_q, S_q, P) fp32.
+ * fp32 arithmetic in a fixed order (products rounded, no FMA). */
+int fq_page_scores_int4(const void* q, int32_t q_dtype, const int64_t q_strides[4],
+                        const void* k_scale, const int64_t ks_strides[4],
+                        const void* k_mn, const int64_t km_strides[4], int32_t meta_dtype,
+                        float* scores, const int64_t sc_strides[4],
+                        int32_t B, int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D,
+                        fq_stream_t stream);
+
+/* select_pages_vectorized (src/flashquest/eager/selection.py:65-126).
+ * scores (B, H, S_q, P) fp32; retention: device fp32 (H,); k_max: the
+ * reference's min(k_max_static, P), or -1 when k_max_static is None.
+ * mask (B, H, S_q, P) u8 (0/1, torch.bool storage).  Ties go to the lower page. */
+int fq_select_pages(const float* scores, const int64_t sc_strides[4],
+                    int32_t B, int32_t H, int32_t S_q, int32_t P,
+                    const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                    uint8_t* mask, const int64_t mask_strides[4], fq_stream_t stream);
+
+/* build_compact_selection (src/flashquest/eager/selection.py:129-164).
+ * mask (B, H, S_q, P) u8 -> ids (B, H, S_q, bucket_max) int32 contiguous:
+ * selected ids in descending order, then -1. */
+int fq_compact_ids(const uint8_t* mask, const int64_t mask_strides[4],
+                   int32_t B, int32_t H, int32_t S_q, int32_t P, int32_t bucket_max,
+                   int32_t* ids, fq_stream_t stream);
+
+/* flash_attn_sparse_int4_fwd (src/flashquest/kernel/sparse_int4_fwd.py:160-248).
+ * mask (L, B, H_q, P) u8.  Writes O and (if non-NULL) lse; an empty
+ * selection gives O = 0, lse = -inf. */
+int fq_sparse_int4_fwd_mask(const fq_int4_cache* cache, const fq_query* query,
+                            const uint8_t* mask, const int64_t mask_strides[4],
+                            void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* flash_attn_sparse_int4_fwd_compact (src/flashquest/kernel/sparse_int4_fwd_compact.py:153-244).
+ * ids (L, B, H_q, bucket) int32; -1 (and any id outside [0, P)) is skipped. */
+int fq_sparse_int4_fwd_ids(const fq_int4_cache* cache, const fq_query* query,
+                           const int32_t* ids, const int64_t id_strides[4], int32_t bucket,
+                           void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* One fused decode step over L layers: score (criticality.py:128-163) ->
+ * select (selection.py:65-126) -> sparse attention (sparse_int4_fwd.py:23-157),
+ * i.e. the completed-page part of llama_persistent_patch.py:220-234.
+ * retention: device fp32 (H_q,).  scores_out (L,B,rows,P) fp32 and
+ * mask_out (L,B,H_q,P) u8 are optional (NULL) diagnostics. */
+int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query,
+                         const float* retention, int32_t num_sinks, int32_t window_pages,
+                         int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out,
+                         void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* The two halves of fq_quest_decode_int4, for callers that time or overlap
+ * them separately.  fq_quest_select_int4 leaves the per-KV-group page lists in
+ * the workspace; fq_quest_attend_int4 consumes them (same cache, query,
+ * k_max / num_sinks / window_pages / select_mode and workspace). */
+int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query,
+                         const float* retention, int32_t num_sinks, int32_t window_pages,
+                         int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out,
+                         void* workspace, size_t workspace_bytes, fq_stream_t stream);
+int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* _merge_two_attentions (src/flashquest/eager/llama_persistent_patch.py:50-61).
+ * O_a/O_b/out (N, D) rows with row strides; lse (N,) fp32.  out dtype = O_a dtype. */
+int fq_merge_attn(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b,
+                  int32_t dtype, int64_t o_row_stride_a, int64_t o_row_stride_b,
+                  void* out, int64_t out_row_stride, float* lse_out,
+                  int32_t N, int32_t D, fq_stream_t stream);
+
+/* _bf16_dense_attn_with_lse (src/flashquest/eager/llama_persistent_patch.py:30-47).
+ * Q (B,H_q,D), K/V (B,H_kv,T,D) bf16 (T <= 1024); out (B,H_q,D) bf16, lse fp32. */
+int fq_dense_tail_attn(const void* q, const int64_t q_strides[3],
+                       const void* k, const int64_t k_strides[4],
+                       const void* v, const int64_t v_strides[4], int32_t kv_dtype,
+                       void* out, const int64_t o_strides[3], float* lse,
+                       int32_t B, int32_t H_q, int32_t H_kv, int32_t T, int32_t D,
+                       fq_stream_t stream);
+
+/* quantize_k_int4 (src/flashquest/kernel/kv_quant.py:131-171): K (B,H,S,D) of
+ * dtype in_dtype -> packed (B,H,S,D/2), scale/mn (B,H,P,D) of meta_dtype.
+ * Scale arithmetic in the input dtype, codes by fp32 IEEE division,
+ * round-half-even, clamp 0..15 (bit-exact with the reference). */
+int fq_quantize_k_int4(const void* k, int32_t in_dtype, const int64_t k_strides[4],
+                       int32_t B, int32_t H, int32_t S, int32_t D, int32_t page_size,
+                       uint8_t* packed, const int64_t p_strides[4],
+                       void* scale, const int64_t s_strides[4],
+                       void* mn, const int64_t m_strides[4], int32_t meta_dtype,
+                       fq_stream_t stream);
+
+/* quantize_v_int4 (src/flashquest/kernel/kv_quant.py:189-205): per token (and
+ * per `group` channels; group = D reproduces the reference), fp32 arithmetic. */
+int fq_quantize_v_int4(const void* v, int32_t in_dtype, const int64_t v_strides[4],
+                       int32_t B, int32_t H, int32_t S, int32_t D, int32_t group,
+                       uint8_t* packed, const int64_t p_strides[4],
+                       void* scale, const int64_t s_strides[4],
+                       void* mn, const int64_t m_strides[4], int32_t meta_dtype,
+                       fq_stream_t stream);
+
+/* wht_along_head_dim (src/flashquest/kernel/wht.py:17-41) over N rows of D
+ * (power of two <= 256).  signs (D,) fp32 or NULL: out = WHT(signs * x) when
+ * inverse == 0, out = signs * WHT(x) when inverse != 0.  arith_dtype rounds
+ * every butterfly stage like the reference's tensor dtype (FQ_F32 = exact fp32). */
+int fq_wht(const void* x, int32_t x_dtype, int64_t x_row_stride,
+           void* out, int32_t out_dtype, int64_t out_row_stride,
+           int32_t N, int32_t D, const float* signs, int32_t inverse, int32_t arith_dtype,
+           fq_stream_t stream);
+
+/* quantize_k_turbo / quantize_v_turbo (kv_quant.py:327-363, 381-405) for one
+ * tensor X (B,H,S,D) bf16: msb (B,H,S,D/8), lsb (B,H,S,D/4), scale (B,H,S,1) bf16. */
+int fq_quantize_turbo(const void* x, int32_t in_dtype, const int64_t x_strides[4],
+                      int32_t B, int32_t H, int32_t S, int32_t D,
+                      uint8_t* msb, const int64_t msb_strides[4],
+                      uint8_t* lsb, const int64_t lsb_strides[4],
+                      void* scale, const int64_t s_strides[4], fq_stream_t stream);
+
+/* flash_attn_sparse_turbo_fwd (src/flashquest/kernel/sparse_turbo_fwd.py:254-346):
+ * Q in the raw basis; the kernel rotates Q, attends over the selected pages of
+ * the rotated K3-V3 cache and rotates O back.  mask (L,B,H_q,P) u8. */
+int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
+                             const uint8_t* mask, const int64_t mask_strides[4],
+                             void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+size_t fq_turbo_workspace_bytes(const fq_turbo_cache* cache, int32_t H_q);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FQ_HIP_H */

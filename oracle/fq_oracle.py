@@ -252,8 +252,10 @@ def _lane_sum_butterfly(prod: np.ndarray) -> np.ndarray:
     """Fixed fp32 reduction over the last axis D.
 
     Lane j (of D/8) sums channels 8j..8j+7 left to right; lanes are then
-    combined by an xor butterfly with offsets D/16, ..., 2, 1 (every lane
-    ends with the same value).  This is the order the HIP scoring kernel uses.
+    combined the way the HIP kernel's DPP steps do: with 16 lanes first
+    v_j += v_(15-j) (row mirror), then within each 8 lanes v_j += v_(7-j)
+    (half mirror), then v_j += v_(j^1), then v_j += v_(j^2).  Each step adds a
+    value to its partner's, so every lane ends with the same sum.
     """
     D = prod.shape[-1]
     nl = D // 8
@@ -262,10 +264,12 @@ def _lane_sum_butterfly(prod: np.ndarray) -> np.ndarray:
     for i in range(1, 8):
         t = (t + p[..., i]).astype(F32)
     idx = np.arange(nl)
-    off = nl // 2
-    while off >= 1:
-        t = (t + t[..., idx ^ off]).astype(F32)
-        off //= 2
+    partners = []
+    if nl == 16:
+        partners.append(15 - idx)
+    partners += [(idx & ~7) | (7 - (idx & 7)), idx ^ 1, idx ^ 2]
+    for pa in partners:
+        t = (t + t[..., pa]).astype(F32)
     return t[..., 0]
 
 
@@ -435,6 +439,48 @@ def sparse_int4_attention(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
     S = keys.shape[-2]
     tm = page_mask_to_token_mask(page_mask, S, page_size)
     return exact_attention(Q, keys, vals, tm, sm_scale)
+
+
+def sparse_int4_attention_selected(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
+                                   page_mask, page_size=64, sm_scale=None):
+    """Same result as ``sparse_int4_attention`` but dequantises only the pages
+    some query head of a KV group selected (the work a sparse CPU path does).
+    fp32 logits/softmax; returns (O fp32, lse fp32)."""
+    Q = np.asarray(Q, F32)
+    B, Hq, D = Q.shape
+    Hkv = K_packed.shape[1]
+    S = K_packed.shape[2]
+    rep = Hq // Hkv
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    O = np.zeros((B, Hq, D), F32)
+    lse = np.full((B, Hq), -np.inf, F32)
+    for b in range(B):
+        for h in range(Hkv):
+            pm = page_mask[b, h * rep:(h + 1) * rep]           # (rep, P)
+            pages = np.nonzero(pm.any(0))[0]
+            if len(pages) == 0:
+                continue
+            tok = (pages[:, None] * page_size + np.arange(page_size)).reshape(-1)
+            keep = tok < S
+            tok = tok[keep]
+            codes_k = unpack_int4(K_packed[b, h, tok]).astype(F32)
+            codes_v = unpack_int4(V_packed[b, h, tok]).astype(F32)
+            pg = tok // page_size
+            k = codes_k * K_scale[b, h, pg] + K_mn[b, h, pg]
+            G = V_scale.shape[-1]
+            v = (codes_v.reshape(len(tok), G, D // G) * V_scale[b, h, tok][..., None]
+                 + V_mn[b, h, tok][..., None]).reshape(len(tok), D)
+            logits = (Q[b, h * rep:(h + 1) * rep] @ k.T) * F32(sm_scale)      # (rep, T)
+            tm = np.repeat(pm[:, pages], page_size, axis=1)[:, keep]
+            logits = np.where(tm, logits, -np.inf)
+            m = logits.max(1, keepdims=True)
+            ok = np.isfinite(m[:, 0])
+            p = np.where(tm, np.exp(logits - np.where(ok[:, None], m, 0)), 0).astype(F32)
+            l = p.sum(1)
+            O[b, h * rep:(h + 1) * rep] = np.where(ok[:, None], (p @ v) / np.where(l > 0, l, 1)[:, None], 0)
+            lse[b, h * rep:(h + 1) * rep] = np.where(ok, m[:, 0] + np.log(np.where(l > 0, l, 1)), -np.inf)
+    return O, lse
 
 
 def compact_ids_to_page_mask(ids, P: int):

@@ -144,3 +144,20 @@ def test_signed_rotation_preserves_dot_products():
     assert np.isclose(O.rotate_signed(x, s) @ O.rotate_signed(y, s), x @ y)
     assert np.allclose(O.unrotate_signed(O.rotate_signed(x, s), s), x)
     assert set(np.unique(s)) == {-1.0, 1.0}
+
+
+def test_selected_pages_path_equals_full_dequant_path():
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, D, ps = 2, 6, 2, 128, 64
+    S = ps * 10 + 5
+    K = O.round_bf16(rng.standard_normal((B, Hkv, S, D)).astype(np.float32))
+    V = O.round_bf16(rng.standard_normal((B, Hkv, S, D)).astype(np.float32))
+    Q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    kp, ks, km = O.quantize_k_int4(K, ps)
+    vp, vs, vm = O.quantize_v_int4(V, 32)
+    mask = rng.random((B, Hq, 11)) < 0.4
+    mask[1, 2] = False
+    a, la = O.sparse_int4_attention(Q, kp, ks, km, vp, vs, vm, mask, ps)
+    b, lb = O.sparse_int4_attention_selected(Q, kp, ks, km, vp, vs, vm, mask, ps)
+    assert np.allclose(a, b, atol=1e-5) and np.allclose(la[np.isfinite(la)], lb[np.isfinite(lb)], atol=1e-5)
+    assert np.array_equal(np.isfinite(la), np.isfinite(lb))
