@@ -12,7 +12,9 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfq_hip.so")
+# FQ_HIP_LIBRARY selects another build of the same library (e.g. a debug build).
+LIB_PATH = os.environ.get("FQ_HIP_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib",
+                                                            "libfq_hip.so")
 
 FQ_OK, FQ_ERR_INVALID, FQ_ERR_UNSUPPORTED, FQ_ERR_HIP, FQ_ERR_WORKSPACE = range(5)
 FQ_BF16, FQ_F16, FQ_F32 = 0, 1, 2

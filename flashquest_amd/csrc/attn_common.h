@@ -61,39 +61,12 @@ FQ_DEV void store_outputs(const QueryArgs& q, int l, int b, int h, const float (
         }
 }
 
-// Merges the lanes' row states and the workgroup's waves.  With one split the
-// workgroup writes O / lse directly; otherwise it stores its partial
-// (m, l, acc) for merge_splits_kernel.
+// Merges the 4 waves' (m, l, acc) states held in s (after a barrier); with one
+// split writes O / lse, otherwise stores the workgroup's split partial.
 template <int D, int NREP, bool ROT>
-FQ_DEV void finish_split(SplitLds<D, NREP>& s, float (&m)[NREP], float (&lsum)[NREP], float (&acc)[NREP][8],
-                         bool active, const QueryArgs& q, const Workspace& ws, int g, int l, int b, int h,
-                         int split, int splits) {
-    constexpr int NCC = D / 8;
-    const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
-    const int cc = lane % NCC, row = lane / NCC;
-    if (!active) return;     // uniform per workgroup
-#pragma unroll
-    for (int off = NCC; off < 64; off <<= 1) {
-#pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-            const float mo = __shfl_xor(m[r], off, 64);
-            float M, ws_, wo;
-            merge_weights(m[r], mo, M, ws_, wo);
-            lsum[r] = lsum[r] * ws_ + __shfl_xor(lsum[r], off, 64) * wo;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[r][j] = acc[r][j] * ws_ + __shfl_xor(acc[r][j], off, 64) * wo;
-            m[r] = M;
-        }
-    }
-    if (row == 0) {
-#pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-            if (cc == 0) { s.m[w][r] = m[r]; s.l[w][r] = lsum[r]; }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s.acc[w][r][cc * 8 + j] = acc[r][j];
-        }
-    }
-    __syncthreads();
+FQ_DEV void merge_waves_and_store(SplitLds<D, NREP>& s, const QueryArgs& q, const Workspace& ws, int g, int l,
+                                  int b, int h, int split, int splits) {
+    const int tid = threadIdx.x;
     const int64_t part = ((int64_t)g * ws.s_max + split) * NREP;
     for (int i = tid; i < NREP * D; i += kThreads) {
         const int r = i / D, d = i % D;
@@ -123,16 +96,53 @@ FQ_DEV void finish_split(SplitLds<D, NREP>& s, float (&m)[NREP], float (&lsum)[N
     }
 }
 
+// Merges the lanes' row states and the workgroup's waves.  With one split the
+// workgroup writes O / lse directly; otherwise it stores its partial
+// (m, l, acc) for merge_splits_kernel.
+template <int D, int NREP, bool ROT>
+FQ_DEV void finish_split(SplitLds<D, NREP>& s, float (&m)[NREP], float (&lsum)[NREP], float (&acc)[NREP][8],
+                         bool active, const QueryArgs& q, const Workspace& ws, int g, int l, int b, int h,
+                         int split, int splits) {
+    constexpr int NCC = D / 8;
+    const int lane = lane_id(), w = wave_id();
+    const int cc = lane % NCC, row = lane / NCC;
+    if (!active) return;     // uniform per workgroup
+#pragma unroll
+    for (int off = NCC; off < 64; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            const float mo = __shfl_xor(m[r], off, 64);
+            float M, ws_, wo;
+            merge_weights(m[r], mo, M, ws_, wo);
+            lsum[r] = lsum[r] * ws_ + __shfl_xor(lsum[r], off, 64) * wo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[r][j] = acc[r][j] * ws_ + __shfl_xor(acc[r][j], off, 64) * wo;
+            m[r] = M;
+        }
+    }
+    if (row == 0) {
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            if (cc == 0) { s.m[w][r] = m[r]; s.l[w][r] = lsum[r]; }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s.acc[w][r][cc * 8 + j] = acc[r][j];
+        }
+    }
+    __syncthreads();
+    merge_waves_and_store<D, NREP, ROT>(s, q, ws, g, l, b, h, split, splits);
+}
+
 // Split merge (the rule of _merge_two_attentions, llama_persistent_patch.py:50-61,
 // in the log2 domain): one workgroup per KV group over its used splits.
+// pps > 0: group g used ceil(n_sel / pps) splits; pps == 0: all `splits` were used.
 template <int D, int NREP, bool ROT>
 __global__ __launch_bounds__(kThreads) void merge_splits_kernel(QueryArgs q, Workspace ws, int Hkv, int B,
-                                                                int pps) {
+                                                                int pps, int splits) {
     __shared__ float s_out[NREP][D];
     __shared__ float s_L[NREP], s_M[NREP];
     const int g = blockIdx.x;
     const int h = g % Hkv, b = (g / Hkv) % B, l = g / (Hkv * B);
-    const int used = (ws.n_sel[g] + pps - 1) / pps;
+    const int used = pps > 0 ? (ws.n_sel[g] + pps - 1) / pps : splits;
     const int64_t base = (int64_t)g * ws.s_max * NREP;
     for (int i = threadIdx.x; i < NREP * D; i += kThreads) {
         const int r = i / D, d = i % D;

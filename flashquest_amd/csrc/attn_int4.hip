@@ -45,6 +45,7 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
     const int e0 = split * a.pps;
     const int e1 = min(n_sel, e0 + a.pps);
     const bool active = e0 < n_sel || a.splits == 1;
+    const bool has_tokens = c.S > 0;
 
     float m[NREP], lsum[NREP], bias[NREP], acc[NREP][8];
 #pragma unroll
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
         const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2] + gi;
         const int* entries = a.ws.entries + (int64_t)g * c.P;
 
-        for (int e = e0 + w; e < e1; e += NW) {
+        for (int e = e0 + w; has_tokens && e < e1; e += NW) {
             const int ent = entries[e];
             const int p = ent & 0xFFFF;
             const int qm = ent >> 16;
@@ -102,62 +103,72 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
                 Cp[r] = cpart;
             }
             const int tok0 = p * c.page;
-            for (int t0 = 0; t0 < c.page; t0 += 4 * NROW) {
-                uint32_t kw[4], vw[4];
-                float vs[4], vm[4];
-                bool valid[4];
+            for (int t0 = 0; t0 < c.page; t0 += 16 * NROW) {
+                // Issue every load of this block of 16 token rows first: rows past the
+                // page or the view are clamped to row S-1 (always in bounds) and masked.
+                uint32_t kw[16], vw[16];
+                uint16_t vsr[16], vmr[16];
+                int vmask = 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 16; ++i) {
                     const int t = t0 + row + NROW * i;
                     const int tok = tok0 + t;
-                    valid[i] = t < c.page && tok < c.S;
-                    kw[i] = valid[i] ? *(const uint32_t*)(kb + (int64_t)tok * c.kp_s[3]) : 0u;
-                    vw[i] = valid[i] ? *(const uint32_t*)(vb + (int64_t)tok * c.vp_s[3]) : 0u;
-                    vs[i] = valid[i] ? half_to_f<MT>(vsc[(int64_t)tok * c.vsc_s[3]]) : 0.f;
-                    vm[i] = valid[i] ? half_to_f<MT>(vmn[(int64_t)tok * c.vmn_s[3]]) : 0.f;
+                    const bool ok = t < c.page && tok < c.S;
+                    vmask |= ok << i;
+                    const int64_t tc = ok ? tok : c.S - 1;
+                    kw[i] = *(const uint32_t*)(kb + tc * c.kp_s[3]);
+                    vw[i] = *(const uint32_t*)(vb + tc * c.vp_s[3]);
+                    vsr[i] = vsc[tc * c.vsc_s[3]];
+                    vmr[i] = vmn[tc * c.vmn_s[3]];
                 }
-                float s[4][NREP];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float code[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) code[j] = (float)((kw[i] >> (4 * j)) & 15u);
-#pragma unroll
-                    for (int r = 0; r < NREP; ++r) {
-                        float d = Cp[r];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) d = fmaf(A[r][j], code[j], d);
-                        d = row_sum<NCC>(d);
-                        s[i][r] = (valid[i] && ((qm >> r) & 1)) ? d : -INFINITY;
-                    }
-                }
-                float vcode[4][8];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) vcode[i][j] = (float)((vw[i] >> (4 * j)) & 15u);
-#pragma unroll
-                for (int r = 0; r < NREP; ++r) {
-                    const float mx = fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r]));
-                    const float mnew = fmaxf(m[r], mx);
-                    if (mnew == -INFINITY) continue;
-                    const float alpha = m[r] == -INFINITY ? 0.f : exp2_fast(m[r] - mnew);
-                    float psum = 0.f;
-                    lsum[r] *= alpha;
-                    bias[r] *= alpha;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
+                for (int i0 = 0; i0 < 16; i0 += 4) {
+                    float s[4][NREP];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float pi = s[i][r] == -INFINITY ? 0.f : exp2_fast(s[i][r] - mnew);
-                        psum += pi;
-                        const float pv = pi * vs[i];
-                        bias[r] = fmaf(pi, vm[i], bias[r]);
+                        float code[8];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(pv, vcode[i][j], acc[r][j]);
+                        for (int j = 0; j < 8; ++j) code[j] = (float)((kw[i0 + i] >> (4 * j)) & 15u);
+#pragma unroll
+                        for (int r = 0; r < NREP; ++r) {
+                            float d = Cp[r];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) d = fmaf(A[r][j], code[j], d);
+                            d = row_sum<NCC>(d);
+                            s[i][r] = (((vmask >> (i0 + i)) & 1) && ((qm >> r) & 1)) ? d : -INFINITY;
+                        }
                     }
-                    lsum[r] += psum;
-                    m[r] = mnew;
+                    float vcode[4][8], vs[4], vm[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        vs[i] = half_to_f<MT>(vsr[i0 + i]);
+                        vm[i] = half_to_f<MT>(vmr[i0 + i]);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) vcode[i][j] = (float)((vw[i0 + i] >> (4 * j)) & 15u);
+                    }
+#pragma unroll
+                    for (int r = 0; r < NREP; ++r) {
+                        const float mx = fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r]));
+                        const float mnew = fmaxf(m[r], mx);
+                        if (mnew == -INFINITY) continue;
+                        const float alpha = m[r] == -INFINITY ? 0.f : exp2_fast(m[r] - mnew);
+                        float psum = 0.f;
+                        lsum[r] *= alpha;
+                        bias[r] *= alpha;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float pi = s[i][r] == -INFINITY ? 0.f : exp2_fast(s[i][r] - mnew);
+                            psum += pi;
+                            const float pv = pi * vs[i];
+                            bias[r] = fmaf(pi, vm[i], bias[r]);
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(pv, vcode[i][j], acc[r][j]);
+                        }
+                        lsum[r] += psum;
+                        m[r] = mnew;
+                    }
                 }
             }
         }
@@ -177,7 +188,7 @@ hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_int4_kernel<D, MT, GV, N>), grid, dim3(kThreads), 0, st, a);          \
         if (a.splits > 1)                                                                               \
             hipLaunchKernelGGL((merge_splits_kernel<D, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, a.pps);                                       \
+                               a.q, a.ws, a.c.Hkv, a.c.B, a.pps, a.splits);                                       \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4) FQ_CASE(8)
 #undef FQ_CASE
@@ -197,6 +208,7 @@ hipError_t launch_gv(const AttnParams& a, dim3 grid, hipStream_t st) {
 
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                             const AttnLaunch& al, hipStream_t st) {
+    if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st);
     AttnParams a{};
     a.c = c; a.q = q; a.ws = ws; a.pps = al.pages_per_split; a.splits = al.splits;
     dim3 grid(al.splits, c.L * c.B * c.Hkv);

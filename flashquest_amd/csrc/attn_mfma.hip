@@ -1,0 +1,541 @@
+// Split-K sparse GQA decode attention over packed INT4 pages on the gfx950
+// matrix cores (v_mfma_i32_16x16x64_i8).  Same semantics as attn_int4.hip
+// (src/flashquest/kernel/sparse_int4_fwd.py:23-157); specialised for
+// head_dim 128, 64-token pages and up to 4 query heads per KV head.
+//
+// Why MFMA on a memory-bound GEMV: with 3 query heads per KV head every INT4
+// code feeds 3 multiply-adds for q.k and 3 for p.v, which is more fp32 VALU
+// work per byte than the CU can issue at HBM speed.  Here the codes go to the
+// matrix core as int8 operands unchanged (a nibble mask is the whole unpack),
+// and the other operand is an exact fixed-point expansion in int8 digits:
+//   q.k : A = q_d * K_scale[p,d], scaled by (2^21-1)/max|A| per page into 3
+//         digits (rows 4r+digit, r = query head), plus sum_d q_d * K_mn[p,d];
+//   p.v : A = p_t * V_scale[t,g] / sigma_g, scaled by 32639 into 2 balanced
+//         8-bit digits (rows 4g+r, g = V channel group), plus sum_t p_t * V_mn[t,g].
+// int32 accumulation is exact; the only rounding is the digit split (2^-21
+// relative for q.k, better than 2^-13 for p.v) and the final fp32 combination.
+//
+// Single pass per page: each wave owns every 4th page of its workgroup's
+// split, loads a page (K, V, metadata) one page ahead of the one it computes,
+// and keeps p.v in int32 accumulators against a running reference: m[r] (the
+// softmax maximum, log2 domain) and sigma[g] (the V-scale bound).  A page that
+// exceeds either (rare after the first pages; both are set with a factor-2
+// headroom) rescales the accumulators once.  The wave states then merge like
+// the VALU kernel's, and splits meet in merge_splits_kernel.
+#include <algorithm>
+
+#include "attn_common.h"
+
+namespace fq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxWgPages = 256;            // pages of one workgroup split (entries staged in LDS)
+constexpr float kQkScale = 2097151.0f;      // 2^21 - 1
+constexpr float kPvScale = 32639.0f;        // largest X with balanced digits (X + 128) >> 8 <= 127
+
+struct MfmaParams {
+    Int4Cache c;
+    QueryArgs q;
+    Workspace ws;
+    int splits;
+};
+
+// A operands of one wave: [k-step or digit][row][k-group, XOR-swizzled][byte].
+// The k-group of row R is stored at position kg ^ ((R >> 2) & 3), which makes
+// the 16-byte operand reads (row = lane & 15, k-group = lane >> 4) conflict-free.
+struct WaveLds {
+    uint8_t aqk[2][16][4][16];      // q.k: [k-step][4r + digit][..]
+    uint8_t apv[2][16][4][16];      // p.v: [digit][4g + r][..]
+};
+FQ_DEV int swz(int row, int kg) { return kg ^ ((row >> 2) & 3); }
+
+FQ_DEV uint32_t lo_nib(uint32_t w) { return w & 0x0F0F0F0Fu; }
+FQ_DEV uint32_t hi_nib(uint32_t w) { return (w >> 4) & 0x0F0F0F0Fu; }
+
+// low bytes of four ints -> one dword (byte 0 = a)
+FQ_DEV uint32_t pack4(int a, int b, int c, int d) {
+    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);
+    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);
+    return ab | cd;
+}
+
+FQ_DEV float wave_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    return fmaxf(v, dpp<kDppXor2>(v));
+}
+FQ_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    return fmaxf(v, dpp<kDppXor2>(v));
+}
+FQ_DEV float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
+
+FQ_DEV void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+// Raw V metadata of one token: G halves (G = 4: 8 bytes, G = 1: 2 bytes).
+struct VMetaRaw { uint2 v; };
+
+template <typename MT, int G>
+FQ_DEV void unpack_vmeta(const VMetaRaw& r, float (&out)[G]) {
+    out[0] = half_to_f<MT>(r.v.x);
+    if constexpr (G == 4) {
+        out[1] = half_to_f<MT>(r.v.x >> 16);
+        out[2] = half_to_f<MT>(r.v.y);
+        out[3] = half_to_f<MT>(r.v.y >> 16);
+    }
+}
+
+// Page data is read with buffer loads.  Each tensor slice (l, b, h) gets one
+// buffer resource whose size is the slice's S tokens, so rows past S of a
+// partial last page read as zero instead of faulting; every per-lane offset is
+// (lane part) + (page part) + an immediate, the same for every page.
+struct SliceRsrc {
+    __amdgpu_buffer_rsrc_t k, v, vs, vm, ks, km;
+};
+
+FQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+FQ_DEV uint4 ld128(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+FQ_DEV uint32_t ld32(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+FQ_DEV uint2 ld64(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v[0], v[1]);
+}
+FQ_DEV uint32_t ld16(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+
+// Raw V metadata of tokens 16T + n16 (T = 0..3); off = byte offset of token n16.
+template <int G>
+FQ_DEV void load_vmeta(VMetaRaw (&m)[4], __amdgpu_buffer_rsrc_t r, int off) {
+#pragma unroll
+    for (int T = 0; T < 4; ++T) {
+        if constexpr (G == 4) m[T].v = ld64(r, off + T * 16 * 8);
+        else m[T].v = make_uint2(ld16(r, off + T * 16 * 2), 0u);
+    }
+}
+
+// Everything one page step reads.
+struct PageBuf {
+    uint4 kt[4];            // K codes: token 16T + n16, bytes 16*lg .. +15
+    uint4 sv, mv;           // K scale / min: channels ch_base .. +7
+    uint32_t vw[16];        // V codes: token 16*(j&3) + 4*(j>>2) + lg, channels 8*n16 .. +7
+    VMetaRaw vs[4], vm[4];  // V scale / min of tokens 16T + n16
+};
+
+// koff: (token n16, byte 16*lg); voff: (token lg, byte 4*n16); moff: token n16's V
+// metadata; soff: K scale / min channel ch_base.  All include the page part.
+template <int G>
+FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int moff, int soff) {
+#pragma unroll
+    for (int T = 0; T < 4; ++T) b.kt[T] = ld128(r.k, koff + T * 16 * 64);
+    b.sv = ld128(r.ks, soff);
+    b.mv = ld128(r.km, soff);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) b.vw[j] = ld32(r.v, voff + (16 * (j & 3) + 4 * (j >> 2)) * 64);
+    load_vmeta<G>(b.vs, r.vs, moff);
+    load_vmeta<G>(b.vm, r.vm, moff);
+}
+
+template <typename MT, int G, int NREP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_int4_mfma_kernel(MfmaParams a) {
+    constexpr int D = 128;
+    __shared__ SplitLds<D, NREP> s_split;
+    __shared__ WaveLds s_wave[4];
+    __shared__ int s_ent[kMaxWgPages];
+
+    const Int4Cache& c = a.c;
+    const QueryArgs& q = a.q;
+    const int g = blockIdx.y, split = blockIdx.x;
+    const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
+    const int L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+    const int n16 = L & 15, lg = L >> 4;
+    WaveLds& W = s_wave[w];
+    const int S = c.S;
+
+    // Prologue: this split's entries and q (as prescaled fp32) go to LDS; every
+    // load is unconditional (clamped index), so all are in flight before the wait.
+    static_assert(kMaxWgPages == kThreads, "one entry per thread");
+    __shared__ float s_q[NREP][D];
+    const int n_sel = a.ws.n_sel[g];
+    const int e0 = (int)((int64_t)n_sel * split / a.splits);       // balanced split: entries [e0, e1)
+    const int e1 = (int)((int64_t)n_sel * (split + 1) / a.splits);
+    {
+        const int tid = threadIdx.x;
+        const int ent = a.ws.entries[(int64_t)g * c.P + min(e0 + tid, c.P - 1)];
+        const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
+        const int i0 = tid, i1 = min(tid + kThreads, NREP * D - 1);
+        const int64_t o0 = qb + (i0 >> 7) * q.q_s[2] + (i0 & 127) * q.q_s[3];
+        const int64_t o1 = qb + (i1 >> 7) * q.q_s[2] + (i1 & 127) * q.q_s[3];
+        float v0, v1;
+        if (q.q_dtype == FQ_F32) {
+            v0 = ((const float*)q.q)[o0];
+            v1 = ((const float*)q.q)[o1];
+        } else {
+            const uint32_t u0 = ((const uint16_t*)q.q)[o0], u1 = ((const uint16_t*)q.q)[o1];
+            v0 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u0) : f16_bits_to_f(u0);
+            v1 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u1) : f16_bits_to_f(u1);
+        }
+        if (tid < e1 - e0) s_ent[tid] = ent;
+        if (i0 < NREP * D) s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+        if (tid + kThreads < NREP * D) s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+    }
+    __syncthreads();
+    // pages of this wave: entries w, w + 4, ... (wave-uniform)
+    const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + 3) / 4 : 0;
+
+    const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
+    const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
+    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
+    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
+    const uint16_t* vsc = (const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2];
+    const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2];
+
+    // A-operand slot of this lane for the q.k digits: k-step qs_s, k-group qs_kg,
+    // operand dword qs_jd; channels ch_base + 2b + par (b = 0..3); heads r0, r0+1.
+    const int Dq = L & 31, qs_s = Dq >> 4, qs_kg = (Dq >> 2) & 3, qs_jd = Dq & 3;
+    const int ch_base = 32 * qs_kg + 16 * qs_s + 8 * (qs_jd >> 1);
+    const int par = qs_jd & 1;
+    const int r0 = 2 * (L >> 5);
+    float qv[2][4];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) qv[hh][bb] = r0 + hh < NREP ? s_q[min(r0 + hh, NREP - 1)][ch_base + 2 * bb + par] : 0.f;
+
+    SliceRsrc rs;
+    rs.k = make_rsrc(kb, (int64_t)S * 64);
+    rs.v = make_rsrc(vb, (int64_t)S * 64);
+    rs.vs = make_rsrc(vsc, (int64_t)S * G * 2);
+    rs.vm = make_rsrc(vmn, (int64_t)S * G * 2);
+    rs.ks = make_rsrc(ksc, (int64_t)c.P * D * 2);
+    rs.km = make_rsrc(kmn, (int64_t)c.P * D * 2);
+    const int koff0 = n16 * 64 + 16 * lg, voff0 = lg * 64 + 4 * n16, moff0 = n16 * G * 2, soff0 = ch_base * 2;
+    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + 4 * k]); };
+    auto issue = [&](PageBuf& bf, int k) {
+        const int p = entry_of(k) & 0xFFFF;
+        // keep the scheduler from moving compute work in front of the loads
+        __builtin_amdgcn_sched_barrier(0);
+        load_page<G>(bf, rs, koff0 + p * 4096, voff0 + p * 4096, moff0 + p * 64 * G * 2, soff0 + p * D * 2);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // running references (wave-uniform) and accumulators
+    float m_run[NREP], s_run[G], inv_pv[G];
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) m_run[r] = -INFINITY;
+#pragma unroll
+    for (int gv = 0; gv < G; ++gv) { s_run[gv] = 0.f; inv_pv[gv] = 0.f; }
+    float m_lane = -INFINITY;                // m_run[lg]
+    v4i pacc[2][8];                          // [digit][tile]: component r = head, lane group lg = V group
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) pacc[d][t] = (v4i){0, 0, 0, 0};
+    float l_acc = 0.f, bias[G];              // head lg: sum p, sum p * V_mn[g] over this lane's tokens
+#pragma unroll
+    for (int gv = 0; gv < G; ++gv) bias[gv] = 0.f;
+
+    auto compute = [&](const PageBuf& cb, int k) {
+        const int ent = entry_of(k);
+        const int p = ent & 0xFFFF, qm = ent >> 16;
+        const int tok0 = p * 64;
+
+        // ---- q.k: digits of q * K_scale, then 2 MFMAs per 16-token tile
+        const uint32_t sw[4] = {cb.sv.x, cb.sv.y, cb.sv.z, cb.sv.w};
+        const uint32_t mw[4] = {cb.mv.x, cb.mv.y, cb.mv.z, cb.mv.w};
+        float A[2][4], cpart[2] = {0.f, 0.f}, amax = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const float sf = half_to_f<MT>(par ? sw[bb] >> 16 : sw[bb]);
+            const float mf = half_to_f<MT>(par ? mw[bb] >> 16 : mw[bb]);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                A[hh][bb] = qv[hh][bb] * sf;
+                cpart[hh] = fmaf(qv[hh][bb], mf, cpart[hh]);
+                amax = fmaxf(amax, fabsf(A[hh][bb]));
+            }
+        }
+        const float sigma = wave_max(amax);
+        const float inv = sigma > 0.f ? kQkScale * __builtin_amdgcn_rcpf(sigma) : 0.f;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            if (r0 + hh < NREP) {
+                int X[4];
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) X[bb] = (int)rintf(A[hh][bb] * inv);
+                const int row = 4 * (r0 + hh);
+                uint32_t* dst = (uint32_t*)&W.aqk[qs_s][row][swz(row, qs_kg)][4 * qs_jd];
+                dst[0] = pack4(X[0] >> 14, X[1] >> 14, X[2] >> 14, X[3] >> 14);
+                dst[64 / 4] = pack4((X[0] >> 7) & 127, (X[1] >> 7) & 127, (X[2] >> 7) & 127, (X[3] >> 7) & 127);
+                dst[128 / 4] = pack4(X[0] & 127, X[1] & 127, X[2] & 127, X[3] & 127);
+            }
+            float cs = cpart[hh];            // sum over the 32 lanes of this half (heads r0 + hh)
+            cs += __shfl_xor(cs, 16, 64);
+            cpart[hh] = row_sum<16>(cs);
+        }
+        // C for head lg lives in half lg >> 1, index lg & 1
+        const float c0 = __shfl(cpart[0], (lg >> 1) * 32, 64);
+        const float c1 = __shfl(cpart[1], (lg >> 1) * 32, 64);
+        const float Cr = (lg & 1) ? c1 : c0;
+        const float unscale = sigma * (1.0f / kQkScale);
+        wave_lds_fence();
+        const v4i a0 = *(const v4i*)&W.aqk[0][n16][swz(n16, lg)][0];
+        const v4i a1 = *(const v4i*)&W.aqk[1][n16][swz(n16, lg)][0];
+        float lg4[4], mp = -INFINITY;
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            const uint4 kt = cb.kt[T];
+            const v4i b0 = {(int)lo_nib(kt.x), (int)hi_nib(kt.x), (int)lo_nib(kt.y), (int)hi_nib(kt.y)};
+            const v4i b1 = {(int)lo_nib(kt.z), (int)hi_nib(kt.z), (int)lo_nib(kt.w), (int)hi_nib(kt.w)};
+            v4i acc = {0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+            const float f = fmaf((float)acc[0], 16384.f, fmaf((float)acc[1], 128.f, (float)acc[2]));
+            const float lgt = fmaf(f, unscale, Cr);
+            const bool ok = lg < NREP && ((qm >> lg) & 1) && tok0 + 16 * T + n16 < S;
+            lg4[T] = ok ? lgt : -INFINITY;
+            mp = fmaxf(mp, lg4[T]);
+        }
+
+        // ---- page maxima: logits per head (row lg), V scale per group (row lg reduces group lg)
+        float vs_t[4][G], vm_t[4][G];
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            unpack_vmeta<MT, G>(cb.vs[T], vs_t[T]);
+            unpack_vmeta<MT, G>(cb.vm[T], vm_t[T]);
+        }
+        float sp = 0.f;
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            float v = vs_t[T][0];
+#pragma unroll
+            for (int gv = 1; gv < G; ++gv) v = lg == gv ? vs_t[T][gv] : v;
+            sp = fmaxf(sp, v);
+        }
+        mp = row16_max(mp);
+        sp = row16_max(sp);
+        bool grow = false;
+        float mp_r[NREP], sp_g[G];
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            mp_r[r] = lane_value(mp, 16 * r);
+            grow |= mp_r[r] > m_run[r];
+        }
+#pragma unroll
+        for (int gv = 0; gv < G; ++gv) {
+            sp_g[gv] = lane_value(sp, 16 * gv);
+            grow |= sp_g[gv] > s_run[gv];
+        }
+        if (grow) {      // wave-uniform: raise the references, rescale what is accumulated
+            float am[NREP], as[G];
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) {
+                const float mn = mp_r[r] > m_run[r] ? mp_r[r] + 1.0f : m_run[r];
+                am[r] = mn == m_run[r] ? 1.0f : exp2_fast(m_run[r] - mn);
+                m_run[r] = mn;
+            }
+#pragma unroll
+            for (int gv = 0; gv < G; ++gv) {
+                const float sn = sp_g[gv] > s_run[gv] ? 2.0f * sp_g[gv] : s_run[gv];
+                as[gv] = sn > 0.f ? s_run[gv] / sn : 1.0f;
+                s_run[gv] = sn;
+                inv_pv[gv] = sn > 0.f ? kPvScale / sn : 0.f;
+            }
+            float a_lg = as[0], am_lg = am[0];
+            m_lane = m_run[0];
+#pragma unroll
+            for (int gv = 1; gv < G; ++gv) a_lg = lg == gv ? as[gv] : a_lg;
+#pragma unroll
+            for (int r = 1; r < NREP; ++r) {
+                am_lg = lg == r ? am[r] : am_lg;
+                m_lane = lg == r ? m_run[r] : m_lane;
+            }
+            l_acc *= am_lg;
+#pragma unroll
+            for (int gv = 0; gv < G; ++gv) bias[gv] *= am_lg;
+            if (k > 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float f = r < NREP ? am[r] * a_lg : 0.f;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const float v = fmaf((float)pacc[0][t][r], 256.f, (float)pacc[1][t][r]);
+                        pacc[0][t][r] = 0;
+                        pacc[1][t][r] = (int)rintf(v * f);
+                    }
+                }
+            }
+        }
+
+        // ---- p.v: digits of p * V_scale / sigma, then 2 MFMAs per 16-channel tile
+        float pr[4];
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            pr[T] = lg4[T] == -INFINITY ? 0.f : exp2_fast(lg4[T] - m_lane);
+            l_acc += pr[T];
+        }
+#pragma unroll
+        for (int gv = 0; gv < G; ++gv) {
+            int d0[4], d1[4];
+#pragma unroll
+            for (int T = 0; T < 4; ++T) {
+                const int X = (int)rintf(pr[T] * vs_t[T][gv] * inv_pv[gv]);
+                d0[T] = (X + 128) >> 8;
+                d1[T] = X - (d0[T] << 8);
+                bias[gv] = fmaf(pr[T], vm_t[T][gv], bias[gv]);
+            }
+            // operand k = 16*kg + 4*ai + bb carries token 16*bb + 4*ai + kg (the order of
+            // the V dwords below), so token 16T + n16 sits at kg = n16&3, byte 4*(n16>>2) + T
+            if (lg < NREP) {
+                const int row = 4 * gv + lg;
+                uint32_t* dst = (uint32_t*)&W.apv[0][row][swz(row, n16 & 3)][4 * (n16 >> 2)];
+                dst[0] = pack4(d0[0], d0[1], d0[2], d0[3]);
+                dst[1024 / 4] = pack4(d1[0], d1[1], d1[2], d1[3]);
+            }
+        }
+        wave_lds_fence();
+        const v4i ap0 = *(const v4i*)&W.apv[0][n16][swz(n16, lg)][0];
+        const v4i ap1 = *(const v4i*)&W.apv[1][n16][swz(n16, lg)][0];
+        uint32_t U[4][4];     // [ai][cc]
+#pragma unroll
+        for (int ai = 0; ai < 4; ++ai) {
+            // 4x4 byte transpose: U[ai][cc] byte bb = byte cc of vw[4*ai + bb]
+            const uint32_t x0 = cb.vw[4 * ai], x1 = cb.vw[4 * ai + 1], x2 = cb.vw[4 * ai + 2], x3 = cb.vw[4 * ai + 3];
+            const uint32_t t0 = __builtin_amdgcn_perm(x1, x0, 0x06020400u);
+            const uint32_t t1 = __builtin_amdgcn_perm(x1, x0, 0x07030501u);
+            const uint32_t t2 = __builtin_amdgcn_perm(x3, x2, 0x06020400u);
+            const uint32_t t3 = __builtin_amdgcn_perm(x3, x2, 0x07030501u);
+            U[ai][0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+            U[ai][1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+            U[ai][2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+            U[ai][3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+        }
+        // tile 2cc: low nibbles (channel 8*n16 + 2cc), tile 2cc+1: high nibbles
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const v4i blo = {(int)lo_nib(U[0][cc]), (int)lo_nib(U[1][cc]), (int)lo_nib(U[2][cc]), (int)lo_nib(U[3][cc])};
+            const v4i bhi = {(int)hi_nib(U[0][cc]), (int)hi_nib(U[1][cc]), (int)hi_nib(U[2][cc]), (int)hi_nib(U[3][cc])};
+            pacc[0][2 * cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap0, blo, pacc[0][2 * cc], 0, 0, 0);
+            pacc[1][2 * cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap1, blo, pacc[1][2 * cc], 0, 0, 0);
+            pacc[0][2 * cc + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap0, bhi, pacc[0][2 * cc + 1], 0, 0, 0);
+            pacc[1][2 * cc + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap1, bhi, pacc[1][2 * cc + 1], 0, 0, 0);
+        }
+        wave_lds_fence();
+    };
+
+    // One page in flight ahead of the one being computed.  Past the end the last
+    // page is reloaded, so every step issues the same loads and the wait before
+    // each compute is the same on every path.
+    {
+        PageBuf b0, b1;
+        if (n_mine > 0) issue(b0, 0);
+        for (int k = 0; k < n_mine; k += 2) {
+            issue(b1, min(k + 1, n_mine - 1));
+            compute(b0, k);
+            issue(b0, min(k + 2, n_mine - 1));
+            if (k + 1 < n_mine) compute(b1, k + 1);
+        }
+    }
+
+    // ------------------------------------------------ wave state -> LDS
+    l_acc = row_sum<16>(l_acc);
+#pragma unroll
+    for (int gv = 0; gv < G; ++gv) bias[gv] = row_sum<16>(bias[gv]);
+    const int ug = G == 1 ? 0 : (n16 >> 2);      // channel group of this lane's columns
+    float bsel = bias[0], ssel = s_run[0];
+#pragma unroll
+    for (int gv = 1; gv < G; ++gv) {
+        if (ug == gv) { bsel = bias[gv]; ssel = s_run[gv]; }
+    }
+    const float pv_unscale = ssel * (1.0f / kPvScale);
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) {
+        const int src = 16 * r + n16;
+        const float ll = __shfl(l_acc, src, 64);
+        const float bb = __shfl(bsel, src, 64);
+        if (lg == ug) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float v = fmaf((float)pacc[0][t][r], 256.f, (float)pacc[1][t][r]);
+                s_split.acc[w][r][8 * n16 + t] = fmaf(v, pv_unscale, bb);
+            }
+            if (n16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = ll; }
+        }
+    }
+    __syncthreads();
+    merge_waves_and_store<D, NREP, false>(s_split, q, a.ws, g, l, b, h, split, a.splits);
+}
+
+template <typename MT, int G>
+hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
+    switch (a.q.nrep) {
+#define FQ_CASE(N)                                                                                     \
+    case N:                                                                                            \
+        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N>), grid, dim3(kThreads), 0, st, a);         \
+        if (a.splits > 1)                                                                              \
+            hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
+                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits);                                \
+        break;
+        FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
+#undef FQ_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Splits per KV group: enough workgroups to keep every CU busy in one pass
+// (two resident per CU), at least 8 pages per split, at most kMaxWgPages.
+int mfma_splits(int groups, int max_entries, int s_max) {
+    constexpr int kResident = 2 * 256;
+    int s = kResident / (groups > 0 ? groups : 1);
+    s = std::min(s, (max_entries + 7) / 8);
+    s = std::max(s, (max_entries + kMaxWgPages - 1) / kMaxWgPages);
+    s = std::max(s, 1);
+    return std::min(s, s_max);
+}
+
+}  // namespace
+
+bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
+    if (c.D != 128 || c.page != 64 || q.nrep > 4) return false;
+    if (c.G != 1 && c.G != 4) return false;
+    if ((int64_t)al.s_max * kMaxWgPages < al.max_entries) return false;
+    // contiguous 64-byte rows of codes, G-element rows of V metadata, 128-element
+    // rows of K metadata; 16-byte aligned code rows and 8-byte aligned metadata
+    if (c.kp_s[3] != 64 || c.vp_s[3] != 64 || c.vsc_s[3] != c.G || c.vmn_s[3] != c.G) return false;
+    if (c.ksc_s[3] != 128 || c.kmn_s[3] != 128) return false;
+    if (c.kp_s[2] % 16 || c.kp_s[1] % 16 || c.kp_s[0] % 16 || ((uintptr_t)c.kp & 15)) return false;
+    if (c.vp_s[2] % 16 || c.vp_s[1] % 16 || c.vp_s[0] % 16 || ((uintptr_t)c.vp & 15)) return false;
+    if (c.ksc_s[2] % 8 || c.ksc_s[1] % 8 || c.ksc_s[0] % 8 || ((uintptr_t)c.ksc & 15)) return false;
+    if (c.kmn_s[2] % 8 || c.kmn_s[1] % 8 || c.kmn_s[0] % 8 || ((uintptr_t)c.kmn & 15)) return false;
+    if (c.G == 4 && (c.vsc_s[2] % 4 || c.vmn_s[2] % 4 || c.vsc_s[1] % 4 || c.vmn_s[1] % 4 || c.vsc_s[0] % 4 ||
+                     c.vmn_s[0] % 4 || ((uintptr_t)c.vsc & 7) || ((uintptr_t)c.vmn & 7)))
+        return false;
+    return true;
+}
+
+hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
+                                 hipStream_t st) {
+    MfmaParams a{};
+    a.c = c; a.q = q; a.ws = ws;
+    const int groups = c.L * c.B * c.Hkv;
+    a.splits = mfma_splits(groups, al.max_entries, al.s_max);
+    dim3 grid(a.splits, groups);
+    if (c.meta_dtype == FQ_BF16)
+        return c.G == 4 ? launch_mfma_nrep<bf16, 4>(a, grid, st) : launch_mfma_nrep<bf16, 1>(a, grid, st);
+    return c.G == 4 ? launch_mfma_nrep<f16, 4>(a, grid, st) : launch_mfma_nrep<f16, 1>(a, grid, st);
+}
+
+}  // namespace fq

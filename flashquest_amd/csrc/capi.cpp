@@ -81,6 +81,7 @@ AttnLaunch choose_split(int G, int max_entries, int s_max) {
     const long target = 1536;
     long pps = ((long)G * max_entries + 4 * target - 1) / (4 * target) * 4;
     if (pps < 4) pps = 4;
+    if (pps > 32) pps = 32;          // <= 8 pages per wave (the MFMA kernel keeps their logits in LDS)
     long splits = (max_entries + pps - 1) / pps;
     if (splits > s_max) {
         pps = ((max_entries + s_max - 1) / s_max + 3) / 4 * 4;
@@ -88,6 +89,8 @@ AttnLaunch choose_split(int G, int max_entries, int s_max) {
     }
     al.pages_per_split = (int)pps;
     al.splits = (int)(splits < 1 ? 1 : splits);
+    al.max_entries = max_entries;
+    al.s_max = s_max;
     return al;
 }
 

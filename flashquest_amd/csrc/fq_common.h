@@ -195,6 +195,8 @@ struct Workspace {
 struct AttnLaunch {
     int pages_per_split;
     int splits;
+    int max_entries;      // bound on any group's union-list length
+    int s_max;            // split partials the workspace holds per group
 };
 
 // Host-side helpers implemented in capi.cpp.
@@ -218,5 +220,8 @@ hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bu
                                  int Hkv, int nrep, int P, const Workspace& ws, hipStream_t st);
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                             const AttnLaunch& al, hipStream_t st);
+bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
+                                 const AttnLaunch& al, hipStream_t st);
 
 }  // namespace fq
