@@ -32,8 +32,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxWgPages = 256;            // pages of one workgroup split (entries staged in LDS)
-constexpr float kQkScale = 2097151.0f;      // 2^21 - 1
-constexpr float kPvScale = 32639.0f;        // largest X with balanced digits (X + 128) >> 8 <= 127
+constexpr float kQkScale = 8323071.0f;      // 2^23 - 2^16 - 1: |X| <= this keeps 3 balanced digits in int8
+constexpr float kPvScale = 32639.0f;        // 2^15 - 129: X + 128 < 2^15 keeps 2 balanced digits in int8
 
 struct MfmaParams {
     Int4Cache c;
@@ -54,12 +54,16 @@ FQ_DEV int swz(int row, int kg) { return kg ^ ((row >> 2) & 3); }
 FQ_DEV uint32_t lo_nib(uint32_t w) { return w & 0x0F0F0F0Fu; }
 FQ_DEV uint32_t hi_nib(uint32_t w) { return (w >> 4) & 0x0F0F0F0Fu; }
 
-// low bytes of four ints -> one dword (byte 0 = a)
-FQ_DEV uint32_t pack4(int a, int b, int c, int d) {
-    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);
-    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);
-    return ab | cd;
+// Balanced base-256 digits: Y = X + 128 * (1 + 256 + ...) >= 0, and digit i of X
+// is byte i of Y minus 128 (as int8: byte ^ 0x80), so sum_i 256^i (b_i - 128) = X.
+// byte_i(y0..y3): byte i of four values packed into one dword (byte 0 from y0).
+template <int I>
+FQ_DEV uint32_t byte_i(uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3) {
+    constexpr uint32_t lo = 0x0C0C0000u | ((4u + I) << 8) | I;          // y0.bI, y1.bI, 0, 0
+    constexpr uint32_t hi = ((4u + I) << 24) | ((uint32_t)I << 16) | 0x0C0Cu;  // 0, 0, y2.bI, y3.bI
+    return __builtin_amdgcn_perm(y1, y0, lo) | __builtin_amdgcn_perm(y3, y2, hi);
 }
+constexpr uint32_t kDigitFlip = 0x80808080u;
 
 FQ_DEV float wave_max(float v) {
     v = fmaxf(v, __shfl_xor(v, 32, 64));
@@ -237,7 +241,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     for (int r = 0; r < NREP; ++r) m_run[r] = -INFINITY;
 #pragma unroll
     for (int gv = 0; gv < G; ++gv) { s_run[gv] = 0.f; inv_pv[gv] = 0.f; }
-    float m_lane = -INFINITY;                // m_run[lg]
+    float m_lane = 0.f;                      // m_run[lg], or 0 while head lg has no logit yet
     v4i pacc[2][8];                          // [digit][tile]: component r = head, lane group lg = V group
 #pragma unroll
     for (int d = 0; d < 2; ++d)
@@ -272,14 +276,15 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             if (r0 + hh < NREP) {
-                int X[4];
+                // Y = round(A * inv) + 0x808080, rounded by the fp32 add itself
+                uint32_t Y[4];
 #pragma unroll
-                for (int bb = 0; bb < 4; ++bb) X[bb] = (int)rintf(A[hh][bb] * inv);
+                for (int bb = 0; bb < 4; ++bb) Y[bb] = (uint32_t)fmaf(A[hh][bb], inv, 8421504.0f);
                 const int row = 4 * (r0 + hh);
                 uint32_t* dst = (uint32_t*)&W.aqk[qs_s][row][swz(row, qs_kg)][4 * qs_jd];
-                dst[0] = pack4(X[0] >> 14, X[1] >> 14, X[2] >> 14, X[3] >> 14);
-                dst[64 / 4] = pack4((X[0] >> 7) & 127, (X[1] >> 7) & 127, (X[2] >> 7) & 127, (X[3] >> 7) & 127);
-                dst[128 / 4] = pack4(X[0] & 127, X[1] & 127, X[2] & 127, X[3] & 127);
+                dst[0] = byte_i<2>(Y[0], Y[1], Y[2], Y[3]) ^ kDigitFlip;           // row 4r: weight 65536
+                dst[64 / 4] = byte_i<1>(Y[0], Y[1], Y[2], Y[3]) ^ kDigitFlip;      // row 4r+1: 256
+                dst[128 / 4] = byte_i<0>(Y[0], Y[1], Y[2], Y[3]) ^ kDigitFlip;     // row 4r+2: 1
             }
             float cs = cpart[hh];            // sum over the 32 lanes of this half (heads r0 + hh)
             cs += __shfl_xor(cs, 16, 64);
@@ -302,7 +307,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             v4i acc = {0, 0, 0, 0};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
-            const float f = fmaf((float)acc[0], 16384.f, fmaf((float)acc[1], 128.f, (float)acc[2]));
+            const float f = fmaf((float)acc[0], 65536.f, fmaf((float)acc[1], 256.f, (float)acc[2]));
             const float lgt = fmaf(f, unscale, Cr);
             const bool ok = lg < NREP && ((qm >> lg) & 1) && tok0 + 16 * T + n16 < S;
             lg4[T] = ok ? lgt : -INFINITY;
@@ -351,17 +356,18 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 const float sn = sp_g[gv] > s_run[gv] ? 2.0f * sp_g[gv] : s_run[gv];
                 as[gv] = sn > 0.f ? s_run[gv] / sn : 1.0f;
                 s_run[gv] = sn;
-                inv_pv[gv] = sn > 0.f ? kPvScale / sn : 0.f;
+                inv_pv[gv] = sn > 0.f ? (kPvScale / 65535.0f) / sn : 0.f;
             }
             float a_lg = as[0], am_lg = am[0];
-            m_lane = m_run[0];
+            float ml = m_run[0];
 #pragma unroll
             for (int gv = 1; gv < G; ++gv) a_lg = lg == gv ? as[gv] : a_lg;
 #pragma unroll
             for (int r = 1; r < NREP; ++r) {
                 am_lg = lg == r ? am[r] : am_lg;
-                m_lane = lg == r ? m_run[r] : m_lane;
+                ml = lg == r ? m_run[r] : ml;
             }
+            m_lane = ml == -INFINITY ? 0.f : ml;
             l_acc *= am_lg;
 #pragma unroll
             for (int gv = 0; gv < G; ++gv) bias[gv] *= am_lg;
@@ -373,36 +379,40 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                     for (int t = 0; t < 8; ++t) {
                         const float v = fmaf((float)pacc[0][t][r], 256.f, (float)pacc[1][t][r]);
                         pacc[0][t][r] = 0;
-                        pacc[1][t][r] = (int)rintf(v * f);
+                        pacc[1][t][r] = (int)rintf(v * f);     // < 2^31: |v| <= 2^15 * 15 * 64 * pages
                     }
                 }
             }
         }
 
-        // ---- p.v: digits of p * V_scale / sigma, then 2 MFMAs per 16-channel tile
+        // ---- p.v: digits of p * V_scale / sigma, then 2 MFMAs per 16-channel tile.
+        // Y = X + 128 comes from cvt_pknorm_u16 (round(x * 65535) of two values at once),
+        // so x = (p * V_scale * kPvScale / sigma + 128) / 65535.
         float pr[4];
 #pragma unroll
         for (int T = 0; T < 4; ++T) {
-            pr[T] = lg4[T] == -INFINITY ? 0.f : exp2_fast(lg4[T] - m_lane);
+            pr[T] = exp2_fast(lg4[T] - m_lane);      // exp2(-inf) = 0 for masked tokens
             l_acc += pr[T];
         }
 #pragma unroll
         for (int gv = 0; gv < G; ++gv) {
-            int d0[4], d1[4];
+            float x[4];
 #pragma unroll
             for (int T = 0; T < 4; ++T) {
-                const int X = (int)rintf(pr[T] * vs_t[T][gv] * inv_pv[gv]);
-                d0[T] = (X + 128) >> 8;
-                d1[T] = X - (d0[T] << 8);
+                x[T] = fmaf(pr[T], vs_t[T][gv] * inv_pv[gv], 128.0f / 65535.0f);
                 bias[gv] = fmaf(pr[T], vm_t[T][gv], bias[gv]);
             }
+            const auto z01 = __builtin_amdgcn_cvt_pknorm_u16(x[0], x[1]);
+            const auto z23 = __builtin_amdgcn_cvt_pknorm_u16(x[2], x[3]);
+            const uint32_t u01 = (uint32_t)z01[0] | ((uint32_t)z01[1] << 16);
+            const uint32_t u23 = (uint32_t)z23[0] | ((uint32_t)z23[1] << 16);
             // operand k = 16*kg + 4*ai + bb carries token 16*bb + 4*ai + kg (the order of
             // the V dwords below), so token 16T + n16 sits at kg = n16&3, byte 4*(n16>>2) + T
             if (lg < NREP) {
                 const int row = 4 * gv + lg;
                 uint32_t* dst = (uint32_t*)&W.apv[0][row][swz(row, n16 & 3)][4 * (n16 >> 2)];
-                dst[0] = pack4(d0[0], d0[1], d0[2], d0[3]);
-                dst[1024 / 4] = pack4(d1[0], d1[1], d1[2], d1[3]);
+                dst[0] = __builtin_amdgcn_perm(u23, u01, 0x07050301u);                    // high digit
+                dst[1024 / 4] = __builtin_amdgcn_perm(u23, u01, 0x06040200u) ^ kDigitFlip;  // low digit
             }
         }
         wave_lds_fence();
