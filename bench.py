@@ -26,6 +26,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from flashquest_amd._lib import KernelTimer  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import quantize_k_int4, quantize_v_int4  # noqa: E402
 
@@ -46,6 +47,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip control / per-layer / per-q-head lines")
     ap.add_argument("--cpu-layers", type=int, default=6, help="layers in the CPU baseline sample")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
     return ap.parse_args()
 
 
@@ -101,23 +104,37 @@ def step_bytes(cache, mask, page=64):
 
 # --------------------------------------------------------------- measurement --
 class Flusher:
-    """Evicts L2 and MALL: a fill kernel over 2 x 256 MB."""
+    """Evicts L2 (4 MB per XCD) and the 256 MB MALL before each step by reading
+    a 1 GiB buffer.  A read leaves clean lines behind; a fill kernel would leave
+    up to 256 MB of dirty lines that the timed kernels then have to write back
+    (``write=True`` measures that variant, reported as an extra)."""
 
-    def __init__(self, dev):
-        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    def __init__(self, dev, write=False):
+        self.buf = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+        self.write = write
 
     def __call__(self):
-        self.buf.fill_(1)
+        if self.write:
+            self.buf.fill_(1)
+        else:
+            torch.sum(self.buf, dtype=torch.int64)
 
 
-def time_steps(fn_pre, fn_timed, steps, warmup, flush):
+def time_steps(fn_pre, fn_timed, steps, warmup, flush, kernel_timer=False):
+    """Mean ms of fn_timed over `steps` runs (events on torch's current stream,
+    which is the stream the library launches on), each after flush() and the
+    untimed fn_pre().  With kernel_timer, also the mean duration of the
+    attention kernel alone (library events around each launch)."""
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for _ in range(warmup):
         flush()
         fn_pre()
         fn_timed()
     torch.cuda.synchronize()
+    timer = KernelTimer(steps) if kernel_timer else None
     t0 = time.perf_counter()
+    if timer:
+        timer.__enter__()
     for i in range(steps):
         flush()
         fn_pre()
@@ -127,7 +144,30 @@ def time_steps(fn_pre, fn_timed, steps, warmup, flush):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = [a.elapsed_time(b) for a, b in ev]
-    return sum(ms) / len(ms), wall
+    kernel_ms = None
+    if timer:
+        timer.__exit__(None, None, None)
+        if timer.launches != steps:
+            raise RuntimeError(f"expected {steps} timed attention launches, got {timer.launches}")
+        kernel_ms = timer.total_ms / timer.launches
+    return sum(ms) / len(ms), wall, kernel_ms
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int4_mfma_config1_traffic.json")
+
+
+def measured_traffic(L, B, P, retention, select):
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy of known size), when it was
+    measured on this exact workload; otherwise None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("workload") != {"layers": L, "batch": B, "pages": P, "retention": retention, "select": select}:
+        return None
+    return t.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(cache, args, n_layers):
@@ -180,6 +220,18 @@ def main():
                             retention=retention, num_sinks=4, window_pages=2, k_max_static=kmax,
                             select_mode=mode, mask_out=mask)
 
+    if args.profile_kernels:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)                      # FETCH = WRITE = 256 MiB of HBM traffic
+        dec = decoder(args.retention, k, args.select)
+        for _ in range(3):
+            flush()
+            dec()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_kernels": "done", "copy_bytes": src.numel()}))
+        return
+
     mask = torch.zeros(L, B, Hq, P, dtype=torch.bool, device=dev)
     dec = decoder(args.retention, k, args.select, mask=mask)
     dec()
@@ -187,23 +239,24 @@ def main():
     scoring_b, attn_b, union = step_bytes(cache, mask)
     dec.mask_out = None
     noop = lambda: None
-    step_ms, wall = time_steps(noop, dec, args.steps, args.warmup, flush)
-    attn_ms, _ = time_steps(dec.select, dec.attend, args.steps, args.warmup, flush)
+    step_ms, wall, _ = time_steps(noop, dec, args.steps, args.warmup, flush)
+    attend_ms, _, attn_ms = time_steps(dec.select, dec.attend, args.steps, args.warmup, flush, kernel_timer=True)
     total_b = scoring_b + attn_b
     extra = {"union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
              "step_GBps": total_b / (step_ms * 1e-3) / 1e9,
              "step_roofline_frac": total_b / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-             "attention_kernel_us": attn_ms * 1e3, "select_mode": args.select}
+             "attention_kernel_us": attn_ms * 1e3, "attend_with_split_merge_us": attend_ms * 1e3,
+             "select_us": None, "select_mode": args.select}
     if not args.no_extra:
         ctl = decoder(1.0, P, args.select)
-        ctl_ms, _ = time_steps(noop, ctl, args.steps, args.warmup, flush)
+        ctl_ms, _, _ = time_steps(noop, ctl, args.steps, args.warmup, flush)
         full_mask = torch.ones(L, B, Hq, P, dtype=torch.bool, device=dev)
         sb, ab, _ = step_bytes(cache, full_mask)
         extra.update({"all_pages_control_us": ctl_ms * 1e3, "sparse_speedup_vs_all_pages": ctl_ms / step_ms,
                       "all_pages_GBps": (sb + ab) / (ctl_ms * 1e-3) / 1e9})
         other = "per_q_head" if args.select == "per_kv_head_sum" else "per_kv_head_sum"
         alt = decoder(args.retention, k, other)
-        alt_ms, _ = time_steps(noop, alt, args.steps, args.warmup, flush)
+        alt_ms, _, _ = time_steps(noop, alt, args.steps, args.warmup, flush)
         extra[f"{other}_us"] = alt_ms * 1e3
         # the reference's per-layer call pattern: 28 sequential (select, attend) pairs in one HIP graph
         per_layer = [decoder(args.retention, k, args.select,
@@ -221,20 +274,27 @@ def main():
                 for d in per_layer:
                     d()
         torch.cuda.synchronize()
-        pl_ms, _ = time_steps(noop, graph.replay, args.steps, args.warmup, flush)
+        pl_ms, _, _ = time_steps(noop, graph.replay, args.steps, args.warmup, flush)
         extra["per_layer_graph_us"] = pl_ms * 1e3
+        sel_ms, _, _ = time_steps(noop, dec.select, args.steps, args.warmup, flush)
+        extra["select_us"] = sel_ms * 1e3
+        wflush = Flusher(dev, write=True)
+        wf_ms, _, _ = time_steps(noop, dec, args.steps, args.warmup, wflush)
+        extra["step_us_after_write_flush"] = wf_ms * 1e3
+        del wflush
 
+    traffic = measured_traffic(L, B, P, args.retention, args.select)
     roof = {"bound": "hbm", "achieved": attn_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": attn_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
-            "kernel": "attn_int4_kernel (split-K sparse GQA attention, all 28 layers per launch)",
-            "algorithmic_bytes_per_launch": attn_b}
+            "frac": attn_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
+            "kernel": "attn_int4_mfma_kernel (split-K sparse GQA attention, all layers in one launch)",
+            "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_b}
     cpu = None
     if not args.no_cpu_baseline and B == 1:
         cpu = cpu_baseline(cache, args, min(args.cpu_layers, L))
     line = {
         "metric": METRIC, "value": step_ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int8 MFMA (exact digit split) + fp32", "data": "synthetic",
         "config": {"workload": f"BASELINE config 1: {L} independent layers x batch {B}, {Hq}/8 heads, D=128, "
                                f"{P} pages x 64 tokens, retention {args.retention} ({args.select} top-{k} + 4 sink "
                                "+ 2 window pages), INT4 K/V with fp16 metadata (V per 32 channels), "

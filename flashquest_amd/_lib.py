@@ -73,6 +73,8 @@ _I64P = ctypes.POINTER(ctypes.c_int64)
 SIGNATURES = {
     "fq_last_error": (ctypes.c_char_p, []),
     "fq_abi_version": (ctypes.c_int, []),
+    "fq_kernel_timer_start": (ctypes.c_int, [_I]),
+    "fq_kernel_timer_stop": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int32)]),
     "fq_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), _I]),
     "fq_turbo_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TurboCache), _I]),
     "fq_page_scores_int4": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
@@ -198,3 +200,21 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _ws[key] = buf
     return buf
+
+
+class KernelTimer:
+    """Times the sparse-attention kernels launched from this thread (HIP events
+    around each launch, recorded by the library on the launch stream)."""
+
+    def __init__(self, max_launches: int):
+        self.max_launches = int(max_launches)
+
+    def __enter__(self):
+        check(lib().fq_kernel_timer_start(self.max_launches), "kernel timer")
+        return self
+
+    def __exit__(self, *exc):
+        ms, n = ctypes.c_float(0.0), ctypes.c_int32(0)
+        check(lib().fq_kernel_timer_stop(ctypes.byref(ms), ctypes.byref(n)), "kernel timer")
+        self.total_ms, self.launches = ms.value, n.value
+        return False

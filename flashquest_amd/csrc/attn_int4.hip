@@ -185,7 +185,9 @@ hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                      \
     case N:                                                                                             \
+        timer_before_launch(st);                                                                       \
         hipLaunchKernelGGL((attn_int4_kernel<D, MT, GV, N>), grid, dim3(kThreads), 0, st, a);          \
+        timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                               \
             hipLaunchKernelGGL((merge_splits_kernel<D, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
                                a.q, a.ws, a.c.Hkv, a.c.B, a.pps, a.splits);                                       \

@@ -493,7 +493,9 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                     \
     case N:                                                                                            \
+        timer_before_launch(st);                                                                       \
         hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N>), grid, dim3(kThreads), 0, st, a);         \
+        timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                              \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
                                a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits);                                \

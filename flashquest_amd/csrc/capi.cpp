@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 #include "fq_common.h"
 
@@ -30,6 +31,14 @@ hipError_t launch_attn_turbo(const fq_turbo_cache& c, const QueryArgs& q, const 
                              const AttnLaunch& al, hipStream_t st);
 
 static thread_local std::string g_err;
+
+// Armed by fq_kernel_timer_start: event pairs recorded around attention kernels.
+struct KernelTimer {
+    std::vector<hipEvent_t> start, stop;
+    int used = 0;
+    bool armed = false;
+};
+static thread_local KernelTimer g_timer;
 
 static int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -153,11 +162,51 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
     return FQ_OK;
 }
 
+void timer_before_launch(hipStream_t st) {
+    KernelTimer& t = g_timer;
+    if (t.armed && t.used < (int)t.start.size()) (void)hipEventRecord(t.start[t.used], st);
+}
+void timer_after_launch(hipStream_t st) {
+    KernelTimer& t = g_timer;
+    if (t.armed && t.used < (int)t.stop.size()) (void)hipEventRecord(t.stop[t.used++], st);
+}
+
 }  // namespace fq
 
 using namespace fq;
 
 extern "C" {
+
+int fq_kernel_timer_start(int32_t max_launches) {
+    KernelTimer& t = g_timer;
+    if (max_launches < 1) return fail(FQ_ERR_INVALID, "max_launches must be positive");
+    while ((int)t.start.size() < max_launches) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return fail(FQ_ERR_HIP, "hipEventCreate failed");
+        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return fail(FQ_ERR_HIP, "hipEventCreate failed"); }
+        t.start.push_back(a);
+        t.stop.push_back(b);
+    }
+    t.used = 0;
+    t.armed = true;
+    return FQ_OK;
+}
+
+int fq_kernel_timer_stop(float* total_ms, int32_t* launches) {
+    KernelTimer& t = g_timer;
+    if (!t.armed) return fail(FQ_ERR_INVALID, "kernel timer not started");
+    t.armed = false;
+    float sum = 0.f;
+    for (int i = 0; i < t.used; ++i) {
+        if (hipEventSynchronize(t.stop[i]) != hipSuccess) return fail(FQ_ERR_HIP, "hipEventSynchronize failed");
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, t.start[i], t.stop[i]) != hipSuccess) return fail(FQ_ERR_HIP, "hipEventElapsedTime failed");
+        sum += ms;
+    }
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = t.used;
+    return FQ_OK;
+}
 
 const char* fq_last_error(void) { return g_err.c_str(); }
 int fq_abi_version(void) { return 1; }

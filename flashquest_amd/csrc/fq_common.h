@@ -200,6 +200,9 @@ struct AttnLaunch {
 };
 
 // Host-side helpers implemented in capi.cpp.
+// Kernel timer hooks around an attention kernel launch (no-ops unless armed).
+void timer_before_launch(hipStream_t st);
+void timer_after_launch(hipStream_t st);
 size_t workspace_bytes(int G, int P, int rows, int nrep, int D);
 Workspace carve_workspace(void* base, int G, int P, int rows, int nrep, int D);
 AttnLaunch choose_split(int G, int max_entries, int s_max);

@@ -19,8 +19,8 @@ struct SelectLds {
     int tmp[8];
 };
 
-// Marks the top-k of keys[0..P) into qmask (|= bit), ties to the lower index.
-FQ_DEV void topk_into_qmask(SelectLds& s, int P, int k, uint8_t bit) {
+// Marks the top-k of keys[0..P) into s.qmask (|= bit), ties to the lower index.
+FQ_DEV void topk_into_qmask(SelectLds& s, const uint32_t* keys, int P, int k, uint8_t bit) {
     const int tid = threadIdx.x;
     if (k <= 0) return;
     if (k >= P) {
@@ -29,17 +29,17 @@ FQ_DEV void topk_into_qmask(SelectLds& s, int P, int k, uint8_t bit) {
         return;
     }
     int take_eq = 0;
-    const uint32_t T = block_radix_select(s.keys, P, k, s.hist, s.tmp, &take_eq);
+    const uint32_t T = block_radix_select(keys, P, k, s.hist, s.tmp, &take_eq);
     // count of keys equal to T (all of them match the final prefix)
     const int n_eq = s.hist[T & 255u];
     if (take_eq >= n_eq) {
         for (int i = tid; i < P; i += kThreads)
-            if (s.keys[i] >= T) s.qmask[i] |= bit;
+            if (keys[i] >= T) s.qmask[i] |= bit;
         __syncthreads();
     } else {
         for (int i = tid; i < P; i += kThreads)
-            if (s.keys[i] > T) s.qmask[i] |= bit;
-        block_compact(P, [&](int i) { return s.keys[i] == T; },
+            if (keys[i] > T) s.qmask[i] |= bit;
+        block_compact(P, [&](int i) { return keys[i] == T; },
                       [&](int i, int rank) { if (rank < take_eq) s.qmask[i] |= bit; }, s.tmp);
     }
 }
@@ -77,6 +77,75 @@ struct ScoreParams {
     int mode;
 };
 
+// Scores of one page for every query row (rows in LDS), computed by the NL lanes
+// of a page; emit(r, score) runs on all of them with the same value.
+template <int D, typename MT, typename Emit>
+FQ_DEV void score_page(const uint4& sv, const uint4& mv, const float (*s_q)[D], const float (*s_qp)[D], int rows,
+                       int lane_in_page, Emit emit) {
+    constexpr int NL = D / 8;
+    float sf[8], mf[8];
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sf[2 * j] = half_to_f<MT>(sw[j]);
+        sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
+        mf[2 * j] = half_to_f<MT>(mw[j]);
+        mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
+    }
+    for (int r = 0; r < rows; ++r) {
+        const float* qr = &s_q[r][lane_in_page * 8];
+        const float* qp = &s_qp[r][lane_in_page * 8];
+        float t1 = __fmul_rn(qr[0], mf[0]);
+        float t2 = __fmul_rn(qp[0], sf[0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            t1 = __fadd_rn(t1, __fmul_rn(qr[j], mf[j]));
+            t2 = __fadd_rn(t2, __fmul_rn(qp[j], sf[j]));
+        }
+        t1 = row_sum<NL>(t1);
+        t2 = row_sum<NL>(t2);
+        emit(r, __fadd_rn(t1, __fmul_rn(t2, 15.0f)));
+    }
+}
+
+// q rows of group g into LDS: s_q = q, s_qp = relu(q).  Every load is issued
+// (clamped index, dtype branch outside) before the first is used.
+template <int D>
+FQ_DEV void load_q_rows(const ScoreParams& a, int l, int b, int h, float (*s_q)[D], float (*s_qp)[D]) {
+    constexpr int kPer = kMaxRows * D / kThreads;
+    const int n = a.rows * D;
+    int64_t off[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = min((int)threadIdx.x + u * kThreads, n - 1);
+        const int r = i / D, d = i % D;
+        const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
+        off[u] = l * a.q_s[0] + b * a.q_s[1] + hq * a.q_s[2] + sq * a.q_s[3] + d * a.q_s[4];
+    }
+    float v[kPer];
+    if (a.q_dtype == FQ_F32) {
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) v[u] = ((const float*)a.q)[off[u]];
+    } else {
+        uint32_t w[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) w[u] = ((const uint16_t*)a.q)[off[u]];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) v[u] = a.q_dtype == FQ_BF16 ? bf16_bits_to_f(w[u]) : f16_bits_to_f(w[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < n) {
+            s_q[i / D][i % D] = v[u];
+            s_qp[i / D][i % D] = v[u] > 0.f ? v[u] : 0.f;
+        }
+    }
+}
+
+constexpr int kPasses = 4;                  // passes of PPP pages per scoring chunk
+
 template <int D, typename MT>
 __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     constexpr int NL = D / 8;
@@ -88,15 +157,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     const int g = blockIdx.y;
     const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
     const int tid = threadIdx.x;
-
-    for (int i = tid; i < a.rows * D; i += kThreads) {
-        const int r = i / D, d = i % D;
-        const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
-        const float v = load_any(a.q, a.q_dtype,
-                                 l * a.q_s[0] + b * a.q_s[1] + hq * a.q_s[2] + sq * a.q_s[3] + d * a.q_s[4]);
-        s_q[r][d] = v;
-        s_qp[r][d] = v > 0.f ? v : 0.f;
-    }
+    load_q_rows<D>(a, l, b, h, s_q, s_qp);
     __syncthreads();
 
     const int lane_in_page = tid % NL;
@@ -105,37 +166,23 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
     float* ws_scores = a.ws_scores ? a.ws_scores + (int64_t)g * a.rows * c.P : nullptr;
 
+    // a chunk is at most kPasses passes: every pass's metadata is loaded before
+    // any is scored, so the chunk costs one memory latency
     const int p_begin = blockIdx.x * a.ppc;
     const int p_end = min(c.P, p_begin + a.ppc);
-    for (int p0 = p_begin; p0 < p_end; p0 += PPP) {
-        const int p = p0 + page_in_pass;
+    uint4 sv[kPasses], mv[kPasses];
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u) {
+        const int p = min(p_begin + u * PPP + page_in_pass, p_end - 1);
+        sv[u] = *(const uint4*)(ksc + p * c.ksc_s[3] + lane_in_page * 8);
+        mv[u] = *(const uint4*)(kmn + p * c.kmn_s[3] + lane_in_page * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u) {
+        const int p = p_begin + u * PPP + page_in_pass;
         if (p < p_end) {
-            const uint4 sv = *(const uint4*)(ksc + p * c.ksc_s[3] + lane_in_page * 8);
-            const uint4 mv = *(const uint4*)(kmn + p * c.kmn_s[3] + lane_in_page * 8);
-            float sf[8], mf[8];
-            const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-            const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sf[2 * j] = half_to_f<MT>(sw[j]);
-                sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
-                mf[2 * j] = half_to_f<MT>(mw[j]);
-                mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
-            }
             float acc_kv = 0.f;
-            for (int r = 0; r < a.rows; ++r) {
-                const float* qr = &s_q[r][lane_in_page * 8];
-                const float* qp = &s_qp[r][lane_in_page * 8];
-                float t1 = __fmul_rn(qr[0], mf[0]);
-                float t2 = __fmul_rn(qp[0], sf[0]);
-#pragma unroll
-                for (int j = 1; j < 8; ++j) {
-                    t1 = __fadd_rn(t1, __fmul_rn(qr[j], mf[j]));
-                    t2 = __fadd_rn(t2, __fmul_rn(qp[j], sf[j]));
-                }
-                t1 = row_sum<NL>(t1);
-                t2 = row_sum<NL>(t2);
-                const float sc = __fadd_rn(t1, __fmul_rn(t2, 15.0f));
+            score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.rows, lane_in_page, [&](int r, float sc) {
                 if (lane_in_page == 0) {
                     const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
                     if (a.scores)
@@ -143,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
                     if (ws_scores && a.mode == FQ_SELECT_PER_Q_HEAD) ws_scores[r * c.P + p] = sc;
                 }
                 acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
-            }
+            });
             if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
                 ws_scores[p] = acc_kv;
         }
@@ -162,27 +209,11 @@ struct GroupSelectParams {
     uint8_t* mask_out;                            // (l, b, h_q, p) contiguous or null
 };
 
-__global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectParams a) {
-    __shared__ SelectLds s;
-    const int g = blockIdx.x, h = g % a.Hkv, tid = threadIdx.x, P = a.P;
-    const int rows = a.mode == FQ_SELECT_PER_Q_HEAD ? a.nrep : 1;
-    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
-    for (int i = tid; i < P; i += kThreads) s.qmask[i] = 0;
-    __syncthreads();
+// Group tail: forced pages, then the ascending union list (page | heads << 16),
+// its length and (optionally) the boolean selection mask, from s.qmask.
+FQ_DEV void finish_group(SelectLds& s, const GroupSelectParams& a, int g) {
+    const int tid = threadIdx.x, P = a.P;
     const uint8_t all_bits = (uint8_t)((1u << a.nrep) - 1u);
-    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
-        for (int r = 0; r < rows; ++r) {
-            for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[r * P + i]);
-            __syncthreads();
-            topk_into_qmask(s, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
-        }
-    } else {
-        float rmax = 0.f;
-        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, a.retention[h * a.nrep + r]);
-        for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[i]);
-        __syncthreads();
-        topk_into_qmask(s, P, k_for(rmax, P, a.k_max), all_bits);
-    }
     force_pages(s, P, a.num_sinks, a.window, all_bits);
     int* entries = a.ws.entries + (int64_t)g * P;
     const int n = block_compact(P, [&](int i) { return s.qmask[i] != 0; },
@@ -195,6 +226,130 @@ __global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectPara
         }
     }
     if (tid == 0) a.ws.n_sel[g] = n;
+}
+
+// Top-k per query head (row r's keys at keys + r * P) or once per KV head from
+// the summed scores (keys[0..P)), into a cleared s.qmask; then the group tail.
+FQ_DEV void select_group(SelectLds& s, const GroupSelectParams& a, int g, const uint32_t* keys) {
+    const int h = g % a.Hkv, P = a.P;
+    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
+        for (int r = 0; r < a.nrep; ++r)
+            topk_into_qmask(s, keys + r * P, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
+    } else {
+        float rmax = 0.f;
+        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, a.retention[h * a.nrep + r]);
+        topk_into_qmask(s, keys, P, k_for(rmax, P, a.k_max), (uint8_t)((1u << a.nrep) - 1u));
+    }
+    finish_group(s, a, g);
+}
+
+__global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectParams a) {
+    __shared__ SelectLds s;
+    const int g = blockIdx.x, tid = threadIdx.x, P = a.P;
+    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
+    for (int i = tid; i < P; i += kThreads) s.qmask[i] = 0;
+    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
+        // one row at a time through s.keys
+        __syncthreads();
+        const int h = g % a.Hkv;
+        for (int r = 0; r < a.nrep; ++r) {
+            for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[r * P + i]);
+            __syncthreads();
+            topk_into_qmask(s, s.keys, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
+        }
+        finish_group(s, a, g);
+    } else {
+        for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[i]);
+        __syncthreads();
+        select_group(s, a, g, s.keys);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The same per-group selection with one wave per group and no workgroup
+// barriers: each lane holds C keys (page i = 64 j + lane), the k-th largest key
+// is found bit by bit with wave-wide counts, ties go to the lower page index by
+// ballot ranks, and the union list is compacted with ballots.  Used for P <= 64 C.
+// ---------------------------------------------------------------------------
+// Marks the k largest of keys (ties to the lower page index) into qm |= bit.
+template <int C>
+FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit, int lane) {
+    if (k <= 0) return;
+    uint32_t T = 0;
+    for (int bitpos = 31; bitpos >= 0; --bitpos) {
+        const uint32_t cand = T | (1u << bitpos);
+        int cnt = 0;                          // wave-wide count, in scalar registers
+#pragma unroll
+        for (int j = 0; j < C; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+        if (cnt >= k) T = cand;
+    }
+    // T is the k-th largest key; keys above it are in, ties fill the rest by index
+    int gt = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) gt += __popcll(__ballot(key[j] > T));
+    int take_eq = k - gt;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        if (key[j] > T) qm[j] |= bit;
+        const uint64_t eq = __ballot(key[j] == T);
+        const int rank = (int)lanes_below(eq);
+        if (key[j] == T && rank < take_eq) qm[j] |= bit;
+        take_eq -= __popcll(eq);
+    }
+}
+
+template <int C>
+__global__ __launch_bounds__(kThreads) void select_groups_wave_kernel(GroupSelectParams a, int G) {
+    const int lane = lane_id();
+    const int g = blockIdx.x * (kThreads / 64) + wave_id();
+    if (g >= G) return;                      // whole wave
+    const int h = g % a.Hkv, P = a.P;
+    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
+    uint32_t key[C];
+    uint8_t qm[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) qm[j] = 0;
+    auto load_row = [&](int r) {
+        float v[C];
+#pragma unroll
+        for (int j = 0; j < C; ++j) v[j] = sc[r * P + min(64 * j + lane, P - 1)];   // all loads in flight
+#pragma unroll
+        for (int j = 0; j < C; ++j) key[j] = 64 * j + lane < P ? sortable_key(v[j]) : 0u;  // 0: below every score
+    };
+    const uint8_t all_bits = (uint8_t)((1u << a.nrep) - 1u);
+    // retention of the group's query heads: lane r holds head r's value
+    const float ret_l = a.retention[h * a.nrep + min(lane, a.nrep - 1)];
+    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
+        for (int r = 0; r < a.nrep; ++r) {
+            load_row(r);
+            const float rr = __shfl(ret_l, r, 64);
+            wave_topk<C>(key, qm, k_for(rr, P, a.k_max), (uint8_t)(1u << r), lane);
+        }
+    } else {
+        float rmax = 0.f;
+        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, __shfl(ret_l, r, 64));
+        load_row(0);
+        wave_topk<C>(key, qm, k_for(rmax, P, a.k_max), all_bits, lane);
+    }
+    // forced sink / window pages (selection.py:110-117)
+    const int ns = a.num_sinks < P ? a.num_sinks : P;
+    const int wnd = a.window < P ? a.window : P;
+    int* entries = a.ws.entries + (int64_t)g * P;
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const int i = 64 * j + lane;
+        if (i < P && (i < ns || (wnd > 0 && i >= P - wnd))) qm[j] |= all_bits;
+        const bool f = i < P && qm[j] != 0;
+        const uint64_t bal = __ballot(f);
+        if (f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
+        n += __popcll(bal);
+        if (a.mask_out && i < P) {
+            uint8_t* mo = a.mask_out + ((int64_t)g * a.nrep) * P;
+            for (int r = 0; r < a.nrep; ++r) mo[(int64_t)r * P + i] = (qm[j] >> r) & 1;
+        }
+    }
+    if (lane == 0) a.ws.n_sel[g] = n;
 }
 
 // ---------------------------------------------------------------------------
@@ -218,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void select_rows_kernel(SelectParams a) {
         s.qmask[i] = 0;
     }
     __syncthreads();
-    topk_into_qmask(s, P, k_for(a.retention[h], P, a.k_max), 1);
+    topk_into_qmask(s, s.keys, P, k_for(a.retention[h], P, a.k_max), 1);
     force_pages(s, P, a.num_sinks, a.window, 1);
     uint8_t* dst = a.mask + b * a.m_s[0] + h * a.m_s[1] + sq * a.m_s[2];
     for (int i = tid; i < P; i += kThreads) dst[i * a.m_s[3]] = s.qmask[i];
@@ -310,17 +465,25 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     a.scores = scores;
     if (sc4_s) for (int i = 0; i < 4; ++i) a.sc_s[i] = sc4_s[i];
     const int G = c.L * c.B * c.Hkv;
-    // pages per chunk: aim for >= ~2 waves of workgroups over 256 CUs
+    // pages per chunk: aim for >= ~2 waves of workgroups over 256 CUs, at most
+    // kPasses passes of ppp pages per workgroup
     const int ppp = kThreads / (c.D / 8);
     int target_chunks = (2048 + G - 1) / G;
     int ppc = (c.P + target_chunks - 1) / target_chunks;
     ppc = ((ppc + ppp - 1) / ppp) * ppp;
     if (ppc < ppp) ppc = ppp;
+    if (ppc > kPasses * ppp) ppc = kPasses * ppp;
     a.ppc = ppc;
     a.nchunks = (c.P + ppc - 1) / ppc;
     a.ws_scores = ws ? ws->scores : nullptr;
     a.mode = select_mode;
     if (a.rows > kMaxRows || c.P > kMaxPages) return hipErrorInvalidValue;
+    GroupSelectParams sp{};
+    if (ws) {
+        sp.ws = *ws; sp.mode = select_mode; sp.nrep = q.nrep; sp.Hkv = c.Hkv; sp.P = c.P;
+        sp.retention = retention; sp.num_sinks = num_sinks; sp.window = window; sp.k_max = k_max;
+        sp.mask_out = mask_out;
+    }
     dim3 grid(a.nchunks, G);
 #define FQ_SCORE(D_, MT_) hipLaunchKernelGGL((score_kernel<D_, MT_>), grid, dim3(kThreads), 0, st, a)
     if (c.D == 128) {
@@ -331,11 +494,10 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
 #undef FQ_SCORE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !ws) return e;
-    GroupSelectParams sp{};
-    sp.ws = *ws; sp.mode = select_mode; sp.nrep = q.nrep; sp.Hkv = c.Hkv; sp.P = c.P;
-    sp.retention = retention; sp.num_sinks = num_sinks; sp.window = window; sp.k_max = k_max;
-    sp.mask_out = mask_out;
-    hipLaunchKernelGGL(select_groups_kernel, dim3(G), dim3(kThreads), 0, st, sp);
+    const dim3 wgrid((G + kThreads / 64 - 1) / (kThreads / 64));
+    if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, wgrid, dim3(kThreads), 0, st, sp, G);
+    else if (c.P <= 64 * 32) hipLaunchKernelGGL(select_groups_wave_kernel<32>, wgrid, dim3(kThreads), 0, st, sp, G);
+    else hipLaunchKernelGGL(select_groups_kernel, dim3(G), dim3(kThreads), 0, st, sp);
     return hipGetLastError();
 }
 

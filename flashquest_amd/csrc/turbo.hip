@@ -161,7 +161,9 @@ hipError_t launch_turbo_nrep(const TurboParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                     \
     case N:                                                                                            \
+        timer_before_launch(st);                                                                      \
         hipLaunchKernelGGL((attn_turbo_kernel<D, N>), grid, dim3(kThreads), 0, st, a);                \
+        timer_after_launch(st);                                                                       \
         if (a.splits > 1)                                                                              \
             hipLaunchKernelGGL((merge_splits_kernel<D, N, true>), dim3(grid.y), dim3(kThreads), 0, st, \
                                a.q, a.ws, a.c.H_kv, a.c.B, a.pps, a.splits);                                   \

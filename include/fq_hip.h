@@ -96,6 +96,15 @@ typedef struct fq_turbo_cache {
 const char* fq_last_error(void);
 int fq_abi_version(void);
 
+/* Kernel timing (no counterpart in the reference; used by bench.py).  After
+ * fq_kernel_timer_start(n), each of the next n sparse-attention kernel launches
+ * (INT4 or turbo, not the split merge) made from this host thread is bracketed by
+ * a pair of HIP events on its stream.  fq_kernel_timer_stop waits for them and
+ * returns the summed kernel time and the number of timed launches.  Not for use
+ * under HIP graph capture. */
+int fq_kernel_timer_start(int32_t max_launches);
+int fq_kernel_timer_stop(float* total_ms, int32_t* launches);
+
 /* Bytes of workspace the attention / decode entries need for this cache and
  * H_q (page lists, scores and split partials; no initialisation needed).
  * Calls that share a workspace must be ordered (same stream). */
