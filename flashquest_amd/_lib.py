@@ -74,6 +74,7 @@ SIGNATURES = {
     "fq_last_error": (ctypes.c_char_p, []),
     "fq_abi_version": (ctypes.c_int, []),
     "fq_kernel_timer_start": (ctypes.c_int, [_I]),
+    "fq_set_attention_splits": (ctypes.c_int, [_I]),
     "fq_kernel_timer_stop": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int32)]),
     "fq_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), _I]),
     "fq_turbo_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TurboCache), _I]),
@@ -217,4 +218,20 @@ class KernelTimer:
         ms, n = ctypes.c_float(0.0), ctypes.c_int32(0)
         check(lib().fq_kernel_timer_stop(ctypes.byref(ms), ctypes.byref(n)), "kernel timer")
         self.total_ms, self.launches = ms.value, n.value
+        return False
+
+
+class attention_splits:
+    """Context manager: fixed workgroups per KV group for the matrix-core INT4
+    attention kernel (tests and tuning); restores the automatic choice on exit."""
+
+    def __init__(self, splits: int):
+        self.splits = int(splits)
+
+    def __enter__(self):
+        check(lib().fq_set_attention_splits(self.splits), "attention splits")
+        return self
+
+    def __exit__(self, *exc):
+        check(lib().fq_set_attention_splits(0), "attention splits")
         return False

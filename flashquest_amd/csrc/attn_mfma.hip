@@ -1,28 +1,29 @@
 // Split-K sparse GQA decode attention over packed INT4 pages on the gfx950
-// matrix cores (v_mfma_i32_16x16x64_i8).  Same semantics as attn_int4.hip
+// matrix cores.  Same semantics as attn_int4.hip
 // (src/flashquest/kernel/sparse_int4_fwd.py:23-157); specialised for
 // head_dim 128, 64-token pages and up to 4 query heads per KV head.
 //
 // Why MFMA on a memory-bound GEMV: with 3 query heads per KV head every INT4
 // code feeds 3 multiply-adds for q.k and 3 for p.v, which is more fp32 VALU
-// work per byte than the CU can issue at HBM speed.  Here the codes go to the
-// matrix core as int8 operands unchanged (a nibble mask is the whole unpack),
-// and the other operand is an exact fixed-point expansion in int8 digits:
-//   q.k : A = q_d * K_scale[p,d], scaled by (2^21-1)/max|A| per page into 3
-//         digits (rows 4r+digit, r = query head), plus sum_d q_d * K_mn[p,d];
-//   p.v : A = p_t * V_scale[t,g] / sigma_g, scaled by 32639 into 2 balanced
-//         8-bit digits (rows 4g+r, g = V channel group), plus sum_t p_t * V_mn[t,g].
-// int32 accumulation is exact; the only rounding is the digit split (2^-21
-// relative for q.k, better than 2^-13 for p.v) and the final fp32 combination.
+// work per byte than the CU can issue at HBM speed.  The codes go to the matrix
+// core unchanged apart from a nibble mask:
+//   q.k : v_mfma_i32_16x16x64_i8.  A = q_d * K_scale[p,d] as an exact 24-bit
+//         fixed-point number per page (3 balanced int8 digits in rows
+//         4r+digit, r = query head), B = the codes; plus sum_d q_d * K_mn[p,d].
+//         int32 accumulation is exact, so the only rounding is 2^-23 of max|A|.
+//   p.v : v_mfma_f32_16x16x32_f16.  A = p_t * V_scale[t,g] in fp16 (rows 4g+r,
+//         g = V channel group), B = the codes as fp16 subnormals (bits = code,
+//         value = code * 2^-24, exact), fp32 accumulation; plus
+//         sum_t p_t * V_mn[t,g].  Rounding is relative to each term (2^-12).
 //
 // Single pass per page: each wave owns every 4th page of its workgroup's
 // split, loads a page (K, V, metadata) one page ahead of the one it computes,
-// and keeps p.v in int32 accumulators against a running reference: m[r] (the
-// softmax maximum, log2 domain) and sigma[g] (the V-scale bound).  A page that
-// exceeds either (rare after the first pages; both are set with a factor-2
-// headroom) rescales the accumulators once.  The wave states then merge like
-// the VALU kernel's, and splits meet in merge_splits_kernel.
+// and accumulates against a running softmax maximum m[r] (log2 domain),
+// rescaling when a page raises it.  With bf16 metadata A is also divided by a
+// running V-scale bound sigma[g] so that it stays in fp16 range.  The wave
+// states merge like the VALU kernel's, and splits meet in merge_splits_kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.h"
 
@@ -30,10 +31,14 @@ namespace fq {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxWgPages = 256;            // pages of one workgroup split (entries staged in LDS)
 constexpr float kQkScale = 8323071.0f;      // 2^23 - 2^16 - 1: |X| <= this keeps 3 balanced digits in int8
-constexpr float kPvScale = 32639.0f;        // 2^15 - 129: X + 128 < 2^15 keeps 2 balanced digits in int8
+constexpr float kSubnormal = 16777216.0f;   // 2^24: fp16 subnormal with bits c has value c * 2^-24
 
 struct MfmaParams {
     Int4Cache c;
@@ -42,12 +47,12 @@ struct MfmaParams {
     int splits;
 };
 
-// A operands of one wave: [k-step or digit][row][k-group, XOR-swizzled][byte].
+// A operands of one wave: [k-step][row][k-group, XOR-swizzled][16 bytes].
 // The k-group of row R is stored at position kg ^ ((R >> 2) & 3), which makes
 // the 16-byte operand reads (row = lane & 15, k-group = lane >> 4) conflict-free.
 struct WaveLds {
-    uint8_t aqk[2][16][4][16];      // q.k: [k-step][4r + digit][..]
-    uint8_t apv[2][16][4][16];      // p.v: [digit][4g + r][..]
+    uint8_t aqk[2][16][4][16];      // q.k: int8 digits, rows 4r + digit
+    uint8_t apv[2][16][4][16];      // p.v: fp16, rows 4g + r (8 halves per k-group)
 };
 FQ_DEV int swz(int row, int kg) { return kg ^ ((row >> 2) & 3); }
 
@@ -235,18 +240,18 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // running references (wave-uniform) and accumulators
-    float m_run[NREP], s_run[G], inv_pv[G];
+    // running references (wave-uniform) and accumulators.  With fp16 metadata
+    // p * V_scale <= 65504 needs no bound; bf16 metadata is divided by s_run.
+    constexpr bool kBound = std::is_same<MT, bf16>::value;
+    float m_run[NREP], s_run[G], inv_s[G];
 #pragma unroll
     for (int r = 0; r < NREP; ++r) m_run[r] = -INFINITY;
 #pragma unroll
-    for (int gv = 0; gv < G; ++gv) { s_run[gv] = 0.f; inv_pv[gv] = 0.f; }
+    for (int gv = 0; gv < G; ++gv) { s_run[gv] = kBound ? 0.f : 1.f; inv_s[gv] = 1.f; }
     float m_lane = 0.f;                      // m_run[lg], or 0 while head lg has no logit yet
-    v4i pacc[2][8];                          // [digit][tile]: component r = head, lane group lg = V group
+    v4f pacc[8];                             // [tile]: component r = head, lane group lg = V group
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) pacc[d][t] = (v4i){0, 0, 0, 0};
+    for (int t = 0; t < 8; ++t) pacc[t] = (v4f){0.f, 0.f, 0.f, 0.f};
     float l_acc = 0.f, bias[G];              // head lg: sum p, sum p * V_mn[g] over this lane's tokens
 #pragma unroll
     for (int gv = 0; gv < G; ++gv) bias[gv] = 0.f;
@@ -321,16 +326,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             unpack_vmeta<MT, G>(cb.vs[T], vs_t[T]);
             unpack_vmeta<MT, G>(cb.vm[T], vm_t[T]);
         }
-        float sp = 0.f;
-#pragma unroll
-        for (int T = 0; T < 4; ++T) {
-            float v = vs_t[T][0];
-#pragma unroll
-            for (int gv = 1; gv < G; ++gv) v = lg == gv ? vs_t[T][gv] : v;
-            sp = fmaxf(sp, v);
-        }
         mp = row16_max(mp);
-        sp = row16_max(sp);
         bool grow = false;
         float mp_r[NREP], sp_g[G];
 #pragma unroll
@@ -338,25 +334,40 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             mp_r[r] = lane_value(mp, 16 * r);
             grow |= mp_r[r] > m_run[r];
         }
+        if constexpr (kBound) {
+            float sp = 0.f;
 #pragma unroll
-        for (int gv = 0; gv < G; ++gv) {
-            sp_g[gv] = lane_value(sp, 16 * gv);
-            grow |= sp_g[gv] > s_run[gv];
+            for (int T = 0; T < 4; ++T) {
+                float v = vs_t[T][0];
+#pragma unroll
+                for (int gv = 1; gv < G; ++gv) v = lg == gv ? vs_t[T][gv] : v;
+                sp = fmaxf(sp, v);
+            }
+            sp = row16_max(sp);
+#pragma unroll
+            for (int gv = 0; gv < G; ++gv) {
+                sp_g[gv] = lane_value(sp, 16 * gv);
+                grow |= sp_g[gv] > s_run[gv];
+            }
         }
         if (grow) {      // wave-uniform: raise the references, rescale what is accumulated
             float am[NREP], as[G];
 #pragma unroll
             for (int r = 0; r < NREP; ++r) {
-                const float mn = mp_r[r] > m_run[r] ? mp_r[r] + 1.0f : m_run[r];
+                const float mn = fmaxf(mp_r[r], m_run[r]);
                 am[r] = mn == m_run[r] ? 1.0f : exp2_fast(m_run[r] - mn);
                 m_run[r] = mn;
             }
 #pragma unroll
             for (int gv = 0; gv < G; ++gv) {
-                const float sn = sp_g[gv] > s_run[gv] ? 2.0f * sp_g[gv] : s_run[gv];
-                as[gv] = sn > 0.f ? s_run[gv] / sn : 1.0f;
-                s_run[gv] = sn;
-                inv_pv[gv] = sn > 0.f ? (kPvScale / 65535.0f) / sn : 0.f;
+                as[gv] = 1.0f;
+                if constexpr (kBound) {
+                    // A = p * V_scale / s_run <= 1/2: bound set with a factor-2 headroom
+                    const float sn = sp_g[gv] > s_run[gv] ? 2.0f * sp_g[gv] : s_run[gv];
+                    as[gv] = sn > 0.f ? s_run[gv] / sn : 1.0f;
+                    s_run[gv] = sn;
+                    inv_s[gv] = sn > 0.f ? 1.0f / sn : 0.f;
+                }
             }
             float a_lg = as[0], am_lg = am[0];
             float ml = m_run[0];
@@ -371,76 +382,72 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             l_acc *= am_lg;
 #pragma unroll
             for (int gv = 0; gv < G; ++gv) bias[gv] *= am_lg;
-            if (k > 0) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float f = r < NREP ? am[r] * a_lg : 0.f;
+            for (int r = 0; r < 4; ++r) {
+                const float f = r < NREP ? am[r] * a_lg : 0.f;
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const float v = fmaf((float)pacc[0][t][r], 256.f, (float)pacc[1][t][r]);
-                        pacc[0][t][r] = 0;
-                        pacc[1][t][r] = (int)rintf(v * f);     // < 2^31: |v| <= 2^15 * 15 * 64 * pages
-                    }
-                }
+                for (int t = 0; t < 8; ++t) pacc[t][r] *= f;
             }
         }
 
-        // ---- p.v: digits of p * V_scale / sigma, then 2 MFMAs per 16-channel tile.
-        // Y = X + 128 comes from cvt_pknorm_u16 (round(x * 65535) of two values at once),
-        // so x = (p * V_scale * kPvScale / sigma + 128) / 65535.
+        // ---- p.v: A = p * V_scale (/ s_run) in fp16, 2 steps of 32 tokens x 8 tiles
         float pr[4];
 #pragma unroll
         for (int T = 0; T < 4; ++T) {
             pr[T] = exp2_fast(lg4[T] - m_lane);      // exp2(-inf) = 0 for masked tokens
             l_acc += pr[T];
         }
+        // Operand k = 8*kg + 2*ai + jj of step s carries token 16*(2s + jj) + 4*ai + kg
+        // (the order of the V dwords below): token 16T + n16 is step T>>1, kg = n16&3,
+        // half 2*(n16>>2) + (T&1) -> one dword per (group, step) from each lane.
 #pragma unroll
         for (int gv = 0; gv < G; ++gv) {
-            float x[4];
+            float a4[4];
 #pragma unroll
             for (int T = 0; T < 4; ++T) {
-                x[T] = fmaf(pr[T], vs_t[T][gv] * inv_pv[gv], 128.0f / 65535.0f);
+                a4[T] = pr[T] * vs_t[T][gv];
+                if constexpr (kBound) a4[T] *= inv_s[gv];
                 bias[gv] = fmaf(pr[T], vm_t[T][gv], bias[gv]);
             }
-            const auto z01 = __builtin_amdgcn_cvt_pknorm_u16(x[0], x[1]);
-            const auto z23 = __builtin_amdgcn_cvt_pknorm_u16(x[2], x[3]);
-            const uint32_t u01 = (uint32_t)z01[0] | ((uint32_t)z01[1] << 16);
-            const uint32_t u23 = (uint32_t)z23[0] | ((uint32_t)z23[1] << 16);
-            // operand k = 16*kg + 4*ai + bb carries token 16*bb + 4*ai + kg (the order of
-            // the V dwords below), so token 16T + n16 sits at kg = n16&3, byte 4*(n16>>2) + T
             if (lg < NREP) {
                 const int row = 4 * gv + lg;
-                uint32_t* dst = (uint32_t*)&W.apv[0][row][swz(row, n16 & 3)][4 * (n16 >> 2)];
-                dst[0] = __builtin_amdgcn_perm(u23, u01, 0x07050301u);                    // high digit
-                dst[1024 / 4] = __builtin_amdgcn_perm(u23, u01, 0x06040200u) ^ kDigitFlip;  // low digit
+                const int q = swz(row, n16 & 3);
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const h2v hv = __builtin_convertvector((f2v){a4[2 * st], a4[2 * st + 1]}, h2v);
+                    *(uint32_t*)&W.apv[st][row][q][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+                }
             }
         }
         wave_lds_fence();
-        const v4i ap0 = *(const v4i*)&W.apv[0][n16][swz(n16, lg)][0];
-        const v4i ap1 = *(const v4i*)&W.apv[1][n16][swz(n16, lg)][0];
-        uint32_t U[4][4];     // [ai][cc]
+        const v8h ap0 = *(const v8h*)&W.apv[0][n16][swz(n16, lg)][0];
+        const v8h ap1 = *(const v8h*)&W.apv[1][n16][swz(n16, lg)][0];
+        // B: nibbles of the V dwords, two tokens per dword as fp16 subnormal bit patterns
+        uint32_t nl[16], nh[16];
 #pragma unroll
-        for (int ai = 0; ai < 4; ++ai) {
-            // 4x4 byte transpose: U[ai][cc] byte bb = byte cc of vw[4*ai + bb]
-            const uint32_t x0 = cb.vw[4 * ai], x1 = cb.vw[4 * ai + 1], x2 = cb.vw[4 * ai + 2], x3 = cb.vw[4 * ai + 3];
-            const uint32_t t0 = __builtin_amdgcn_perm(x1, x0, 0x06020400u);
-            const uint32_t t1 = __builtin_amdgcn_perm(x1, x0, 0x07030501u);
-            const uint32_t t2 = __builtin_amdgcn_perm(x3, x2, 0x06020400u);
-            const uint32_t t3 = __builtin_amdgcn_perm(x3, x2, 0x07030501u);
-            U[ai][0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-            U[ai][1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-            U[ai][2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-            U[ai][3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+        for (int j = 0; j < 16; ++j) {
+            nl[j] = lo_nib(cb.vw[j]);
+            nh[j] = hi_nib(cb.vw[j]);
         }
-        // tile 2cc: low nibbles (channel 8*n16 + 2cc), tile 2cc+1: high nibbles
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
-            const v4i blo = {(int)lo_nib(U[0][cc]), (int)lo_nib(U[1][cc]), (int)lo_nib(U[2][cc]), (int)lo_nib(U[3][cc])};
-            const v4i bhi = {(int)hi_nib(U[0][cc]), (int)hi_nib(U[1][cc]), (int)hi_nib(U[2][cc]), (int)hi_nib(U[3][cc])};
-            pacc[0][2 * cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap0, blo, pacc[0][2 * cc], 0, 0, 0);
-            pacc[1][2 * cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap1, blo, pacc[1][2 * cc], 0, 0, 0);
-            pacc[0][2 * cc + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap0, bhi, pacc[0][2 * cc + 1], 0, 0, 0);
-            pacc[1][2 * cc + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ap1, bhi, pacc[1][2 * cc + 1], 0, 0, 0);
+            // bytes [cc of token j0, 0, cc of token j1, 0]
+            const uint32_t sel = 0x0C000C00u | ((4u + cc) << 16) | (uint32_t)cc;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint32_t bl[4], bh[4];
+#pragma unroll
+                for (int ai = 0; ai < 4; ++ai) {
+                    const int j0 = 4 * ai + 2 * st;
+                    bl[ai] = __builtin_amdgcn_perm(nl[j0 + 1], nl[j0], sel);
+                    bh[ai] = __builtin_amdgcn_perm(nh[j0 + 1], nh[j0], sel);
+                }
+                const v8h blo = __builtin_bit_cast(v8h, (v4i){(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]});
+                const v8h bhi = __builtin_bit_cast(v8h, (v4i){(int)bh[0], (int)bh[1], (int)bh[2], (int)bh[3]});
+                const v8h a = st ? ap1 : ap0;
+                pacc[2 * cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo, pacc[2 * cc], 0, 0, 0);
+                pacc[2 * cc + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi, pacc[2 * cc + 1], 0, 0, 0);
+            }
         }
         wave_lds_fence();
     };
@@ -469,7 +476,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     for (int gv = 1; gv < G; ++gv) {
         if (ug == gv) { bsel = bias[gv]; ssel = s_run[gv]; }
     }
-    const float pv_unscale = ssel * (1.0f / kPvScale);
+    const float pv_unscale = ssel * kSubnormal;
 #pragma unroll
     for (int r = 0; r < NREP; ++r) {
         const int src = 16 * r + n16;
@@ -478,8 +485,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         if (lg == ug) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const float v = fmaf((float)pacc[0][t][r], 256.f, (float)pacc[1][t][r]);
-                s_split.acc[w][r][8 * n16 + t] = fmaf(v, pv_unscale, bb);
+                s_split.acc[w][r][8 * n16 + t] = fmaf(pacc[t][r], pv_unscale, bb);
             }
             if (n16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = ll; }
         }
@@ -509,10 +515,11 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
 
 // Splits per KV group: enough workgroups to keep every CU busy in one pass
 // (two resident per CU), at least 8 pages per split, at most kMaxWgPages.
-int mfma_splits(int groups, int max_entries, int s_max) {
+// `request` > 0 overrides the first two rules.
+int mfma_splits(int groups, int max_entries, int s_max, int request) {
     constexpr int kResident = 2 * 256;
-    int s = kResident / (groups > 0 ? groups : 1);
-    s = std::min(s, (max_entries + 7) / 8);
+    int s = request > 0 ? request : kResident / (groups > 0 ? groups : 1);
+    if (request <= 0) s = std::min(s, (max_entries + 7) / 8);
     s = std::max(s, (max_entries + kMaxWgPages - 1) / kMaxWgPages);
     s = std::max(s, 1);
     return std::min(s, s_max);
@@ -543,7 +550,7 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
     MfmaParams a{};
     a.c = c; a.q = q; a.ws = ws;
     const int groups = c.L * c.B * c.Hkv;
-    a.splits = mfma_splits(groups, al.max_entries, al.s_max);
+    a.splits = mfma_splits(groups, al.max_entries, al.s_max, attention_splits_request());
     dim3 grid(a.splits, groups);
     if (c.meta_dtype == FQ_BF16)
         return c.G == 4 ? launch_mfma_nrep<bf16, 4>(a, grid, st) : launch_mfma_nrep<bf16, 1>(a, grid, st);

@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <string>
 #include <vector>
 
@@ -162,6 +163,9 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
     return FQ_OK;
 }
 
+static std::atomic<int> g_split_request{0};
+int attention_splits_request() { return g_split_request.load(std::memory_order_relaxed); }
+
 void timer_before_launch(hipStream_t st) {
     KernelTimer& t = g_timer;
     if (t.armed && t.used < (int)t.start.size()) (void)hipEventRecord(t.start[t.used], st);
@@ -176,6 +180,12 @@ void timer_after_launch(hipStream_t st) {
 using namespace fq;
 
 extern "C" {
+
+int fq_set_attention_splits(int32_t splits) {
+    if (splits < 0) return fail(FQ_ERR_INVALID, "splits must be >= 0");
+    g_split_request.store(splits, std::memory_order_relaxed);
+    return FQ_OK;
+}
 
 int fq_kernel_timer_start(int32_t max_launches) {
     KernelTimer& t = g_timer;

@@ -203,6 +203,8 @@ struct AttnLaunch {
 // Kernel timer hooks around an attention kernel launch (no-ops unless armed).
 void timer_before_launch(hipStream_t st);
 void timer_after_launch(hipStream_t st);
+// fq_set_attention_splits value (0 = automatic).
+int attention_splits_request();
 size_t workspace_bytes(int G, int P, int rows, int nrep, int D);
 Workspace carve_workspace(void* base, int G, int P, int rows, int nrep, int D);
 AttnLaunch choose_split(int G, int max_entries, int s_max);

@@ -105,6 +105,13 @@ int fq_abi_version(void);
 int fq_kernel_timer_start(int32_t max_launches);
 int fq_kernel_timer_stop(float* total_ms, int32_t* launches);
 
+/* Split-count override for the matrix-core INT4 attention kernel (no
+ * counterpart in the reference; for tests and tuning).  0 restores the
+ * automatic choice; n > 0 asks for n workgroups per KV group, raised if a split
+ * would exceed the kernel's page limit and lowered to the workspace capacity.
+ * Process-wide. */
+int fq_set_attention_splits(int32_t splits);
+
 /* Bytes of workspace the attention / decode entries need for this cache and
  * H_q (page lists, scores and split partials; no initialisation needed).
  * Calls that share a workspace must be ordered (same stream). */

@@ -1,0 +1,109 @@
+"""Matrix-core INT4 attention (head_dim 128, 64-token pages): the paths that only
+show with many pages per wave, compared with the CPU oracle (MI355X).
+
+The kernel keeps p.v in int32 against a running softmax maximum and V-scale
+bound and rescales when a page exceeds either; these cases force such events on
+every page (growing logits, growing V scales), none after the first (shrinking),
+waves without pages, a partial last page, and every supported query-head ratio
+and V grouping.  Splits per KV group are pinned so each wave gets many pages.
+"""
+import numpy as np
+import pytest
+import torch
+
+from flashquest_amd import _lib as L
+from oracle import fq_oracle as O
+from tests.cases import Int4Case, max_err, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL_O = 2e-3
+
+
+def _tol(case, ref_o):
+    ulp = 2.0 ** (-8 if case.dtype == "bf16" else -11)
+    return TOL_O + ulp * float(np.abs(ref_o).max())
+
+
+def _requantise(case):
+    case.kp, case.ks, case.km = O.quantize_k_int4(case.K, case.page, case.dtype, case.meta)
+    case.vp, case.vs, case.vm = O.quantize_v_int4(case.V, case.vgroup, case.meta)
+
+
+def _ramp(case, direction, v_growth):
+    """Page p's keys lean towards each KV head's mean query by an amount that
+    grows (direction +1) or shrinks (-1) with p; V is scaled by v_growth**p."""
+    rnd = O.rounder(case.dtype)
+    nrep = case.Hq // case.Hkv
+    qdir = case.Q.reshape(case.B, case.Hkv, nrep, case.D).mean(2)
+    qdir /= np.linalg.norm(qdir, axis=-1, keepdims=True)
+    P, page = case.P, case.page
+    for p in range(P):
+        frac = p / max(P - 1, 1)
+        a = 6.0 * (frac if direction > 0 else 1.0 - frac)
+        sl = slice(p * page, min((p + 1) * page, case.S))
+        case.K[:, :, sl] = rnd(case.K[:, :, sl] * 0.5 + a * qdir[:, :, None, :])
+        case.V[:, :, sl] = rnd(case.V[:, :, sl] * np.float32(v_growth ** p))
+    _requantise(case)
+
+
+def _run(case, mask, splits):
+    from flashquest_amd.kernel import flash_attn_sparse_int4_fwd
+    with L.attention_splits(splits):
+        o, lse = flash_attn_sparse_int4_fwd(case.q_dev(), **case.device(),
+                                            selection_mask=to_dev(mask)[:, :, None, :])
+    torch.cuda.synchronize()
+    return o, lse
+
+
+@pytest.mark.parametrize("direction,v_growth", [(1, 1.08), (-1, 1.0), (1, 0.93)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_rescale_events_on_every_page(direction, v_growth, splits):
+    case = Int4Case(seed=40 + splits, B=1, Hq=6, Hkv=2, S=64 * 64, D=128, page=64, dtype="f16", meta="f16",
+                    vgroup=32)
+    _ramp(case, direction, v_growth)
+    mask = np.ones((1, 6, case.P), bool)
+    ref_o, ref_l = case.oracle(mask)
+    o, lse = _run(case, mask, splits)
+    assert max_err(o[:, :, 0], ref_o) <= _tol(case, ref_o)
+    assert max_err(lse[:, :, 0], ref_l) <= 1e-4
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(2, 2), (4, 2), (12, 4), (8, 2)])
+@pytest.mark.parametrize("vgroup,meta", [(None, "bf16"), (32, "f16"), (32, "bf16")])
+def test_head_ratios_groups_partial_page(Hq, Hkv, vgroup, meta):
+    case = Int4Case(seed=Hq * 7 + Hkv + (vgroup or 0), B=2, Hq=Hq, Hkv=Hkv, S=64 * 40 + 33, D=128, page=64,
+                    dtype="bf16", meta=meta, vgroup=vgroup)
+    mask = case.rng.random((2, Hq, case.P)) < 0.5
+    mask[:, :, -1] = True                 # the partial last page is always in
+    mask[1, 0] = False                    # an empty head
+    ref_o, ref_l = case.oracle(mask)
+    for splits in (1, 0):
+        o, lse = _run(case, mask, splits)
+        assert max_err(o[:, :, 0], ref_o) <= _tol(case, ref_o), splits
+        assert max_err(lse[:, :, 0], ref_l) <= 1e-4, splits
+
+
+def test_waves_without_pages_and_empty_groups():
+    case = Int4Case(seed=5, B=2, Hq=6, Hkv=2, S=64 * 24, D=128, page=64, dtype="f16", meta="f16", vgroup=32)
+    mask = np.zeros((2, 6, case.P), bool)
+    mask[0, 0, 5] = True                  # one page in the group: three idle waves
+    mask[0, 4, [1, 9]] = True             # two pages, other group
+    mask[1, :3, 7] = True                 # same page for all heads of a group
+    ref_o, ref_l = case.oracle(mask)      # group (1, head 1) is empty
+    for splits in (1, 2, 0):
+        o, lse = _run(case, mask, splits)
+        assert max_err(o[:, :, 0], ref_o) <= _tol(case, ref_o), splits
+        assert max_err(lse[:, :, 0], ref_l) <= 1e-4, splits
+
+
+def test_split_override_is_restored_and_validated():
+    assert L.lib().fq_set_attention_splits(-1) != 0
+    with L.attention_splits(2):
+        pass
+    case = Int4Case(seed=9, B=1, Hq=6, Hkv=2, S=64 * 8, D=128, page=64)
+    mask = np.ones((1, 6, case.P), bool)
+    ref_o, _ = case.oracle(mask)
+    from flashquest_amd.kernel import flash_attn_sparse_int4_fwd
+    o, _ = flash_attn_sparse_int4_fwd(case.q_dev(), **case.device(), selection_mask=to_dev(mask)[:, :, None, :])
+    assert max_err(o[:, :, 0], ref_o) <= _tol(case, ref_o)
