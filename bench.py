@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--select", default="per_kv_head_sum", choices=["per_kv_head_sum", "per_q_head"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip control / per-layer / per-q-head lines")
-    ap.add_argument("--cpu-layers", type=int, default=6, help="layers in the CPU baseline sample")
+    ap.add_argument("--cpu-layers", type=int, default=10, help="layers in the CPU baseline sample")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
     return ap.parse_args()
@@ -88,9 +88,12 @@ def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda")
 
 
 def step_bytes(cache, mask, page=64):
-    """Algorithmic HBM bytes of one step: (scoring, attention) = K metadata of
-    every page; codes + V metadata of the union of selected pages per KV group,
-    plus Q in and O / lse out."""
+    """Algorithmic HBM bytes of one step, each input read once and each output
+    written once: scoring = K scale/min of every page; the step's attention
+    part = K/V codes + V scale/min of the union of selected pages per KV group,
+    plus Q in and O / lse out.  The attention kernel on its own also reads the
+    K scale/min of the selected pages (which scoring already counted for the
+    step): returned as the third value, the kernel's own algorithmic bytes."""
     L, B, Hkv, P, D = cache["K_scale"].shape
     Hq = cache["Q"].shape[2]
     meta = cache["K_scale"].element_size()
@@ -99,7 +102,9 @@ def step_bytes(cache, mask, page=64):
     union = mask.view(L, B, Hkv, Hq // Hkv, P).any(3).sum().item()
     per_page = 2 * page * D // 2 + 2 * page * G * meta
     qo = L * B * Hq * (D * 2 * 2 + 4)
-    return scoring, union * per_page + qo, union
+    attn_step = union * per_page + qo
+    attn_kernel = attn_step + union * 2 * D * meta
+    return scoring, attn_step, attn_kernel, union
 
 
 # --------------------------------------------------------------- measurement --
@@ -110,14 +115,14 @@ class Flusher:
     (``write=True`` measures that variant, reported as an extra)."""
 
     def __init__(self, dev, write=False):
-        self.buf = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+        self.buf = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         self.write = write
 
     def __call__(self):
         if self.write:
-            self.buf.fill_(1)
+            self.buf.fill_(1.0)
         else:
-            torch.sum(self.buf, dtype=torch.int64)
+            torch.sum(self.buf)             # one read pass, a 4-byte result
 
 
 def time_steps(fn_pre, fn_timed, steps, warmup, flush, kernel_timer=False):
@@ -171,34 +176,31 @@ def measured_traffic(L, B, P, retention, select):
 
 
 def cpu_baseline(cache, args, n_layers):
-    """Oracle restatement timed on the host (1 thread): fixed-order fp32 scores,
-    top-k selection, fp32 dequant of the selected pages only, fp32 attention."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-
-    from oracle import fq_oracle as O
-    page = 64
+    """The reference's eager CPU path restated in PyTorch (oracle/torch_eager.py:
+    two fp32 matmuls for the scores, topk + forced pages, fp32 dequant of the
+    selected pages, fp32 softmax attention), timed on the host with all of the
+    box's CPU share; median layer time x layers."""
+    from oracle import torch_eager as TE
+    threads = max(1, min(16, os.cpu_count() or 1))        # a one-GPU box's CPU share is 16
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
     host = {k: v[:n_layers, 0].cpu() for k, v in cache.items()}
-    f32 = {k: (t.float().numpy() if t.dtype == torch.float16 else t.numpy()) for k, t in host.items()}
-    Hq, Hkv = f32["Q"].shape[1], f32["K_scale"].shape[1]
     times = []
-    with threadpool_limits(1):
-        for l in range(n_layers):
-            t0 = time.perf_counter()
-            q = f32["Q"][l][None, :, 0, :]
-            sc = O.page_scores_fixed(q, f32["K_scale"][l][None], f32["K_mn"][l][None], args.select)
-            k = math.ceil(args.retention * sc.shape[-1])
-            m = O.select_pages_vectorized(sc[:, :, None, :], args.retention, 4, 2, k)[:, :, 0, :]
-            if args.select == "per_kv_head_sum":
-                m = np.repeat(m, Hq // Hkv, axis=1)
-            O.sparse_int4_attention_selected(q, f32["K_packed"][l][None], f32["K_scale"][l][None],
-                                             f32["K_mn"][l][None], f32["V_packed"][l][None],
-                                             f32["V_scale"][l][None], f32["V_mn"][l][None], m, page)
-            times.append(time.perf_counter() - t0)
+    try:
+        for rep in range(2):                               # first pass warms up
+            for l in range(n_layers):
+                t0 = time.perf_counter()
+                TE.decode_layer(host["Q"][l, :, 0].float(), host["K_packed"][l], host["K_scale"][l],
+                                host["K_mn"][l], host["V_packed"][l], host["V_scale"][l], host["V_mn"][l],
+                                retention=args.retention, select=args.select)
+                if rep:
+                    times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
     per_layer = sorted(times)[len(times) // 2]
-    return {"value": per_layer * args.layers * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+    return {"value": per_layer * args.layers * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n_layers} layers of the same workload (batch 1), median layer time x {args.layers}; "
-                      "numpy oracle, BLAS limited to 1 thread"}
+                      f"eager PyTorch restatement of the reference CPU path, {threads} threads"}
 
 
 def main():
@@ -236,7 +238,7 @@ def main():
     dec = decoder(args.retention, k, args.select, mask=mask)
     dec()
     torch.cuda.synchronize()
-    scoring_b, attn_b, union = step_bytes(cache, mask)
+    scoring_b, attn_b, attn_kernel_b, union = step_bytes(cache, mask)
     dec.mask_out = None
     noop = lambda: None
     step_ms, wall, _ = time_steps(noop, dec, args.steps, args.warmup, flush)
@@ -251,7 +253,7 @@ def main():
         ctl = decoder(1.0, P, args.select)
         ctl_ms, _, _ = time_steps(noop, ctl, args.steps, args.warmup, flush)
         full_mask = torch.ones(L, B, Hq, P, dtype=torch.bool, device=dev)
-        sb, ab, _ = step_bytes(cache, full_mask)
+        sb, ab, _, _ = step_bytes(cache, full_mask)
         extra.update({"all_pages_control_us": ctl_ms * 1e3, "sparse_speedup_vs_all_pages": ctl_ms / step_ms,
                       "all_pages_GBps": (sb + ab) / (ctl_ms * 1e-3) / 1e9})
         other = "per_q_head" if args.select == "per_kv_head_sum" else "per_kv_head_sum"
@@ -284,10 +286,10 @@ def main():
         del wflush
 
     traffic = measured_traffic(L, B, P, args.retention, args.select)
-    roof = {"bound": "hbm", "achieved": attn_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": attn_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
+    roof = {"bound": "hbm", "achieved": attn_kernel_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": attn_kernel_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
             "kernel": "attn_int4_mfma_kernel (split-K sparse GQA attention, all layers in one launch)",
-            "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_b}
+            "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_kernel_b}
     cpu = None
     if not args.no_cpu_baseline and B == 1:
         cpu = cpu_baseline(cache, args, min(args.cpu_layers, L))

@@ -161,3 +161,27 @@ def test_selected_pages_path_equals_full_dequant_path():
     b, lb = O.sparse_int4_attention_selected(Q, kp, ks, km, vp, vs, vm, mask, ps)
     assert np.allclose(a, b, atol=1e-5) and np.allclose(la[np.isfinite(la)], lb[np.isfinite(lb)], atol=1e-5)
     assert np.array_equal(np.isfinite(la), np.isfinite(lb))
+
+
+def test_torch_eager_baseline_matches_oracle():
+    # oracle/torch_eager.py is bench.py's CPU baseline: same selection and output as the numpy oracle
+    import torch
+
+    from oracle import torch_eager as TE
+    rng = np.random.default_rng(21)
+    Hkv, Hq, D, page, P = 2, 6, 128, 64, 16
+    K = O.round_f16(rng.standard_normal((1, Hkv, P * page, D)).astype(np.float32))
+    V = O.round_f16(rng.standard_normal((1, Hkv, P * page, D)).astype(np.float32))
+    Q = rng.standard_normal((1, Hq, D)).astype(np.float32)
+    kp, ks, km = O.quantize_k_int4(K, page, "f16", "f16")
+    vp, vs, vm = O.quantize_v_int4(V, 32, "f16")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    for mode in ("per_kv_head_sum", "per_q_head"):
+        sc = O.page_scores_fixed(Q, ks, km, mode)
+        m = O.select_pages_vectorized(sc[:, :, None, :], 0.25, 4, 2, math.ceil(0.25 * P))[:, :, 0, :]
+        if mode == "per_kv_head_sum":
+            m = np.repeat(m, Hq // Hkv, axis=1)
+        ref, _ = O.sparse_int4_attention(Q, kp, ks, km, vp, vs, vm, m, page)
+        out = TE.decode_layer(t(Q[0]), t(kp[0]), t(ks[0]).half(), t(km[0]).half(), t(vp[0]), t(vs[0]).half(),
+                              t(vm[0]).half(), retention=0.25, select=mode)
+        assert float((out - t(ref[0])).abs().max()) < 1e-5
