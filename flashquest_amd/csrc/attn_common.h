@@ -26,10 +26,10 @@ FQ_DEV void merge_weights(float m_self, float m_other, float& M, float& w_self, 
 // Walsh-Hadamard entry H[i][j] / sqrt(D) with the Sylvester sign (-1)^popc(i&j).
 FQ_DEV float hadamard_sign(int i, int j) { return (__popc(i & j) & 1) ? -1.f : 1.f; }
 
-template <int D, int NREP>
+template <int D, int NREP, int NW = 4>
 struct SplitLds {
-    float m[4][NREP], l[4][NREP];
-    float acc[4][NREP][D];
+    float m[NW][NREP], l[NW][NREP];
+    float acc[NW][NREP][D];
     float out[NREP][D];
     float L[NREP], M[NREP];
 };
@@ -37,12 +37,12 @@ struct SplitLds {
 // Writes O (vals[r][d] = acc / l, rotated back when ROT) and lse for the NREP
 // query heads of KV group (l, b, h).  Must be called by the whole workgroup
 // after vals / Ls / Ms are complete in LDS.
-template <int D, int NREP, bool ROT>
+template <int D, int NREP, bool ROT, int NT = kThreads>
 FQ_DEV void store_outputs(const QueryArgs& q, int l, int b, int h, const float (*vals)[D], const float* Ls,
                           const float* Ms) {
     const int tid = threadIdx.x;
     const float inv = 1.0f / sqrtf((float)D);
-    for (int i = tid; i < NREP * D; i += kThreads) {
+    for (int i = tid; i < NREP * D; i += NT) {
         const int r = i / D, d = i % D;
         float o = vals[r][d];
         if constexpr (ROT) {
@@ -54,25 +54,26 @@ FQ_DEV void store_outputs(const QueryArgs& q, int l, int b, int h, const float (
         store_any(q.out, q.out_dtype, l * q.o_s[0] + b * q.o_s[1] + hq * q.o_s[2] + d * q.o_s[3], o);
     }
     if (q.lse)
-        for (int r = tid; r < NREP; r += kThreads) {
+        for (int r = tid; r < NREP; r += NT) {
             const int hq = h * NREP + r;
             q.lse[l * q.lse_s[0] + b * q.lse_s[1] + hq * q.lse_s[2]] =
                 Ls[r] > 0.f ? (Ms[r] + log2f(Ls[r])) * kLn2 : -INFINITY;
         }
 }
 
-// Merges the 4 waves' (m, l, acc) states held in s (after a barrier); with one
+// Merges the NW waves' (m, l, acc) states held in s (after a barrier); with one
 // split writes O / lse, otherwise stores the workgroup's split partial.
-template <int D, int NREP, bool ROT>
-FQ_DEV void merge_waves_and_store(SplitLds<D, NREP>& s, const QueryArgs& q, const Workspace& ws, int g, int l,
+template <int D, int NREP, bool ROT, int NW = 4>
+FQ_DEV void merge_waves_and_store(SplitLds<D, NREP, NW>& s, const QueryArgs& q, const Workspace& ws, int g, int l,
                                   int b, int h, int split, int splits) {
+    constexpr int NT = 64 * NW;
     const int tid = threadIdx.x;
     const int64_t part = ((int64_t)g * ws.s_max + split) * NREP;
-    for (int i = tid; i < NREP * D; i += kThreads) {
+    for (int i = tid; i < NREP * D; i += NT) {
         const int r = i / D, d = i % D;
         float M = -INFINITY, L = 0.f, A = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
+        for (int ww = 0; ww < NW; ++ww) {
             float Mn, w_s, w_o;
             merge_weights(M, s.m[ww][r], Mn, w_s, w_o);
             L = L * w_s + s.l[ww][r] * w_o;
@@ -92,7 +93,7 @@ FQ_DEV void merge_waves_and_store(SplitLds<D, NREP>& s, const QueryArgs& q, cons
     }
     if (splits == 1) {
         __syncthreads();
-        store_outputs<D, NREP, ROT>(q, l, b, h, s.out, s.L, s.M);
+        store_outputs<D, NREP, ROT, NT>(q, l, b, h, s.out, s.L, s.M);
     }
 }
 

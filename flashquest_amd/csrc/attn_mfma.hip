@@ -36,7 +36,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
-constexpr int kMaxWgPages = 256;            // pages of one workgroup split (entries staged in LDS)
+constexpr int kMaxWgPages = 1024;           // pages of one workgroup split (entries staged in LDS)
 constexpr float kQkScale = 8323071.0f;      // 2^23 - 2^16 - 1: |X| <= this keeps 3 balanced digits in int8
 constexpr float kSubnormal = 16777216.0f;   // 2^24: fp16 subnormal with bits c has value c * 2^-24
 
@@ -156,12 +156,14 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
     load_vmeta<G>(b.vm, r.vm, moff);
 }
 
-template <typename MT, int G, int NREP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW waves per workgroup (4, or 8 when one workgroup takes a whole KV group).
+template <typename MT, int G, int NREP, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int4_mfma_kernel(MfmaParams a) {
     constexpr int D = 128;
-    __shared__ SplitLds<D, NREP> s_split;
-    __shared__ WaveLds s_wave[4];
+    constexpr int NT = 64 * NW;
+    __shared__ SplitLds<D, NREP, NW> s_split;
+    __shared__ WaveLds s_wave[NW];
     __shared__ int s_ent[kMaxWgPages];
 
     const Int4Cache& c = a.c;
@@ -175,16 +177,19 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 
     // Prologue: this split's entries and q (as prescaled fp32) go to LDS; every
     // load is unconditional (clamped index), so all are in flight before the wait.
-    static_assert(kMaxWgPages == kThreads, "one entry per thread");
+    constexpr int kEntPer = kMaxWgPages / NT;
+    static_assert(kMaxWgPages % NT == 0 && NREP * D <= 2 * NT, "prologue sizes");
     __shared__ float s_q[NREP][D];
     const int n_sel = a.ws.n_sel[g];
     const int e0 = (int)((int64_t)n_sel * split / a.splits);       // balanced split: entries [e0, e1)
     const int e1 = (int)((int64_t)n_sel * (split + 1) / a.splits);
     {
         const int tid = threadIdx.x;
-        const int ent = a.ws.entries[(int64_t)g * c.P + min(e0 + tid, c.P - 1)];
+        int ent[kEntPer];
+#pragma unroll
+        for (int u = 0; u < kEntPer; ++u) ent[u] = a.ws.entries[(int64_t)g * c.P + min(e0 + tid + u * NT, c.P - 1)];
         const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
-        const int i0 = tid, i1 = min(tid + kThreads, NREP * D - 1);
+        const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
         const int64_t o0 = qb + (i0 >> 7) * q.q_s[2] + (i0 & 127) * q.q_s[3];
         const int64_t o1 = qb + (i1 >> 7) * q.q_s[2] + (i1 & 127) * q.q_s[3];
         float v0, v1;
@@ -196,13 +201,15 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             v0 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u0) : f16_bits_to_f(u0);
             v1 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u1) : f16_bits_to_f(u1);
         }
-        if (tid < e1 - e0) s_ent[tid] = ent;
-        if (i0 < NREP * D) s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
-        if (tid + kThreads < NREP * D) s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+#pragma unroll
+        for (int u = 0; u < kEntPer; ++u)
+            if (tid + u * NT < e1 - e0) s_ent[tid + u * NT] = ent[u];
+        if (tid < NREP * D) s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+        if (tid + NT < NREP * D) s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
     }
     __syncthreads();
-    // pages of this wave: entries w, w + 4, ... (wave-uniform)
-    const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + 3) / 4 : 0;
+    // pages of this wave: entries w, w + NW, ... (wave-uniform)
+    const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;
 
     const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
     const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
@@ -231,7 +238,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     rs.ks = make_rsrc(ksc, (int64_t)c.P * D * 2);
     rs.km = make_rsrc(kmn, (int64_t)c.P * D * 2);
     const int koff0 = n16 * 64 + 16 * lg, voff0 = lg * 64 + 4 * n16, moff0 = n16 * G * 2, soff0 = ch_base * 2;
-    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + 4 * k]); };
+    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
     auto issue = [&](PageBuf& bf, int k) {
         const int p = entry_of(k) & 0xFFFF;
         // keep the scheduler from moving compute work in front of the loads
@@ -491,16 +498,16 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         }
     }
     __syncthreads();
-    merge_waves_and_store<D, NREP, false>(s_split, q, a.ws, g, l, b, h, split, a.splits);
+    merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits);
 }
 
-template <typename MT, int G>
+template <typename MT, int G, int NW>
 hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                     \
     case N:                                                                                            \
         timer_before_launch(st);                                                                       \
-        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N>), grid, dim3(kThreads), 0, st, a);         \
+        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW>), grid, dim3(64 * NW), 0, st, a);      \
         timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                              \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
@@ -513,16 +520,20 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Splits per KV group: enough workgroups to keep every CU busy in one pass
-// (two resident per CU), at least 8 pages per split, at most kMaxWgPages.
-// `request` > 0 overrides the first two rules.
-int mfma_splits(int groups, int max_entries, int s_max, int request) {
+// Work split.  With enough KV groups to cover most CUs, one workgroup of 8
+// waves takes a whole group (no split partials, no merge launch).  Otherwise
+// workgroups of 4 waves take balanced slices: enough to keep every CU busy in
+// one pass (two resident per CU), at least 8 pages per slice.  `request` > 0
+// pins the slices per group (4-wave workgroups).
+struct MfmaSplit { int splits, waves; };
+MfmaSplit mfma_splits(int groups, int max_entries, int s_max, int request) {
     constexpr int kResident = 2 * 256;
+    if (request <= 0 && groups >= 192 && max_entries <= kMaxWgPages) return {1, 8};
     int s = request > 0 ? request : kResident / (groups > 0 ? groups : 1);
     if (request <= 0) s = std::min(s, (max_entries + 7) / 8);
     s = std::max(s, (max_entries + kMaxWgPages - 1) / kMaxWgPages);
     s = std::max(s, 1);
-    return std::min(s, s_max);
+    return {std::min(s, s_max), 4};
 }
 
 }  // namespace
@@ -550,11 +561,13 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
     MfmaParams a{};
     a.c = c; a.q = q; a.ws = ws;
     const int groups = c.L * c.B * c.Hkv;
-    a.splits = mfma_splits(groups, al.max_entries, al.s_max, attention_splits_request());
+    const MfmaSplit sp = mfma_splits(groups, al.max_entries, al.s_max, attention_splits_request());
+    a.splits = sp.splits;
     dim3 grid(a.splits, groups);
-    if (c.meta_dtype == FQ_BF16)
-        return c.G == 4 ? launch_mfma_nrep<bf16, 4>(a, grid, st) : launch_mfma_nrep<bf16, 1>(a, grid, st);
-    return c.G == 4 ? launch_mfma_nrep<f16, 4>(a, grid, st) : launch_mfma_nrep<f16, 1>(a, grid, st);
+#define FQ_W(MT_, G_) (sp.waves == 8 ? launch_mfma_nrep<MT_, G_, 8>(a, grid, st) : launch_mfma_nrep<MT_, G_, 4>(a, grid, st))
+    if (c.meta_dtype == FQ_BF16) return c.G == 4 ? FQ_W(bf16, 4) : FQ_W(bf16, 1);
+    return c.G == 4 ? FQ_W(f16, 4) : FQ_W(f16, 1);
+#undef FQ_W
 }
 
 }  // namespace fq

@@ -146,7 +146,43 @@ FQ_DEV void load_q_rows(const ScoreParams& a, int l, int b, int h, float (*s_q)[
 
 constexpr int kPasses = 4;                  // passes of PPP pages per scoring chunk
 
-template <int D, typename MT>
+// Same arithmetic as score_page with the lane's q values of NR rows in
+// registers (loaded once per workgroup instead of once per page).
+template <int NR, typename MT, typename Emit>
+FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[NR][8], const float (&qp)[NR][8],
+                            Emit emit) {
+    float sf[8], mf[8];
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sf[2 * j] = half_to_f<MT>(sw[j]);
+        sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
+        mf[2 * j] = half_to_f<MT>(mw[j]);
+        mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
+    }
+    float t1[NR], t2[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        t1[r] = __fmul_rn(qr[r][0], mf[0]);
+        t2[r] = __fmul_rn(qp[r][0], sf[0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            t1[r] = __fadd_rn(t1[r], __fmul_rn(qr[r][j], mf[j]));
+            t2[r] = __fadd_rn(t2[r], __fmul_rn(qp[r][j], sf[j]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        t1[r] = row_sum<16>(t1[r]);
+        t2[r] = row_sum<16>(t2[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
+}
+
+// NR > 0: D = 128 and exactly NR query rows, q held in registers; NR = 0: any rows.
+template <int D, typename MT, int NR>
 __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     constexpr int NL = D / 8;
     constexpr int PPP = kThreads / NL;           // pages per pass
@@ -157,42 +193,59 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     const int g = blockIdx.y;
     const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
     const int tid = threadIdx.x;
-    load_q_rows<D>(a, l, b, h, s_q, s_qp);
-    __syncthreads();
-
     const int lane_in_page = tid % NL;
     const int page_in_pass = tid / NL;
     const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
     const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
     float* ws_scores = a.ws_scores ? a.ws_scores + (int64_t)g * a.rows * c.P : nullptr;
 
-    // a chunk is at most kPasses passes: every pass's metadata is loaded before
-    // any is scored, so the chunk costs one memory latency
+    // The workgroup streams its chunk pass by pass (PPP pages per pass) with
+    // kPasses passes of metadata in flight ahead of the one being scored; past
+    // the end the loads repeat the last page, so every step issues the same loads.
     const int p_begin = blockIdx.x * a.ppc;
     const int p_end = min(c.P, p_begin + a.ppc);
+    const int npass = (p_end - p_begin + PPP - 1) / PPP;
     uint4 sv[kPasses], mv[kPasses];
-#pragma unroll
-    for (int u = 0; u < kPasses; ++u) {
-        const int p = min(p_begin + u * PPP + page_in_pass, p_end - 1);
+    auto fetch = [&](int u, int pass) {
+        const int p = min(p_begin + pass * PPP + page_in_pass, p_end - 1);
         sv[u] = *(const uint4*)(ksc + p * c.ksc_s[3] + lane_in_page * 8);
         mv[u] = *(const uint4*)(kmn + p * c.kmn_s[3] + lane_in_page * 8);
-    }
+    };
 #pragma unroll
-    for (int u = 0; u < kPasses; ++u) {
-        const int p = p_begin + u * PPP + page_in_pass;
-        if (p < p_end) {
-            float acc_kv = 0.f;
-            score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.rows, lane_in_page, [&](int r, float sc) {
-                if (lane_in_page == 0) {
-                    const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
-                    if (a.scores)
-                        a.scores[(l * c.B + b) * a.sc_s[0] + hq * a.sc_s[1] + sq * a.sc_s[2] + p * a.sc_s[3]] = sc;
-                    if (ws_scores && a.mode == FQ_SELECT_PER_Q_HEAD) ws_scores[r * c.P + p] = sc;
-                }
-                acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
-            });
-            if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
-                ws_scores[p] = acc_kv;
+    for (int u = 0; u < kPasses; ++u) fetch(u, u);
+    load_q_rows<D>(a, l, b, h, s_q, s_qp);
+    __syncthreads();
+    float qr[NR > 0 ? NR : 1][8], qp[NR > 0 ? NR : 1][8];
+    if constexpr (NR > 0) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                qr[r][j] = s_q[r][lane_in_page * 8 + j];
+                qp[r][j] = s_qp[r][lane_in_page * 8 + j];
+            }
+    }
+    for (int pass0 = 0; pass0 < npass; pass0 += kPasses) {
+#pragma unroll
+        for (int u = 0; u < kPasses; ++u) {
+            const int p = p_begin + (pass0 + u) * PPP + page_in_pass;
+            if (pass0 + u < npass && p < p_end) {
+                float acc_kv = 0.f;
+                auto emit = [&](int r, float sc) {
+                    if (lane_in_page == 0) {
+                        const int hq = h * a.nrep + r / a.Sq, sq = r % a.Sq;
+                        if (a.scores)
+                            a.scores[(l * c.B + b) * a.sc_s[0] + hq * a.sc_s[1] + sq * a.sc_s[2] + p * a.sc_s[3]] = sc;
+                        if (ws_scores && a.mode == FQ_SELECT_PER_Q_HEAD) ws_scores[r * c.P + p] = sc;
+                    }
+                    acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
+                };
+                if constexpr (NR > 0) score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, emit);
+                else score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.rows, lane_in_page, emit);
+                if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
+                    ws_scores[p] = acc_kv;
+            }
+            fetch(u, pass0 + u + kPasses);
         }
     }
 }
@@ -465,14 +518,13 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     a.scores = scores;
     if (sc4_s) for (int i = 0; i < 4; ++i) a.sc_s[i] = sc4_s[i];
     const int G = c.L * c.B * c.Hkv;
-    // pages per chunk: aim for >= ~2 waves of workgroups over 256 CUs, at most
-    // kPasses passes of ppp pages per workgroup
+    // pages per chunk: about two workgroups per CU in one pass over the GPU,
+    // each streaming a whole number of passes of ppp pages
     const int ppp = kThreads / (c.D / 8);
-    int target_chunks = (2048 + G - 1) / G;
+    int target_chunks = (512 + G - 1) / G;
     int ppc = (c.P + target_chunks - 1) / target_chunks;
     ppc = ((ppc + ppp - 1) / ppp) * ppp;
     if (ppc < ppp) ppc = ppp;
-    if (ppc > kPasses * ppp) ppc = kPasses * ppp;
     a.ppc = ppc;
     a.nchunks = (c.P + ppc - 1) / ppc;
     a.ws_scores = ws ? ws->scores : nullptr;
@@ -485,12 +537,21 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
         sp.mask_out = mask_out;
     }
     dim3 grid(a.nchunks, G);
-#define FQ_SCORE(D_, MT_) hipLaunchKernelGGL((score_kernel<D_, MT_>), grid, dim3(kThreads), 0, st, a)
-    if (c.D == 128) {
-        if (c.meta_dtype == FQ_BF16) FQ_SCORE(128, bf16); else FQ_SCORE(128, f16);
-    } else {
-        if (c.meta_dtype == FQ_BF16) FQ_SCORE(64, bf16); else FQ_SCORE(64, f16);
+#define FQ_SCORE(D_, MT_, NR_) hipLaunchKernelGGL((score_kernel<D_, MT_, NR_>), grid, dim3(kThreads), 0, st, a)
+#define FQ_SCORE_NR(MT_)                                                   \
+    switch (a.rows) {                                                      \
+        case 1: FQ_SCORE(128, MT_, 1); break;                              \
+        case 2: FQ_SCORE(128, MT_, 2); break;                              \
+        case 3: FQ_SCORE(128, MT_, 3); break;                              \
+        case 4: FQ_SCORE(128, MT_, 4); break;                              \
+        default: FQ_SCORE(128, MT_, 0); break;                             \
     }
+    if (c.D == 128) {
+        if (c.meta_dtype == FQ_BF16) { FQ_SCORE_NR(bf16) } else { FQ_SCORE_NR(f16) }
+    } else {
+        if (c.meta_dtype == FQ_BF16) FQ_SCORE(64, bf16, 0); else FQ_SCORE(64, f16, 0);
+    }
+#undef FQ_SCORE_NR
 #undef FQ_SCORE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !ws) return e;
