@@ -208,9 +208,14 @@ hipError_t launch_gv(const AttnParams& a, dim3 grid, hipStream_t st) {
 
 }  // namespace
 
+bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
+    return mfma_select_in_kernel(c, q, al);
+}
+
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                            const AttnLaunch& al, hipStream_t st) {
-    if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st);
+                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel) {
+    if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st, sel);
+    if (sel && sel->enabled) return hipErrorInvalidValue;
     AttnParams a{};
     a.c = c; a.q = q; a.ws = ws; a.pps = al.pages_per_split; a.splits = al.splits;
     dim3 grid(al.splits, c.L * c.B * c.Hkv);

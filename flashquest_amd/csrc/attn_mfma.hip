@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "attn_common.h"
+#include "select_common.h"
 
 namespace fq {
 namespace {
@@ -37,6 +38,7 @@ typedef float f2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxWgPages = 1024;           // pages of one workgroup split (entries staged in LDS)
+constexpr int kSelC = 8;                    // in-kernel selection: pages per lane (P <= 512)
 constexpr float kQkScale = 8323071.0f;      // 2^23 - 2^16 - 1: |X| <= this keeps 3 balanced digits in int8
 constexpr float kSubnormal = 16777216.0f;   // 2^24: fp16 subnormal with bits c has value c * 2^-24
 
@@ -45,6 +47,7 @@ struct MfmaParams {
     QueryArgs q;
     Workspace ws;
     int splits;
+    SelectArgs sel;         // sel.enabled: the workgroup scores and selects its group's pages (splits == 1)
 };
 
 // A operands of one wave: [k-step][row][k-group, XOR-swizzled][16 bytes].
@@ -156,6 +159,64 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
     load_vmeta<G>(b.vm, r.vm, moff);
 }
 
+// Page scores of one KV group (P <= 64 * kSelC pages) by a whole workgroup of
+// NT threads: 16 lanes per page, NT / 16 pages per pass, all passes' metadata
+// loaded before the first is scored.  Writes s_sc[r * P + p] per
+// query head, or (SUM, per_kv_head_sum) s_sc[p] for the group's summed query --
+// score_kernel's arithmetic and order exactly.
+template <typename MT, int NREP, int NT, bool SUM>
+FQ_DEV void score_group_impl(const Int4Cache& c, const float (*s_qraw)[128], float* s_sc, int tid, int l, int b,
+                             int h) {
+    constexpr int PPP = NT / 16;
+    const int lip = tid & 15, pip = tid >> 4;
+    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2] + lip * 8;
+    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2] + lip * 8;
+    const int P = c.P;
+    // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
+    // relu applied per head before the sum; per_q_head scores every head
+    constexpr int NR = SUM ? 1 : NREP;
+    float qr[NR][8], qp[NR][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (SUM) {
+            float qs = s_qraw[0][lip * 8 + j];
+            float ps = qs > 0.f ? qs : 0.f;
+#pragma unroll
+            for (int r = 1; r < NREP; ++r) {
+                const float v = s_qraw[r][lip * 8 + j];
+                qs = __fadd_rn(qs, v);
+                ps = __fadd_rn(ps, v > 0.f ? v : 0.f);
+            }
+            qr[0][j] = qs;
+            qp[0][j] = ps;
+        } else {
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) {
+                qr[r][j] = s_qraw[r][lip * 8 + j];
+                qp[r][j] = qr[r][j] > 0.f ? qr[r][j] : 0.f;
+            }
+        }
+    }
+    // P <= 64 * kSelC, so one pass per PPP pages covers the group: every load
+    // is issued before the first score (pages past P re-read page P-1 and
+    // are scored but not stored), with no branch between loads and use.
+    constexpr int NPASS = 64 * kSelC / PPP;
+    uint4 sv[NPASS], mv[NPASS];
+#pragma unroll
+    for (int u = 0; u < NPASS; ++u) {
+        const int p = min(u * PPP + pip, P - 1);
+        sv[u] = *(const uint4*)(ksc + p * 128);
+        mv[u] = *(const uint4*)(kmn + p * 128);
+    }
+#pragma unroll
+    for (int u = 0; u < NPASS; ++u) {
+        const int p = u * PPP + pip;
+        score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, [&](int r, float sc) {
+            if (lip == 0 && p < P) s_sc[r * P + p] = sc;
+        });
+    }
+}
+
 // NW waves per workgroup (4, or 8 when one workgroup takes a whole KV group).
 template <typename MT, int G, int NREP, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -175,24 +236,22 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     WaveLds& W = s_wave[w];
     const int S = c.S;
 
-    // Prologue: this split's entries and q (as prescaled fp32) go to LDS; every
-    // load is unconditional (clamped index), so all are in flight before the wait.
+    // Prologue: q (as prescaled fp32) and this split's page entries go to LDS.
+    // Every load is unconditional (clamped index), so all are in flight before
+    // the first wait.  The entries either come from the workspace (written by a
+    // selection kernel) or, with sel.enabled, the workgroup scores its group's
+    // pages and wave 0 selects them.
     constexpr int kEntPer = kMaxWgPages / NT;
     static_assert(kMaxWgPages % NT == 0 && NREP * D <= 2 * NT, "prologue sizes");
     __shared__ float s_q[NREP][D];
-    const int n_sel = a.ws.n_sel[g];
-    const int e0 = (int)((int64_t)n_sel * split / a.splits);       // balanced split: entries [e0, e1)
-    const int e1 = (int)((int64_t)n_sel * (split + 1) / a.splits);
+    __shared__ int s_nsel;
+    const int tid = threadIdx.x;
+    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
+    const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
+    float v0, v1;
     {
-        const int tid = threadIdx.x;
-        int ent[kEntPer];
-#pragma unroll
-        for (int u = 0; u < kEntPer; ++u) ent[u] = a.ws.entries[(int64_t)g * c.P + min(e0 + tid + u * NT, c.P - 1)];
-        const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
-        const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
         const int64_t o0 = qb + (i0 >> 7) * q.q_s[2] + (i0 & 127) * q.q_s[3];
         const int64_t o1 = qb + (i1 >> 7) * q.q_s[2] + (i1 & 127) * q.q_s[3];
-        float v0, v1;
         if (q.q_dtype == FQ_F32) {
             v0 = ((const float*)q.q)[o0];
             v1 = ((const float*)q.q)[o1];
@@ -201,15 +260,55 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             v0 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u0) : f16_bits_to_f(u0);
             v1 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u1) : f16_bits_to_f(u1);
         }
+    }
+    auto score_group = [&](const float (*qraw)[D], float* sc, int t, int l_, int b_, int h_) {
+        if constexpr (NW == 8) {   // in-kernel selection runs only in the 8-wave kernel
+            if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_impl<MT, NREP, NT, true>(c, qraw, sc, t, l_, b_, h_);
+            else score_group_impl<MT, NREP, NT, false>(c, qraw, sc, t, l_, b_, h_);
+        }
+    };
+    int e0, e1;
+    if (a.sel.enabled == kScoreSelect) {
+        // Fused decode: score every page of the group from its K metadata
+        // (the arithmetic of score_kernel), keep the scores in LDS, select.
+        __shared__ float s_qraw[NREP][D];
+        __shared__ float s_sc[NREP * 64 * kSelC];
+        if (tid < NREP * D) {
+            s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+            s_qraw[i0 >> 7][i0 & 127] = v0;
+        }
+        if (tid + NT < NREP * D) {
+            s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+            s_qraw[i1 >> 7][i1 & 127] = v1;
+        }
+        __syncthreads();
+        score_group(s_qraw, s_sc, tid, l, b, h);
+        __syncthreads();
+        if (w == 0) {
+            const int n = wave_select_group<kSelC>(s_sc, c.P, NREP, a.sel.mode, a.sel.retention + h * NREP,
+                                                   a.sel.k_max, a.sel.num_sinks, a.sel.window, s_ent, nullptr);
+            if (L == 0) s_nsel = n;
+        }
+        __syncthreads();
+        e0 = 0;
+        e1 = s_nsel;
+    } else {
+        const int n_sel = a.ws.n_sel[g];
+        e0 = (int)((int64_t)n_sel * split / a.splits);           // balanced split: entries [e0, e1)
+        e1 = (int)((int64_t)n_sel * (split + 1) / a.splits);
+        int ent[kEntPer];
+#pragma unroll
+        for (int u = 0; u < kEntPer; ++u) ent[u] = a.ws.entries[(int64_t)g * c.P + min(e0 + tid + u * NT, c.P - 1)];
 #pragma unroll
         for (int u = 0; u < kEntPer; ++u)
             if (tid + u * NT < e1 - e0) s_ent[tid + u * NT] = ent[u];
         if (tid < NREP * D) s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
         if (tid + NT < NREP * D) s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+        __syncthreads();
     }
-    __syncthreads();
-    // pages of this wave: entries w, w + NW, ... (wave-uniform)
-    const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;
+    // Wave w takes entries w, w + NW, ... (a fixed assignment, so the fp32
+    // accumulation order, and the result, do not depend on timing).
+    const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;   // pages w, w + NW, ...
 
     const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
     const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
@@ -238,6 +337,8 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     rs.ks = make_rsrc(ksc, (int64_t)c.P * D * 2);
     rs.km = make_rsrc(kmn, (int64_t)c.P * D * 2);
     const int koff0 = n16 * 64 + 16 * lg, voff0 = lg * 64 + 4 * n16, moff0 = n16 * G * 2, soff0 = ch_base * 2;
+    // k: this wave's k-th page (entry w + NW * k); callers clamp k to the last
+    // page, so every step issues the same loads and the waits match on every path
     auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
     auto issue = [&](PageBuf& bf, int k) {
         const int p = entry_of(k) & 0xFFFF;
@@ -459,12 +560,13 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         wave_lds_fence();
     };
 
-    // One page in flight ahead of the one being computed.  Past the end the last
-    // page is reloaded, so every step issues the same loads and the wait before
-    // each compute is the same on every path.
+    // One page in flight ahead of the one being computed.
     {
+        // issued unconditionally: an idle wave reads some page of the slice (or
+        // zeros past its end) and discards it, but every path into the loop
+        // then has the same loads in flight
         PageBuf b0, b1;
-        if (n_mine > 0) issue(b0, 0);
+        issue(b0, 0);
         for (int k = 0; k < n_mine; k += 2) {
             issue(b1, min(k + 1, n_mine - 1));
             compute(b0, k);
@@ -556,13 +658,23 @@ bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al
     return true;
 }
 
+bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
+    if (!mfma_supported(c, q, al) || c.P > 64 * kSelC) return false;
+    const MfmaSplit sp = mfma_splits(c.L * c.B * c.Hkv, al.max_entries, al.s_max, attention_splits_request());
+    return sp.splits == 1 && sp.waves == 8;
+}
+
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
-                                 hipStream_t st) {
+                                 hipStream_t st, const SelectArgs* sel) {
     MfmaParams a{};
     a.c = c; a.q = q; a.ws = ws;
     const int groups = c.L * c.B * c.Hkv;
     const MfmaSplit sp = mfma_splits(groups, al.max_entries, al.s_max, attention_splits_request());
     a.splits = sp.splits;
+    if (sel && sel->enabled) {
+        if (!mfma_select_in_kernel(c, q, al)) return hipErrorInvalidValue;
+        a.sel = *sel;
+    }
     dim3 grid(a.splits, groups);
 #define FQ_W(MT_, G_) (sp.waves == 8 ? launch_mfma_nrep<MT_, G_, 8>(a, grid, st) : launch_mfma_nrep<MT_, G_, 4>(a, grid, st))
     if (c.meta_dtype == FQ_BF16) return c.G == 4 ? FQ_W(bf16, 4) : FQ_W(bf16, 1);

@@ -336,6 +336,16 @@ static int quest_bound(const Int4Cache& c, const QueryArgs& q, int num_sinks, in
     return (int)bound;
 }
 
+// The fused decode's attention kernel scores and selects its own pages when it
+// takes a whole KV group per workgroup; fq_quest_select_int4 then launches
+// nothing unless the caller asks for the scores or the mask.
+static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, int num_sinks, int window_pages,
+                                        int k_max, int select_mode, const Workspace& ws) {
+    const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
+                                                                      select_mode), ws.s_max);
+    return attn_selects_in_kernel(c, q, al);
+}
+
 int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
                          int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                          float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
@@ -354,25 +364,33 @@ int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, cons
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};   // (L*B, H_q, 1, P) contiguous
     float* sc_user = (scores_out && select_mode == FQ_SELECT_PER_Q_HEAD) ? scores_out : nullptr;
+    if (!mask_out && !sc_user && decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws))
+        return FQ_OK;
     return hip_status(launch_score(c, q, 1, q4, sc_user, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                    k_max, mask_out, (hipStream_t)stream),
                       "score+select");
 }
 
-int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks,
-                         int32_t window_pages, int32_t k_max, int32_t select_mode, void* workspace,
-                         size_t workspace_bytes_, fq_stream_t stream) {
+int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
     int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
     if (st) return st;
+    if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
     if (num_sinks < 0) num_sinks = 0;
     if (window_pages < 0) window_pages = 0;
     if (k_max > c.P) k_max = c.P;
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
-    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream), "sparse int4 attention");
+    SelectArgs sel{};
+    if (attn_selects_in_kernel(c, q, al)) {
+        sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
+        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
+    }
+    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel), "sparse int4 attention");
 }
 
 int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
@@ -382,7 +400,7 @@ int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, cons
     int st = fq_quest_select_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out,
                                   mask_out, workspace, workspace_bytes_, stream);
     if (st) return st;
-    return fq_quest_attend_int4(cache, query, num_sinks, window_pages, k_max, select_mode, workspace,
+    return fq_quest_attend_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, workspace,
                                 workspace_bytes_, stream);
 }
 

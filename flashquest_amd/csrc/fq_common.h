@@ -192,6 +192,17 @@ struct Workspace {
     int s_max;
 };
 
+// Page-selection arguments for an attention kernel that selects its own pages
+// (fused decode): retention per query head, forced pages, k_max, policy.
+// enabled: 0 = pages from the workspace lists, kScoreSelect = the attention
+// kernel scores and selects the pages itself (one launch per decode step).
+constexpr int kScoreSelect = 2;
+struct SelectArgs {
+    const float* retention;
+    int num_sinks, window, k_max, mode;
+    int enabled;
+};
+
 struct AttnLaunch {
     int pages_per_split;
     int splits;
@@ -210,6 +221,8 @@ Workspace carve_workspace(void* base, int G, int P, int rows, int nrep, int D);
 AttnLaunch choose_split(int G, int max_entries, int s_max);
 
 // Launchers (return hipError_t of the launch).
+// Scores into the user buffer and/or ws->scores; with ws, also the per-group
+// selection (union lists, n_sel, optional mask_out).
 hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const int64_t* q4_s,
                         float* scores, const int64_t* sc4_s, const Workspace* ws, int select_mode,
                         const float* retention, int num_sinks, int window, int k_max,
@@ -223,10 +236,14 @@ hipError_t launch_union_from_mask(const uint8_t* mask, const int64_t* m_s, int L
                                   int nrep, int P, const Workspace& ws, hipStream_t st);
 hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bucket, int L, int B,
                                  int Hkv, int nrep, int P, const Workspace& ws, hipStream_t st);
+// sel (may be null): the kernel scores and selects the pages itself; only valid
+// when attn_selects_in_kernel() says so for the same arguments.
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                            const AttnLaunch& al, hipStream_t st);
+                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel = nullptr);
+bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                                 const AttnLaunch& al, hipStream_t st);
+                                 const AttnLaunch& al, hipStream_t st, const SelectArgs* sel);
 
 }  // namespace fq

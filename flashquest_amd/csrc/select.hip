@@ -5,7 +5,7 @@
 //   scoring   src/flashquest/eager/criticality.py:128-163
 //   selection src/flashquest/eager/selection.py:65-126
 //   compact   src/flashquest/eager/selection.py:129-164
-#include "fq_common.h"
+#include "select_common.h"
 
 namespace fq {
 namespace {
@@ -44,13 +44,6 @@ FQ_DEV void topk_into_qmask(SelectLds& s, const uint32_t* keys, int P, int k, ui
     }
 }
 
-FQ_DEV int k_for(float r, int P, int k_max) {
-    // selection.py:103: ceil(fp32(r) * fp32(P)) clamped to [0, P]
-    float kf = ceilf(__fmul_rn(r, (float)P));
-    int k = kf <= 0.f ? 0 : (kf >= (float)P ? P : (int)kf);
-    if (k_max >= 0 && k > k_max) k = k_max;
-    return k;
-}
 
 FQ_DEV void force_pages(SelectLds& s, int P, int num_sinks, int window, uint8_t bits) {
     const int ns = num_sinks < P ? num_sinks : P;
@@ -75,6 +68,7 @@ struct ScoreParams {
     int ppc, nchunks;
     float* ws_scores;                             // [G][nrep][P] (per-q) or [G][1][P] (summed), or null
     int mode;
+    int sum_rows;                                 // per_kv_head_sum: score the group's summed query (one row)
 };
 
 // Scores of one page for every query row (rows in LDS), computed by the NL lanes
@@ -142,44 +136,27 @@ FQ_DEV void load_q_rows(const ScoreParams& a, int l, int b, int h, float (*s_q)[
             s_qp[i / D][i % D] = v[u] > 0.f ? v[u] : 0.f;
         }
     }
+    if (a.sum_rows) {
+        // row 0 <- (q_0 + q_1) + ... and (relu q_0 + relu q_1) + ..., heads in order
+        __syncthreads();
+        float qs = 0.f, ps = 0.f;
+        if (threadIdx.x < D) {
+            qs = s_q[0][threadIdx.x];
+            ps = s_qp[0][threadIdx.x];
+            for (int r = 1; r < a.rows; ++r) {
+                qs = __fadd_rn(qs, s_q[r][threadIdx.x]);
+                ps = __fadd_rn(ps, s_qp[r][threadIdx.x]);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < D) {
+            s_q[0][threadIdx.x] = qs;
+            s_qp[0][threadIdx.x] = ps;
+        }
+    }
 }
 
 constexpr int kPasses = 4;                  // passes of PPP pages per scoring chunk
-
-// Same arithmetic as score_page with the lane's q values of NR rows in
-// registers (loaded once per workgroup instead of once per page).
-template <int NR, typename MT, typename Emit>
-FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[NR][8], const float (&qp)[NR][8],
-                            Emit emit) {
-    float sf[8], mf[8];
-    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        sf[2 * j] = half_to_f<MT>(sw[j]);
-        sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
-        mf[2 * j] = half_to_f<MT>(mw[j]);
-        mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
-    }
-    float t1[NR], t2[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        t1[r] = __fmul_rn(qr[r][0], mf[0]);
-        t2[r] = __fmul_rn(qp[r][0], sf[0]);
-#pragma unroll
-        for (int j = 1; j < 8; ++j) {
-            t1[r] = __fadd_rn(t1[r], __fmul_rn(qr[r][j], mf[j]));
-            t2[r] = __fadd_rn(t2[r], __fmul_rn(qp[r][j], sf[j]));
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        t1[r] = row_sum<16>(t1[r]);
-        t2[r] = row_sum<16>(t2[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
-}
 
 // NR > 0: D = 128 and exactly NR query rows, q held in registers; NR = 0: any rows.
 template <int D, typename MT, int NR>
@@ -241,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
                     acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
                 };
                 if constexpr (NR > 0) score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, emit);
-                else score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.rows, lane_in_page, emit);
+                else score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.sum_rows ? 1 : a.rows, lane_in_page, emit);
                 if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
                     ws_scores[p] = acc_kv;
             }
@@ -320,89 +297,18 @@ __global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectPara
 
 // ---------------------------------------------------------------------------
 // The same per-group selection with one wave per group and no workgroup
-// barriers: each lane holds C keys (page i = 64 j + lane), the k-th largest key
-// is found bit by bit with wave-wide counts, ties go to the lower page index by
-// ballot ranks, and the union list is compacted with ballots.  Used for P <= 64 C.
+// barriers (wave_select_group, select_common.h).  Used for P <= 64 C.
 // ---------------------------------------------------------------------------
-// Marks the k largest of keys (ties to the lower page index) into qm |= bit.
-template <int C>
-FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit, int lane) {
-    if (k <= 0) return;
-    uint32_t T = 0;
-    for (int bitpos = 31; bitpos >= 0; --bitpos) {
-        const uint32_t cand = T | (1u << bitpos);
-        int cnt = 0;                          // wave-wide count, in scalar registers
-#pragma unroll
-        for (int j = 0; j < C; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-        if (cnt >= k) T = cand;
-    }
-    // T is the k-th largest key; keys above it are in, ties fill the rest by index
-    int gt = 0;
-#pragma unroll
-    for (int j = 0; j < C; ++j) gt += __popcll(__ballot(key[j] > T));
-    int take_eq = k - gt;
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-        if (key[j] > T) qm[j] |= bit;
-        const uint64_t eq = __ballot(key[j] == T);
-        const int rank = (int)lanes_below(eq);
-        if (key[j] == T && rank < take_eq) qm[j] |= bit;
-        take_eq -= __popcll(eq);
-    }
-}
-
 template <int C>
 __global__ __launch_bounds__(kThreads) void select_groups_wave_kernel(GroupSelectParams a, int G) {
-    const int lane = lane_id();
     const int g = blockIdx.x * (kThreads / 64) + wave_id();
     if (g >= G) return;                      // whole wave
     const int h = g % a.Hkv, P = a.P;
-    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
-    uint32_t key[C];
-    uint8_t qm[C];
-#pragma unroll
-    for (int j = 0; j < C; ++j) qm[j] = 0;
-    auto load_row = [&](int r) {
-        float v[C];
-#pragma unroll
-        for (int j = 0; j < C; ++j) v[j] = sc[r * P + min(64 * j + lane, P - 1)];   // all loads in flight
-#pragma unroll
-        for (int j = 0; j < C; ++j) key[j] = 64 * j + lane < P ? sortable_key(v[j]) : 0u;  // 0: below every score
-    };
-    const uint8_t all_bits = (uint8_t)((1u << a.nrep) - 1u);
-    // retention of the group's query heads: lane r holds head r's value
-    const float ret_l = a.retention[h * a.nrep + min(lane, a.nrep - 1)];
-    if (a.mode == FQ_SELECT_PER_Q_HEAD) {
-        for (int r = 0; r < a.nrep; ++r) {
-            load_row(r);
-            const float rr = __shfl(ret_l, r, 64);
-            wave_topk<C>(key, qm, k_for(rr, P, a.k_max), (uint8_t)(1u << r), lane);
-        }
-    } else {
-        float rmax = 0.f;
-        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, __shfl(ret_l, r, 64));
-        load_row(0);
-        wave_topk<C>(key, qm, k_for(rmax, P, a.k_max), all_bits, lane);
-    }
-    // forced sink / window pages (selection.py:110-117)
-    const int ns = a.num_sinks < P ? a.num_sinks : P;
-    const int wnd = a.window < P ? a.window : P;
     int* entries = a.ws.entries + (int64_t)g * P;
-    int n = 0;
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-        const int i = 64 * j + lane;
-        if (i < P && (i < ns || (wnd > 0 && i >= P - wnd))) qm[j] |= all_bits;
-        const bool f = i < P && qm[j] != 0;
-        const uint64_t bal = __ballot(f);
-        if (f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
-        n += __popcll(bal);
-        if (a.mask_out && i < P) {
-            uint8_t* mo = a.mask_out + ((int64_t)g * a.nrep) * P;
-            for (int r = 0; r < a.nrep; ++r) mo[(int64_t)r * P + i] = (qm[j] >> r) & 1;
-        }
-    }
-    if (lane == 0) a.ws.n_sel[g] = n;
+    uint8_t* mo = a.mask_out ? a.mask_out + ((int64_t)g * a.nrep) * P : nullptr;
+    const int n = wave_select_group<C>(a.ws.scores + (int64_t)g * a.nrep * P, P, a.nrep, a.mode,
+                                       a.retention + h * a.nrep, a.k_max, a.num_sinks, a.window, entries, mo);
+    if (lane_id() == 0) a.ws.n_sel[g] = n;
 }
 
 // ---------------------------------------------------------------------------
@@ -529,6 +435,7 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     a.nchunks = (c.P + ppc - 1) / ppc;
     a.ws_scores = ws ? ws->scores : nullptr;
     a.mode = select_mode;
+    a.sum_rows = ws && select_mode == FQ_SELECT_PER_KV_HEAD_SUM && S_q == 1 && !scores;
     if (a.rows > kMaxRows || c.P > kMaxPages) return hipErrorInvalidValue;
     GroupSelectParams sp{};
     if (ws) {
@@ -539,7 +446,7 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     dim3 grid(a.nchunks, G);
 #define FQ_SCORE(D_, MT_, NR_) hipLaunchKernelGGL((score_kernel<D_, MT_, NR_>), grid, dim3(kThreads), 0, st, a)
 #define FQ_SCORE_NR(MT_)                                                   \
-    switch (a.rows) {                                                      \
+    switch (a.sum_rows ? 1 : a.rows) {                                     \
         case 1: FQ_SCORE(128, MT_, 1); break;                              \
         case 2: FQ_SCORE(128, MT_, 2); break;                              \
         case 3: FQ_SCORE(128, MT_, 3); break;                              \

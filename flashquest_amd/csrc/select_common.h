@@ -1,0 +1,142 @@
+// Wave-level page selection shared by the selection kernels and the fused
+// attention prologue.  Reference semantics: src/flashquest/eager/selection.py:65-126.
+#pragma once
+
+#include "fq_common.h"
+
+namespace fq {
+
+FQ_DEV int k_for(float r, int P, int k_max) {
+    // selection.py:103: ceil(fp32(r) * fp32(P)) clamped to [0, P]
+    float kf = ceilf(__fmul_rn(r, (float)P));
+    int k = kf <= 0.f ? 0 : (kf >= (float)P ? P : (int)kf);
+    if (k_max >= 0 && k > k_max) k = k_max;
+    return k;
+}
+
+// Marks the k largest of keys (lane holds key[j] of page 64 j + lane; ties to the
+// lower page index) into qm |= bit.  The k-th largest key is found bit by bit
+// with wave-wide counts (ballots, scalar popcounts); ties are ranked by ballots.
+template <int C>
+FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit) {
+    if (k <= 0) return;
+    uint32_t T = 0;
+    for (int bitpos = 31; bitpos >= 0; --bitpos) {
+        const uint32_t cand = T | (1u << bitpos);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < C; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+        if (cnt >= k) T = cand;
+    }
+    // T is the k-th largest key; keys above it are in, ties fill the rest by index
+    int gt = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) gt += __popcll(__ballot(key[j] > T));
+    int take_eq = k - gt;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        if (key[j] > T) qm[j] |= bit;
+        const uint64_t eq = __ballot(key[j] == T);
+        const int rank = (int)lanes_below(eq);
+        if (key[j] == T && rank < take_eq) qm[j] |= bit;
+        take_eq -= __popcll(eq);
+    }
+}
+
+// One KV group's selection by one wave (P <= 64 C): scores of row r at
+// sc[r * P + p] (nrep rows per query head, or one summed row), top-k per
+// query head or once per KV head with the group's largest retention, forced
+// sink / window pages (selection.py:110-117), then the ascending union list
+// entries[i] = page | selecting-heads << 16 (LDS or global) and, if mask_out,
+// the per-head boolean rows mask_out[r * P + p].  Returns the list length.
+template <int C>
+FQ_DEV int wave_select_group(const float* sc, int P, int nrep, int mode, const float* retention, int k_max,
+                             int num_sinks, int window, int* entries, uint8_t* mask_out) {
+    const int lane = lane_id();
+    uint32_t key[C];
+    uint8_t qm[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) qm[j] = 0;
+    // Every row's loads are issued one row ahead, and the first row's together
+    // with the retention load, so the wave waits for memory once per row at most.
+    float v[2][C];
+    auto fetch = [&](int buf, int r) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) v[buf][j] = sc[r * P + min(64 * j + lane, P - 1)];
+    };
+    auto make_keys = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) key[j] = 64 * j + lane < P ? sortable_key(v[buf][j]) : 0u;  // 0: below every score
+    };
+    const float ret_l = retention[min(lane, nrep - 1)];      // lane r: head r's retention
+    fetch(0, 0);
+    const uint8_t all_bits = (uint8_t)((1u << nrep) - 1u);
+    if (mode == FQ_SELECT_PER_Q_HEAD) {
+        for (int r = 0; r < nrep; ++r) {
+            if (r + 1 < nrep) fetch((r + 1) & 1, r + 1);
+            make_keys(r & 1);
+            wave_topk<C>(key, qm, k_for(__shfl(ret_l, r, 64), P, k_max), (uint8_t)(1u << r));
+        }
+    } else {
+        float rmax = 0.f;
+        for (int r = 0; r < nrep; ++r) rmax = fmaxf(rmax, __shfl(ret_l, r, 64));
+        make_keys(0);
+        wave_topk<C>(key, qm, k_for(rmax, P, k_max), all_bits);
+    }
+    const int ns = num_sinks < P ? num_sinks : P;
+    const int wnd = window < P ? window : P;
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const int i = 64 * j + lane;
+        if (i < P && (i < ns || (wnd > 0 && i >= P - wnd))) qm[j] |= all_bits;
+        const bool f = i < P && qm[j] != 0;
+        const uint64_t bal = __ballot(f);
+        if (f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
+        n += __popcll(bal);
+        if (mask_out && i < P)
+            for (int r = 0; r < nrep; ++r) mask_out[(int64_t)r * P + i] = (qm[j] >> r) & 1;
+    }
+    return n;
+}
+
+// Quest page score (criticality.py:128-163) of one page for NR query rows, by
+// the 16 lanes of a DPP row, each owning 8 channels (q values in registers).
+// The fp32 order is fixed (and restated by the CPU oracle): a lane sums its 8
+// products left to right (products rounded, no FMA), lanes combine by the DPP
+// butterfly in row_sum<16>, score = t1 + t2 * 15.  emit(r, score) runs on all
+// 16 lanes with the same value.
+template <int NR, typename MT, typename Emit>
+FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[NR][8], const float (&qp)[NR][8],
+                            Emit emit) {
+    float sf[8], mf[8];
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sf[2 * j] = half_to_f<MT>(sw[j]);
+        sf[2 * j + 1] = half_to_f<MT>(sw[j] >> 16);
+        mf[2 * j] = half_to_f<MT>(mw[j]);
+        mf[2 * j + 1] = half_to_f<MT>(mw[j] >> 16);
+    }
+    float t1[NR], t2[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        t1[r] = __fmul_rn(qr[r][0], mf[0]);
+        t2[r] = __fmul_rn(qp[r][0], sf[0]);
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            t1[r] = __fadd_rn(t1[r], __fmul_rn(qr[r][j], mf[j]));
+            t2[r] = __fadd_rn(t2[r], __fmul_rn(qp[r][j], sf[j]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        t1[r] = row_sum<16>(t1[r]);
+        t2[r] = row_sum<16>(t2[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
+}
+
+}  // namespace fq

@@ -119,8 +119,10 @@ def quest_decode_int4(
 class QuestDecoder:
     """A reusable fused decode over fixed cache tensors (the bench's timed unit).
 
-    Builds the C descriptors once; ``select()`` and ``attend()`` launch the two
-    kernels of fq_quest_decode_int4 separately, ``__call__`` launches both.
+    Builds the C descriptors once; ``select()`` (scoring, and the selection
+    kernel where the attention kernel does not select for itself) and
+    ``attend()`` are the two halves of fq_quest_decode_int4, ``__call__`` runs
+    both.
     Every launch goes to torch's current stream, so the calls can be captured
     in a HIP graph after one eager call has sized the workspace.
     """
@@ -151,8 +153,8 @@ class QuestDecoder:
                                              self.ws.numel(), L.stream_handle(self.device)), "quest select")
 
     def attend(self):
-        L.check(L.lib().fq_quest_attend_int4(self.cache, self.query, self.sinks, self.window, self.k_max,
-                                             self.mode, self.ws.data_ptr(), self.ws.numel(),
+        L.check(L.lib().fq_quest_attend_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
+                                             self.k_max, self.mode, self.ws.data_ptr(), self.ws.numel(),
                                              L.stream_handle(self.device)), "quest attend")
 
     def __call__(self):

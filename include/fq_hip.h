@@ -168,16 +168,20 @@ int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
 /* The two halves of fq_quest_decode_int4, for callers that time or overlap
- * them separately.  fq_quest_select_int4 leaves the per-KV-group page lists in
- * the workspace; fq_quest_attend_int4 consumes them (same cache, query,
- * k_max / num_sinks / window_pages / select_mode and workspace). */
+ * them separately; call both with the same cache, query, retention, k_max,
+ * num_sinks, window_pages, select_mode and workspace.  fq_quest_select_int4
+ * leaves the page scores (and, where the attention kernel cannot select for
+ * itself, the per-KV-group page lists) in the workspace; fq_quest_attend_int4
+ * selects from the scores inside the attention kernel when it takes a whole KV
+ * group per workgroup, and otherwise consumes the lists. */
 int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query,
                          const float* retention, int32_t num_sinks, int32_t window_pages,
                          int32_t k_max, int32_t select_mode,
                          float* scores_out, uint8_t* mask_out,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query,
-                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         const float* retention, int32_t num_sinks, int32_t window_pages,
+                         int32_t k_max, int32_t select_mode,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
 /* _merge_two_attentions (src/flashquest/eager/llama_persistent_patch.py:50-61).

@@ -279,28 +279,34 @@ def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head"):
     Per (query head r, page p): t1 = sum_d q_d*mn_d, t2 = sum_d relu(q_d)*scale_d
     (products rounded, no FMA, order of ``_lane_sum_butterfly``);
     score = t1 + t2*15 (term2 is scaled before the add, criticality.py:161-162).
-    mode "per_q_head": (B, H_q, P).  mode "per_kv_head_sum": (B, H_kv, P) =
-    ((s_0 + s_1) + s_2) + ... over the group's query heads.
+    mode "per_q_head": (B, H_q, P).
+    mode "per_kv_head_sum": (B, H_kv, P), the score of the group's summed query:
+    the same formula with q = (q_0 + q_1) + ... and relu(q) = (relu(q_0) +
+    relu(q_1)) + ... (fp32, heads in order).  In exact arithmetic it equals the
+    sum of the group's per-head scores (both terms are linear in q, relu(q)).
     """
     Q = np.asarray(Q, F32)
     B, Hq, D = Q.shape
     Hkv, P = K_scale.shape[1], K_scale.shape[2]
     rep = Hq // Hkv
     qg = Q.reshape(B, Hkv, rep, 1, D)
+    qpos = np.where(qg > 0, qg, F32(0))
+    if mode == "per_kv_head_sum":
+        qs, ps = qg[:, :, 0].copy(), qpos[:, :, 0].copy()
+        for r in range(1, rep):
+            qs = (qs + qg[:, :, r]).astype(F32)
+            ps = (ps + qpos[:, :, r]).astype(F32)
+        qg, qpos = qs[:, :, None], ps[:, :, None]               # one summed row per group
+    elif mode != "per_q_head":
+        raise ValueError(mode)
     mn = np.asarray(K_mn, F32)[:, :, None, :, :]
     sc = np.asarray(K_scale, F32)[:, :, None, :, :]
     t1 = _lane_sum_butterfly((qg * mn).astype(F32))
-    qpos = np.where(qg > 0, qg, F32(0))
     t2 = _lane_sum_butterfly((qpos * sc).astype(F32))
-    s = (t1 + (t2 * F32(15.0)).astype(F32)).astype(F32)      # (B, Hkv, rep, P)
+    s = (t1 + (t2 * F32(15.0)).astype(F32)).astype(F32)      # (B, Hkv, rows, P)
     if mode == "per_q_head":
         return s.reshape(B, Hq, P)
-    if mode == "per_kv_head_sum":
-        acc = s[:, :, 0, :].copy()
-        for r in range(1, rep):
-            acc = (acc + s[:, :, r, :]).astype(F32)
-        return acc
-    raise ValueError(mode)
+    return s[:, :, 0, :]
 
 
 # ----------------------------------------------------------------------------

@@ -107,3 +107,29 @@ def test_split_override_is_restored_and_validated():
     from flashquest_amd.kernel import flash_attn_sparse_int4_fwd
     o, _ = flash_attn_sparse_int4_fwd(case.q_dev(), **case.device(), selection_mask=to_dev(mask)[:, :, None, :])
     assert max_err(o[:, :, 0], ref_o) <= _tol(case, ref_o)
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+@pytest.mark.parametrize("want_mask", [False, True])
+def test_fused_decode_selecting_inside_attention(mode, want_mask):
+    # >= 192 KV groups: one workgroup per group, which selects its own pages from the
+    # scores (no selection kernel unless the mask is requested); a partial last page
+    from flashquest_amd.eager import quest_decode_int4
+    L_, Hq, Hkv, P = 24, 24, 8, 24
+    cases = [Int4Case(seed=300 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * (P - 1) + 40, D=128, page=64, dtype="f16",
+                      meta="f16", vgroup=32) for i in range(L_)]
+    r = np.linspace(0.05, 0.6, Hq).astype(np.float32)
+    dev = [c.device() for c in cases]
+    stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+    q = torch.stack([c.q_dev() for c in cases])
+    out = quest_decode_int4(q, **stacked, retention=torch.from_numpy(r), num_sinks=3, window_pages=2,
+                            k_max_static=12, select_mode=mode, return_selection=want_mask)
+    torch.cuda.synchronize()
+    o, lse = out[0], out[1]
+    for i, c in enumerate(cases):
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=r, num_sinks=3, window_pages=2,
+                            mode=mode, k_max_static=12)
+        if want_mask:
+            assert np.array_equal(out[2][i].cpu().numpy(), ref["mask"]), i
+        assert max_err(o[i][:, :, 0], ref["O"]) <= _tol(c, ref["O"]), i
+        assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
