@@ -244,7 +244,6 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     constexpr int kEntPer = kMaxWgPages / NT;
     static_assert(kMaxWgPages % NT == 0 && NREP * D <= 2 * NT, "prologue sizes");
     __shared__ float s_q[NREP][D];
-    __shared__ int s_nsel;
     const int tid = threadIdx.x;
     const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
     const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
@@ -261,6 +260,8 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             v1 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u1) : f16_bits_to_f(u1);
         }
     }
+    // retention of query head L of the group (lanes past NREP repeat the last)
+    const float ret_l = a.sel.enabled == kScoreSelect ? a.sel.retention[h * NREP + min(L, NREP - 1)] : 0.f;
     auto score_group = [&](const float (*qraw)[D], float* sc, int t, int l_, int b_, int h_) {
         if constexpr (NW == 8) {   // in-kernel selection runs only in the 8-wave kernel
             if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_impl<MT, NREP, NT, true>(c, qraw, sc, t, l_, b_, h_);
@@ -284,14 +285,13 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         __syncthreads();
         score_group(s_qraw, s_sc, tid, l, b, h);
         __syncthreads();
-        if (w == 0) {
-            const int n = wave_select_group<kSelC>(s_sc, c.P, NREP, a.sel.mode, a.sel.retention + h * NREP,
-                                                   a.sel.k_max, a.sel.num_sinks, a.sel.window, s_ent, nullptr);
-            if (L == 0) s_nsel = n;
-        }
-        __syncthreads();
+        __shared__ BlockSelectLds s_bsel;
         e0 = 0;
-        e1 = s_nsel;
+        if constexpr (NW == 8)
+            e1 = block_select_group<kSelC, NW, NREP>(s_sc, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
+                                                     a.sel.window, s_ent, s_bsel);
+        else
+            e1 = 0;
     } else {
         const int n_sel = a.ws.n_sel[g];
         e0 = (int)((int64_t)n_sel * split / a.splits);           // balanced split: entries [e0, e1)
@@ -364,7 +364,22 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 #pragma unroll
     for (int gv = 0; gv < G; ++gv) bias[gv] = 0.f;
 
+    // With 8 waves two share a SIMD (waves w and w ^ 4) and the issue arbiter
+    // favours the older one, which would leave the younger wave's pages to
+    // run alone at the end.  Each wave publishes its remaining page count and
+    // takes the higher priority while it has more left than its partner.  The
+    // priority changes only timing, never which wave computes which page.
+    __shared__ int s_left[NW];
+    auto balance = [&](int k) {
+        if constexpr (NW == 8) {
+            s_left[w] = n_mine - k;
+            const int other = __builtin_amdgcn_readfirstlane(s_left[w ^ 4]);
+            if (n_mine - k > other) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
+    };
     auto compute = [&](const PageBuf& cb, int k) {
+        balance(k);
         const int ent = entry_of(k);
         const int p = ent & 0xFFFF, qm = ent >> 16;
         const int tok0 = p * 64;
@@ -566,6 +581,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         // zeros past its end) and discards it, but every path into the loop
         // then has the same loads in flight
         PageBuf b0, b1;
+        if constexpr (NW == 8) s_left[w] = n_mine;
         issue(b0, 0);
         for (int k = 0; k < n_mine; k += 2) {
             issue(b1, min(k + 1, n_mine - 1));
@@ -573,6 +589,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             issue(b0, min(k + 2, n_mine - 1));
             if (k + 1 < n_mine) compute(b1, k + 1);
         }
+        __builtin_amdgcn_s_setprio(0);
     }
 
     // ------------------------------------------------ wave state -> LDS

@@ -139,4 +139,114 @@ FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[
     for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
 }
 
+// Workgroup-wide selection for one KV group, same result as wave_select_group
+// (P <= 64 C pages, NW waves).  Every wave holds every key (C per lane per
+// row) and the k-th largest key of each row is found 4 bits per round: wave w
+// counts the keys >= T | v << s for candidates v = 2w+1, 2w+2 of each row, the
+// 15 counts meet in LDS (double-buffered by round parity, so one barrier per
+// round), and every wave takes the largest v whose count reaches k.  Ties, the
+// forced pages and the ascending entry list follow wave_topk / wave_select_group;
+// wave w writes the entries of pages 64 j + lane with j = w (mod NW).
+// NROWS = 1: one top-k of the summed row with the group's largest retention
+// (per_kv_head_sum); NROWS = nrep: one per query head.  ret_l: lane r holds
+// query head r's retention.  All control flow is wave-uniform.  Ends with a
+// barrier; returns the list length in every thread.
+struct BlockSelectLds {
+    int cnt[2][4][16];      // [round parity][row][candidate]
+};
+
+template <int C, int NW, int NROWS, int NREP>
+FQ_DEV int block_select_rows(const float* sc, int P, float ret_l, int k_max, int num_sinks, int window,
+                             int* entries, BlockSelectLds& sl) {
+    static_assert(2 * NW >= 15 && NROWS <= 4, "15 candidates per round over NW waves; at most 4 rows");
+    const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+    constexpr uint8_t kAll = (uint8_t)((1u << NREP) - 1u);
+    uint32_t key[NROWS][C];
+    int k[NROWS];
+    uint32_t T[NROWS];
+    float rmax = 0.f;
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) rmax = fmaxf(rmax, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)));
+#pragma unroll
+    for (int r = 0; r < NROWS; ++r) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int i = 64 * j + lane;
+            const float v = sc[r * P + min(i, P - 1)];
+            key[r][j] = i < P ? sortable_key(v) : 0u;             // 0: below every score
+        }
+        k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
+        T[r] = 0u;
+    }
+    const int v0 = 2 * w + 1;                 // w = 7: v = 16 is counted but never written
+#pragma unroll 1
+    for (int rd = 0; rd < 8; ++rd) {
+        const int s = 28 - 4 * rd;
+        int* cnt = &sl.cnt[rd & 1][0][0];
+#pragma unroll
+        for (int r = 0; r < NROWS; ++r) {
+            int n[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t cand = T[r] | ((uint32_t)(v0 + u) << s);
+                n[u] = 0;
+#pragma unroll
+                for (int j = 0; j < C; ++j) n[u] += __popcll(__ballot(key[r][j] >= cand));
+            }
+            // every lane stores the same value: no branch on the lane
+            cnt[r * 16 + v0] = n[0];
+            if (v0 + 1 <= 15) cnt[r * 16 + v0 + 1] = n[1];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < NROWS; ++r) {
+            const int n = cnt[r * 16 + (lane & 15)];
+            const uint64_t ok = __ballot(lane == 0 || (lane < 16 && n >= k[r]));
+            T[r] |= (uint32_t)(63 - __clzll((long long)ok)) << s;
+        }
+    }
+    // ties at T: the lowest page indices (wave_topk's rule); identical in every wave
+    uint8_t qm[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) qm[j] = 0;
+#pragma unroll
+    for (int r = 0; r < NROWS; ++r) {
+        if (k[r] <= 0) continue;
+        const uint8_t bit = NROWS == 1 ? kAll : (uint8_t)(1u << r);
+        int gt = 0;
+#pragma unroll
+        for (int j = 0; j < C; ++j) gt += __popcll(__ballot(key[r][j] > T[r]));
+        int take_eq = k[r] - gt;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const uint64_t eq = __ballot(key[r][j] == T[r]);
+            const bool in = key[r][j] > T[r] || (key[r][j] == T[r] && (int)lanes_below(eq) < take_eq);
+            qm[j] |= in ? bit : (uint8_t)0;
+            take_eq -= __popcll(eq);
+        }
+    }
+    const int ns = num_sinks < P ? num_sinks : P;
+    const int wnd = window < P ? window : P;
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const int i = 64 * j + lane;
+        if (i < P && (i < ns || (wnd > 0 && i >= P - wnd))) qm[j] |= kAll;
+        const bool f = i < P && qm[j] != 0;
+        const uint64_t bal = __ballot(f);
+        if (j % NW == w && f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
+        n += __popcll(bal);
+    }
+    __syncthreads();
+    return n;
+}
+
+template <int C, int NW, int NREP>
+FQ_DEV int block_select_group(const float* sc, int P, int mode, float ret_l, int k_max, int num_sinks, int window,
+                              int* entries, BlockSelectLds& sl) {
+    if (mode == FQ_SELECT_PER_Q_HEAD)
+        return block_select_rows<C, NW, NREP, NREP>(sc, P, ret_l, k_max, num_sinks, window, entries, sl);
+    return block_select_rows<C, NW, 1, NREP>(sc, P, ret_l, k_max, num_sinks, window, entries, sl);
+}
+
 }  // namespace fq
