@@ -29,6 +29,7 @@ sys.path.insert(0, ROOT)
 from flashquest_amd._lib import KernelTimer  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import quantize_k_int4, quantize_v_int4  # noqa: E402
+from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402
 
 METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
@@ -47,14 +48,28 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip control / per-layer / per-q-head lines")
     ap.add_argument("--cpu-layers", type=int, default=10, help="layers in the CPU baseline sample")
+    ap.add_argument("--no-batch16", dest="batch16", action="store_false",
+                    help="skip the batch-16 line (BASELINE config 4) among the extras")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
     return ap.parse_args()
 
 
 # --------------------------------------------------------------------- data --
-def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda"):
-    """Seeded synthetic INT4 cache, one (sequence, layer) at a time (seed 1000*b + l)."""
+ROT_SEED = 4242
+
+
+def rotation_signs(D=128, dev="cuda"):
+    """The seeded +-1 vector of the randomised WHT."""
+    g = torch.Generator()
+    g.manual_seed(ROT_SEED)
+    return (torch.randint(0, 2, (D,), generator=g) * 2 - 1).float().to(dev)
+
+
+def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda", signs=None):
+    """Seeded synthetic INT4 cache, one (sequence, layer) at a time (seed 1000*b + l).
+    With ``signs`` (config 3) K and V are rotated by WHT(signs * x) before
+    quantisation; Q stays in the raw basis (the step rotates it)."""
     S = P * page
     kp = torch.empty(L, B, Hkv, S, D // 2, dtype=torch.uint8, device=dev)
     vp = torch.empty_like(kp)
@@ -80,6 +95,9 @@ def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda")
                 for p in pages.tolist():
                     noise = torch.randn(page, D, generator=g, device=dev)
                     K[0, h, p * page:(p + 1) * page] = rms[h] * (0.8 * math.sqrt(D) * qhat[h] + 0.6 * noise)
+            if signs is not None:
+                K = wht_along_head_dim(K, signs=signs)
+                V = wht_along_head_dim(V, signs=signs)
             quantize_k_int4(K.half(), page, out=(kp[l, b:b + 1], ks[l, b:b + 1], km[l, b:b + 1]))
             quantize_v_int4(V.half(), v_group=32, out=(vp[l, b:b + 1], vs[l, b:b + 1], vm[l, b:b + 1]))
             Q[l, b, :, 0] = q.half()
@@ -161,16 +179,17 @@ def time_steps(fn_pre, fn_timed, steps, warmup, flush, kernel_timer=False):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int4_mfma_config1_traffic.json")
 
 
-def measured_traffic(L, B, P, retention, select):
-    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a copy of known size), when it was
-    measured on this exact workload; otherwise None."""
+def measured_traffic(L, B, P, retention, select, fused):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known size),
+    when it was measured on this exact workload and kernel; otherwise None."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("workload") != {"layers": L, "batch": B, "pages": P, "retention": retention, "select": select}:
+    if t.get("workload") != {"layers": L, "batch": B, "pages": P, "retention": retention, "select": select,
+                              "fused": fused}:
         return None
     return t.get("hbm_bytes_per_launch")
 
@@ -285,11 +304,59 @@ def main():
         extra["step_us_after_write_flush"] = wf_ms * 1e3
         del wflush
 
-    traffic = measured_traffic(L, B, P, args.retention, args.select)
-    roof = {"bound": "hbm", "achieved": attn_kernel_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": attn_kernel_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
-            "kernel": "attn_int4_mfma_kernel (split-K sparse GQA attention, all layers in one launch)",
-            "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": attn_kernel_b}
+        # rotated INT4 (K, V rotated by WHT(signs * x) before
+        # quantisation).  The step rotates Q, decodes, and rotates O back.
+        signs = rotation_signs(dev=dev)
+        rc = make_cache(L, B, P=P, dev=dev, signs=signs)
+        q_raw = rc["Q"].clone()
+        rmask = torch.zeros(L, B, Hq, P, dtype=torch.bool, device=dev)
+        wht_along_head_dim(q_raw, signs=signs, out=rc["Q"])
+        rdec = decoder(args.retention, k, args.select, c=rc, mask=rmask)
+        rdec()
+        torch.cuda.synchronize()
+        rs_b, ra_b, _, _ = step_bytes(rc, rmask)
+        rdec.mask_out = None
+        o_raw = torch.empty_like(rdec.O3)
+
+        def rot_step():
+            wht_along_head_dim(q_raw, signs=signs, out=rc["Q"])                  # Q_rot = WHT(s * Q)
+            rdec()
+            wht_along_head_dim(rdec.O3, signs=signs, inverse=True, out=o_raw)    # O = s * WHT(O_rot)
+
+        r_ms, _, _ = time_steps(noop, rot_step, args.steps, args.warmup, flush)
+        extra.update({"config3_rotated_us": r_ms * 1e3, "config3_step_GBps": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9,
+                      "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        del rc, rdec, q_raw, o_raw, rmask
+
+        # batch 16 independent sequences, 28 layers, 32k each
+        if B == 1 and args.batch16:
+            bc = make_cache(L, 16, P=P, dev=dev)
+            bmask = torch.zeros(L, 16, Hq, P, dtype=torch.bool, device=dev)
+            bdec = decoder(args.retention, k, args.select, c=bc, mask=bmask)
+            bdec()
+            torch.cuda.synchronize()
+            bs_b, ba_b, _, _ = step_bytes(bc, bmask)
+            bdec.mask_out = None
+            b_ms, _, _ = time_steps(noop, bdec, args.steps, args.warmup, flush)
+            extra.update({"config4_batch16_us": b_ms * 1e3, "config4_step_bytes": bs_b + ba_b,
+                          "config4_step_GBps": (bs_b + ba_b) / (b_ms * 1e-3) / 1e9,
+                          "config4_roofline_frac": (bs_b + ba_b) / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "config4_fused": bdec.fused})
+            del bc, bdec, bmask
+
+    # The dominant kernel: with one workgroup per KV group the attention kernel
+    # scores and selects its own pages, so one launch is the whole step and its
+    # algorithmic bytes are the step's (every page's K scale/min once, the
+    # selected pages' codes and V scale/min, Q, O, lse).  Otherwise the
+    # attention kernel alone, which also reads the selected pages' K scale/min.
+    fused = dec.fused
+    kernel_b = scoring_b + attn_b if fused else attn_kernel_b
+    kname = ("attn_int4_mfma_kernel, fused: score + select + sparse attention for all layers in one launch"
+             if fused else "attn_int4_mfma_kernel (sparse GQA attention, all layers in one launch)")
+    traffic = measured_traffic(L, B, P, args.retention, args.select, fused)
+    roof = {"bound": "hbm", "achieved": kernel_b / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": kernel_b / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
+            "kernel": kname, "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": kernel_b}
     cpu = None
     if not args.no_cpu_baseline and B == 1:
         cpu = cpu_baseline(cache, args, min(args.cpu_layers, L))

@@ -160,18 +160,36 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
 }
 
 // Page scores of one KV group (P <= 64 * kSelC pages) by a whole workgroup of
-// NT threads: 16 lanes per page, NT / 16 pages per pass, all passes' metadata
-// loaded before the first is scored.  Writes s_sc[r * P + p] per
-// query head, or (SUM, per_kv_head_sum) s_sc[p] for the group's summed query --
-// score_kernel's arithmetic and order exactly.
-template <typename MT, int NREP, int NT, bool SUM>
-FQ_DEV void score_group_impl(const Int4Cache& c, const float (*s_qraw)[128], float* s_sc, int tid, int l, int b,
-                             int h) {
+// NT threads: 16 lanes per page, NT / 16 pages per pass.  score_group_load
+// issues every pass's metadata loads (pages past P re-read page P-1, so there
+// is no branch between loads and use); score_group_regs scores them --
+// score_kernel's arithmetic and order exactly -- and stores the sortable keys
+// s_key[r * 64 kSelC + p] per query head, or (SUM, per_kv_head_sum) s_key[p]
+// for the group's summed query, with 0 (below every score) for p >= P.
+template <int NT>
+struct ScoreRegs {
+    static constexpr int kPass = 64 * kSelC / (NT / 16);
+    uint4 sv[kPass], mv[kPass];
+};
+
+template <typename MT, int NT>
+FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int l, int b, int h) {
     constexpr int PPP = NT / 16;
     const int lip = tid & 15, pip = tid >> 4;
     const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2] + lip * 8;
     const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2] + lip * 8;
-    const int P = c.P;
+#pragma unroll
+    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
+        const int p = min(u * PPP + pip, c.P - 1);
+        sr.sv[u] = *(const uint4*)(ksc + p * 128);
+        sr.mv[u] = *(const uint4*)(kmn + p * 128);
+    }
+}
+
+template <typename MT, int NREP, int NT, bool SUM>
+FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P) {
+    constexpr int PPP = NT / 16;
+    const int lip = tid & 15, pip = tid >> 4;
     // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
     // relu applied per head before the sum; per_q_head scores every head
     constexpr int NR = SUM ? 1 : NREP;
@@ -197,30 +215,22 @@ FQ_DEV void score_group_impl(const Int4Cache& c, const float (*s_qraw)[128], flo
             }
         }
     }
-    // P <= 64 * kSelC, so one pass per PPP pages covers the group: every load
-    // is issued before the first score (pages past P re-read page P-1 and
-    // are scored but not stored), with no branch between loads and use.
-    constexpr int NPASS = 64 * kSelC / PPP;
-    uint4 sv[NPASS], mv[NPASS];
 #pragma unroll
-    for (int u = 0; u < NPASS; ++u) {
-        const int p = min(u * PPP + pip, P - 1);
-        sv[u] = *(const uint4*)(ksc + p * 128);
-        mv[u] = *(const uint4*)(kmn + p * 128);
-    }
-#pragma unroll
-    for (int u = 0; u < NPASS; ++u) {
+    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
         const int p = u * PPP + pip;
-        score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, [&](int r, float sc) {
-            if (lip == 0 && p < P) s_sc[r * P + p] = sc;
+        score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
+            if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
         });
     }
 }
 
 // NW waves per workgroup (4, or 8 when one workgroup takes a whole KV group).
-template <typename MT, int G, int NREP, int NW>
+// FUSED (8 waves only): the workgroup scores and selects its group's pages
+// itself (a.sel); otherwise the pages come from the workspace lists.
+template <typename MT, int G, int NREP, int NW, bool FUSED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int4_mfma_kernel(MfmaParams a) {
+    static_assert(!FUSED || NW == 8, "in-kernel selection runs in the 8-wave kernel");
     constexpr int D = 128;
     constexpr int NT = 64 * NW;
     __shared__ SplitLds<D, NREP, NW> s_split;
@@ -247,51 +257,105 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     const int tid = threadIdx.x;
     const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
     const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
-    float v0, v1;
+    // q (raw bits) and the retention go out first, then, in the fused decode,
+    // the group's K metadata loads for scoring: loads complete in order, so q
+    // can be used while the metadata is still in flight.
+    // Branch-free, so the compiler can count the loads still in flight: two
+    // 16-bit loads per element, both always used (the high one re-reads the
+    // low one for 16-bit q types and is masked off).
+    const bool q32 = q.q_dtype == FQ_F32;
+    const int esz = q32 ? 4 : 2;
+    uint32_t hi_mask = (0u - (uint32_t)q32) & 0xFFFF0000u;
+    asm volatile("" : "+s"(hi_mask));       // opaque: both loads stay unconditional
+    uint32_t l0, h0, l1, h1;
     {
-        const int64_t o0 = qb + (i0 >> 7) * q.q_s[2] + (i0 & 127) * q.q_s[3];
-        const int64_t o1 = qb + (i1 >> 7) * q.q_s[2] + (i1 & 127) * q.q_s[3];
-        if (q.q_dtype == FQ_F32) {
-            v0 = ((const float*)q.q)[o0];
-            v1 = ((const float*)q.q)[o1];
-        } else {
-            const uint32_t u0 = ((const uint16_t*)q.q)[o0], u1 = ((const uint16_t*)q.q)[o1];
-            v0 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u0) : f16_bits_to_f(u0);
-            v1 = q.q_dtype == FQ_BF16 ? bf16_bits_to_f(u1) : f16_bits_to_f(u1);
-        }
+        const char* qc = (const char*)q.q;
+        const int64_t o0 = (qb + (i0 >> 7) * q.q_s[2] + (i0 & 127) * q.q_s[3]) * esz;
+        const int64_t o1 = (qb + (i1 >> 7) * q.q_s[2] + (i1 & 127) * q.q_s[3]) * esz;
+        l0 = *(const uint16_t*)(qc + o0);
+        h0 = *(const uint16_t*)(qc + o0 + esz - 2);
+        l1 = *(const uint16_t*)(qc + o1);
+        h1 = *(const uint16_t*)(qc + o1 + esz - 2);
     }
+    __builtin_amdgcn_sched_barrier(0);      // q's loads go out before the metadata loads
     // retention of query head L of the group (lanes past NREP repeat the last)
-    const float ret_l = a.sel.enabled == kScoreSelect ? a.sel.retention[h * NREP + min(L, NREP - 1)] : 0.f;
-    auto score_group = [&](const float (*qraw)[D], float* sc, int t, int l_, int b_, int h_) {
-        if constexpr (NW == 8) {   // in-kernel selection runs only in the 8-wave kernel
-            if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_impl<MT, NREP, NT, true>(c, qraw, sc, t, l_, b_, h_);
-            else score_group_impl<MT, NREP, NT, false>(c, qraw, sc, t, l_, b_, h_);
-        }
+    float ret_l = 0.f;
+    ScoreRegs<NT> sr;
+    if constexpr (FUSED) {
+        ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
+        score_group_load<MT, NT>(sr, c, tid, l, b, h);
+    }
+    const bool qbf = q.q_dtype == FQ_BF16;
+    auto q_float = [&](uint32_t u) {
+        const float fh = f16_bits_to_f(u), fb = bf16_bits_to_f(u);
+        return q32 ? __uint_as_float(u) : (qbf ? fb : fh);
     };
+    const float v0 = q_float((l0 & ~hi_mask) | ((h0 << 16) & hi_mask));
+    const float v1 = q_float((l1 & ~hi_mask) | ((h1 << 16) & hi_mask));
+
+    const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
+    const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
+    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
+    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
+    const uint16_t* vsc = (const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2];
+    const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2];
+
+    // A-operand slot of this lane for the q.k digits: k-step qs_s, k-group qs_kg,
+    // operand dword qs_jd; channels ch_base + 2b + par (b = 0..3); heads r0, r0+1.
+    const int Dq = L & 31, qs_s = Dq >> 4, qs_kg = (Dq >> 2) & 3, qs_jd = Dq & 3;
+    const int ch_base = 32 * qs_kg + 16 * qs_s + 8 * (qs_jd >> 1);
+    const int par = qs_jd & 1;
+    const int r0 = 2 * (L >> 5);
+
+    SliceRsrc rs;
+    rs.k = make_rsrc(kb, (int64_t)S * 64);
+    rs.v = make_rsrc(vb, (int64_t)S * 64);
+    rs.vs = make_rsrc(vsc, (int64_t)S * G * 2);
+    rs.vm = make_rsrc(vmn, (int64_t)S * G * 2);
+    rs.ks = make_rsrc(ksc, (int64_t)c.P * D * 2);
+    rs.km = make_rsrc(kmn, (int64_t)c.P * D * 2);
+    const int koff0 = n16 * 64 + 16 * lg, voff0 = lg * 64 + 4 * n16, moff0 = n16 * G * 2, soff0 = ch_base * 2;
+    auto issue_page = [&](PageBuf& bf, int p) {
+        // keep the scheduler from moving compute work in front of the loads
+        __builtin_amdgcn_sched_barrier(0);
+        load_page<G>(bf, rs, koff0 + p * 4096, voff0 + p * 4096, moff0 + p * 64 * G * 2, soff0 + p * D * 2);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Page buffers: one page in flight ahead of the one being computed.
+    PageBuf b0, b1;
+    bool first_issued = false;       // b0 already holds this wave's first page
+
     int e0, e1;
-    if (a.sel.enabled == kScoreSelect) {
+    if constexpr (FUSED) {
         // Fused decode: score every page of the group from its K metadata
         // (the arithmetic of score_kernel), keep the scores in LDS, select.
+        // The forced pages (always selected, first in the entry list) are
+        // loaded while the selection runs.
         __shared__ float s_qraw[NREP][D];
-        __shared__ float s_sc[NREP * 64 * kSelC];
-        if (tid < NREP * D) {
-            s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
-            s_qraw[i0 >> 7][i0 & 127] = v0;
-        }
-        if (tid + NT < NREP * D) {
-            s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
-            s_qraw[i1 >> 7][i1 & 127] = v1;
-        }
-        __syncthreads();
-        score_group(s_qraw, s_sc, tid, l, b, h);
-        __syncthreads();
+        __shared__ uint32_t s_key[NREP * 64 * kSelC];
         __shared__ BlockSelectLds s_bsel;
         e0 = 0;
-        if constexpr (NW == 8)
-            e1 = block_select_group<kSelC, NW, NREP>(s_sc, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
+        {
+            if (tid < NREP * D) {
+                s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+                s_qraw[i0 >> 7][i0 & 127] = v0;
+            }
+            if (tid + NT < NREP * D) {
+                s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+                s_qraw[i1 >> 7][i1 & 127] = v1;
+            }
+            __syncthreads();
+            if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+            else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
+            const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
+            if (S > 0 && w < fp.count) {
+                issue_page(b0, fp.page(w));
+                first_issued = true;
+            }
+            __syncthreads();
+            e1 = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
                                                      a.sel.window, s_ent, s_bsel);
-        else
-            e1 = 0;
+        }
     } else {
         const int n_sel = a.ws.n_sel[g];
         e0 = (int)((int64_t)n_sel * split / a.splits);           // balanced split: entries [e0, e1)
@@ -310,43 +374,16 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // accumulation order, and the result, do not depend on timing).
     const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;   // pages w, w + NW, ...
 
-    const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
-    const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
-    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
-    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
-    const uint16_t* vsc = (const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2];
-    const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2];
-
-    // A-operand slot of this lane for the q.k digits: k-step qs_s, k-group qs_kg,
-    // operand dword qs_jd; channels ch_base + 2b + par (b = 0..3); heads r0, r0+1.
-    const int Dq = L & 31, qs_s = Dq >> 4, qs_kg = (Dq >> 2) & 3, qs_jd = Dq & 3;
-    const int ch_base = 32 * qs_kg + 16 * qs_s + 8 * (qs_jd >> 1);
-    const int par = qs_jd & 1;
-    const int r0 = 2 * (L >> 5);
     float qv[2][4];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) qv[hh][bb] = r0 + hh < NREP ? s_q[min(r0 + hh, NREP - 1)][ch_base + 2 * bb + par] : 0.f;
 
-    SliceRsrc rs;
-    rs.k = make_rsrc(kb, (int64_t)S * 64);
-    rs.v = make_rsrc(vb, (int64_t)S * 64);
-    rs.vs = make_rsrc(vsc, (int64_t)S * G * 2);
-    rs.vm = make_rsrc(vmn, (int64_t)S * G * 2);
-    rs.ks = make_rsrc(ksc, (int64_t)c.P * D * 2);
-    rs.km = make_rsrc(kmn, (int64_t)c.P * D * 2);
-    const int koff0 = n16 * 64 + 16 * lg, voff0 = lg * 64 + 4 * n16, moff0 = n16 * G * 2, soff0 = ch_base * 2;
     // k: this wave's k-th page (entry w + NW * k); callers clamp k to the last
     // page, so every step issues the same loads and the waits match on every path
     auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
-    auto issue = [&](PageBuf& bf, int k) {
-        const int p = entry_of(k) & 0xFFFF;
-        // keep the scheduler from moving compute work in front of the loads
-        __builtin_amdgcn_sched_barrier(0);
-        load_page<G>(bf, rs, koff0 + p * 4096, voff0 + p * 4096, moff0 + p * 64 * G * 2, soff0 + p * D * 2);
-        __builtin_amdgcn_sched_barrier(0);
-    };
+    auto issue = [&](PageBuf& bf, int k) { issue_page(bf, entry_of(k) & 0xFFFF); };
 
     // running references (wave-uniform) and accumulators.  With fp16 metadata
     // p * V_scale <= 65504 needs no bound; bf16 metadata is divided by s_run.
@@ -580,9 +617,8 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         // issued unconditionally: an idle wave reads some page of the slice (or
         // zeros past its end) and discards it, but every path into the loop
         // then has the same loads in flight
-        PageBuf b0, b1;
         if constexpr (NW == 8) s_left[w] = n_mine;
-        issue(b0, 0);
+        if (!first_issued) issue(b0, 0);
         for (int k = 0; k < n_mine; k += 2) {
             issue(b1, min(k + 1, n_mine - 1));
             compute(b0, k);
@@ -620,13 +656,13 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits);
 }
 
-template <typename MT, int G, int NW>
+template <typename MT, int G, int NW, bool FUSED>
 hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                     \
     case N:                                                                                            \
         timer_before_launch(st);                                                                       \
-        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW>), grid, dim3(64 * NW), 0, st, a);      \
+        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
         timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                              \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
@@ -693,7 +729,10 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
         a.sel = *sel;
     }
     dim3 grid(a.splits, groups);
-#define FQ_W(MT_, G_) (sp.waves == 8 ? launch_mfma_nrep<MT_, G_, 8>(a, grid, st) : launch_mfma_nrep<MT_, G_, 4>(a, grid, st))
+#define FQ_W(MT_, G_)                                                                       \
+    (a.sel.enabled ? launch_mfma_nrep<MT_, G_, 8, true>(a, grid, st)                        \
+                   : sp.waves == 8 ? launch_mfma_nrep<MT_, G_, 8, false>(a, grid, st)       \
+                                   : launch_mfma_nrep<MT_, G_, 4, false>(a, grid, st))
     if (c.meta_dtype == FQ_BF16) return c.G == 4 ? FQ_W(bf16, 4) : FQ_W(bf16, 1);
     return c.G == 4 ? FQ_W(f16, 4) : FQ_W(f16, 1);
 #undef FQ_W

@@ -393,6 +393,24 @@ int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, cons
     return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel), "sparse int4 attention");
 }
 
+int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,
+                        int32_t k_max, int32_t select_mode) {
+    Int4Cache c{};
+    QueryArgs q{};
+    int st = check_cache(cache, &c);
+    if (st) return -st;
+    st = check_query(query, c.D, c.Hkv, &q);
+    if (st) return -st;
+    if (select_mode != FQ_SELECT_PER_Q_HEAD && select_mode != FQ_SELECT_PER_KV_HEAD_SUM)
+        return -fail(FQ_ERR_INVALID, "select_mode=%d", select_mode);
+    if (num_sinks < 0) num_sinks = 0;
+    if (window_pages < 0) window_pages = 0;
+    if (k_max > c.P) k_max = c.P;
+    const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max, select_mode),
+                                       s_max_for(c.P));
+    return attn_selects_in_kernel(c, q, al) ? 1 : 0;
+}
+
 int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
                          int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                          float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,

@@ -129,34 +129,50 @@ struct WhtParams {
     const float* signs; int inverse; int arith;
 };
 
+// One wave per row (D = 128: lane l holds elements l and l + 64) or 64 / D
+// rows per wave (D <= 64: one element per lane), so loads and stores are
+// coalesced.  The butterflies run in the reference's order, h = 1, 2, ..., D/2
+// (partners h < 64 apart by a lane shuffle, h = 64 within the lane), each
+// sum and difference rounded to the arithmetic dtype as before.
 template <int D>
 __global__ __launch_bounds__(kThreads) void wht_kernel(WhtParams a) {
-    const int n = blockIdx.x * kThreads + threadIdx.x;
-    if (n >= a.N) return;
-    float v[D];
+    constexpr int E = D > 64 ? 2 : 1;               // elements per lane
+    constexpr int RPW = D >= 64 ? 1 : 64 / D;        // rows per wave
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const int64_t row = wave * RPW + (D >= 64 ? 0 : lane / D);
+    const int e0 = D >= 64 ? lane : lane % D;
+    const bool live = row < a.N;
+    const int64_t r = live ? row : 0;
+    float v[E];
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        float x = load_any(a.x, a.x_dtype, (int64_t)n * a.x_rs + d);
+    for (int k = 0; k < E; ++k) {
+        const int d = e0 + 64 * k;
+        float x = load_any(a.x, a.x_dtype, r * a.x_rs + d);
         if (a.signs && !a.inverse) x *= a.signs[d];
-        v[d] = x;
+        v[k] = x;
     }
 #pragma unroll
-    for (int hh = 1; hh < D; hh <<= 1) {
+    for (int h = 1; h < (D < 64 ? D : 64); h <<= 1) {
 #pragma unroll
-        for (int i = 0; i < D; ++i) {
-            if ((i & hh) == 0) {
-                const float x = v[i], y = v[i + hh];
-                v[i] = round_to(x + y, a.arith);
-                v[i + hh] = round_to(x - y, a.arith);
-            }
+        for (int k = 0; k < E; ++k) {
+            const float y = __shfl_xor(v[k], h, 64);
+            v[k] = (e0 & h) ? round_to(y - v[k], a.arith) : round_to(v[k] + y, a.arith);
         }
     }
+    if constexpr (D == 128) {
+        const float x = v[0], y = v[1];
+        v[0] = round_to(x + y, a.arith);
+        v[1] = round_to(x - y, a.arith);
+    }
     const float inv = 1.0f / sqrtf((float)D);
+    if (!live) return;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        float y = round_to(v[d] * inv, a.arith);
+    for (int k = 0; k < E; ++k) {
+        const int d = e0 + 64 * k;
+        float y = round_to(v[k] * inv, a.arith);
         if (a.signs && a.inverse) y *= a.signs[d];
-        store_any(a.out, a.out_dtype, (int64_t)n * a.o_rs + d, y);
+        store_any(a.out, a.out_dtype, r * a.o_rs + d, y);
     }
 }
 
@@ -346,7 +362,9 @@ hipError_t launch_wht(const void* x, int x_dtype, int64_t x_rs, void* out, int o
                       int N, int D, const float* signs, int inverse, int arith, hipStream_t st) {
     WhtParams a{x, x_dtype, x_rs, out, out_dtype, o_rs, N, signs, inverse, arith};
     if (N == 0) return hipSuccess;
-    dim3 grid(blocks_for(N));
+    const int64_t rows_per_wave = D >= 64 ? 1 : 64 / D;
+    const int64_t waves = (N + rows_per_wave - 1) / rows_per_wave;
+    dim3 grid((unsigned)((waves * 64 + kThreads - 1) / kThreads));
     switch (D) {
         case 8: hipLaunchKernelGGL(wht_kernel<8>, grid, dim3(kThreads), 0, st, a); break;
         case 16: hipLaunchKernelGGL(wht_kernel<16>, grid, dim3(kThreads), 0, st, a); break;

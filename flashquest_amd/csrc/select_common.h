@@ -17,9 +17,10 @@ FQ_DEV int k_for(float r, int P, int k_max) {
 // Marks the k largest of keys (lane holds key[j] of page 64 j + lane; ties to the
 // lower page index) into qm |= bit.  The k-th largest key is found bit by bit
 // with wave-wide counts (ballots, scalar popcounts); ties are ranked by ballots.
+// The k-th largest of the wave's 64 C keys (k >= 1), found bit by bit: T keeps
+// the largest prefix that at least k keys reach.  Wave-uniform, no LDS.
 template <int C>
-FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit) {
-    if (k <= 0) return;
+FQ_DEV uint32_t wave_kth_largest(const uint32_t (&key)[C], int k) {
     uint32_t T = 0;
     for (int bitpos = 31; bitpos >= 0; --bitpos) {
         const uint32_t cand = T | (1u << bitpos);
@@ -28,6 +29,13 @@ FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t
         for (int j = 0; j < C; ++j) cnt += __popcll(__ballot(key[j] >= cand));
         if (cnt >= k) T = cand;
     }
+    return T;
+}
+
+template <int C>
+FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit) {
+    if (k <= 0) return;
+    const uint32_t T = wave_kth_largest<C>(key, k);
     // T is the k-th largest key; keys above it are in, ties fill the rest by index
     int gt = 0;
 #pragma unroll
@@ -139,72 +147,68 @@ FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[
     for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
 }
 
+// The forced pages of a P-page row (selection.py:110-117): sinks [0, ns) and
+// the window [start, P) with start = max(ns, P - window), in ascending order;
+// forced entry f is page f (f < ns) or start + f - ns.
+struct ForcedPages {
+    int ns, start, count;
+    FQ_DEV bool contains(int i) const { return i < ns || i >= start; }
+    FQ_DEV int index(int i) const { return i < ns ? i : ns + i - start; }
+    FQ_DEV int page(int f) const { return f < ns ? f : start + f - ns; }
+};
+FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
+    ForcedPages fp;
+    fp.ns = num_sinks < P ? (num_sinks > 0 ? num_sinks : 0) : P;
+    const int wnd = window < P ? (window > 0 ? window : 0) : P;
+    fp.start = P - wnd > fp.ns ? P - wnd : fp.ns;
+    fp.count = fp.ns + P - fp.start;
+    return fp;
+}
+
 // Workgroup-wide selection for one KV group, same result as wave_select_group
-// (P <= 64 C pages, NW waves).  Every wave holds every key (C per lane per
-// row) and the k-th largest key of each row is found 4 bits per round: wave w
-// counts the keys >= T | v << s for candidates v = 2w+1, 2w+2 of each row, the
-// 15 counts meet in LDS (double-buffered by round parity, so one barrier per
-// round), and every wave takes the largest v whose count reaches k.  Ties, the
-// forced pages and the ascending entry list follow wave_topk / wave_select_group;
-// wave w writes the entries of pages 64 j + lane with j = w (mod NW).
-// NROWS = 1: one top-k of the summed row with the group's largest retention
-// (per_kv_head_sum); NROWS = nrep: one per query head.  ret_l: lane r holds
-// query head r's retention.  All control flow is wave-uniform.  Ends with a
-// barrier; returns the list length in every thread.
+// (P <= 64 C pages, NW waves).  keys[r * 64 C + p] holds sortable_key of row
+// r's score of page p, and 0 (below every score) for p >= P.  Every wave loads
+// every key (C per lane per row); wave r finds row r's k-th largest key with
+// wave_kth_largest (no barrier inside), the thresholds meet in LDS, and every
+// wave then ranks the ties and lists the pages.  Ties and forced pages follow
+// wave_topk / wave_select_group; the entry list holds the forced pages first,
+// then the other selected pages, each part ascending; wave w writes the entries
+// of pages 64 j + lane with j = w (mod NW).  NROWS = 1: one top-k of the summed
+// row with the group's largest retention (per_kv_head_sum); NROWS = nrep: one
+// per query head.  ret_l: lane r holds query head r's retention.  All control
+// flow is wave-uniform.  Ends with a barrier; returns the list length in
+// every thread.
 struct BlockSelectLds {
-    int cnt[2][4][16];      // [round parity][row][candidate]
+    uint32_t T[4];          // k-th largest key per row
 };
 
 template <int C, int NW, int NROWS, int NREP>
-FQ_DEV int block_select_rows(const float* sc, int P, float ret_l, int k_max, int num_sinks, int window,
+FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max, int num_sinks, int window,
                              int* entries, BlockSelectLds& sl) {
-    static_assert(2 * NW >= 15 && NROWS <= 4, "15 candidates per round over NW waves; at most 4 rows");
+    static_assert(NROWS <= NW && NROWS <= 4, "one wave per row; at most 4 rows");
     const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
     constexpr uint8_t kAll = (uint8_t)((1u << NREP) - 1u);
     uint32_t key[NROWS][C];
     int k[NROWS];
     uint32_t T[NROWS];
+#pragma unroll
+    for (int r = 0; r < NROWS; ++r)
+#pragma unroll
+        for (int j = 0; j < C; ++j) key[r][j] = keys[r * 64 * C + 64 * j + lane];
     float rmax = 0.f;
 #pragma unroll
     for (int r = 0; r < NREP; ++r) rmax = fmaxf(rmax, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)));
 #pragma unroll
     for (int r = 0; r < NROWS; ++r) {
-#pragma unroll
-        for (int j = 0; j < C; ++j) {
-            const int i = 64 * j + lane;
-            const float v = sc[r * P + min(i, P - 1)];
-            key[r][j] = i < P ? sortable_key(v) : 0u;             // 0: below every score
-        }
         k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
-        T[r] = 0u;
-    }
-    const int v0 = 2 * w + 1;                 // w = 7: v = 16 is counted but never written
-#pragma unroll 1
-    for (int rd = 0; rd < 8; ++rd) {
-        const int s = 28 - 4 * rd;
-        int* cnt = &sl.cnt[rd & 1][0][0];
-#pragma unroll
-        for (int r = 0; r < NROWS; ++r) {
-            int n[2];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t cand = T[r] | ((uint32_t)(v0 + u) << s);
-                n[u] = 0;
-#pragma unroll
-                for (int j = 0; j < C; ++j) n[u] += __popcll(__ballot(key[r][j] >= cand));
-            }
-            // every lane stores the same value: no branch on the lane
-            cnt[r * 16 + v0] = n[0];
-            if (v0 + 1 <= 15) cnt[r * 16 + v0 + 1] = n[1];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < NROWS; ++r) {
-            const int n = cnt[r * 16 + (lane & 15)];
-            const uint64_t ok = __ballot(lane == 0 || (lane < 16 && n >= k[r]));
-            T[r] |= (uint32_t)(63 - __clzll((long long)ok)) << s;
+        if (w == r) {
+            const uint32_t t = k[r] > 0 ? wave_kth_largest<C>(key[r], k[r]) : 0u;
+            if (lane == 0) sl.T[r] = t;
         }
     }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NROWS; ++r) T[r] = sl.T[r];
     // ties at T: the lowest page indices (wave_topk's rule); identical in every wave
     uint8_t qm[C];
 #pragma unroll
@@ -225,16 +229,20 @@ FQ_DEV int block_select_rows(const float* sc, int P, float ret_l, int k_max, int
             take_eq -= __popcll(eq);
         }
     }
-    const int ns = num_sinks < P ? num_sinks : P;
-    const int wnd = window < P ? window : P;
-    int n = 0;
+    // The list: the forced pages first (ascending; forced_page() gives entry f
+    // without the selection), then every other selected page ascending.
+    const ForcedPages fp = forced_pages(P, num_sinks, window);
+    int n = fp.count;
 #pragma unroll
     for (int j = 0; j < C; ++j) {
         const int i = 64 * j + lane;
-        if (i < P && (i < ns || (wnd > 0 && i >= P - wnd))) qm[j] |= kAll;
-        const bool f = i < P && qm[j] != 0;
+        const bool forced = i < P && fp.contains(i);
+        const bool f = i < P && !forced && qm[j] != 0;
         const uint64_t bal = __ballot(f);
-        if (j % NW == w && f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
+        if (j % NW == w) {
+            if (forced) entries[fp.index(i)] = i | ((int)kAll << 16);
+            if (f) entries[n + (int)lanes_below(bal)] = i | ((int)qm[j] << 16);
+        }
         n += __popcll(bal);
     }
     __syncthreads();
@@ -242,11 +250,11 @@ FQ_DEV int block_select_rows(const float* sc, int P, float ret_l, int k_max, int
 }
 
 template <int C, int NW, int NREP>
-FQ_DEV int block_select_group(const float* sc, int P, int mode, float ret_l, int k_max, int num_sinks, int window,
+FQ_DEV int block_select_group(const uint32_t* keys, int P, int mode, float ret_l, int k_max, int num_sinks, int window,
                               int* entries, BlockSelectLds& sl) {
     if (mode == FQ_SELECT_PER_Q_HEAD)
-        return block_select_rows<C, NW, NREP, NREP>(sc, P, ret_l, k_max, num_sinks, window, entries, sl);
-    return block_select_rows<C, NW, 1, NREP>(sc, P, ret_l, k_max, num_sinks, window, entries, sl);
+        return block_select_rows<C, NW, NREP, NREP>(keys, P, ret_l, k_max, num_sinks, window, entries, sl);
+    return block_select_rows<C, NW, 1, NREP>(keys, P, ret_l, k_max, num_sinks, window, entries, sl);
 }
 
 }  // namespace fq

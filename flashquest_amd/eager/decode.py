@@ -147,6 +147,15 @@ class QuestDecoder:
         self.device = Q.device
         self.ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(self.cache, H_q))
 
+    @property
+    def fused(self) -> bool:
+        """True when attend() is the whole step: one attention kernel that scores
+        and selects its own pages (select() then launches nothing)."""
+        r = L.lib().fq_quest_fused_int4(self.cache, self.query, self.sinks, self.window, self.k_max, self.mode)
+        if r < 0:
+            L.check(-r, "quest fused query")
+        return r == 1
+
     def select(self):
         L.check(L.lib().fq_quest_select_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
                                              self.k_max, self.mode, None, L.ptr(self.mask_out), self.ws.data_ptr(),

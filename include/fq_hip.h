@@ -184,6 +184,15 @@ int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query,
                          int32_t k_max, int32_t select_mode,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* Whether fq_quest_attend_int4 scores and selects the pages inside its one
+ * attention kernel for these arguments (1; fq_quest_select_int4 then launches
+ * nothing unless scores_out or mask_out is given) or consumes page lists left
+ * by fq_quest_select_int4 (0).  Negative: an FQ_ERR_* code for invalid
+ * arguments.  No reference counterpart: it tells a caller (the benchmark) which
+ * kernels one decode step runs. */
+int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query,
+                        int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode);
+
 /* _merge_two_attentions (src/flashquest/eager/llama_persistent_patch.py:50-61).
  * O_a/O_b/out (N, D) rows with row strides; lse (N,) fp32.  out dtype = O_a dtype. */
 int fq_merge_attn(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b,

@@ -111,24 +111,27 @@ def test_split_override_is_restored_and_validated():
 
 @pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
 @pytest.mark.parametrize("want_mask", [False, True])
-def test_fused_decode_selecting_inside_attention(mode, want_mask):
+@pytest.mark.parametrize("sinks,window,P", [(3, 2, 24), (0, 0, 24), (4, 2, 5), (9, 1, 12), (1, 30, 20)])
+def test_fused_decode_selecting_inside_attention(mode, want_mask, sinks, window, P):
     # >= 192 KV groups: one workgroup per group, which selects its own pages from the
-    # scores (no selection kernel unless the mask is requested); a partial last page
+    # scores (no selection kernel unless the mask is requested); a partial last page.
+    # The forced pages go first in the workgroup's list and are loaded before the
+    # selection: none, sinks overlapping the window, forced pages covering every page.
     from flashquest_amd.eager import quest_decode_int4
-    L_, Hq, Hkv, P = 24, 24, 8, 24
+    L_, Hq, Hkv = 24, 24, 8
     cases = [Int4Case(seed=300 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * (P - 1) + 40, D=128, page=64, dtype="f16",
                       meta="f16", vgroup=32) for i in range(L_)]
     r = np.linspace(0.05, 0.6, Hq).astype(np.float32)
     dev = [c.device() for c in cases]
     stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
     q = torch.stack([c.q_dev() for c in cases])
-    out = quest_decode_int4(q, **stacked, retention=torch.from_numpy(r), num_sinks=3, window_pages=2,
+    out = quest_decode_int4(q, **stacked, retention=torch.from_numpy(r), num_sinks=sinks, window_pages=window,
                             k_max_static=12, select_mode=mode, return_selection=want_mask)
     torch.cuda.synchronize()
     o, lse = out[0], out[1]
     for i, c in enumerate(cases):
-        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=r, num_sinks=3, window_pages=2,
-                            mode=mode, k_max_static=12)
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=r, num_sinks=sinks,
+                            window_pages=window, mode=mode, k_max_static=12)
         if want_mask:
             assert np.array_equal(out[2][i].cpu().numpy(), ref["mask"]), i
         assert max_err(o[i][:, :, 0], ref["O"]) <= _tol(c, ref["O"]), i

@@ -126,17 +126,25 @@ def test_build_compact_selection_kats():
 def test_wht_matches_reference_order(dtype):
     from flashquest_amd.kernel import wht_along_head_dim
     rng = np.random.default_rng(5)
-    for D in (64, 128):
-        x = O.rounder(dtype)(rng.standard_normal((3, 5, D)).astype(np.float32))
-        tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-        got = wht_along_head_dim(torch.from_numpy(x).to(tdt).cuda()).float().cpu().numpy()
-        assert np.array_equal(got, O.wht(x, dtype))
+    # every supported width; row counts that leave part of a wave (and of a
+    # workgroup) idle, and rows spread over several workgroups
+    for D in (8, 16, 32, 64, 128):
+        for shape in ((3, 5, D), (67, D), (1, D)):
+            x = O.rounder(dtype)(rng.standard_normal(shape).astype(np.float32))
+            tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+            got = wht_along_head_dim(torch.from_numpy(x).to(tdt).cuda()).float().cpu().numpy()
+            assert np.array_equal(got, O.wht(x, dtype)), (D, shape)
     s = O.random_signs(1, 128)
     x = rng.standard_normal((4, 128)).astype(np.float32)
     fx = wht_along_head_dim(torch.from_numpy(x).cuda(), signs=torch.from_numpy(s))
     assert np.allclose(fx.cpu().numpy(), O.rotate_signed(x, s), atol=1e-5)
     back = wht_along_head_dim(fx, signs=torch.from_numpy(s), inverse=True)
     assert np.allclose(back.cpu().numpy(), x, atol=1e-5)
+    out = torch.empty_like(fx)
+    assert wht_along_head_dim(fx, signs=torch.from_numpy(s), inverse=True, out=out) is out
+    assert torch.equal(out, back)
+    with pytest.raises(ValueError):
+        wht_along_head_dim(fx, out=torch.empty(4, 64, device=fx.device))
 
 
 def test_turbo_quant_bit_exact():
