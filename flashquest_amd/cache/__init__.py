@@ -1,0 +1,6 @@
+"""Persistent quantised KV caches (src/flashquest/cache/): preallocated
+per-layer buffers in the packed layout the decode kernels read."""
+from .persistent_int4 import PersistentInt4KVCache
+from .persistent_turbo import PersistentTurboKVCache
+
+__all__ = ["PersistentInt4KVCache", "PersistentTurboKVCache"]

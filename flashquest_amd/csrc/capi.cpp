@@ -107,6 +107,14 @@ AttnLaunch choose_split(int G, int max_entries, int s_max) {
 static bool is_half(int dt) { return dt == FQ_BF16 || dt == FQ_F16; }
 static bool is_float_dtype(int dt) { return dt == FQ_BF16 || dt == FQ_F16 || dt == FQ_F32; }
 
+// 16-byte aligned base and rows: every stride but the innermost, in bytes.
+static bool rows_aligned16(const void* p, const int64_t* strides, int n_outer, int esize) {
+    if ((uintptr_t)p & 15) return false;
+    for (int i = 0; i < n_outer; ++i)
+        if ((strides[i] * esize) % 16) return false;
+    return true;
+}
+
 static int check_cache(const fq_int4_cache* c, Int4Cache* out) {
     if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
     if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
@@ -452,6 +460,10 @@ int fq_quantize_k_int4(const void* k, int32_t in_dtype, const int64_t k_strides[
     if (D % 2) return fail(FQ_ERR_INVALID, "quantize_k_int4 requires even head_dim; got %d", D);
     if (page_size < 1) return fail(FQ_ERR_INVALID, "page_size must be >= 1");
     if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    if (page_quant_k_ok(D, page_size, in_dtype, k, k_strides, packed, p_strides, scale, s_strides, mn, m_strides))
+        return hip_status(launch_quant_k_pages(k, in_dtype, k_strides, B, H, S, D, packed, p_strides, scale, s_strides,
+                                               mn, m_strides, meta_dtype, (hipStream_t)stream),
+                          "quantize k");
     return hip_status(launch_quant_k(k, in_dtype, k_strides, B, H, S, D, page_size, packed, p_strides, scale,
                                      s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream),
                       "quantize k");
@@ -464,9 +476,43 @@ int fq_quantize_v_int4(const void* v, int32_t in_dtype, const int64_t v_strides[
     if (D % 2) return fail(FQ_ERR_INVALID, "quantize_v_int4 requires even head_dim; got %d", D);
     if (group < 2 || group % 2 || D % group) return fail(FQ_ERR_INVALID, "bad V group %d for D=%d", group, D);
     if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    if (page_quant_v_ok(D, group, in_dtype, v, v_strides, packed, p_strides, s_strides, m_strides))
+        return hip_status(launch_quant_v_pages(v, in_dtype, v_strides, B, H, S, D, group, packed, p_strides, scale,
+                                               s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream),
+                          "quantize v");
     return hip_status(launch_quant_v(v, in_dtype, v_strides, B, H, S, D, group, packed, p_strides, scale,
                                      s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream),
                       "quantize v");
+}
+
+int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer, void* k_partial, const int64_t kpart_strides[5],
+                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype, const void* k_new,
+                         const int64_t kn_strides[4], const void* v_new, const int64_t vn_strides[4], int32_t seen,
+                         int32_t S_new, fq_stream_t stream) {
+    Int4Cache c{};
+    int st = check_cache(cache, &c);
+    if (st) return st;
+    if (layer < 0 || layer >= c.L) return fail(FQ_ERR_INVALID, "layer_idx %d out of range [0, %d)", layer, c.L);
+    if (seen < 0 || S_new < 0) return fail(FQ_ERR_INVALID, "negative seen / S_new");
+    if ((int64_t)seen + S_new > c.S)
+        return fail(FQ_ERR_INVALID, "seen+new=%lld exceeds max_seq_len=%d", (long long)seen + S_new, c.S);
+    if (c.page != 64) return fail(FQ_ERR_UNSUPPORTED, "page_size=%d (the append kernel takes 64)", c.page);
+    if ((int64_t)(seen + S_new + c.page - 1) / c.page > c.P) return fail(FQ_ERR_INVALID, "page metadata too short");
+    if (partial_dtype != FQ_BF16 && partial_dtype != FQ_F16)
+        return fail(FQ_ERR_UNSUPPORTED, "partial tail dtype must be bf16 or fp16");
+    if (!k_partial || !v_partial || (!k_new && S_new) || (!v_new && S_new)) return fail(FQ_ERR_INVALID, "NULL tensor");
+    const int64_t pk3[4] = {kpart_strides[1], kpart_strides[2], kpart_strides[3], kpart_strides[4]};
+    const int64_t pv3[4] = {vpart_strides[1], vpart_strides[2], vpart_strides[3], vpart_strides[4]};
+    if (!rows_aligned16(k_partial, kpart_strides, 4, 2) || !rows_aligned16(v_partial, vpart_strides, 4, 2) ||
+        kpart_strides[4] != 1 || vpart_strides[4] != 1 || pk3[3] != 1 || pv3[3] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "partial tails need 16-byte aligned contiguous rows");
+    if (S_new > 0 && (!rows_aligned16(k_new, kn_strides, 3, 2) || !rows_aligned16(v_new, vn_strides, 3, 2) ||
+                      kn_strides[3] != 1 || vn_strides[3] != 1))
+        return fail(FQ_ERR_UNSUPPORTED, "new K/V need 16-byte aligned contiguous rows");
+    if (((uintptr_t)c.vsc | (uintptr_t)c.vmn) & 1) return fail(FQ_ERR_UNSUPPORTED, "V metadata must be 2-byte aligned");
+    return hip_status(launch_int4_append(c, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype,
+                                         k_new, kn_strides, v_new, vn_strides, seen, S_new, (hipStream_t)stream),
+                      "int4 cache append");
 }
 
 int fq_wht(const void* x, int32_t x_dtype, int64_t x_row_stride, void* out, int32_t out_dtype,

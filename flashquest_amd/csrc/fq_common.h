@@ -240,6 +240,21 @@ hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bu
 // when attn_selects_in_kernel() says so for the same arguments.
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                             const AttnLaunch& al, hipStream_t st, const SelectArgs* sel = nullptr);
+// Page-tile INT4 quantisers (cache.hip): eligibility of a layout, whole-tensor
+// quantisation, and the cache append of update_quantized.
+bool page_quant_k_ok(int D, int page, int in_dtype, const void* k, const int64_t* k_s, const uint8_t* packed,
+                     const int64_t* p_s, const void* scale, const int64_t* s_s, const void* mn, const int64_t* m_s);
+bool page_quant_v_ok(int D, int group, int in_dtype, const void* v, const int64_t* v_s, const uint8_t* packed,
+                     const int64_t* p_s, const int64_t* s_s, const int64_t* m_s);
+hipError_t launch_quant_k_pages(const void* k, int in_dtype, const int64_t* k_s, int B, int H, int S, int D,
+                                uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s, void* mn,
+                                const int64_t* m_s, int meta_dtype, hipStream_t st);
+hipError_t launch_quant_v_pages(const void* v, int in_dtype, const int64_t* v_s, int B, int H, int S, int D,
+                                int group, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
+                                void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
+hipError_t launch_int4_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
+                              const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
+                              const void* vnew, const int64_t* vn_s, int seen, int S_new, hipStream_t st);
 bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);

@@ -106,14 +106,17 @@ def dequantize_v_int4(V_packed, scale, mn) -> torch.Tensor:
     return out.view(B, H, S, D).to(torch.bfloat16)
 
 
-def _turbo_planes(X: torch.Tensor):
+def _turbo_planes(X: torch.Tensor, out=None):
     L.require_device(X)
     B, H, S, D = X.shape
     if D % 8 != 0:
         raise ValueError(f"turbo quantisation requires head_dim multiple of 8; got {D}")
-    msb = torch.empty(B, H, S, D // 8, dtype=torch.uint8, device=X.device)
-    lsb = torch.empty(B, H, S, D // 4, dtype=torch.uint8, device=X.device)
-    scale = torch.empty(B, H, S, 1, dtype=torch.bfloat16, device=X.device)
+    if out is None:
+        msb = torch.empty(B, H, S, D // 8, dtype=torch.uint8, device=X.device)
+        lsb = torch.empty(B, H, S, D // 4, dtype=torch.uint8, device=X.device)
+        scale = torch.empty(B, H, S, 1, dtype=torch.bfloat16, device=X.device)
+    else:
+        msb, lsb, scale = out
     L.check(L.lib().fq_quantize_turbo(
         X.data_ptr(), L.dtype_code(X.dtype), L.strides(X, 4), B, H, S, D,
         msb.data_ptr(), L.strides(msb, 4), lsb.data_ptr(), L.strides(lsb, 4),
@@ -121,14 +124,22 @@ def _turbo_planes(X: torch.Tensor):
     return msb, lsb, scale
 
 
-def quantize_k_turbo(K: torch.Tensor, page_size: int):
+def quantize_k_turbo(K: torch.Tensor, page_size: int, *, out=None):
     """kv_quant.py:327-363: (K_msb, K_lsb, K_scale_turbo, K_scale_raw, K_mn_raw).
-    The raw INT4-equivalent page metadata (for scoring) is bf16."""
-    msb, lsb, st = _turbo_planes(K)
-    _, sr, mr = quantize_k_int4(K, page_size, meta_dtype=torch.bfloat16)
+    The raw INT4-equivalent page metadata (for scoring) is bf16.  ``out`` =
+    the five tensors (possibly strided views) to write into."""
+    if out is None:
+        msb, lsb, st = _turbo_planes(K)
+        _, sr, mr = quantize_k_int4(K, page_size, meta_dtype=torch.bfloat16)
+        return msb, lsb, st, sr, mr
+    msb, lsb, st, sr, mr = out
+    _turbo_planes(K, out=(msb, lsb, st))
+    # the codes of this INT4 pass are not kept; only the page scale/min are
+    scratch = torch.empty(K.shape[:-1] + (K.shape[-1] // 2,), dtype=torch.uint8, device=K.device)
+    quantize_k_int4(K, page_size, meta_dtype=sr.dtype, out=(scratch, sr, mr))
     return msb, lsb, st, sr, mr
 
 
-def quantize_v_turbo(V: torch.Tensor):
+def quantize_v_turbo(V: torch.Tensor, *, out=None):
     """kv_quant.py:381-405: (V_msb, V_lsb, V_scale_turbo)."""
-    return _turbo_planes(V)
+    return _turbo_planes(V, out=out)

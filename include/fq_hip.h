@@ -184,6 +184,23 @@ int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query,
                          int32_t k_max, int32_t select_mode,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* PersistentInt4KVCache.update_quantized (src/flashquest/cache/persistent_int4.py:69-132)
+ * for one layer of the preallocated cache described by `cache` (S = max_seq_len,
+ * P = max_pages, page_size 64): the pages that the append of S_new tokens
+ * completes are quantised from (the layer's partial tail, the new tokens) into
+ * K_packed / K_scale / K_mn / V_packed / V_scale / V_mn, then the remaining
+ * tokens are staged in the tail.  Partial tails (L, B, H_kv, page_size, D) and
+ * K_new / V_new (B, H_kv, S_new, D) share one dtype (bf16 or fp16), with
+ * contiguous 16-byte aligned rows.  `seen` is the layer's token count before
+ * the append; the caller advances it.  Codes and metadata are those of
+ * fq_quantize_k_int4 / fq_quantize_v_int4 on the concatenated stream. */
+int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer,
+                         void* k_partial, const int64_t kpart_strides[5],
+                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype,
+                         const void* k_new, const int64_t kn_strides[4],
+                         const void* v_new, const int64_t vn_strides[4],
+                         int32_t seen, int32_t S_new, fq_stream_t stream);
+
 /* Whether fq_quest_attend_int4 scores and selects the pages inside its one
  * attention kernel for these arguments (1; fq_quest_select_int4 then launches
  * nothing unless scores_out or mask_out is given) or consumes page lists left
