@@ -28,7 +28,8 @@ sys.path.insert(0, ROOT)
 
 from flashquest_amd._lib import KernelTimer  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
-from flashquest_amd.kernel.kv_quant import quantize_k_int4, quantize_v_int4  # noqa: E402
+from flashquest_amd.kernel.kv_quant import (quantize_k_int4, quantize_k_turbo, quantize_v_int4,  # noqa: E402
+                                            quantize_v_turbo)
 from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402
 
 METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
@@ -66,8 +67,31 @@ def rotation_signs(D=128, dev="cuda"):
     return (torch.randint(0, 2, (D,), generator=g) * 2 - 1).float().to(dev)
 
 
+def gen_layer(l, b, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda"):
+    """Seeded fp32 K, V (1, Hkv, S, D) and q (Hq, D) of (sequence b, layer l),
+    seed 1000*b + l: N(0,1) K with lognormal(0,1) channel factors, 4 planted
+    pages per KV head whose keys point along the group's mean query, N(0,1) V."""
+    S = P * page
+    rep = Hq // Hkv
+    g = torch.Generator(device=dev)
+    g.manual_seed(1000 * b + l)
+    K = torch.randn(1, Hkv, S, D, generator=g, device=dev)
+    K *= torch.exp(torch.randn(1, Hkv, 1, D, generator=g, device=dev))      # lognormal(0,1) channels
+    V = torch.randn(1, Hkv, S, D, generator=g, device=dev)
+    q = torch.randn(Hq, D, generator=g, device=dev)
+    qhat = q.view(Hkv, rep, D).mean(1)
+    qhat = qhat / qhat.norm(dim=-1, keepdim=True)
+    rms = K[0].pow(2).mean(dim=(1, 2)).sqrt()
+    for h in range(Hkv):
+        pages = torch.randperm(P - 6, generator=g, device=dev)[:planted] + 4
+        for p in pages.tolist():
+            noise = torch.randn(page, D, generator=g, device=dev)
+            K[0, h, p * page:(p + 1) * page] = rms[h] * (0.8 * math.sqrt(D) * qhat[h] + 0.6 * noise)
+    return K, V, q
+
+
 def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda", signs=None):
-    """Seeded synthetic INT4 cache, one (sequence, layer) at a time (seed 1000*b + l).
+    """Seeded synthetic INT4 cache, one (sequence, layer) at a time (gen_layer).
     With ``signs`` (config 3) K and V are rotated by WHT(signs * x) before
     quantisation; Q stays in the raw basis (the step rotates it)."""
     S = P * page
@@ -78,23 +102,9 @@ def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda",
     vs = torch.empty(L, B, Hkv, S, D // 32, dtype=torch.float16, device=dev)
     vm = torch.empty_like(vs)
     Q = torch.empty(L, B, Hq, 1, D, dtype=torch.float16, device=dev)
-    rep = Hq // Hkv
     for l in range(L):
         for b in range(B):
-            g = torch.Generator(device=dev)
-            g.manual_seed(1000 * b + l)
-            K = torch.randn(1, Hkv, S, D, generator=g, device=dev)
-            K *= torch.exp(torch.randn(1, Hkv, 1, D, generator=g, device=dev))      # lognormal(0,1) channels
-            V = torch.randn(1, Hkv, S, D, generator=g, device=dev)
-            q = torch.randn(Hq, D, generator=g, device=dev)
-            qhat = q.view(Hkv, rep, D).mean(1)
-            qhat = qhat / qhat.norm(dim=-1, keepdim=True)
-            rms = K[0].pow(2).mean(dim=(1, 2)).sqrt()
-            for h in range(Hkv):
-                pages = torch.randperm(P - 6, generator=g, device=dev)[:planted] + 4
-                for p in pages.tolist():
-                    noise = torch.randn(page, D, generator=g, device=dev)
-                    K[0, h, p * page:(p + 1) * page] = rms[h] * (0.8 * math.sqrt(D) * qhat[h] + 0.6 * noise)
+            K, V, q = gen_layer(l, b, Hq, Hkv, P, D, page, planted, dev)
             if signs is not None:
                 K = wht_along_head_dim(K, signs=signs)
                 V = wht_along_head_dim(V, signs=signs)
@@ -103,6 +113,30 @@ def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda",
             Q[l, b, :, 0] = q.half()
     torch.cuda.synchronize()
     return dict(Q=Q, K_packed=kp, K_scale=ks, K_mn=km, V_packed=vp, V_scale=vs, V_mn=vm)
+
+
+def make_turbo_cache(L, Hq=24, Hkv=8, P=512, D=128, page=64, dev="cuda"):
+    """The same synthetic layers (batch 1) in the reference's TurboQuant K3-V3
+    layout, layers folded into the batch axis: planes, per-token bf16 scales,
+    the un-rotated K's bf16 page scale/min for scoring, bf16 Q."""
+    S = P * page
+    c = {"K_msb": torch.empty(L, Hkv, S, D // 8, dtype=torch.uint8, device=dev),
+         "K_lsb": torch.empty(L, Hkv, S, D // 4, dtype=torch.uint8, device=dev),
+         "K_scale_turbo": torch.empty(L, Hkv, S, 1, dtype=torch.bfloat16, device=dev),
+         "K_scale_raw": torch.empty(L, Hkv, P, D, dtype=torch.bfloat16, device=dev),
+         "K_mn_raw": torch.empty(L, Hkv, P, D, dtype=torch.bfloat16, device=dev),
+         "V_msb": torch.empty(L, Hkv, S, D // 8, dtype=torch.uint8, device=dev),
+         "V_lsb": torch.empty(L, Hkv, S, D // 4, dtype=torch.uint8, device=dev),
+         "V_scale_turbo": torch.empty(L, Hkv, S, 1, dtype=torch.bfloat16, device=dev),
+         "Q": torch.empty(L, Hq, 1, D, dtype=torch.bfloat16, device=dev)}
+    for l in range(L):
+        K, V, q = gen_layer(l, 0, Hq, Hkv, P, D, page, 4, dev)
+        quantize_k_turbo(K.bfloat16(), page, out=tuple(c[k][l:l + 1] for k in
+                                                       ("K_msb", "K_lsb", "K_scale_turbo", "K_scale_raw", "K_mn_raw")))
+        quantize_v_turbo(V.bfloat16(), out=tuple(c[k][l:l + 1] for k in ("V_msb", "V_lsb", "V_scale_turbo")))
+        c["Q"][l, :, 0] = q.bfloat16()
+    torch.cuda.synchronize()
+    return c
 
 
 def step_bytes(cache, mask, page=64):
@@ -327,6 +361,30 @@ def main():
         extra.update({"config3_rotated_us": r_ms * 1e3, "config3_step_GBps": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9,
                       "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
         del rc, rdec, q_raw, o_raw, rmask
+
+        # TurboQuant K3-V3 (the reference's kv_bits == 3 path): its operator
+        # sequence -- page scores from the raw K metadata, per-query-head
+        # top-k, sparse turbo attention -- over all layers at once
+        from flashquest_amd.eager.criticality import page_scores_int4_fast
+        from flashquest_amd.eager.selection import select_pages_vectorized
+        from flashquest_amd.kernel.sparse_turbo_fwd import flash_attn_sparse_turbo_fwd
+        tc = make_turbo_cache(L, P=P, dev=dev)
+
+        def turbo_step():
+            sc = page_scores_int4_fast(tc["Q"], tc["K_scale_raw"], tc["K_mn_raw"])
+            m = select_pages_vectorized(sc, args.retention, 4, 2, k_max_static=k)
+            return flash_attn_sparse_turbo_fwd(tc["Q"], tc["K_msb"], tc["K_lsb"], tc["K_scale_turbo"], tc["V_msb"],
+                                               tc["V_lsb"], tc["V_scale_turbo"], selection_mask=m)[0], m
+
+        _, tmask = turbo_step()
+        torch.cuda.synchronize()
+        t_union = tmask[:, :, 0].view(L, 8, Hq // 8, P).any(2).sum().item()
+        t_bytes = (L * 8 * P * 128 * 2 * 2 + t_union * 64 * (2 * (16 + 32) + 2 * 2) + L * Hq * (128 * 2 * 2 + 4))
+        t_ms, _, _ = time_steps(noop, turbo_step, args.steps, args.warmup, flush)
+        extra.update({"turbo_3bit_per_q_head_us": t_ms * 1e3, "turbo_union_pages_per_kv_head": t_union / (L * 8),
+                      "turbo_step_GBps": t_bytes / (t_ms * 1e-3) / 1e9,
+                      "turbo_roofline_frac": t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        del tc
 
         # batch 16 independent sequences, 28 layers, 32k each
         if B == 1 and args.batch16:
