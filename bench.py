@@ -362,29 +362,42 @@ def main():
                       "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
         del rc, rdec, q_raw, o_raw, rmask
 
-        # TurboQuant K3-V3 (the reference's kv_bits == 3 path): its operator
-        # sequence -- page scores from the raw K metadata, per-query-head
-        # top-k, sparse turbo attention -- over all layers at once
+        # TurboQuant K3-V3 (the reference's kv_bits == 3 path) over all layers:
+        # the fused decode (scores from the raw K page metadata, selection,
+        # turbo attention) in both selection modes, and the reference's operator
+        # sequence (page scores, per-query-head top-k, mask attention)
         from flashquest_amd.eager.criticality import page_scores_int4_fast
+        from flashquest_amd.eager.decode import quest_decode_turbo
         from flashquest_amd.eager.selection import select_pages_vectorized
         from flashquest_amd.kernel.sparse_turbo_fwd import flash_attn_sparse_turbo_fwd
         tc = make_turbo_cache(L, P=P, dev=dev)
+        planes = [tc[x] for x in ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")]
 
-        def turbo_step():
+        def turbo_bytes(mask):
+            union = mask.view(L, 8, Hq // 8, P).any(2).sum().item()
+            return (L * 8 * P * 128 * 2 * 2 + union * 64 * (2 * (16 + 32) + 2 * 2) + L * Hq * (128 * 2 * 2 + 4)), union
+
+        for mode in ("per_kv_head_sum", "per_q_head"):
+            _, _, tmask = quest_decode_turbo(tc["Q"], *planes, tc["K_scale_raw"], tc["K_mn_raw"], retention=args.retention,
+                                             num_sinks=4, window_pages=2, k_max_static=k, select_mode=mode,
+                                             return_selection=True)
+            torch.cuda.synchronize()
+            t_bytes, t_union = turbo_bytes(tmask)
+            t_ms, _, _ = time_steps(noop, lambda: quest_decode_turbo(
+                tc["Q"], *planes, tc["K_scale_raw"], tc["K_mn_raw"], retention=args.retention, num_sinks=4,
+                window_pages=2, k_max_static=k, select_mode=mode), args.steps, args.warmup, flush)
+            extra.update({f"turbo_{mode}_us": t_ms * 1e3, f"turbo_{mode}_union_pages_per_kv_head": t_union / (L * 8),
+                          f"turbo_{mode}_step_GBps": t_bytes / (t_ms * 1e-3) / 1e9,
+                          f"turbo_{mode}_roofline_frac": t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+
+        def turbo_ops_step():
             sc = page_scores_int4_fast(tc["Q"], tc["K_scale_raw"], tc["K_mn_raw"])
             m = select_pages_vectorized(sc, args.retention, 4, 2, k_max_static=k)
-            return flash_attn_sparse_turbo_fwd(tc["Q"], tc["K_msb"], tc["K_lsb"], tc["K_scale_turbo"], tc["V_msb"],
-                                               tc["V_lsb"], tc["V_scale_turbo"], selection_mask=m)[0], m
+            return flash_attn_sparse_turbo_fwd(tc["Q"], *planes, selection_mask=m)[0]
 
-        _, tmask = turbo_step()
-        torch.cuda.synchronize()
-        t_union = tmask[:, :, 0].view(L, 8, Hq // 8, P).any(2).sum().item()
-        t_bytes = (L * 8 * P * 128 * 2 * 2 + t_union * 64 * (2 * (16 + 32) + 2 * 2) + L * Hq * (128 * 2 * 2 + 4))
-        t_ms, _, _ = time_steps(noop, turbo_step, args.steps, args.warmup, flush)
-        extra.update({"turbo_3bit_per_q_head_us": t_ms * 1e3, "turbo_union_pages_per_kv_head": t_union / (L * 8),
-                      "turbo_step_GBps": t_bytes / (t_ms * 1e-3) / 1e9,
-                      "turbo_roofline_frac": t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
-        del tc
+        t_ms, _, _ = time_steps(noop, turbo_ops_step, args.steps, args.warmup, flush)
+        extra["turbo_reference_operator_sequence_us"] = t_ms * 1e3
+        del tc, planes
 
         # batch 16 independent sequences, 28 layers, 32k each
         if B == 1 and args.batch16:

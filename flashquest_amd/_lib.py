@@ -92,6 +92,8 @@ SIGNATURES = {
                                             _P, _P, _P, ctypes.c_size_t, _P]),
     "fq_int4_cache_append": (ctypes.c_int, [ctypes.POINTER(Int4Cache), _I, _P, _I64P, _P, _I64P, _I, _P, _I64P,
                                             _P, _I64P, _I, _I, _P]),
+    "fq_quest_decode_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, ctypes.POINTER(Query),
+                                             _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
     "fq_quest_fused_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
     "fq_quest_attend_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, ctypes.c_size_t, _P]),

@@ -26,7 +26,7 @@
 #include <type_traits>
 
 #include "attn_common.h"
-#include "select_common.h"
+#include "fused_common.h"
 
 namespace fq {
 namespace {
@@ -37,8 +37,6 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
-constexpr int kMaxWgPages = 1024;           // pages of one workgroup split (entries staged in LDS)
-constexpr int kSelC = 8;                    // in-kernel selection: pages per lane (P <= 512)
 constexpr float kQkScale = 8323071.0f;      // 2^23 - 2^16 - 1: |X| <= this keeps 3 balanced digits in int8
 constexpr float kSubnormal = 16777216.0f;   // 2^24: fp16 subnormal with bits c has value c * 2^-24
 
@@ -73,22 +71,6 @@ FQ_DEV uint32_t byte_i(uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3) {
 }
 constexpr uint32_t kDigitFlip = 0x80808080u;
 
-FQ_DEV float wave_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, dpp<kDppMirror>(v));
-    v = fmaxf(v, dpp<kDppHalfMirror>(v));
-    v = fmaxf(v, dpp<kDppXor1>(v));
-    return fmaxf(v, dpp<kDppXor2>(v));
-}
-FQ_DEV float row16_max(float v) {
-    v = fmaxf(v, dpp<kDppMirror>(v));
-    v = fmaxf(v, dpp<kDppHalfMirror>(v));
-    v = fmaxf(v, dpp<kDppXor1>(v));
-    return fmaxf(v, dpp<kDppXor2>(v));
-}
-FQ_DEV float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
-
 FQ_DEV void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // Raw V metadata of one token: G halves (G = 4: 8 bytes, G = 1: 2 bytes).
@@ -111,21 +93,6 @@ FQ_DEV void unpack_vmeta(const VMetaRaw& r, float (&out)[G]) {
 struct SliceRsrc {
     __amdgpu_buffer_rsrc_t k, v, vs, vm, ks, km;
 };
-
-FQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-FQ_DEV uint4 ld128(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
-FQ_DEV uint32_t ld32(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
-FQ_DEV uint2 ld64(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-    return make_uint2(v[0], v[1]);
-}
-FQ_DEV uint32_t ld16(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 
 // Raw V metadata of tokens 16T + n16 (T = 0..3); off = byte offset of token n16.
 template <int G>
@@ -157,71 +124,6 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
     for (int j = 0; j < 16; ++j) b.vw[j] = ld32(r.v, voff + (16 * (j & 3) + 4 * (j >> 2)) * 64);
     load_vmeta<G>(b.vs, r.vs, moff);
     load_vmeta<G>(b.vm, r.vm, moff);
-}
-
-// Page scores of one KV group (P <= 64 * kSelC pages) by a whole workgroup of
-// NT threads: 16 lanes per page, NT / 16 pages per pass.  score_group_load
-// issues every pass's metadata loads (pages past P re-read page P-1, so there
-// is no branch between loads and use); score_group_regs scores them --
-// score_kernel's arithmetic and order exactly -- and stores the sortable keys
-// s_key[r * 64 kSelC + p] per query head, or (SUM, per_kv_head_sum) s_key[p]
-// for the group's summed query, with 0 (below every score) for p >= P.
-template <int NT>
-struct ScoreRegs {
-    static constexpr int kPass = 64 * kSelC / (NT / 16);
-    uint4 sv[kPass], mv[kPass];
-};
-
-template <typename MT, int NT>
-FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int l, int b, int h) {
-    constexpr int PPP = NT / 16;
-    const int lip = tid & 15, pip = tid >> 4;
-    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2] + lip * 8;
-    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2] + lip * 8;
-#pragma unroll
-    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
-        const int p = min(u * PPP + pip, c.P - 1);
-        sr.sv[u] = *(const uint4*)(ksc + p * 128);
-        sr.mv[u] = *(const uint4*)(kmn + p * 128);
-    }
-}
-
-template <typename MT, int NREP, int NT, bool SUM>
-FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P) {
-    constexpr int PPP = NT / 16;
-    const int lip = tid & 15, pip = tid >> 4;
-    // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
-    // relu applied per head before the sum; per_q_head scores every head
-    constexpr int NR = SUM ? 1 : NREP;
-    float qr[NR][8], qp[NR][8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        if constexpr (SUM) {
-            float qs = s_qraw[0][lip * 8 + j];
-            float ps = qs > 0.f ? qs : 0.f;
-#pragma unroll
-            for (int r = 1; r < NREP; ++r) {
-                const float v = s_qraw[r][lip * 8 + j];
-                qs = __fadd_rn(qs, v);
-                ps = __fadd_rn(ps, v > 0.f ? v : 0.f);
-            }
-            qr[0][j] = qs;
-            qp[0][j] = ps;
-        } else {
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) {
-                qr[r][j] = s_qraw[r][lip * 8 + j];
-                qp[r][j] = qr[r][j] > 0.f ? qr[r][j] : 0.f;
-            }
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
-        const int p = u * PPP + pip;
-        score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
-            if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
-        });
-    }
 }
 
 // NW waves per workgroup (4, or 8 when one workgroup takes a whole KV group).

@@ -568,8 +568,71 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
                                            ws, s),
                     "page union");
     if (st) return st;
+    if (turbo_fused_supported(*cache, q))
+        return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, cache->P, nullptr, s), "sparse turbo attention");
     const AttnLaunch al = choose_split(G, cache->P, ws.s_max);
     return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "sparse turbo attention");
+}
+
+int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
+                          const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
+                          const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                          int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                          fq_stream_t stream) {
+    if (!cache) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    if (cache->D != 64 && cache->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", cache->D);
+    if (cache->P < 1 || cache->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", cache->P);
+    if (cache->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
+    if (cache->kmsb_strides[4] != 1 || cache->klsb_strides[4] != 1 || cache->vmsb_strides[4] != 1 ||
+        cache->vlsb_strides[4] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "innermost turbo plane axis must be contiguous");
+    if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
+    if (select_mode != FQ_SELECT_PER_Q_HEAD && select_mode != FQ_SELECT_PER_KV_HEAD_SUM)
+        return fail(FQ_ERR_INVALID, "select_mode=%d", select_mode);
+    QueryArgs q{};
+    int st = check_query(query, cache->D, cache->H_kv, &q);
+    if (st) return st;
+    if (((uintptr_t)q.q) & 1) return fail(FQ_ERR_UNSUPPORTED, "query must be 2-byte aligned");
+    // the raw page metadata as an INT4 cache descriptor (scoring reads only K scale/min)
+    if (!k_scale_raw || !k_mn_raw) return fail(FQ_ERR_INVALID, "NULL raw K metadata");
+    if (ksr_strides[4] != 1 || kmr_strides[4] != 1) return fail(FQ_ERR_UNSUPPORTED, "raw K metadata channel axis must be contiguous");
+    for (int i = 0; i < 4; ++i)
+        if (ksr_strides[i] % 8 || kmr_strides[i] % 8)
+            return fail(FQ_ERR_UNSUPPORTED, "raw K metadata strides must be multiples of 8 elements");
+    if (((uintptr_t)k_scale_raw | (uintptr_t)k_mn_raw) & 15)
+        return fail(FQ_ERR_UNSUPPORTED, "raw K metadata must be 16-byte aligned");
+    Int4Cache c{};
+    c.ksc = k_scale_raw; c.kmn = k_mn_raw;
+    for (int i = 0; i < 4; ++i) { c.ksc_s[i] = ksr_strides[i]; c.kmn_s[i] = kmr_strides[i]; }
+    c.L = cache->L; c.B = cache->B; c.Hkv = cache->H_kv; c.S = cache->S; c.P = cache->P; c.D = cache->D;
+    c.page = cache->page_size; c.G = 1; c.meta_dtype = FQ_BF16;
+    const int G = c.L * c.B * c.Hkv;
+    const size_t need = workspace_bytes(G, c.P, q.nrep, q.nrep, c.D);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
+    if ((uintptr_t)workspace & 255) return fail(FQ_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    Workspace ws = carve_workspace(workspace, G, c.P, q.nrep, q.nrep, c.D);
+    if (num_sinks < 0) num_sinks = 0;
+    if (window_pages < 0) window_pages = 0;
+    if (k_max > c.P) k_max = c.P;
+    hipStream_t s = (hipStream_t)stream;
+    const int bound = quest_bound(c, q, num_sinks, window_pages, k_max, select_mode);
+    const bool fusable = turbo_fused_supported(*cache, q);
+    if (fusable && !mask_out && G >= 192 && c.P <= 64 * 8) {
+        SelectArgs sel{};
+        sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
+        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
+        return hip_status(launch_attn_turbo_fused(*cache, &c, q, ws, bound, &sel, s), "quest turbo decode");
+    }
+    const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
+    int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};
+    st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
+                                 k_max, mask_out, s),
+                    "score+select");
+    if (st) return st;
+    if (fusable) return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, nullptr, s), "quest turbo decode");
+    const AttnLaunch al = choose_split(G, bound, ws.s_max);
+    return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "quest turbo decode");
 }
 
 }  // extern "C"

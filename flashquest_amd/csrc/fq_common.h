@@ -255,6 +255,11 @@ hipError_t launch_quant_v_pages(const void* v, int in_dtype, const int64_t* v_s,
 hipError_t launch_int4_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
                               const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
                               const void* vnew, const int64_t* vn_s, int seen, int S_new, hipStream_t st);
+// Fused-layout TurboQuant attention (turbo_fused.hip): D = 128, 64-token pages,
+// <= 3 query heads per KV head.  raw + sel: score and select in the kernel.
+bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q);
+hipError_t launch_attn_turbo_fused(const fq_turbo_cache& c, const Int4Cache* raw, const QueryArgs& q,
+                                   const Workspace& ws, int max_entries, const SelectArgs* sel, hipStream_t st);
 bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);

@@ -116,6 +116,75 @@ def quest_decode_int4(
     return O, lse_out
 
 
+def quest_decode_turbo(
+    Q: torch.Tensor,
+    K_msb: torch.Tensor,
+    K_lsb: torch.Tensor,
+    K_scale_turbo: torch.Tensor,
+    V_msb: torch.Tensor,
+    V_lsb: torch.Tensor,
+    V_scale_turbo: torch.Tensor,
+    K_scale_raw: torch.Tensor,
+    K_mn_raw: torch.Tensor,
+    *,
+    retention: float | torch.Tensor,
+    num_sinks: int = 4,
+    window_pages: int = 2,
+    k_max_static: int | None = None,
+    page_size: int = 64,
+    select_mode: str = "per_q_head",
+    sm_scale: float | None = None,
+    return_lse: bool = True,
+    return_selection: bool = False,
+):
+    """The reference's TurboQuant decode over completed pages, fused: page scores
+    from the un-rotated K page metadata (criticality.py:128-163), selection
+    (selection.py:65-126), flash_attn_sparse_turbo_fwd (sparse_turbo_fwd.py:254-346).
+
+    One layer: Q (B,H_q,1,D) raw basis, cache tensors 4D (B,H_kv,...).  L layers
+    at once: Q (L,B,H_q,1,D), cache tensors 5D.  Returns (O like Q in the raw
+    basis, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
+    """
+    if select_mode not in L.SELECT_MODES:
+        raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
+    L.require_device(Q, K_msb, K_scale_raw)
+    if Q.shape[-2] != 1:
+        raise NotImplementedError(f"quest_decode_turbo: decode-only (S_q={Q.shape[-2]})")
+    D = Q.shape[-1]
+    if D not in (64, 128):
+        raise NotImplementedError(f"head_dim={D} not in (64, 128)")
+    if K_scale_raw.dtype != torch.bfloat16 or K_mn_raw.dtype != torch.bfloat16:
+        raise AssertionError("K_scale_raw / K_mn_raw must be bf16")
+    Q3 = Q[..., 0, :]
+    H_q = Q3.shape[-2]
+    P = K_scale_raw.shape[-2]
+    O3 = torch.empty_like(Q3)
+    lse = torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device) if return_lse else None
+    cache, keep = _ops.turbo_cache(K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo, P, page_size)
+    if H_q % cache.H_kv:
+        raise ValueError(f"H_q={H_q} must be divisible by H_kv={cache.H_kv}")
+    lead = 5 - K_scale_raw.dim()
+    ksr = K_scale_raw if K_scale_raw.stride(-1) == 1 else K_scale_raw.contiguous()
+    kmr = K_mn_raw if K_mn_raw.stride(-1) == 1 else K_mn_raw.contiguous()
+    query = _ops.query(Q3, O3, lse, sm_scale)
+    r = _ops.retention_tensor(retention, H_q, Q.device)
+    k_max = -1 if k_max_static is None else min(int(k_max_static), P)
+    mask = None
+    if return_selection:
+        mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
+    ws = L.workspace(Q.device, L.lib().fq_turbo_workspace_bytes(cache, H_q))
+    L.check(L.lib().fq_quest_decode_turbo(cache, ksr.data_ptr(), L.strides(ksr, 5, lead), kmr.data_ptr(),
+                                          L.strides(kmr, 5, lead), query, r.data_ptr(), int(num_sinks),
+                                          int(window_pages), k_max, L.SELECT_MODES[select_mode],
+                                          None if mask is None else mask.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          L.stream_handle(Q.device)), "quest_decode_turbo")
+    O = O3.unsqueeze(-2)
+    lse_out = lse.unsqueeze(-1) if lse is not None else None
+    if return_selection:
+        return O, lse_out, mask
+    return O, lse_out
+
+
 class QuestDecoder:
     """A reusable fused decode over fixed cache tensors (the bench's timed unit).
 

@@ -272,6 +272,23 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
 
 size_t fq_turbo_workspace_bytes(const fq_turbo_cache* cache, int32_t H_q);
 
+/* The reference's TurboQuant decode branch for completed pages
+ * (llama_persistent_patch.py:152-160 with the selection of 196-245):
+ * page scores from the un-rotated K's page scale/min (K_scale_raw / K_mn_raw,
+ * (L, B, H_kv, P, D) bf16; criticality.py:128-163), top-k selection
+ * (selection.py:65-126, or one selection per KV head from the summed group
+ * scores with FQ_SELECT_PER_KV_HEAD_SUM), then flash_attn_sparse_turbo_fwd
+ * (sparse_turbo_fwd.py:254-346) over the selected pages, for every
+ * (layer, batch, KV head) at once.  With enough KV groups to fill the GPU,
+ * D = 128, 64-token pages and mask_out NULL this is one kernel launch.
+ * mask_out (optional): the (L*B, H_q, P) selection, as fq_quest_select_int4. */
+int fq_quest_decode_turbo(const fq_turbo_cache* cache,
+                          const void* k_scale_raw, const int64_t ksr_strides[5],
+                          const void* k_mn_raw, const int64_t kmr_strides[5],
+                          const fq_query* query, const float* retention,
+                          int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                          uint8_t* mask_out, void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
