@@ -56,9 +56,9 @@ FQ_DEV void force_pages(SelectLds& s, int P, int num_sinks, int window, uint8_t 
 // ---------------------------------------------------------------------------
 // Scoring.  One workgroup scores `ppc` pages of one KV group for all of its
 // query rows; NL = D/8 lanes cooperate on a page, each owning 8 channels.
-// Order (matched by the CPU oracle): lane sums its 8 products left to right
-// (products rounded, no FMA), lanes combine by the 16-lane DPP butterfly;
-// score = t1 + t2 * 15.
+// Order (matched by the CPU oracle): a lane starts from its first product and
+// adds the other 7 left to right by fused multiply-adds, lanes combine by the
+// 16-lane DPP butterfly; score = t1 + t2 * 15.
 // ---------------------------------------------------------------------------
 struct ScoreParams {
     Int4Cache c;

@@ -110,10 +110,11 @@ FQ_DEV int wave_select_group(const float* sc, int P, int nrep, int mode, const f
 
 // Quest page score (criticality.py:128-163) of one page for NR query rows, by
 // the 16 lanes of a DPP row, each owning 8 channels (q values in registers).
-// The fp32 order is fixed (and restated by the CPU oracle): a lane sums its 8
-// products left to right (products rounded, no FMA), lanes combine by the DPP
-// butterfly in row_sum<16>, score = t1 + t2 * 15.  emit(r, score) runs on all
-// 16 lanes with the same value.
+// The fp32 order is fixed (and restated by the CPU oracle): a lane starts from
+// its first product (rounded) and adds the other 7 by fused multiply-adds, one
+// rounding each (fp16 metadata feeds v_fma_mix_f32 with no conversion); lanes
+// combine by the DPP butterfly in row_sum<16>, score = t1 + t2 * 15.
+// emit(r, score) runs on all 16 lanes with the same value.
 template <int NR, typename MT, typename Emit>
 FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[NR][8], const float (&qp)[NR][8],
                             Emit emit) {
@@ -134,8 +135,8 @@ FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[
         t2[r] = __fmul_rn(qp[r][0], sf[0]);
 #pragma unroll
         for (int j = 1; j < 8; ++j) {
-            t1[r] = __fadd_rn(t1[r], __fmul_rn(qr[r][j], mf[j]));
-            t2[r] = __fadd_rn(t2[r], __fmul_rn(qp[r][j], sf[j]));
+            t1[r] = __builtin_fmaf(qr[r][j], mf[j], t1[r]);
+            t2[r] = __builtin_fmaf(qp[r][j], sf[j], t2[r]);
         }
     }
 #pragma unroll

@@ -248,28 +248,59 @@ def page_scores_int4_exact(Q, K_scale, K_mn):
     return (t1 + 15.0 * t2).reshape(B, Hq, -1)
 
 
-def _lane_sum_butterfly(prod: np.ndarray) -> np.ndarray:
-    """Fixed fp32 reduction over the last axis D.
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded fp32 fused multiply-add RN(a*b + c), elementwise, for
+    finite fp32 inputs (the GPU's v_fma_f32 / v_fma_mix_f32 semantics).
 
-    Lane j (of D/8) sums channels 8j..8j+7 left to right; lanes are then
-    combined the way the HIP kernel's DPP steps do: with 16 lanes first
+    a*b is exact in fp64 (at most 48 significant bits); TwoSum splits the fp64
+    sum into s + e exactly; RN32(s) equals RN32(s + e) except when s lies
+    exactly halfway between two fp32 neighbours and e != 0, where e decides.
+    """
+    a = np.asarray(a, F32).astype(np.float64)
+    b = np.asarray(b, F32).astype(np.float64)
+    c = np.asarray(c, F32).astype(np.float64)
+    x = a * b
+    s = x + c
+    bb = s - x
+    e = (x - (s - bb)) + (c - bb)
+    r = s.astype(F32)
+    d = s - r.astype(np.float64)
+    toward = np.where(d > 0, np.float32(np.inf), np.float32(-np.inf)).astype(F32)
+    nb = np.nextafter(r, toward)
+    gap = np.abs(nb.astype(np.float64) - r.astype(np.float64))
+    mid = (d != 0) & (2.0 * np.abs(d) == gap) & (e != 0)
+    up = mid & ((e > 0) == (d > 0))       # past the midpoint, away from r
+    down = mid & ~up                      # short of the midpoint: r itself
+    out = np.where(up, nb, r)
+    out = np.where(down, r, out)
+    return out.astype(F32)
+
+
+def _lane_fma_butterfly(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Fixed fp32 evaluation of sum_d a_d * b_d over the last axis D.
+
+    Lane j (of D/8) owns channels 8j..8j+7: t = a_0*b_0 (rounded), then
+    t = fma(a_i, b_i, t) for i = 1..7 (fused, one rounding each); lanes are
+    then combined the way the HIP kernel's DPP steps do: with 16 lanes first
     v_j += v_(15-j) (row mirror), then within each 8 lanes v_j += v_(7-j)
     (half mirror), then v_j += v_(j^1), then v_j += v_(j^2).  Each step adds a
     value to its partner's, so every lane ends with the same sum.
     """
-    D = prod.shape[-1]
+    a, b = np.broadcast_arrays(np.asarray(a, F32), np.asarray(b, F32))
+    D = a.shape[-1]
     nl = D // 8
-    p = prod.reshape(*prod.shape[:-1], nl, 8)
-    t = p[..., 0].copy()
+    pa = a.reshape(*a.shape[:-1], nl, 8)
+    pb = b.reshape(*b.shape[:-1], nl, 8)
+    t = (pa[..., 0] * pb[..., 0]).astype(F32)
     for i in range(1, 8):
-        t = (t + p[..., i]).astype(F32)
+        t = fma32(pa[..., i], pb[..., i], t)
     idx = np.arange(nl)
     partners = []
     if nl == 16:
         partners.append(15 - idx)
     partners += [(idx & ~7) | (7 - (idx & 7)), idx ^ 1, idx ^ 2]
-    for pa in partners:
-        t = (t + t[..., pa]).astype(F32)
+    for pr in partners:
+        t = (t + t[..., pr]).astype(F32)
     return t[..., 0]
 
 
@@ -277,7 +308,7 @@ def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head"):
     """criticality.py:128-163 with this build's fixed fp32 evaluation order.
 
     Per (query head r, page p): t1 = sum_d q_d*mn_d, t2 = sum_d relu(q_d)*scale_d
-    (products rounded, no FMA, order of ``_lane_sum_butterfly``);
+    (per lane an FMA chain, then the butterfly of ``_lane_fma_butterfly``);
     score = t1 + t2*15 (term2 is scaled before the add, criticality.py:161-162).
     mode "per_q_head": (B, H_q, P).
     mode "per_kv_head_sum": (B, H_kv, P), the score of the group's summed query:
@@ -301,8 +332,8 @@ def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head"):
         raise ValueError(mode)
     mn = np.asarray(K_mn, F32)[:, :, None, :, :]
     sc = np.asarray(K_scale, F32)[:, :, None, :, :]
-    t1 = _lane_sum_butterfly((qg * mn).astype(F32))
-    t2 = _lane_sum_butterfly((qpos * sc).astype(F32))
+    t1 = _lane_fma_butterfly(qg, mn)
+    t2 = _lane_fma_butterfly(qpos, sc)
     s = (t1 + (t2 * F32(15.0)).astype(F32)).astype(F32)      # (B, Hkv, rows, P)
     if mode == "per_q_head":
         return s.reshape(B, Hq, P)

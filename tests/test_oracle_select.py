@@ -155,3 +155,88 @@ def test_scores_fixed_per_kv_sum_and_sensitivity():
     no_relu = (Q.reshape(1, 2, 3, 128).astype(np.float64) @ (mn + 15 * sc).transpose(0, 1, 3, 2).astype(np.float64)).reshape(1, 6, 5)
     assert np.abs(ex - no_relu).max() > 1.0
     assert np.allclose(per_q, ex, rtol=1e-4, atol=1e-3)
+
+
+def _rn32_exact(fr):
+    """Round a Fraction to the nearest fp32 (ties to even) with integer arithmetic."""
+    from fractions import Fraction
+    if fr == 0:
+        return np.float32(0.0)
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()   # 2^e ~ a
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    q = max(e - 23, -149)                      # quantum of the fp32 grid at a
+    m = a / Fraction(2) ** q
+    lo = m.numerator // m.denominator
+    rem = m - lo
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and lo % 2 == 1):
+        lo += 1
+    return np.float32(sign * lo * 2.0 ** q)
+
+
+def test_fma32_is_correctly_rounded():
+    # fma32 against exact rational arithmetic: random triples over a wide range of
+    # magnitudes, products with fp16/bf16 operands (the scoring case), and triples
+    # built so that the fp64 sum lands exactly halfway between fp32 neighbours
+    # (where fp64-then-fp32 rounding would round twice)
+    from fractions import Fraction
+    rng = np.random.default_rng(123)
+    a = (rng.standard_normal(4000) * 2.0 ** rng.integers(-20, 20, 4000)).astype(np.float32)
+    b = O.round_f16(rng.standard_normal(4000).astype(np.float32))
+    c = (rng.standard_normal(4000) * 2.0 ** rng.integers(-30, 30, 4000)).astype(np.float32)
+    # ties: products of exactly half an ulp of c (ties go to even)
+    n = 200
+    c3 = np.full(n, 1.0 + 2.0 ** -23, np.float32)
+    a3 = np.full(n, 2.0 ** -24, np.float32)
+    b3 = rng.choice([-1.0, 1.0], n).astype(np.float32)
+    # double-rounding traps: a*b = +-2^-24 (1 - 2^-36) on c = +-(1 + 2^-23); the fp64
+    # sum lands exactly on the fp32 midpoint, the exact sum just short of it
+    a4 = np.array([1.0 + 2.0 ** -18, -(1.0 + 2.0 ** -18)], np.float32)
+    b4 = np.array([2.0 ** -24 * (1.0 - 2.0 ** -18)] * 2, np.float32)
+    c4 = np.array([1.0 + 2.0 ** -23, -(1.0 + 2.0 ** -23)], np.float32)
+    A = np.concatenate([a, a3, a4])
+    B = np.concatenate([b, b3, b4])
+    C = np.concatenate([c, c3, c4])
+    got = O.fma32(A, B, C)
+    for x, y, z, g in zip(A, B, C, got):
+        want = _rn32_exact(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z)))
+        assert g == want, (x, y, z, g, want)
+    # the traps: exact results 1 + 2^-23 (rounding the fp64 sum again would give 1 + 2^-22)
+    assert got[-2] == np.float32(1.0 + 2.0 ** -23) and got[-1] == np.float32(-(1.0 + 2.0 ** -23))
+    naive = (A[-2:].astype(np.float64) * B[-2:] + C[-2:]).astype(np.float32)
+    assert naive[0] == np.float32(1.0 + 2.0 ** -22)          # the trap is real
+
+
+def test_scores_fixed_order_brute_force():
+    # page_scores_fixed restated one lane at a time with scalar exact FMAs
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    Q = rng.standard_normal((1, 2, 128)).astype(np.float32)
+    mn = O.round_f16(rng.standard_normal((1, 1, 3, 128)).astype(np.float32))
+    sc = O.round_f16(np.abs(rng.standard_normal((1, 1, 3, 128))).astype(np.float32))
+    got = O.page_scores_fixed(Q, sc, mn)
+
+    def lane_sums(q, m):
+        t = []
+        for j in range(16):
+            acc = np.float32(q[8 * j] * m[8 * j])
+            for i in range(1, 8):
+                d = 8 * j + i
+                acc = _rn32_exact(Fraction(float(q[d])) * Fraction(float(m[d])) + Fraction(float(acc)))
+            t.append(acc)
+        t = np.array(t, np.float32)
+        idx = np.arange(16)
+        for pa in (15 - idx, (idx & ~7) | (7 - (idx & 7)), idx ^ 1, idx ^ 2):
+            t = (t + t[pa]).astype(np.float32)
+        return t[0]
+    for h in range(2):
+        for p in range(3):
+            q = Q[0, h]
+            t1 = lane_sums(q, mn[0, 0, p])
+            t2 = lane_sums(np.maximum(q, 0).astype(np.float32), sc[0, 0, p])
+            want = np.float32(t1 + np.float32(t2 * np.float32(15.0)))
+            assert got[0, h, p] == want
