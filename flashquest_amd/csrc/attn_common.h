@@ -136,28 +136,55 @@ FQ_DEV void finish_split(SplitLds<D, NREP>& s, float (&m)[NREP], float (&lsum)[N
 // Split merge (the rule of _merge_two_attentions, llama_persistent_patch.py:50-61,
 // in the log2 domain): one workgroup per KV group over its used splits.
 // pps > 0: group g used ceil(n_sel / pps) splits; pps == 0: all `splits` were used.
+// Two parallel phases instead of a serial walk over the splits: wave r reduces
+// head r's (m, l) over the splits into per-split weights in LDS (its lanes
+// stride over the splits), then every output element sums its splits'
+// weighted partials with the loads issued 8 at a time.  Per split the weight is
+// exp2(m_s - M) with M the maximum over the splits (0 for an empty split).
+constexpr int kMergeMaxSplits = 2048;
+
 template <int D, int NREP, bool ROT>
 __global__ __launch_bounds__(kThreads) void merge_splits_kernel(QueryArgs q, Workspace ws, int Hkv, int B,
                                                                 int pps, int splits) {
     __shared__ float s_out[NREP][D];
     __shared__ float s_L[NREP], s_M[NREP];
+    __shared__ float s_w[NREP][kMergeMaxSplits];
     const int g = blockIdx.x;
     const int h = g % Hkv, b = (g / Hkv) % B, l = g / (Hkv * B);
-    const int used = pps > 0 ? (ws.n_sel[g] + pps - 1) / pps : splits;
+    const int used = min(pps > 0 ? (ws.n_sel[g] + pps - 1) / pps : splits, kMergeMaxSplits);
     const int64_t base = (int64_t)g * ws.s_max * NREP;
+    const int lane = lane_id(), w = wave_id();
+    for (int r = w; r < NREP; r += kThreads / 64) {
+        float M = -INFINITY;
+        for (int sp = lane; sp < used; sp += 64) M = fmaxf(M, ws.part_ml[(base + (int64_t)sp * NREP + r) * 2]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        float Lsum = 0.f;
+        for (int sp = lane; sp < used; sp += 64) {
+            const int64_t pr = base + (int64_t)sp * NREP + r;
+            const float m = ws.part_ml[pr * 2];
+            const float wt = m == -INFINITY ? 0.f : exp2_fast(m - M);
+            s_w[r][sp] = wt;
+            Lsum += wt * ws.part_ml[pr * 2 + 1];
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) Lsum += __shfl_xor(Lsum, off, 64);
+        if (lane == 0) { s_L[r] = Lsum; s_M[r] = M; }
+    }
+    __syncthreads();
     for (int i = threadIdx.x; i < NREP * D; i += kThreads) {
         const int r = i / D, d = i % D;
-        float M = -INFINITY, L = 0.f, A = 0.f;
-        for (int sp = 0; sp < used; ++sp) {
-            const int64_t pr = base + (int64_t)sp * NREP + r;
-            float Mn, w_s, w_o;
-            merge_weights(M, ws.part_ml[pr * 2], Mn, w_s, w_o);
-            L = L * w_s + ws.part_ml[pr * 2 + 1] * w_o;
-            A = A * w_s + ws.part_acc[pr * D + d] * w_o;
-            M = Mn;
+        float A = 0.f;
+        int sp = 0;
+        for (; sp + 8 <= used; sp += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ws.part_acc[(base + (int64_t)(sp + u) * NREP + r) * D + d];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) A = fmaf(s_w[r][sp + u], v[u], A);
         }
-        s_out[r][d] = L > 0.f ? A / L : 0.f;
-        if (d == 0) { s_L[r] = L; s_M[r] = M; }
+        for (; sp < used; ++sp) A = fmaf(s_w[r][sp], ws.part_acc[(base + (int64_t)sp * NREP + r) * D + d], A);
+        s_out[r][d] = s_L[r] > 0.f ? A / s_L[r] : 0.f;
     }
     __syncthreads();
     store_outputs<D, NREP, ROT>(q, l, b, h, s_out, s_L, s_M);

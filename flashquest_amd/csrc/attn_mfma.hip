@@ -45,7 +45,7 @@ struct MfmaParams {
     QueryArgs q;
     Workspace ws;
     int splits;
-    SelectArgs sel;         // sel.enabled: the workgroup scores and selects its group's pages (splits == 1)
+    SelectArgs sel;         // sel.enabled: every workgroup scores and selects its group's pages itself
 };
 
 // A operands of one wave: [k-step][row][k-group, XOR-swizzled][16 bytes].
@@ -128,7 +128,8 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
 
 // NW waves per workgroup (4, or 8 when one workgroup takes a whole KV group).
 // FUSED (8 waves only): the workgroup scores and selects its group's pages
-// itself (a.sel); otherwise the pages come from the workspace lists.
+// itself (a.sel) and attends split `split` of the list; otherwise the pages
+// come from the workspace lists.
 template <typename MT, int G, int NREP, int NW, bool FUSED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int4_mfma_kernel(MfmaParams a) {
@@ -227,7 +228,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     PageBuf b0, b1;
     bool first_issued = false;       // b0 already holds this wave's first page
 
-    int e0, e1;
+    int e0, e1, ent_base = 0;          // this split's entries are s_ent[ent_base ..]
     if constexpr (FUSED) {
         // Fused decode: score every page of the group from its K metadata
         // (the arithmetic of score_kernel), keep the scores in LDS, select.
@@ -250,13 +251,18 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
             else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
             const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
-            if (S > 0 && w < fp.count) {
+            if (S > 0 && split == 0 && w < fp.count) {       // split 0's first entries are the forced pages
                 issue_page(b0, fp.page(w));
                 first_issued = true;
             }
             __syncthreads();
-            e1 = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
-                                                     a.sel.window, s_ent, s_bsel);
+            // every split of the group selects the same list; split s takes
+            // the balanced slice [e0, e1) of it
+            const int total = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max,
+                                                                  a.sel.num_sinks, a.sel.window, s_ent, s_bsel);
+            e0 = (int)((int64_t)total * split / a.splits);
+            e1 = (int)((int64_t)total * (split + 1) / a.splits);
+            ent_base = e0;
         }
     } else {
         const int n_sel = a.ws.n_sel[g];
@@ -284,7 +290,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 
     // k: this wave's k-th page (entry w + NW * k); callers clamp k to the last
     // page, so every step issues the same loads and the waits match on every path
-    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
+    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[ent_base + w + NW * k]); };
     auto issue = [&](PageBuf& bf, int k) { issue_page(bf, entry_of(k) & 0xFFFF); };
 
     // running references (wave-uniform) and accumulators.  With fp16 metadata
@@ -593,6 +599,17 @@ MfmaSplit mfma_splits(int groups, int max_entries, int s_max, int request) {
     return {std::min(s, s_max), 4};
 }
 
+// The fused decode: one workgroup of 8 waves per KV group when the groups
+// fill the GPU; otherwise every group is split over enough workgroups for one
+// per CU, each scoring and selecting the group's pages itself (the same list
+// in every split) and attending a balanced slice of it, at least 8 pages.
+int fused_splits(int groups, int max_entries, int s_max) {
+    if (groups >= 192) return 1;
+    int s = (256 + groups - 1) / std::max(groups, 1);
+    s = std::min(s, (max_entries + 7) / 8);
+    return std::max(1, std::min(s, s_max));
+}
+
 }  // namespace
 
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
@@ -614,9 +631,8 @@ bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al
 }
 
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
-    if (!mfma_supported(c, q, al) || c.P > 64 * kSelC) return false;
-    const MfmaSplit sp = mfma_splits(c.L * c.B * c.Hkv, al.max_entries, al.s_max, attention_splits_request());
-    return sp.splits == 1 && sp.waves == 8;
+    return mfma_supported(c, q, al) && c.P <= 64 * kSelC && al.max_entries <= kMaxWgPages &&
+           attention_splits_request() <= 0;
 }
 
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
@@ -629,6 +645,7 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
     if (sel && sel->enabled) {
         if (!mfma_select_in_kernel(c, q, al)) return hipErrorInvalidValue;
         a.sel = *sel;
+        a.splits = fused_splits(groups, al.max_entries, al.s_max);
     }
     dim3 grid(a.splits, groups);
 #define FQ_W(MT_, G_)                                                                       \
