@@ -331,8 +331,38 @@ def main():
         torch.cuda.synchronize()
         pl_ms, _, _ = time_steps(noop, graph.replay, args.steps, args.warmup, flush)
         extra["per_layer_graph_us"] = pl_ms * 1e3
+        # the same, with a 37-token bf16 partial page per layer (the usual decode
+        # step): the tail is attended in the split-merge launch
+        T_tail = 37
+        kt = torch.randn(L, B, 8, T_tail, 128, device=dev).bfloat16()
+        vt = torch.randn(L, B, 8, T_tail, 128, device=dev).bfloat16()
+        tdec = QuestDecoder(cache["Q"], cache["K_packed"], cache["K_scale"], cache["K_mn"], cache["V_packed"],
+                            cache["V_scale"], cache["V_mn"], retention=args.retention, num_sinks=4, window_pages=2,
+                            k_max_static=k, select_mode=args.select, K_tail=kt, V_tail=vt)
+        tt_ms, _, _ = time_steps(noop, tdec, args.steps, args.warmup, flush)
+        extra["step_with_tail_us"] = tt_ms * 1e3
+        per_layer_t = [QuestDecoder(*[cache[key][l] for key in ("Q", "K_packed", "K_scale", "K_mn", "V_packed",
+                                                                "V_scale", "V_mn")], retention=args.retention,
+                                    num_sinks=4, window_pages=2, k_max_static=k, select_mode=args.select,
+                                    K_tail=kt[l], V_tail=vt[l]) for l in range(L)]
+        for d in per_layer_t:
+            d()
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(torch.cuda.current_stream())
+        graph_t = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s2):
+            for d in per_layer_t:
+                d()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph_t, stream=s2):
+                for d in per_layer_t:
+                    d()
+        torch.cuda.synchronize()
+        plt_ms, _, _ = time_steps(noop, graph_t.replay, args.steps, args.warmup, flush)
+        extra["per_layer_graph_with_tail_us"] = plt_ms * 1e3
+        del kt, vt, tdec, per_layer_t, graph_t
         sel_ms, _, _ = time_steps(noop, dec.select, args.steps, args.warmup, flush)
-        extra["select_us"] = sel_ms * 1e3
+        extra["select_us"] = sel_ms * 1e3 if not dec.fused else None
         wflush = Flusher(dev, write=True)
         wf_ms, _, _ = time_steps(noop, dec, args.steps, args.warmup, wflush)
         extra["step_us_after_write_flush"] = wf_ms * 1e3

@@ -51,6 +51,14 @@ class Query(ctypes.Structure):
     ]
 
 
+class Tail(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p), ("k_strides", _I64x5),
+        ("v", ctypes.c_void_p), ("v_strides", _I64x5),
+        ("dtype", ctypes.c_int32), ("len", ctypes.c_int32), ("D", ctypes.c_int32),
+    ]
+
+
 class TurboCache(ctypes.Structure):
     _fields_ = [
         ("k_msb", ctypes.c_void_p), ("kmsb_strides", _I64x5),
@@ -94,6 +102,8 @@ SIGNATURES = {
                                             _P, _I64P, _I, _I, _P]),
     "fq_quest_decode_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, ctypes.POINTER(Query),
                                              _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quest_decode_int4_tail": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), ctypes.POINTER(Tail),
+                                                 _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "fq_quest_fused_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
     "fq_quest_attend_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, ctypes.c_size_t, _P]),

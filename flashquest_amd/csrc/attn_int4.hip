@@ -190,7 +190,7 @@ hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
         timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                               \
             hipLaunchKernelGGL((merge_splits_kernel<D, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, a.pps, a.splits);                                       \
+                               a.q, a.ws, a.c.Hkv, a.c.B, a.pps, a.splits, TailArgs{});                                       \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4) FQ_CASE(8)
 #undef FQ_CASE
@@ -213,9 +213,9 @@ bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLa
 }
 
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel) {
-    if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st, sel);
-    if (sel && sel->enabled) return hipErrorInvalidValue;
+                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel, const TailArgs* tail) {
+    if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st, sel, tail);
+    if ((sel && sel->enabled) || (tail && tail->len > 0)) return hipErrorInvalidValue;
     AttnParams a{};
     a.c = c; a.q = q; a.ws = ws; a.pps = al.pages_per_split; a.splits = al.splits;
     dim3 grid(al.splits, c.L * c.B * c.Hkv);

@@ -46,6 +46,7 @@ struct MfmaParams {
     Workspace ws;
     int splits;
     SelectArgs sel;         // sel.enabled: every workgroup scores and selects its group's pages itself
+    TailArgs tail;          // tail.len > 0: the split merge also attends the partial-page tail
 };
 
 // A operands of one wave: [k-step][row][k-group, XOR-swizzled][16 bytes].
@@ -561,7 +562,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         }
     }
     __syncthreads();
-    merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits);
+    merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits > 1 || a.tail.len > 0);
 }
 
 template <typename MT, int G, int NW, bool FUSED>
@@ -572,9 +573,9 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
         timer_before_launch(st);                                                                       \
         hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
         timer_after_launch(st);                                                                        \
-        if (a.splits > 1)                                                                              \
+        if (a.splits > 1 || a.tail.len > 0)                                                            \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits);                                \
+                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits, a.tail);                           \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE
@@ -636,9 +637,10 @@ bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLau
 }
 
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
-                                 hipStream_t st, const SelectArgs* sel) {
+                                 hipStream_t st, const SelectArgs* sel, const TailArgs* tail) {
     MfmaParams a{};
     a.c = c; a.q = q; a.ws = ws;
+    if (tail) a.tail = *tail;
     const int groups = c.L * c.B * c.Hkv;
     const MfmaSplit sp = mfma_splits(groups, al.max_entries, al.s_max, attention_splits_request());
     a.splits = sp.splits;

@@ -379,9 +379,9 @@ int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, cons
                       "score+select");
 }
 
-int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
-                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
-                         void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const float* retention, int32_t num_sinks,
+                        int32_t window_pages, int32_t k_max, int32_t select_mode, const TailArgs* tail,
+                        void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
@@ -393,12 +393,42 @@ int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, cons
     if (k_max > c.P) k_max = c.P;
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
+    if (tail && tail->len > 0 && !mfma_supported(c, q, al))
+        return fail(FQ_ERR_UNSUPPORTED, "the fused tail needs the matrix-core attention layout");
     SelectArgs sel{};
     if (attn_selects_in_kernel(c, q, al)) {
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
     }
-    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel), "sparse int4 attention");
+    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail), "sparse int4 attention");
+}
+
+int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr, workspace,
+                        workspace_bytes_, stream);
+}
+
+int fq_quest_decode_int4_tail(const fq_int4_cache* cache, const fq_query* query, const fq_tail* tail,
+                              const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                              int32_t select_mode, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+    TailArgs t{};
+    if (tail && tail->len > 0) {
+        if (tail->len > kTailMax) return fail(FQ_ERR_UNSUPPORTED, "tail of %d tokens (at most %d)", tail->len, kTailMax);
+        if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
+        if (!is_float_dtype(tail->dtype)) return fail(FQ_ERR_INVALID, "tail dtype");
+        if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
+            return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
+        t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
+        for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
+        if (cache && cache->D != tail->D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, cache->D);
+    }
+    int st = fq_quest_select_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr,
+                                  nullptr, workspace, workspace_bytes_, stream);
+    if (st) return st;
+    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, t.len > 0 ? &t : nullptr,
+                        workspace, workspace_bytes_, stream);
 }
 
 int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,

@@ -183,6 +183,17 @@ struct QueryArgs {
 };
 
 // Workspace regions (device pointers) for one decode / attention call.
+// Dense attention over the partial-page tail (bf16 / fp16 / fp32 K and V,
+// (l, b, h, t) element strides, channels contiguous), folded into the split
+// merge.  len == 0: no tail.
+constexpr int kTailMax = 64;
+struct TailArgs {
+    const void* k; int64_t ks[4];
+    const void* v; int64_t vs[4];
+    int dtype, len;
+    int in_kernel;      // the fused decode kernel attends the tail (2-byte dtype, 16-byte aligned rows)
+};
+
 struct Workspace {
     int* n_sel;           // [G]   union-list length
     int* entries;         // [G][P] page | qmask << 16, ascending page order
@@ -239,7 +250,8 @@ hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bu
 // sel (may be null): the kernel scores and selects the pages itself; only valid
 // when attn_selects_in_kernel() says so for the same arguments.
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel = nullptr);
+                            const AttnLaunch& al, hipStream_t st, const SelectArgs* sel = nullptr,
+                            const TailArgs* tail = nullptr);
 // Page-tile INT4 quantisers (cache.hip): eligibility of a layout, whole-tensor
 // quantisation, and the cache append of update_quantized.
 bool page_quant_k_ok(int D, int page, int in_dtype, const void* k, const int64_t* k_s, const uint8_t* packed,
@@ -264,6 +276,7 @@ bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLa
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
-                                 const AttnLaunch& al, hipStream_t st, const SelectArgs* sel);
+                                 const AttnLaunch& al, hipStream_t st, const SelectArgs* sel,
+                                 const TailArgs* tail = nullptr);
 
 }  // namespace fq

@@ -299,7 +299,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         }
     }
     __syncthreads();
-    merge_waves_and_store<D, NREP, true, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits);
+    merge_waves_and_store<D, NREP, true, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits > 1);
 }
 
 template <bool FUSED>
@@ -312,7 +312,7 @@ hipError_t launch_turbo_fused_nrep(const TurboFusedParams& a, dim3 grid, hipStre
         timer_after_launch(st);                                                                             \
         if (a.splits > 1)                                                                                   \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, true>), dim3(grid.y), dim3(kThreads), 0, st, a.q, \
-                               a.ws, a.c.H_kv, a.c.B, 0, a.splits);                                         \
+                               a.ws, a.c.H_kv, a.c.B, 0, a.splits, TailArgs{});                                         \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE

@@ -70,6 +70,8 @@ def quest_decode_int4(
     return_lse: bool = True,
     return_selection: bool = False,
     out: torch.Tensor | None = None,
+    K_tail: torch.Tensor | None = None,
+    V_tail: torch.Tensor | None = None,
 ):
     """Fused score -> select -> sparse attention over completed pages.
 
@@ -78,6 +80,10 @@ def quest_decode_int4(
     ``select_mode`` "per_q_head" is the reference's selection
     (selection.py:103-117); "per_kv_head_sum" selects once per KV head from
     the fp32 sum of its query heads' scores.
+    ``K_tail`` / ``V_tail`` (..., H_kv, T, D), T <= 64: the partial page,
+    attended with the selected pages (llama_persistent_patch.py:229-240); O and
+    lse are then those of the merged attention.  Raises NotImplementedError for
+    shapes the fused tail does not take (``sparse_decode_layer`` falls back).
     Returns (O like Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
     """
     if select_mode not in L.SELECT_MODES:
@@ -104,11 +110,29 @@ def quest_decode_int4(
     if return_selection:
         mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
     ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q))
-    L.check(L.lib().fq_quest_decode_int4(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
-                                         L.SELECT_MODES[select_mode], None,
-                                         None if mask is None else mask.data_ptr(),
-                                         ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
-            "quest_decode_int4")
+    tail = None
+    if K_tail is not None and K_tail.shape[-2] > 0:
+        if return_selection:
+            raise ValueError("return_selection is not available together with a fused tail")
+        L.require_device(K_tail, V_tail)
+        if K_tail.shape != V_tail.shape or K_tail.dtype != V_tail.dtype or K_tail.shape[-1] != D:
+            raise AssertionError("K_tail / V_tail must share shape (..., H_kv, T, D) and dtype")
+        kt = K_tail if K_tail.stride(-1) == 1 else K_tail.contiguous()
+        vt = V_tail if V_tail.stride(-1) == 1 else V_tail.contiguous()
+        lead = 5 - kt.dim()
+        tail = L.Tail(kt.data_ptr(), L.strides(kt, 5, lead), vt.data_ptr(), L.strides(vt, 5, lead),
+                      L.dtype_code(kt.dtype), kt.shape[-2], D)
+    if tail is not None:
+        L.check(L.lib().fq_quest_decode_int4_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
+                                                  int(window_pages), k_max, L.SELECT_MODES[select_mode],
+                                                  ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                "quest_decode_int4 (tail)")
+    else:
+        L.check(L.lib().fq_quest_decode_int4(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
+                                             L.SELECT_MODES[select_mode], None,
+                                             None if mask is None else mask.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                "quest_decode_int4")
     O = O3.unsqueeze(-2)
     lse_out = lse.unsqueeze(-1) if lse is not None else None
     if return_selection:
@@ -198,7 +222,7 @@ class QuestDecoder:
 
     def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
                  window_pages=2, k_max_static=None, page_size=64, select_mode="per_q_head", sm_scale=None,
-                 out=None, lse=None, mask_out=None):
+                 out=None, lse=None, mask_out=None, K_tail=None, V_tail=None):
         if select_mode not in L.SELECT_MODES:
             raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
         self.Q3 = Q[..., 0, :]
@@ -215,6 +239,13 @@ class QuestDecoder:
         self.mask_out = mask_out
         self.device = Q.device
         self.ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(self.cache, H_q))
+        self.tail = None
+        if K_tail is not None and K_tail.shape[-2] > 0:
+            lead = 5 - K_tail.dim()
+            self._tail_keep = (K_tail, V_tail)
+            self.tail = L.Tail(K_tail.data_ptr(), L.strides(K_tail, 5, lead), V_tail.data_ptr(),
+                               L.strides(V_tail, 5, lead), L.dtype_code(K_tail.dtype), K_tail.shape[-2],
+                               K_tail.shape[-1])
 
     @property
     def fused(self) -> bool:
@@ -231,12 +262,19 @@ class QuestDecoder:
                                              self.ws.numel(), L.stream_handle(self.device)), "quest select")
 
     def attend(self):
+        if self.tail is not None:      # selection (when a kernel does it), attention, tail and merge
+            L.check(L.lib().fq_quest_decode_int4_tail(self.cache, self.query, self.tail, self.r.data_ptr(),
+                                                      self.sinks, self.window, self.k_max, self.mode,
+                                                      self.ws.data_ptr(), self.ws.numel(),
+                                                      L.stream_handle(self.device)), "quest attend (tail)")
+            return
         L.check(L.lib().fq_quest_attend_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
                                              self.k_max, self.mode, self.ws.data_ptr(), self.ws.numel(),
                                              L.stream_handle(self.device)), "quest attend")
 
     def __call__(self):
-        self.select()
+        if self.tail is None:
+            self.select()
         self.attend()
         return self.O3.unsqueeze(-2)
 
@@ -253,10 +291,18 @@ def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: i
     if completed == 0:
         o, _ = bf16_dense_attn_with_lse(q, views["K_partial"], views["V_partial"])
         return o.to(q.dtype)
-    o_sparse, lse_sparse = quest_decode_int4(
-        q, views["K_packed"], views["K_scale"], views["K_mn"], views["V_packed"], views["V_scale"],
-        views["V_mn"], retention=retention, num_sinks=num_sinks, window_pages=window_pages,
-        k_max_static=k_max_static, page_size=page_size, select_mode=select_mode)
+    args = (q, views["K_packed"], views["K_scale"], views["K_mn"], views["V_packed"], views["V_scale"],
+            views["V_mn"])
+    kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
+              page_size=page_size, select_mode=select_mode)
+    if partial > 0:
+        try:
+            # one fused call: the tail is attended in the split-merge launch
+            o, _ = quest_decode_int4(*args, K_tail=views["K_partial"], V_tail=views["V_partial"], **kw)
+            return o
+        except NotImplementedError:
+            pass                              # layouts the fused tail does not take: three operators
+    o_sparse, lse_sparse = quest_decode_int4(*args, **kw)
     if partial == 0:
         return o_sparse
     o_tail, lse_tail = bf16_dense_attn_with_lse(q.to(views["K_partial"].dtype), views["K_partial"],

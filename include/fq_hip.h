@@ -93,6 +93,15 @@ typedef struct fq_turbo_cache {
     int32_t L, B, H_kv, S, P, D, page_size;
 } fq_turbo_cache;
 
+/* The partial-page tail of one decode step (PersistentInt4KVCache.K_partial /
+ * V_partial views, persistent_int4.py:56-57): K and V (L, B, H_kv, T, D) with
+ * T = len <= 64 tokens, any float dtype (bf16 in the reference). */
+typedef struct fq_tail {
+    const void* k; int64_t k_strides[5];
+    const void* v; int64_t v_strides[5];
+    int32_t dtype, len, D;
+} fq_tail;
+
 const char* fq_last_error(void);
 int fq_abi_version(void);
 
@@ -200,6 +209,21 @@ int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer,
                          const void* k_new, const int64_t kn_strides[4],
                          const void* v_new, const int64_t vn_strides[4],
                          int32_t seen, int32_t S_new, fq_stream_t stream);
+
+/* The whole decode branch of the reference's attention patch for a step with
+ * a partial page (llama_persistent_patch.py:202-240): score, select and
+ * attend the completed pages, attend the tail densely
+ * (_bf16_dense_attn_with_lse, 30-47, sm_scale of the query) and merge
+ * (_merge_two_attentions, 50-61) -- as softmax attention over the selected
+ * pages and the tail together, the tail attended inside the split-merge
+ * launch.  O and lse (if given) are those of the merged attention.  A NULL or
+ * empty tail is fq_quest_decode_int4 without scores_out / mask_out.
+ * FQ_ERR_UNSUPPORTED for shapes the matrix-core attention kernel does not take
+ * (the caller then runs the three operators). */
+int fq_quest_decode_int4_tail(const fq_int4_cache* cache, const fq_query* query, const fq_tail* tail,
+                              const float* retention, int32_t num_sinks, int32_t window_pages,
+                              int32_t k_max, int32_t select_mode,
+                              void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
 /* Whether fq_quest_attend_int4 scores and selects the pages inside its one
  * attention kernel for these arguments (1; fq_quest_select_int4 then launches

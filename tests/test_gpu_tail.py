@@ -1,0 +1,80 @@
+"""The decode step with a partial page (llama_persistent_patch.py:202-240): the
+fused entry attends the selected pages and the bf16 tail together (the tail in
+the split-merge launch); the result must match the oracle's sparse attention
+merged with the dense tail attention (_merge_two_attentions, fp64 here) for
+many layers at once (one workgroup per KV group) and for one layer (split
+groups), tails of 1..64 tokens in bf16 and fp16, and an empty selection
+(the tail alone)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fq_oracle as O
+from tests.cases import Int4Case, max_err, to_dev_half
+
+pytestmark = pytest.mark.gpu
+
+
+def _merged_ref(case, Kt, Vt, retention, sinks, window, mode):
+    ref = O.decode_step(case.Q, case.kp, case.ks, case.km, case.vp, case.vs, case.vm, retention=retention,
+                        num_sinks=sinks, window_pages=window, mode=mode, k_max_static=None)
+    ot, lt = O.dense_attn_with_lse(case.Q, Kt, Vt)
+    o = O.merge_two_attentions(ref["O"], ref["lse"], ot, lt)
+    m = np.maximum(ref["lse"], lt)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        lse = m + np.log(np.exp(ref["lse"] - m) + np.exp(lt - m))
+    return o, lse
+
+
+@pytest.mark.parametrize("layers,T,tdt,mode", [(24, 37, "bf16", "per_kv_head_sum"), (24, 64, "f16", "per_q_head"),
+                                               (1, 1, "bf16", "per_q_head"), (1, 63, "bf16", "per_kv_head_sum")])
+def test_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode):
+    from flashquest_amd.eager import quest_decode_int4
+    rng = np.random.default_rng(40 + T)
+    Hq, Hkv, P = 24, 8, 14
+    cases = [Int4Case(seed=500 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, page=64, dtype="bf16", meta="f16",
+                      vgroup=32) for i in range(layers)]
+    tails = [(O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32)),
+              O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32))) for _ in range(layers)]
+    dev = [c.device() for c in cases]
+    if layers > 1:
+        stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+        q = torch.stack([c.q_dev() for c in cases])
+        kt = torch.stack([to_dev_half(t[0], tdt) for t in tails])
+        vt = torch.stack([to_dev_half(t[1], tdt) for t in tails])
+    else:
+        stacked, q = dev[0], cases[0].q_dev()
+        kt, vt = to_dev_half(tails[0][0], tdt), to_dev_half(tails[0][1], tdt)
+    o, lse = quest_decode_int4(q, **stacked, retention=0.3, num_sinks=2, window_pages=1, select_mode=mode,
+                               K_tail=kt, V_tail=vt)
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        ro, rl = _merged_ref(c, tails[i][0], tails[i][1], 0.3, 2, 1, mode)
+        oi = o[i] if layers > 1 else o
+        li = lse[i] if layers > 1 else lse
+        assert max_err(oi[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max(), i
+        assert max_err(li[:, :, 0], rl) <= 1e-4, i
+
+
+def test_fused_tail_with_empty_selection_is_tail_attention():
+    from flashquest_amd.eager import quest_decode_int4
+    rng = np.random.default_rng(3)
+    c = Int4Case(seed=9, B=1, Hq=6, Hkv=2, S=64 * 5, D=128, page=64, dtype="bf16", meta="bf16")
+    Kt = O.round_bf16(rng.standard_normal((1, 2, 20, 128)).astype(np.float32))
+    Vt = O.round_bf16(rng.standard_normal((1, 2, 20, 128)).astype(np.float32))
+    o, lse = quest_decode_int4(c.q_dev(), **c.device(), retention=0.0, num_sinks=0, window_pages=0,
+                               K_tail=to_dev_half(Kt, "bf16"), V_tail=to_dev_half(Vt, "bf16"))
+    ro, rl = O.dense_attn_with_lse(c.Q, Kt, Vt)
+    assert max_err(o[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max()
+    assert max_err(lse[:, :, 0], rl) <= 1e-4
+
+
+def test_fused_tail_rejects_long_tails_and_selection_output():
+    from flashquest_amd.eager import quest_decode_int4
+    c = Int4Case(seed=1, B=1, Hq=6, Hkv=2, S=64 * 3, D=128, page=64, dtype="bf16", meta="bf16")
+    kt = torch.zeros(1, 2, 65, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(NotImplementedError):
+        quest_decode_int4(c.q_dev(), **c.device(), retention=0.5, K_tail=kt, V_tail=kt)
+    with pytest.raises(ValueError):
+        quest_decode_int4(c.q_dev(), **c.device(), retention=0.5, K_tail=kt[:, :, :3], V_tail=kt[:, :, :3],
+                          return_selection=True)
