@@ -46,7 +46,7 @@ struct MfmaParams {
     Workspace ws;
     int splits;
     SelectArgs sel;         // sel.enabled: every workgroup scores and selects its group's pages itself
-    TailArgs tail;          // tail.len > 0: the split merge also attends the partial-page tail
+    TailArgs tail;          // tail.len > 0: the tail is attended (in_kernel: by the fused kernel, else the split merge)
 };
 
 // A operands of one wave: [k-step][row][k-group, XOR-swizzled][16 bytes].
@@ -137,7 +137,9 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     static_assert(!FUSED || NW == 8, "in-kernel selection runs in the 8-wave kernel");
     constexpr int D = 128;
     constexpr int NT = 64 * NW;
-    __shared__ SplitLds<D, NREP, NW> s_split;
+    constexpr int NSLOT = FUSED ? NW + 1 : NW;      // the fused kernel's extra slot: the partial-page tail
+    constexpr int TTOK = FUSED ? kTailMax : 1;
+    __shared__ SplitLds<D, NREP, NSLOT> s_split;
     __shared__ WaveLds s_wave[NW];
     __shared__ int s_ent[kMaxWgPages];
 
@@ -185,8 +187,26 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // retention of query head L of the group (lanes past NREP repeat the last)
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
+    // Partial-page tail (fused kernel, tail.in_kernel): its <= 64 raw 16-bit
+    // K / V rows go to LDS with q, before scoring needs the metadata.  The
+    // loads are unconditional: without a tail the buffer is empty and they read 0.
+    __shared__ uint16_t s_tk[TTOK][D], s_tv[TTOK][D];
+    __shared__ float s_tp[NREP][TTOK];
+    uint4 tkr[2], tvr[2];
+    const int tail_T = FUSED && a.tail.in_kernel ? a.tail.len : 0;
     if constexpr (FUSED) {
         ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
+        const TailArgs& t = a.tail;
+        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + h * t.ks[2]) : nullptr;
+        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + h * t.vs[2]) : nullptr;
+        const auto rk = make_rsrc(tkb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.ks[3] + 2 * D : 0);
+        const auto rv = make_rsrc(tvb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.vs[3] + 2 * D : 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + NT * u, tt = i >> 4, j = i & 15;       // token tt, bytes 16j .. 16j+15
+            tkr[u] = ld128(rk, (int)(2 * tt * t.ks[3]) + 16 * j);
+            tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
+        }
         score_group_load<MT, NT>(sr, c, tid, l, b, h);
     }
     const bool qbf = q.q_dtype == FQ_BF16;
@@ -247,6 +267,12 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             if (tid + NT < NREP * D) {
                 s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
                 s_qraw[i1 >> 7][i1 & 127] = v1;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int i = tid + NT * u;
+                *(uint4*)&s_tk[i >> 4][8 * (i & 15)] = tkr[u];
+                *(uint4*)&s_tv[i >> 4][8 * (i & 15)] = tvr[u];
             }
             __syncthreads();
             if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
@@ -561,8 +587,17 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             if (n16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = ll; }
         }
     }
+    int nslots = NW;
+    if constexpr (FUSED) {
+        if (tail_T > 0) {       // uniform; the tail state is the merge's last slot
+            tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
+                                        s_split.l[NW], s_split.acc[NW]);
+            nslots = NW + 1;
+        }
+    }
     __syncthreads();
-    merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits > 1 || a.tail.len > 0);
+    merge_waves_and_store<D, NREP, false, NSLOT, NT>(s_split, q, a.ws, g, l, b, h, split,
+                                                     a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel), nslots);
 }
 
 template <typename MT, int G, int NW, bool FUSED>
@@ -573,7 +608,7 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
         timer_before_launch(st);                                                                       \
         hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
         timer_after_launch(st);                                                                        \
-        if (a.splits > 1 || a.tail.len > 0)                                                            \
+        if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                     \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
                                a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits, a.tail);                           \
         break;
@@ -648,6 +683,14 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
         if (!mfma_select_in_kernel(c, q, al)) return hipErrorInvalidValue;
         a.sel = *sel;
         a.splits = fused_splits(groups, al.max_entries, al.s_max);
+        // one workgroup per group: the kernel attends a 16-bit tail itself
+        // (16-byte aligned rows, at least D apart), so no merge launch follows
+        const TailArgs& t = a.tail;
+        const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
+        auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
+        a.tail.in_kernel = a.splits == 1 && t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 &&
+                           t.vs[3] >= 128 && ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
+                           2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
     }
     dim3 grid(a.splits, groups);
 #define FQ_W(MT_, G_)                                                                       \

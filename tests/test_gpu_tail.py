@@ -2,9 +2,10 @@
 fused entry attends the selected pages and the bf16 tail together (the tail in
 the split-merge launch); the result must match the oracle's sparse attention
 merged with the dense tail attention (_merge_two_attentions, fp64 here) for
-many layers at once (one workgroup per KV group) and for one layer (split
-groups), tails of 1..64 tokens in bf16 and fp16, and an empty selection
-(the tail alone)."""
+many layers at once (one workgroup per KV group: the fused kernel attends a
+16-bit tail itself; fp32 and padded-row tails) and for one layer (split
+groups, the tail in the split merge), tails of 1..64 tokens in bf16, fp16 and
+fp32, and an empty selection (the tail alone)."""
 import numpy as np
 import pytest
 import torch
@@ -13,6 +14,10 @@ from oracle import fq_oracle as O
 from tests.cases import Int4Case, max_err, to_dev_half
 
 pytestmark = pytest.mark.gpu
+
+
+def _dev(x, tdt):
+    return torch.from_numpy(x).cuda() if tdt == "f32" else to_dev_half(x, tdt)
 
 
 def _merged_ref(case, Kt, Vt, retention, sinks, window, mode):
@@ -26,9 +31,14 @@ def _merged_ref(case, Kt, Vt, retention, sinks, window, mode):
     return o, lse
 
 
-@pytest.mark.parametrize("layers,T,tdt,mode", [(24, 37, "bf16", "per_kv_head_sum"), (24, 64, "f16", "per_q_head"),
-                                               (1, 1, "bf16", "per_q_head"), (1, 63, "bf16", "per_kv_head_sum")])
-def test_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode):
+@pytest.mark.parametrize("layers,T,tdt,mode,pad", [(24, 37, "bf16", "per_kv_head_sum", 0),
+                                                   (24, 64, "f16", "per_q_head", 0),
+                                                   (24, 5, "bf16", "per_q_head", 8),
+                                                   (24, 64, "bf16", "per_kv_head_sum", 24),
+                                                   (24, 33, "f32", "per_q_head", 0),
+                                                   (1, 1, "bf16", "per_q_head", 0),
+                                                   (1, 63, "bf16", "per_kv_head_sum", 0)])
+def test_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode, pad):
     from flashquest_amd.eager import quest_decode_int4
     rng = np.random.default_rng(40 + T)
     Hq, Hkv, P = 24, 8, 14
@@ -40,11 +50,17 @@ def test_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode):
     if layers > 1:
         stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
         q = torch.stack([c.q_dev() for c in cases])
-        kt = torch.stack([to_dev_half(t[0], tdt) for t in tails])
-        vt = torch.stack([to_dev_half(t[1], tdt) for t in tails])
+        kt = torch.stack([_dev(t[0], tdt) for t in tails])
+        vt = torch.stack([_dev(t[1], tdt) for t in tails])
+        if pad:      # rows `pad` elements apart beyond D: views into wider buffers
+            kw = torch.zeros(*kt.shape[:-1], 128 + pad, dtype=kt.dtype, device=kt.device)
+            vw = torch.zeros_like(kw)
+            kw[..., :128] = kt
+            vw[..., :128] = vt
+            kt, vt = kw[..., :128], vw[..., :128]
     else:
         stacked, q = dev[0], cases[0].q_dev()
-        kt, vt = to_dev_half(tails[0][0], tdt), to_dev_half(tails[0][1], tdt)
+        kt, vt = _dev(tails[0][0], tdt), _dev(tails[0][1], tdt)
     o, lse = quest_decode_int4(q, **stacked, retention=0.3, num_sinks=2, window_pages=1, select_mode=mode,
                                K_tail=kt, V_tail=vt)
     torch.cuda.synchronize()
