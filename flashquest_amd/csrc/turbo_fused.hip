@@ -12,14 +12,9 @@
 // Otherwise the pages come from the workspace lists and splits of a group
 // meet in merge_splits_kernel.
 //
-// Layout: lane = (c16 = lane & 7: channels 16 c16 .. +15, slot = lane >> 3:
-// tokens 8 slot .. +7 of the page).  Per token a lane loads 2 bytes of the MSB
-// plane and 4 bytes of the LSB plane (its 16 channels).  Codes decode two
-// channels at a time through a 64-entry LDS table: the index is
-// (lsb field d0 | lsb field d1 << 2 | msb d0 << 4 | msb d1 << 5) and the entry
-// the two fp32 codebook values (one 8-byte LDS read per channel pair).  q.k sums the lane's 16 channels and reduces over the 8 lanes
-// of a slot; p.v accumulates the lane's 16 channels over its tokens and reduces
-// over the slots once, at the end.
+// Layout: the page loop runs on the matrix cores (attn_turbo_fused_kernel
+// below); the wave merge, the inverse rotation of O and the split merge are
+// the INT4 kernels' (attn_common.h).
 #include "attn_common.h"
 #include "fused_common.h"
 
@@ -38,13 +33,23 @@ struct TurboFusedParams {
     SelectArgs sel;
 };
 
-// One page step of a lane: 8 tokens' MSB (16 bits) and LSB (32 bits) words of
-// K and V for its 16 channels, and the K and V scale of one token of its slot
-// (token 8 slot + c16; the slot's 8 lanes exchange them by shuffles), so
-// every scale load is exactly in range on a partial last page.
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+
+// Everything one page step of a lane reads (lane = (n16 = lane & 15, lg = lane >> 4)):
+//   q.k (B operand: token 16T + n16, channels 32 lg .. 32 lg + 31):
+//     km[T]: K MSB dword (channel 32 lg + c at bit c), kl[T]: K LSB 8 bytes
+//     (channel 32 lg + c at bits 2c, 2c + 1), ks[T]: K scale of the token;
+//   p.v (B operand: channels 8 n16 .. 8 n16 + 7 of token 16 T + 4 ai + lg):
+//     vm[4T + ai]: V MSB byte, vl[4T + ai]: V LSB half; vs[T]: V scale of token 16T + n16.
 struct TurboPage {
-    uint32_t km[8], kl[8], vm[8], vl[8];
-    uint32_t ks, vs;
+    uint32_t km[4];
+    uint2 kl[4];
+    uint32_t ks[4], vs[4];
+    uint32_t vm[16], vl[16];
 };
 
 struct TurboRsrc {
@@ -52,47 +57,67 @@ struct TurboRsrc {
     int km_t, kl_t, vm_t, vl_t, ks_t, vs_t;     // token strides in bytes
 };
 
-FQ_DEV void load_turbo_page(TurboPage& b, const TurboRsrc& r, int tok0, int c16) {
+FQ_DEV uint32_t ld8(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0); }
+
+FQ_DEV void load_turbo_page(TurboPage& b, const TurboRsrc& r, int tok0, int n16, int lg) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int t = tok0 + i;
-        b.km[i] = ld16(r.km, t * r.km_t + 2 * c16);
-        b.kl[i] = ld32(r.kl, t * r.kl_t + 4 * c16);
+    for (int T = 0; T < 4; ++T) {
+        const int t = tok0 + 16 * T + n16;
+        b.km[T] = ld32(r.km, t * r.km_t + 4 * lg);
+        b.kl[T] = ld64(r.kl, t * r.kl_t + 8 * lg);
+        b.ks[T] = ld16(r.ks, t * r.ks_t);
     }
-    b.ks = ld16(r.ks, (tok0 + c16) * r.ks_t);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int t = tok0 + i;
-        b.vm[i] = ld16(r.vm, t * r.vm_t + 2 * c16);
-        b.vl[i] = ld32(r.vl, t * r.vl_t + 4 * c16);
+    for (int i = 0; i < 16; ++i) {
+        const int t = tok0 + 16 * (i >> 2) + 4 * (i & 3) + lg;
+        b.vm[i] = ld8(r.vm, t * r.vm_t + n16);
+        b.vl[i] = ld16(r.vl, t * r.vl_t + 2 * n16);
     }
-    b.vs = ld16(r.vs, (tok0 + c16) * r.vs_t);
+#pragma unroll
+    for (int T = 0; T < 4; ++T) b.vs[T] = ld16(r.vs, (tok0 + 16 * T + n16) * r.vs_t);
 }
 
-FQ_DEV uint32_t lut_index(uint32_t lsb, uint32_t msb, int jp) {
-    return __builtin_amdgcn_ubfe(lsb, 4 * jp, 4) | (__builtin_amdgcn_ubfe(msb, 2 * jp, 2) << 4);
-}
-// scale of token i of the lane's slot, held by lane (slot base + i)
-FQ_DEV float scale_of(uint32_t s, int lane, int i) {
-    return bf16_bits_to_f(__shfl(s, (lane & ~7) | i, 64) & 0xFFFFu);
+// Both fp16 parts (hi = fp16(x), lo = fp16(x - hi)) of a float.
+FQ_DEV void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
 }
 
+// Sparse decode attention over the TurboQuant cache on the matrix cores.
+//
+// q.k (v_mfma_f32_16x16x32_f16, 16 tokens x 32 channels per step): A rows
+// 4r + {0, 1} hold query head r's fp16 hi / lo parts (q = hi + lo to fp32
+// precision), B the codebook values of 8 channels of a token, once as fp16 hi
+// and once as fp16 lo parts, looked up two channels at a time from a 64-entry
+// LDS table (index lsb d0 | lsb d1 << 2 | msb d0 << 4 | msb d1 << 5); the fp32
+// sum of the four products is q . codebook to fp32 precision.  Logit = that
+// times the token's K scale (q is pre-scaled by sm_scale * log2 e / sqrt(D)
+// after the rotation).
+//
+// p.v (v_mfma_f32_16x16x32_f16, 32 tokens x 16 channels per step): A = p *
+// V_scale / s_run in fp16 (rows = query heads, s_run a running bound of the
+// V scales), B = fp16 codebook values built in registers: byte permutes
+// assemble each token's 3-bit code and look it up in the 8-entry fp16 table
+// (low bytes, high bytes) with v_perm.  Column n16 of channel tile j is
+// channel 8 n16 + j.
 template <int NREP, bool FUSED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_turbo_fused_kernel(TurboFusedParams a) {
     constexpr int D = 128, NW = 8, NT = 512;
+    static_assert(NREP <= 4, "query heads per KV head");
     __shared__ SplitLds<D, NREP, NW> s_split;
     __shared__ int s_ent[kMaxWgPages];
-    __shared__ float2 s_lut[64];
+    __shared__ uint2 s_lut[64];
     __shared__ float s_qraw[NREP][D];
     __shared__ float s_qrot[NREP][D];
+    __shared__ uint8_t s_apv[NW][2][16][4][16];     // p.v A operands per wave: [step][row][k-group, swizzled][16 bytes]
 
     const fq_turbo_cache& c = a.c;
     const QueryArgs& q = a.q;
     const int g = blockIdx.y, split = blockIdx.x;
     const int h = g % c.H_kv, b = (g / c.H_kv) % c.B, l = g / (c.H_kv * c.B);
     const int tid = threadIdx.x, L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
-    const int c16 = L & 7, slot = L >> 3;
+    const int n16 = L & 15, lg = L >> 4;
     const int S = c.S;
 
     // q (raw basis): element tid of the group's NREP heads
@@ -108,7 +133,10 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     if (tid < 64) {
         const float c0 = kTurboCodebookF[((tid >> 2) & 4) | (tid & 3)];
         const float c1 = kTurboCodebookF[((tid >> 3) & 4) | ((tid >> 2) & 3)];
-        s_lut[tid] = make_float2(c0, c1);
+        _Float16 h0, l0, h1, l1;
+        split_f16(c0, h0, l0);
+        split_f16(c1, h1, l1);
+        s_lut[tid] = make_uint2(__builtin_bit_cast(uint32_t, (h2v){h0, h1}), __builtin_bit_cast(uint32_t, (h2v){l0, l1}));
     }
     if (tid < NREP * D) s_qraw[qi >> 7][qi & 127] = qv_raw;
     __syncthreads();
@@ -120,7 +148,6 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         s_qrot[r][d] = v * (q.qk_scale / sqrtf((float)D));
     }
 
-    // page buffers and the loads of one page (tokens 8 slot .. +7)
     TurboRsrc rs;
     {
         const int64_t bl = l;
@@ -142,7 +169,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     }
     auto issue_page = [&](TurboPage& bf, int p) {
         __builtin_amdgcn_sched_barrier(0);
-        load_turbo_page(bf, rs, p * 64 + 8 * slot, c16);
+        load_turbo_page(bf, rs, p * 64, n16, lg);
         __builtin_amdgcn_sched_barrier(0);
     };
     TurboPage b0, b1;
@@ -172,97 +199,187 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     }
     const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;
 
-    float qv[NREP][16];
+    // q.k A operands: row n16 = 4 r + part (part 0: hi, 1: lo, 2-3: zero), k-group
+    // lg of step ks = channels 32 lg + 8 ks .. + 7
+    v8h aqk[4];
+    {
+        const int r = n16 >> 2, part = n16 & 3;
 #pragma unroll
-    for (int r = 0; r < NREP; ++r)
+        for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) qv[r][j] = s_qrot[r][16 * c16 + j];
-
-    float m_run[NREP], l_acc[NREP], acc[NREP][16];
+            for (int i = 0; i < 8; ++i) {
+                const float x = r < NREP ? s_qrot[min(r, NREP - 1)][32 * lg + 8 * ks + i] : 0.f;
+                _Float16 hi, lo;
+                split_f16(x, hi, lo);
+                aqk[ks][i] = part == 0 ? hi : (part == 1 ? lo : (_Float16)0.f);
+            }
+        }
+    }
+    // fp16 codebook as byte tables for v_perm: low bytes of codes 0-3 / 4-7, high bytes
+    uint32_t tl0 = 0, tl1 = 0, th0 = 0, th1 = 0;
 #pragma unroll
-    for (int r = 0; r < NREP; ++r) {
-        m_run[r] = -INFINITY;
-        l_acc[r] = 0.f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[r][j] = 0.f;
+    for (int v = 0; v < 8; ++v) {
+        const uint32_t bits = __builtin_bit_cast(uint16_t, (_Float16)kTurboCodebookF[v]);
+        if (v < 4) { tl0 |= (bits & 0xFFu) << (8 * v); th0 |= (bits >> 8) << (8 * v); }
+        else { tl1 |= (bits & 0xFFu) << (8 * (v - 4)); th1 |= (bits >> 8) << (8 * (v - 4)); }
     }
 
     auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
+
+    float m_run[NREP];
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) m_run[r] = -INFINITY;
+    float s_run = 0.f, inv_s = 1.f;          // running bound of V scales (p * V_scale / s_run <= 1/2)
+    float m_lane = 0.f;                      // m_run[lg], or 0 while head lg has no logit yet
+    v4f pacc[8];                             // [channel tile]: component r = head r
+#pragma unroll
+    for (int t = 0; t < 8; ++t) pacc[t] = (v4f){0.f, 0.f, 0.f, 0.f};
+    float l_acc = 0.f;
+    auto& W = s_apv[w];
+
+    // the idle partner-wave priority rule of the INT4 fused decode: two waves
+    // share a SIMD; the one with more pages left takes the higher priority
+    __shared__ int s_left[NW];
+    auto balance = [&](int k) {
+        s_left[w] = n_mine - k;
+        const int other = __builtin_amdgcn_readfirstlane(s_left[w ^ 4]);
+        if (n_mine - k > other) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+    };
+
     auto compute = [&](const TurboPage& pb, int k) {
+        balance(k);
         const int ent = entry_of(k);
         const int p = ent & 0xFFFF, qm = ent >> 16;
-        const int tok0 = p * 64 + 8 * slot;
-        // ---- logits of the lane's 8 tokens (summed over the slot's 8 lanes)
-        float s[8][NREP];
+        const int tok0 = p * 64;
+        // ---- q.k
+        float lg4[4], mp = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float d[NREP];
+        for (int T = 0; T < 4; ++T) {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < NREP; ++r) d[r] = 0.f;
+            for (int ks = 0; ks < 4; ++ks) {
+                const uint32_t lw = (ks >> 1) ? pb.kl[T].y : pb.kl[T].x;
+                uint32_t bh[4], bl[4];
 #pragma unroll
-            for (int jp = 0; jp < 8; ++jp) {
-                const float2 pr = s_lut[lut_index(pb.kl[i], pb.km[i], jp)];
-                const float k0 = pr.x, k1 = pr.y;
-#pragma unroll
-                for (int r = 0; r < NREP; ++r) d[r] = fmaf(qv[r][2 * jp + 1], k1, fmaf(qv[r][2 * jp], k0, d[r]));
+                for (int jp = 0; jp < 4; ++jp) {
+                    const uint32_t idx = __builtin_amdgcn_ubfe(lw, 16 * (ks & 1) + 4 * jp, 4) |
+                                         (__builtin_amdgcn_ubfe(pb.km[T], 8 * ks + 2 * jp, 2) << 4);
+                    const uint2 e = s_lut[idx];
+                    bh[jp] = e.x;
+                    bl[jp] = e.y;
+                }
+                const v8h Bh = __builtin_bit_cast(v8h, (v4i){(int)bh[0], (int)bh[1], (int)bh[2], (int)bh[3]});
+                const v8h Bl = __builtin_bit_cast(v8h, (v4i){(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]});
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[ks], Bh, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[ks], Bl, acc, 0, 0, 0);
             }
-            const float ksc = scale_of(pb.ks, L, i);
-            const bool tok_ok = tok0 + i < S;
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) {
-                float v = d[r];
-                v += __shfl_xor(v, 1, 64);
-                v += __shfl_xor(v, 2, 64);
-                v += __shfl_xor(v, 4, 64);
-                s[i][r] = (tok_ok && ((qm >> r) & 1)) ? v * ksc : -INFINITY;
-            }
+            const float lgt = (acc[0] + acc[1]) * bf16_bits_to_f(pb.ks[T] & 0xFFFFu);
+            const bool ok = lg < NREP && ((qm >> lg) & 1) && tok0 + 16 * T + n16 < S;
+            lg4[T] = ok ? lgt : -INFINITY;
+            mp = fmaxf(mp, lg4[T]);
         }
-        // ---- online softmax (wave-uniform maxima per head)
-        float vsc[8];
+        // ---- page maxima, running references
+        float vs_t[4], sp = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vsc[i] = scale_of(pb.vs, L, i);
-        float pw[8][NREP];
+        for (int T = 0; T < 4; ++T) {
+            vs_t[T] = bf16_bits_to_f(pb.vs[T] & 0xFFFFu);
+            sp = fmaxf(sp, vs_t[T]);
+        }
+        mp = row16_max(mp);
+        sp = lane_value(row16_max(sp), 0);
+        bool grow = sp > s_run;
+        float mp_r[NREP];
 #pragma unroll
         for (int r = 0; r < NREP; ++r) {
-            float mx = s[0][r];
+            mp_r[r] = lane_value(mp, 16 * r);
+            grow |= mp_r[r] > m_run[r];
+        }
+        if (grow) {      // wave-uniform
+            float am[NREP];
 #pragma unroll
-            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m_run[r], mx);
-            if (mn > m_run[r]) {
-                const float al = m_run[r] == -INFINITY ? 0.f : exp2_fast(m_run[r] - mn);
-                l_acc[r] *= al;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[r][j] *= al;
+            for (int r = 0; r < NREP; ++r) {
+                const float mn = fmaxf(mp_r[r], m_run[r]);
+                am[r] = mn == m_run[r] ? 1.0f : exp2_fast(m_run[r] - mn);
                 m_run[r] = mn;
             }
-            const float mref = m_run[r] == -INFINITY ? 0.f : m_run[r];
+            const float sn = sp > s_run ? 2.0f * sp : s_run;
+            const float as = sn > 0.f ? s_run / sn : 1.0f;
+            s_run = sn;
+            inv_s = sn > 0.f ? 1.0f / sn : 0.f;
+            float am_lg = am[0], ml = m_run[0];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float pe = exp2_fast(s[i][r] - mref);      // exp2(-inf) = 0
-                l_acc[r] += pe;
-                pw[i][r] = pe * vsc[i];
+            for (int r = 1; r < NREP; ++r) {
+                am_lg = lg == r ? am[r] : am_lg;
+                ml = lg == r ? m_run[r] : ml;
+            }
+            m_lane = ml == -INFINITY ? 0.f : ml;
+            l_acc *= am_lg;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float f = r < NREP ? am[r] * as : 0.f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) pacc[t][r] *= f;
             }
         }
-        // ---- p.v over the lane's 16 channels
+        // ---- p.v A: p * V_scale / s_run (fp16); operand k = 8 kg + 2 ai + jj of
+        // step s is token 16 (2s + jj) + 4 ai + kg
+        float pr[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int T = 0; T < 4; ++T) {
+            pr[T] = exp2_fast(lg4[T] - m_lane);
+            l_acc += pr[T];
+        }
+        if (lg < NREP) {
+            const int row = lg, kq = n16 & 3 ^ ((row >> 2) & 3);
 #pragma unroll
-            for (int jp = 0; jp < 8; ++jp) {
-                const float2 pr = s_lut[lut_index(pb.vl[i], pb.vm[i], jp)];
-                const float v0 = pr.x, v1 = pr.y;
+            for (int st = 0; st < 2; ++st) {
+                const float x0 = pr[2 * st] * vs_t[2 * st] * inv_s, x1 = pr[2 * st + 1] * vs_t[2 * st + 1] * inv_s;
+                const h2v hv = __builtin_convertvector((f2v){x0, x1}, h2v);
+                *(uint32_t*)&W[st][row][kq][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const int kr = lg ^ ((n16 >> 2) & 3);
+        const v8h ap0 = *(const v8h*)&W[0][n16][kr][0];
+        const v8h ap1 = *(const v8h*)&W[1][n16][kr][0];
+        // ---- p.v B: codes of channel 8 n16 + j for the step's 8 tokens, 4 at a time
 #pragma unroll
-                for (int r = 0; r < NREP; ++r) {
-                    acc[r][2 * jp] = fmaf(pw[i][r], v0, acc[r][2 * jp]);
-                    acc[r][2 * jp + 1] = fmaf(pw[i][r], v1, acc[r][2 * jp + 1]);
+        for (int st = 0; st < 2; ++st) {
+            uint32_t bw[8][4];       // [channel tile j][dword]
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                // operand k = 4 hh + kk: token index i = 4 (2 st + (kk & 1)) + 2 hh + (kk >> 1)
+                const int i0 = 8 * st + 2 * hh, i1 = i0 + 4, i2 = i0 + 1, i3 = i0 + 5;
+                const uint32_t m4 = pb.vm[i0] | (pb.vm[i1] << 8) | (pb.vm[i2] << 16) | (pb.vm[i3] << 24);
+                const uint32_t x01 = __builtin_amdgcn_perm(pb.vl[i1], pb.vl[i0], 0x05010400u);
+                const uint32_t x23 = __builtin_amdgcn_perm(pb.vl[i3], pb.vl[i2], 0x05010400u);
+                const uint32_t ll = __builtin_amdgcn_perm(x23, x01, 0x05040100u);   // low bytes: channels 0-3
+                const uint32_t lh = __builtin_amdgcn_perm(x23, x01, 0x07060302u);   // high bytes: channels 4-7
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t lx = j < 4 ? ll : lh;
+                    // byte k: msb bit j of token k at bit 2, its lsb field j below
+                    const uint32_t mj = j >= 2 ? m4 >> (j - 2) : m4 << (2 - j);
+                    const uint32_t sel = (mj & 0x04040404u) | ((lx >> (2 * (j & 3))) & 0x03030303u);
+                    const uint32_t lo = __builtin_amdgcn_perm(tl1, tl0, sel);
+                    const uint32_t hi = __builtin_amdgcn_perm(th1, th0, sel);
+                    bw[j][2 * hh] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                    bw[j][2 * hh + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
                 }
             }
+            const v8h a = st ? ap1 : ap0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const v8h bv = __builtin_bit_cast(v8h, (v4i){(int)bw[j][0], (int)bw[j][1], (int)bw[j][2], (int)bw[j][3]});
+                pacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, pacc[j], 0, 0, 0);
+            }
         }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     };
 
     {
+        s_left[w] = n_mine;
         if (!first_issued) issue_page(b0, n_mine > 0 ? entry_of(0) & 0xFFFF : 0);
         for (int k = 0; k < n_mine; k += 2) {
             issue_page(b1, entry_of(min(k + 1, n_mine - 1)) & 0xFFFF);
@@ -270,32 +387,19 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             issue_page(b0, entry_of(min(k + 2, n_mine - 1)) & 0xFFFF);
             if (k + 1 < n_mine) compute(b1, k + 1);
         }
+        __builtin_amdgcn_s_setprio(0);
     }
 
-    // ---- wave state -> LDS: l over the slots (the slot's 8 lanes hold the same
-    // values), acc over the slots for the lane's 16 channels
+    // ---- wave state -> LDS: head r's sums in lane group r (over the 16 token
+    // columns); outputs of channel 8 n16 + j in lane group 0, component r
+    l_acc = row_sum<16>(l_acc);
 #pragma unroll
     for (int r = 0; r < NREP; ++r) {
-        float lv = l_acc[r];
-        lv += __shfl_xor(lv, 8, 64);
-        lv += __shfl_xor(lv, 16, 64);
-        lv += __shfl_xor(lv, 32, 64);
-        l_acc[r] = lv;
+        const float ll = __shfl(l_acc, 16 * r + n16, 64);
+        if (lg == 0) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = acc[r][j];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[r][j] = v;
-        }
-    }
-    if (slot == 0) {
-#pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s_split.acc[w][r][16 * c16 + j] = acc[r][j];
-            if (c16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = l_acc[r]; }
+            for (int j = 0; j < 8; ++j) s_split.acc[w][r][8 * n16 + j] = pacc[j][r] * s_run;
+            if (n16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = ll; }
         }
     }
     __syncthreads();
@@ -324,18 +428,16 @@ hipError_t launch_turbo_fused_nrep(const TurboFusedParams& a, dim3 grid, hipStre
 }  // namespace
 
 bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q) {
-    // 4 query heads per KV head would spill registers: the split kernel takes them
-    if (c.D != 128 || c.page_size != 64 || q.nrep > 3 || c.P > kMaxWgPages) return false;
+    if (c.D != 128 || c.page_size != 64 || q.nrep > 4 || c.P > kMaxWgPages) return false;
     if (c.kmsb_strides[4] != 1 || c.klsb_strides[4] != 1 || c.vmsb_strides[4] != 1 || c.vlsb_strides[4] != 1)
         return false;
-    // 2-byte MSB and 4-byte LSB words per lane
-    if (c.kmsb_strides[3] % 2 || c.vmsb_strides[3] % 2 || c.klsb_strides[3] % 4 || c.vlsb_strides[3] % 4) return false;
+    // K: 4-byte MSB and 8-byte LSB words per lane; V: 2-byte LSB words
+    if (c.kmsb_strides[3] % 4 || c.klsb_strides[3] % 4 || c.vlsb_strides[3] % 2) return false;
     for (int i = 0; i < 3; ++i) {
-        if (c.kmsb_strides[i] % 2 || c.vmsb_strides[i] % 2 || c.klsb_strides[i] % 4 || c.vlsb_strides[i] % 4)
-            return false;
+        if (c.kmsb_strides[i] % 4 || c.klsb_strides[i] % 4 || c.vlsb_strides[i] % 2) return false;
     }
-    if (((uintptr_t)c.k_msb | (uintptr_t)c.v_msb) & 1) return false;
-    if (((uintptr_t)c.k_lsb | (uintptr_t)c.v_lsb) & 3) return false;
+    if ((uintptr_t)c.k_msb & 3) return false;
+    if (((uintptr_t)c.k_lsb & 3) || ((uintptr_t)c.v_lsb & 1)) return false;
     if (((uintptr_t)c.k_scale | (uintptr_t)c.v_scale) & 1) return false;
     return true;
 }
