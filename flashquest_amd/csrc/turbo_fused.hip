@@ -59,22 +59,30 @@ struct TurboRsrc {
 
 FQ_DEV uint32_t ld8(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0); }
 
-FQ_DEV void load_turbo_page(TurboPage& b, const TurboRsrc& r, int tok0, int n16, int lg) {
+// Per-lane offsets of the page loads (page 0).  Token rows are dense (16-byte
+// MSB, 32-byte LSB rows, 2-byte scales), so every other offset of a page is
+// an immediate and a page costs one add per plane.
+struct TurboLaneOff {
+    int km, kl, ks, vm, vl, vs;
+};
+
+FQ_DEV void load_turbo_page(TurboPage& b, const TurboRsrc& r, const TurboLaneOff& o, int p) {
+    const int km = o.km + p * 64 * 16, kl = o.kl + p * 64 * 32, ks = o.ks + p * 64 * 2;
+    const int vm = o.vm + p * 64 * 16, vl = o.vl + p * 64 * 32, vs = o.vs + p * 64 * 2;
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
-        const int t = tok0 + 16 * T + n16;
-        b.km[T] = ld32(r.km, t * r.km_t + 4 * lg);
-        b.kl[T] = ld64(r.kl, t * r.kl_t + 8 * lg);
-        b.ks[T] = ld16(r.ks, t * r.ks_t);
+        b.km[T] = ld32(r.km, km + 16 * T * 16);
+        b.kl[T] = ld64(r.kl, kl + 16 * T * 32);
+        b.ks[T] = ld16(r.ks, ks + 16 * T * 2);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int t = tok0 + 16 * (i >> 2) + 4 * (i & 3) + lg;
-        b.vm[i] = ld8(r.vm, t * r.vm_t + n16);
-        b.vl[i] = ld16(r.vl, t * r.vl_t + 2 * n16);
+        const int t = 16 * (i >> 2) + 4 * (i & 3);
+        b.vm[i] = ld8(r.vm, vm + t * 16);
+        b.vl[i] = ld16(r.vl, vl + t * 32);
     }
 #pragma unroll
-    for (int T = 0; T < 4; ++T) b.vs[T] = ld16(r.vs, (tok0 + 16 * T + n16) * r.vs_t);
+    for (int T = 0; T < 4; ++T) b.vs[T] = ld16(r.vs, vs + 16 * T * 2);
 }
 
 // Both fp16 parts (hi = fp16(x), lo = fp16(x - hi)) of a float.
@@ -107,7 +115,9 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     static_assert(NREP <= 4, "query heads per KV head");
     __shared__ SplitLds<D, NREP, NW> s_split;
     __shared__ int s_ent[kMaxWgPages];
-    __shared__ uint2 s_lut[64];
+    // q.k codebook table: entry e (lsb byte of 4 channels | their msb nibble << 8)
+    // holds the fp16 hi parts of the 4 channels' codebook values, then the lo parts
+    __shared__ uint4 s_lut[4096];
     __shared__ float s_qraw[NREP][D];
     __shared__ float s_qrot[NREP][D];
     __shared__ uint8_t s_apv[NW][2][16][4][16];     // p.v A operands per wave: [step][row][k-group, swizzled][16 bytes]
@@ -130,13 +140,34 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
         score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
     }
-    if (tid < 64) {
-        const float c0 = kTurboCodebookF[((tid >> 2) & 4) | (tid & 3)];
-        const float c1 = kTurboCodebookF[((tid >> 3) & 4) | ((tid >> 2) & 3)];
-        _Float16 h0, l0, h1, l1;
-        split_f16(c0, h0, l0);
-        split_f16(c1, h1, l1);
-        s_lut[tid] = make_uint2(__builtin_bit_cast(uint32_t, (h2v){h0, h1}), __builtin_bit_cast(uint32_t, (h2v){l0, l1}));
+    {
+        // byte tables of the codebook's fp16 parts for v_perm: [part][low / high byte][codes 0-3 / 4-7]
+        uint32_t tb[2][2][2] = {};
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            _Float16 hi, lo;
+            split_f16(kTurboCodebookF[v], hi, lo);
+            const uint32_t bh = __builtin_bit_cast(uint16_t, hi), bl = __builtin_bit_cast(uint16_t, lo);
+            tb[0][0][v >> 2] |= (bh & 0xFFu) << (8 * (v & 3));
+            tb[0][1][v >> 2] |= (bh >> 8) << (8 * (v & 3));
+            tb[1][0][v >> 2] |= (bl & 0xFFu) << (8 * (v & 3));
+            tb[1][1][v >> 2] |= (bl >> 8) << (8 * (v & 3));
+        }
+        for (int e = tid; e < 4096; e += NT) {
+            // byte i of sel: code of channel i = msb bit i << 2 | lsb field i
+            const uint32_t lf = (e & 3) | ((e & 0xC) << 6) | ((e & 0x30) << 12) | ((e & 0xC0) << 18);
+            const uint32_t mf = ((e >> 8) & 1) | (((e >> 9) & 1) << 8) | (((e >> 10) & 1) << 16) | (((e >> 11) & 1) << 24);
+            const uint32_t sel = lf | (mf << 2);
+            uint32_t o[4];
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                const uint32_t lo8 = __builtin_amdgcn_perm(tb[part][0][1], tb[part][0][0], sel);
+                const uint32_t hi8 = __builtin_amdgcn_perm(tb[part][1][1], tb[part][1][0], sel);
+                o[2 * part] = __builtin_amdgcn_perm(hi8, lo8, 0x05010400u);
+                o[2 * part + 1] = __builtin_amdgcn_perm(hi8, lo8, 0x07030602u);
+            }
+            s_lut[e] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     }
     if (tid < NREP * D) s_qraw[qi >> 7][qi & 127] = qv_raw;
     __syncthreads();
@@ -167,9 +198,16 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         rs.ks = make_rsrc(ks, (int64_t)S * rs.ks_t);
         rs.vs = make_rsrc(vs, (int64_t)S * rs.vs_t);
     }
+    TurboLaneOff loff;
+    loff.km = n16 * 16 + 4 * lg;
+    loff.kl = n16 * 32 + 8 * lg;
+    loff.ks = n16 * 2;
+    loff.vm = lg * 16 + n16;
+    loff.vl = lg * 32 + 2 * n16;
+    loff.vs = n16 * 2;
     auto issue_page = [&](TurboPage& bf, int p) {
         __builtin_amdgcn_sched_barrier(0);
-        load_turbo_page(bf, rs, p * 64, n16, lg);
+        load_turbo_page(bf, rs, loff, p);
         __builtin_amdgcn_sched_barrier(0);
     };
     TurboPage b0, b1;
@@ -199,19 +237,22 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     }
     const int n_mine = S > 0 && w < e1 - e0 ? (e1 - e0 - w + NW - 1) / NW : 0;
 
-    // q.k A operands: row n16 = 4 r + part (part 0: hi, 1: lo, 2-3: zero), k-group
-    // lg of step ks = channels 32 lg + 8 ks .. + 7
-    v8h aqk[4];
+    // q.k A operands: row n16 = 4 r + part (part 0: hi, 1: lo, 2-3: zero); k-group
+    // lg of step kk = channels 32 lg + 4 kk .. + 3 against their codebook hi
+    // parts (k 0-3), then the same channels against the lo parts (k 4-7)
+    v8h aqk[8];
     {
         const int r = n16 >> 2, part = n16 & 3;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = r < NREP ? s_qrot[min(r, NREP - 1)][32 * lg + 8 * ks + i] : 0.f;
+            for (int i = 0; i < 4; ++i) {
+                const float x = r < NREP ? s_qrot[min(r, NREP - 1)][32 * lg + 4 * kk + i] : 0.f;
                 _Float16 hi, lo;
                 split_f16(x, hi, lo);
-                aqk[ks][i] = part == 0 ? hi : (part == 1 ? lo : (_Float16)0.f);
+                const _Float16 v = part == 0 ? hi : (part == 1 ? lo : (_Float16)0.f);
+                aqk[kk][i] = v;
+                aqk[kk][i + 4] = v;
             }
         }
     }
@@ -258,21 +299,15 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         for (int T = 0; T < 4; ++T) {
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const uint32_t lw = (ks >> 1) ? pb.kl[T].y : pb.kl[T].x;
-                uint32_t bh[4], bl[4];
-#pragma unroll
-                for (int jp = 0; jp < 4; ++jp) {
-                    const uint32_t idx = __builtin_amdgcn_ubfe(lw, 16 * (ks & 1) + 4 * jp, 4) |
-                                         (__builtin_amdgcn_ubfe(pb.km[T], 8 * ks + 2 * jp, 2) << 4);
-                    const uint2 e = s_lut[idx];
-                    bh[jp] = e.x;
-                    bl[jp] = e.y;
-                }
-                const v8h Bh = __builtin_bit_cast(v8h, (v4i){(int)bh[0], (int)bh[1], (int)bh[2], (int)bh[3]});
-                const v8h Bl = __builtin_bit_cast(v8h, (v4i){(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]});
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[ks], Bh, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[ks], Bl, acc, 0, 0, 0);
+            for (int kk = 0; kk < 8; ++kk) {
+                // table entry of channels 32 lg + 4 kk .. + 3: their LSB byte, MSB nibble
+                const uint32_t lw = (kk >> 2) ? pb.kl[T].y : pb.kl[T].x;
+                const int lsh = 8 * (kk & 3) - 4, msh = 4 * kk - 12;      // entry * 16, in bytes
+                const uint32_t a_l = (lsh >= 0 ? lw >> lsh : lw << -lsh) & 0xFF0u;
+                const uint32_t a_m = (msh >= 0 ? pb.km[T] >> msh : pb.km[T] << -msh) & 0xF000u;
+                const uint4 e = *(const uint4*)((const char*)s_lut + (a_l | a_m));
+                const v8h B = __builtin_bit_cast(v8h, (v4i){(int)e.x, (int)e.y, (int)e.z, (int)e.w});
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[kk], B, acc, 0, 0, 0);
             }
             const float lgt = (acc[0] + acc[1]) * bf16_bits_to_f(pb.ks[T] & 0xFFFFu);
             const bool ok = lg < NREP && ((qm >> lg) & 1) && tok0 + 16 * T + n16 < S;
@@ -431,8 +466,11 @@ bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q) {
     if (c.D != 128 || c.page_size != 64 || q.nrep > 4 || c.P > kMaxWgPages) return false;
     if (c.kmsb_strides[4] != 1 || c.klsb_strides[4] != 1 || c.vmsb_strides[4] != 1 || c.vlsb_strides[4] != 1)
         return false;
-    // K: 4-byte MSB and 8-byte LSB words per lane; V: 2-byte LSB words
-    if (c.kmsb_strides[3] % 4 || c.klsb_strides[3] % 4 || c.vlsb_strides[3] % 2) return false;
+    // dense token rows (16-byte MSB, 32-byte LSB rows, 2-byte scales); K: 4-byte
+    // MSB and 8-byte LSB words per lane; V: 2-byte LSB words
+    if (c.kmsb_strides[3] != 16 || c.klsb_strides[3] != 32 || c.vmsb_strides[3] != 16 || c.vlsb_strides[3] != 32)
+        return false;
+    if (c.kst_strides[3] != 1 || c.vst_strides[3] != 1) return false;
     for (int i = 0; i < 3; ++i) {
         if (c.kmsb_strides[i] % 4 || c.klsb_strides[i] % 4 || c.vlsb_strides[i] % 2) return false;
     }
