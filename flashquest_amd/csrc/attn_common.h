@@ -36,6 +36,22 @@ struct SplitLds {
     float L[NREP], M[NREP];
 };
 
+// Unnormalised Sylvester Hadamard transform of a 128-vector held by one wave
+// (lane holds elements lane and lane + 64): y_i = sum_j (-1)^popc(i & j) x_j,
+// by butterflies (a + b, a - b) for h = 1, 2, ..., 64.
+FQ_DEV void wave_hadamard128(float& v0, float& v1) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        const float y0 = __shfl_xor(v0, h, 64), y1 = __shfl_xor(v1, h, 64);
+        v0 = (lane & h) ? y0 - v0 : v0 + y0;
+        v1 = (lane & h) ? y1 - v1 : v1 + y1;
+    }
+    const float a = v0, c = v1;
+    v0 = a + c;
+    v1 = a - c;
+}
+
 // Writes O (vals[r][d] = acc / l, rotated back when ROT) and lse for the NREP
 // query heads of KV group (l, b, h).  Must be called by the whole workgroup
 // after vals / Ls / Ms are complete in LDS.
@@ -44,6 +60,16 @@ FQ_DEV void store_outputs(const QueryArgs& q, int l, int b, int h, const float (
                           const float* Ms) {
     const int tid = threadIdx.x;
     const float inv = 1.0f / sqrtf((float)D);
+    if constexpr (ROT && D == 128) {        // one wave per head
+        const int lane = lane_id();
+        for (int r = wave_id(); r < NREP; r += NT / 64) {
+            float v0 = vals[r][lane], v1 = vals[r][lane + 64];
+            wave_hadamard128(v0, v1);
+            const int64_t ob = l * q.o_s[0] + b * q.o_s[1] + (h * NREP + r) * q.o_s[2];
+            store_any(q.out, q.out_dtype, ob + lane * q.o_s[3], v0 * inv);
+            store_any(q.out, q.out_dtype, ob + (lane + 64) * q.o_s[3], v1 * inv);
+        }
+    } else
     for (int i = tid; i < NREP * D; i += NT) {
         const int r = i / D, d = i % D;
         float o = vals[r][d];

@@ -130,15 +130,33 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     const int n16 = L & 15, lg = L >> 4;
     const int S = c.S;
 
-    // q (raw basis): element tid of the group's NREP heads
+    // q (raw basis): element tid of the group's NREP heads.  Branch-free (two
+    // 16-bit loads, the high one masked off for 16-bit q types), so the
+    // metadata loads below go out before the first wait.
     const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
     const int qi = min(tid, NREP * D - 1);
-    const float qv_raw = load_any(q.q, q.q_dtype, qb + (qi >> 7) * q.q_s[2] + (qi & 127) * q.q_s[3]);
+    const bool q32 = q.q_dtype == FQ_F32;
+    const int esz = q32 ? 4 : 2;
+    uint32_t hi_mask = (0u - (uint32_t)q32) & 0xFFFF0000u;
+    asm volatile("" : "+s"(hi_mask));
+    uint32_t ql, qh;
+    {
+        const char* qc = (const char*)q.q + (qb + (qi >> 7) * q.q_s[2] + (qi & 127) * q.q_s[3]) * esz;
+        ql = *(const uint16_t*)qc;
+        qh = *(const uint16_t*)(qc + esz - 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
     if constexpr (FUSED) {
         ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
         score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
+    }
+    float qv_raw;
+    {
+        const uint32_t u = (ql & ~hi_mask) | ((qh << 16) & hi_mask);
+        const float fh = f16_bits_to_f(u), fb = bf16_bits_to_f(u);
+        qv_raw = q32 ? __uint_as_float(u) : (q.q_dtype == FQ_BF16 ? fb : fh);
     }
     {
         // byte tables of the codebook's fp16 parts for v_perm: [part][low / high byte][codes 0-3 / 4-7]
@@ -171,12 +189,14 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     }
     if (tid < NREP * D) s_qraw[qi >> 7][qi & 127] = qv_raw;
     __syncthreads();
-    // q_rot = WHT(q) / sqrt(D) (Sylvester order), pre-scaled by sm_scale * log2(e)
-    if (tid < NREP * D) {
-        const int r = tid >> 7, d = tid & 127;
-        float v = 0.f;
-        for (int k = 0; k < D; ++k) v = fmaf(hadamard_sign(d, k), s_qraw[r][k], v);
-        s_qrot[r][d] = v * (q.qk_scale / sqrtf((float)D));
+    // q_rot = WHT(q) / sqrt(D) (Sylvester order), pre-scaled by sm_scale * log2(e);
+    // wave r rotates head r
+    if (w < NREP) {
+        float v0 = s_qraw[w][L], v1 = s_qraw[w][L + 64];
+        wave_hadamard128(v0, v1);
+        const float sc = q.qk_scale / sqrtf((float)D);
+        s_qrot[w][L] = v0 * sc;
+        s_qrot[w][L + 64] = v1 * sc;
     }
 
     TurboRsrc rs;
