@@ -170,7 +170,8 @@ FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
 // (P <= 64 C pages, NW waves).  keys[r * 64 C + p] holds sortable_key of row
 // r's score of page p, and 0 (below every score) for p >= P.  Every wave loads
 // every key (C per lane per row); wave r finds row r's k-th largest key with
-// wave_kth_largest (no barrier inside), the thresholds meet in LDS, and every
+// wave_kth_largest (no barrier inside), or, for one row in 8 waves, all waves
+// find it together (block_kth_largest); the thresholds meet in LDS, and every
 // wave then ranks the ties and lists the pages.  Ties and forced pages follow
 // wave_topk / wave_select_group; the entry list holds the forced pages first,
 // then the other selected pages, each part ascending; wave w writes the entries
@@ -181,7 +182,49 @@ FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
 // every thread.
 struct BlockSelectLds {
     uint32_t T[4];          // k-th largest key per row
+    int cnt[2][16];         // block_kth_largest: per-round candidate counts (double-buffered)
 };
+
+// The k-th largest of the keys (k >= 1) by all 8 waves of the workgroup, each
+// holding every key (C per lane): a radix-16 search from the top digit, where
+// wave w counts the keys reaching candidate digits w + 1 and w + 9 and the
+// counts meet in LDS (one barrier per digit).  T keeps the largest prefix
+// that at least k keys reach; the search stops early once exactly k keys
+// reach T (then {key >= T} is the top-k set with no tie across its boundary,
+// which the callers' rule -- keys above T, then ties at T by page index up to
+// k -- selects unchanged).  Otherwise T ends as the k-th largest key, as with
+// wave_kth_largest.  Wave-uniform.
+template <int C>
+FQ_DEV uint32_t block_kth_largest(const uint32_t (&key)[C], int k, BlockSelectLds& sl) {
+    const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+    uint32_t T = 0;
+    for (int round = 0; round < 8; ++round) {
+        const int shift = 28 - 4 * round;
+        const int d0 = w + 1, d1 = w + 9;          // d1 = 16 (wave 7) tests nothing
+        const uint32_t c0 = T | ((uint32_t)d0 << shift), c1 = T | ((uint32_t)(d1 & 15) << shift);
+        int n0 = 0, n1 = 0;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            n0 += __popcll(__ballot(key[j] >= c0));
+            n1 += __popcll(__ballot(key[j] >= c1));
+        }
+        int* cnt = sl.cnt[round & 1];
+        if (lane == 0) {
+            cnt[d0] = n0;
+            if (d1 < 16) cnt[d1] = n1;
+        }
+        __syncthreads();
+        const bool live = lane >= 1 && lane < 16;
+        const int cl = live ? cnt[lane] : 0;
+        const uint64_t ok = __ballot(live && cl >= k);       // counts fall as the digit rises
+        if (ok) {
+            const int d = 63 - __clzll(ok);
+            T |= (uint32_t)d << shift;
+            if (__builtin_amdgcn_readlane(cl, d) == k) break;
+        }
+    }
+    return T;
+}
 
 template <int C, int NW, int NROWS, int NREP>
 FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max, int num_sinks, int window,
@@ -202,7 +245,14 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
 #pragma unroll
     for (int r = 0; r < NROWS; ++r) {
         k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
-        if (w == r) {
+        if constexpr (NROWS == 1 && NW == 8) {      // one row: every wave takes part
+            if (k[r] > 0) {
+                const uint32_t t = block_kth_largest<C>(key[r], k[r], sl);
+                if (w == 0 && lane == 0) sl.T[r] = t;
+            } else if (w == 0 && lane == 0) {
+                sl.T[r] = 0u;
+            }
+        } else if (w == r) {
             const uint32_t t = k[r] > 0 ? wave_kth_largest<C>(key[r], k[r]) : 0u;
             if (lane == 0) sl.T[r] = t;
         }

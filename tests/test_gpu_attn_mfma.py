@@ -136,3 +136,30 @@ def test_fused_decode_selecting_inside_attention(mode, want_mask, sinks, window,
             assert np.array_equal(out[2][i].cpu().numpy(), ref["mask"]), i
         assert max_err(o[i][:, :, 0], ref["O"]) <= _tol(c, ref["O"]), i
         assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
+
+
+@pytest.mark.parametrize("mode", ["per_q_head", "per_kv_head_sum"])
+def test_fused_decode_ties_take_the_lower_pages(mode):
+    # Pages 6.. share one K scale/min (so their scores tie exactly) but not their
+    # codes: the top-k boundary cuts through the tie, and the in-kernel selection
+    # must keep the lower page indices (selection.py's order), which the output shows.
+    from flashquest_amd.eager import quest_decode_int4
+    L_, Hq, Hkv, P = 24, 24, 8, 48
+    cases = []
+    for i in range(L_):
+        c = Int4Case(seed=700 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, page=64, dtype="bf16", meta="bf16")
+        c.ks[:, :, 6:, :] = c.ks[:, :, 6:7, :]
+        c.km[:, :, 6:, :] = c.km[:, :, 6:7, :]
+        cases.append(c)
+    r = np.full(Hq, 0.3, np.float32)
+    dev = [c.device() for c in cases]
+    stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+    q = torch.stack([c.q_dev() for c in cases])
+    o, lse = quest_decode_int4(q, **stacked, retention=torch.from_numpy(r), num_sinks=1, window_pages=1,
+                               select_mode=mode)
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=r, num_sinks=1,
+                            window_pages=1, mode=mode)
+        assert max_err(o[i][:, :, 0], ref["O"]) <= _tol(c, ref["O"]), i
+        assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
