@@ -53,6 +53,8 @@ def parse():
                     help="skip the batch-16 line (BASELINE config 4) among the extras")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
+    ap.add_argument("--profile-turbo", action="store_true",
+                    help="for rocprofv3 runs: 10 flushed fused TurboQuant decode steps (--select mode) only")
     return ap.parse_args()
 
 
@@ -265,6 +267,20 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L, B, P = args.layers, args.batch, args.pages
+    if args.profile_turbo:
+        from flashquest_amd.eager.decode import quest_decode_turbo
+        tc = make_turbo_cache(L, P=P, dev=dev)
+        planes = [tc[x] for x in ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")]
+        flush = Flusher(dev)
+        k = math.ceil(args.retention * P)
+        for _ in range(10):
+            flush()
+            quest_decode_turbo(tc["Q"], *planes, tc["K_scale_raw"], tc["K_mn_raw"], retention=args.retention,
+                               num_sinks=4, window_pages=2, k_max_static=k, select_mode=args.select)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_turbo": "done", "select": args.select}))
+        return
+
     cache = make_cache(L, B, P=P, dev=dev)
     Hq = cache["Q"].shape[2]
     flush = Flusher(dev)
