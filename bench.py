@@ -28,8 +28,8 @@ sys.path.insert(0, ROOT)
 
 from flashquest_amd._lib import KernelTimer  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
-from flashquest_amd.kernel.kv_quant import (quantize_k_int4, quantize_k_turbo, quantize_v_int4,  # noqa: E402
-                                            quantize_v_turbo)
+from flashquest_amd.kernel.kv_quant import (quantize_k, quantize_k_int4, quantize_k_turbo, quantize_v,  # noqa: E402
+                                            quantize_v_int4, quantize_v_turbo)
 from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402
 
 METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
@@ -115,6 +115,27 @@ def make_cache(L, B, Hq=24, Hkv=8, P=512, D=128, page=64, planted=4, dev="cuda",
             Q[l, b, :, 0] = q.half()
     torch.cuda.synchronize()
     return dict(Q=Q, K_packed=kp, K_scale=ks, K_mn=km, V_packed=vp, V_scale=vs, V_mn=vm)
+
+
+def make_int8_cache(L, Hq=24, Hkv=8, P=512, D=128, page=64, dev="cuda"):
+    """The same synthetic layers (batch 1) in the reference's INT8 layout
+    (persistent_int8.py: uint8 codes, bf16 K page / V token metadata), layers
+    folded into the batch axis, bf16 Q."""
+    S = P * page
+    c = {"K_uint8": torch.empty(L, Hkv, S, D, dtype=torch.uint8, device=dev),
+         "K_scale": torch.empty(L, Hkv, P, D, dtype=torch.bfloat16, device=dev),
+         "K_mn": torch.empty(L, Hkv, P, D, dtype=torch.bfloat16, device=dev),
+         "V_uint8": torch.empty(L, Hkv, S, D, dtype=torch.uint8, device=dev),
+         "V_scale": torch.empty(L, Hkv, S, 1, dtype=torch.bfloat16, device=dev),
+         "V_mn": torch.empty(L, Hkv, S, 1, dtype=torch.bfloat16, device=dev),
+         "Q": torch.empty(L, Hq, 1, D, dtype=torch.bfloat16, device=dev)}
+    for l in range(L):
+        K, V, q = gen_layer(l, 0, Hq, Hkv, P, D, page, 4, dev)
+        quantize_k(K.bfloat16(), page, out=tuple(c[k][l:l + 1] for k in ("K_uint8", "K_scale", "K_mn")))
+        quantize_v(V.bfloat16(), out=tuple(c[k][l:l + 1] for k in ("V_uint8", "V_scale", "V_mn")))
+        c["Q"][l, :, 0] = q.bfloat16()
+    torch.cuda.synchronize()
+    return c
 
 
 def make_turbo_cache(L, Hq=24, Hkv=8, P=512, D=128, page=64, dev="cuda"):
@@ -444,6 +465,24 @@ def main():
         t_ms, _, _ = time_steps(noop, turbo_ops_step, args.steps, args.warmup, flush)
         extra["turbo_reference_operator_sequence_us"] = t_ms * 1e3
         del tc, planes
+
+        # INT8 KV (the reference dispatcher's default kv_bits = 8): score
+        # (255 levels) -> select -> flash_attn_sparse_fwd over all layers
+        from flashquest_amd.eager.decode import quest_decode_int8
+        ic = make_int8_cache(L, P=P, dev=dev)
+        iplanes = [ic[x] for x in ("K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")]
+        _, _, imask = quest_decode_int8(ic["Q"], *iplanes, retention=args.retention, num_sinks=4, window_pages=2,
+                                        k_max_static=k, select_mode=args.select, return_selection=True)
+        torch.cuda.synchronize()
+        i_union = imask.view(L, 8, Hq // 8, P).any(2).sum().item()
+        i_bytes = L * 8 * P * 128 * 2 * 2 + i_union * 64 * (2 * 128 + 2 * 2) + L * Hq * (128 * 2 * 2 + 4)
+        i_ms, _, _ = time_steps(noop, lambda: quest_decode_int8(
+            ic["Q"], *iplanes, retention=args.retention, num_sinks=4, window_pages=2, k_max_static=k,
+            select_mode=args.select), args.steps, args.warmup, flush)
+        extra.update({"int8_us": i_ms * 1e3, "int8_step_bytes": i_bytes,
+                      "int8_step_GBps": i_bytes / (i_ms * 1e-3) / 1e9,
+                      "int8_roofline_frac": i_bytes / (i_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        del ic, iplanes
 
         # batch 16 independent sequences, 28 layers, 32k each
         if B == 1 and args.batch16:

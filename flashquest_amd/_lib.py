@@ -119,6 +119,18 @@ SIGNATURES = {
     "fq_quantize_turbo": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P, _P]),
     "fq_sparse_turbo_fwd_mask": (ctypes.c_int, [ctypes.POINTER(TurboCache), ctypes.POINTER(Query), _P, _I64P,
                                                 _P, ctypes.c_size_t, _P]),
+    # INT8 family (fq_int8_cache has the fq_int4_cache layout)
+    "fq_int8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), _I]),
+    "fq_page_scores_int8": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
+                                           _I, _I, _I, _I, _I, _I, _P]),
+    "fq_sparse_int8_fwd_mask": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I64P,
+                                               _P, ctypes.c_size_t, _P]),
+    "fq_quest_decode_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
+                                            _P, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quantize_k_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
+                                          _I, _P]),
+    "fq_quantize_v_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
+                                          _I, _P]),
 }
 
 _lib = None

@@ -55,6 +55,19 @@ def int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size: int)
     return c, (kp, vp, ks, km, vs, vm)
 
 
+def int8_cache(K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, page_size: int):
+    """Describe an INT8 cache view (one code byte per channel; V metadata per
+    token): 4D (B,H,S,D) per layer or 5D (L,B,H,S,D).  Same descriptor layout
+    as the INT4 one.  Returns (descriptor, keepalive tensors)."""
+    ku = _ensure_inner_contiguous(K_uint8, 8)
+    vu = _ensure_inner_contiguous(V_uint8, 8)
+    c, keep = int4_cache(ku, K_scale, K_mn, vu, V_scale, V_mn, page_size)
+    c.D = ku.shape[-1]
+    if c.v_groups != 1:
+        raise AssertionError("INT8 V metadata must be per token: (..., S, 1)")
+    return c, keep
+
+
 def turbo_cache(K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale, num_pages: int, page_size: int):
     ts = [_ensure_inner_contiguous(t) for t in (K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale)]
     lead = _lead(ts[0], 5)

@@ -14,6 +14,8 @@
 // through a workspace: the last workgroup of a group to arrive merges the
 // split partials (the same rule as _merge_two_attentions,
 // llama_persistent_patch.py:50-61) and writes O and lse.
+#include <type_traits>
+
 #include "attn_common.h"
 
 namespace fq {
@@ -27,8 +29,15 @@ struct AttnParams {
     int splits;   // gridDim.x
 };
 
-template <int D, typename MT, int GV, int NREP>
+// BITS = 8: the INT8 cache of flash_attn_sparse_fwd (sparse_fwd.py:23-157),
+// one code byte per channel, the same math with codes 0..255.
+template <int D, typename MT, int GV, int NREP, int BITS>
 __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
+    using CodeWord = typename std::conditional<BITS == 8, uint2, uint32_t>::type;     // 8 codes of a lane
+    auto code_of = [](const CodeWord& wv, int j) -> float {
+        if constexpr (BITS == 8) return (float)(((j < 4 ? wv.x : wv.y) >> (8 * (j & 3))) & 255u);
+        else return (float)((wv >> (4 * j)) & 15u);
+    };
     constexpr int NCC = D / 8;
     constexpr int NROW = 64 / NCC;
     constexpr int NW = kThreads / 64;
@@ -65,8 +74,8 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
                                     l * q.q_s[0] + b * q.q_s[1] + (h * NREP + r) * q.q_s[2] +
                                         (cc * 8 + j) * q.q_s[3]) * q.qk_scale;
 
-        const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2] + cc * 4;
-        const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2] + cc * 4;
+        const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2] + cc * BITS;
+        const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2] + cc * BITS;
         const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2] + cc * 8;
         const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2] + cc * 8;
         const int gi = GV == 1 ? 0 : (cc * 8) / (D / GV);
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
             for (int t0 = 0; t0 < c.page; t0 += 16 * NROW) {
                 // Issue every load of this block of 16 token rows first: rows past the
                 // page or the view are clamped to row S-1 (always in bounds) and masked.
-                uint32_t kw[16], vw[16];
+                CodeWord kw[16], vw[16];
                 uint16_t vsr[16], vmr[16];
                 int vmask = 0;
 #pragma unroll
@@ -116,8 +125,8 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
                     const bool ok = t < c.page && tok < c.S;
                     vmask |= ok << i;
                     const int64_t tc = ok ? tok : c.S - 1;
-                    kw[i] = *(const uint32_t*)(kb + tc * c.kp_s[3]);
-                    vw[i] = *(const uint32_t*)(vb + tc * c.vp_s[3]);
+                    kw[i] = *(const CodeWord*)(kb + tc * c.kp_s[3]);
+                    vw[i] = *(const CodeWord*)(vb + tc * c.vp_s[3]);
                     vsr[i] = vsc[tc * c.vsc_s[3]];
                     vmr[i] = vmn[tc * c.vmn_s[3]];
                 }
@@ -128,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
                     for (int i = 0; i < 4; ++i) {
                         float code[8];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) code[j] = (float)((kw[i0 + i] >> (4 * j)) & 15u);
+                        for (int j = 0; j < 8; ++j) code[j] = code_of(kw[i0 + i], j);
 #pragma unroll
                         for (int r = 0; r < NREP; ++r) {
                             float d = Cp[r];
@@ -144,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
                         vs[i] = half_to_f<MT>(vsr[i0 + i]);
                         vm[i] = half_to_f<MT>(vmr[i0 + i]);
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) vcode[i][j] = (float)((vw[i0 + i] >> (4 * j)) & 15u);
+                        for (int j = 0; j < 8; ++j) vcode[i][j] = code_of(vw[i0 + i], j);
                     }
 #pragma unroll
                     for (int r = 0; r < NREP; ++r) {
@@ -180,13 +189,13 @@ __global__ __launch_bounds__(kThreads) void attn_int4_kernel(AttnParams a) {
     finish_split<D, NREP, false>(s_split, m, lsum, acc, active, q, a.ws, g, l, b, h, split, a.splits);
 }
 
-template <int D, typename MT, int GV>
+template <int D, typename MT, int GV, int BITS>
 hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
     switch (a.q.nrep) {
 #define FQ_CASE(N)                                                                                      \
     case N:                                                                                             \
         timer_before_launch(st);                                                                       \
-        hipLaunchKernelGGL((attn_int4_kernel<D, MT, GV, N>), grid, dim3(kThreads), 0, st, a);          \
+        hipLaunchKernelGGL((attn_int4_kernel<D, MT, GV, N, BITS>), grid, dim3(kThreads), 0, st, a);    \
         timer_after_launch(st);                                                                        \
         if (a.splits > 1)                                                                               \
             hipLaunchKernelGGL((merge_splits_kernel<D, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
@@ -201,8 +210,9 @@ hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
 
 template <int D, typename MT>
 hipError_t launch_gv(const AttnParams& a, dim3 grid, hipStream_t st) {
-    if (a.c.G == 1) return launch_nrep<D, MT, 1>(a, grid, st);
-    if (a.c.G == D / 32) return launch_nrep<D, MT, D / 32>(a, grid, st);
+    if (a.c.bits == 8) return a.c.G == 1 ? launch_nrep<D, MT, 1, 8>(a, grid, st) : hipErrorInvalidValue;
+    if (a.c.G == 1) return launch_nrep<D, MT, 1, 4>(a, grid, st);
+    if (a.c.G == D / 32) return launch_nrep<D, MT, D / 32, 4>(a, grid, st);
     return hipErrorInvalidValue;
 }
 

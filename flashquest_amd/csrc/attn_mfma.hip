@@ -649,7 +649,7 @@ int fused_splits(int groups, int max_entries, int s_max) {
 }  // namespace
 
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al) {
-    if (c.D != 128 || c.page != 64 || q.nrep > 4) return false;
+    if (c.D != 128 || c.page != 64 || q.nrep > 4 || c.bits == 8) return false;
     if (c.G != 1 && c.G != 4) return false;
     if ((int64_t)al.s_max * kMaxWgPages < al.max_entries) return false;
     // contiguous 64-byte rows of codes, G-element rows of V metadata, 128-element

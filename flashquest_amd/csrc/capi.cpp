@@ -13,10 +13,10 @@
 namespace fq {
 hipError_t launch_quant_k(const void* k, int in_dtype, const int64_t* k_s, int B, int H, int S, int D,
                           int page, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
-                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st, int bits = 4);
 hipError_t launch_quant_v(const void* v, int in_dtype, const int64_t* v_s, int B, int H, int S, int D,
                           int group, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
-                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st, int bits = 4);
 hipError_t launch_wht(const void* x, int x_dtype, int64_t x_rs, void* out, int out_dtype, int64_t o_rs,
                       int N, int D, const float* signs, int inverse, int arith, hipStream_t st);
 hipError_t launch_turbo_quant(const void* x, int in_dtype, const int64_t* x_s, int B, int H, int S, int D,
@@ -115,7 +115,9 @@ static bool rows_aligned16(const void* p, const int64_t* strides, int n_outer, i
     return true;
 }
 
-static int check_cache(const fq_int4_cache* c, Int4Cache* out) {
+// bits = 4: packed INT4 (two codes per byte); bits = 8: one code byte per
+// channel (the INT8 cache of flash_attn_sparse_fwd), V metadata per token.
+static int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits = 4) {
     if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
     if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
     if (!is_half(c->meta_dtype)) return fail(FQ_ERR_UNSUPPORTED, "metadata dtype must be bf16 or fp16");
@@ -125,19 +127,20 @@ static int check_cache(const fq_int4_cache* c, Int4Cache* out) {
     if (c->S < 0) return fail(FQ_ERR_INVALID, "negative S");
     if (c->v_groups != 1 && c->v_groups != c->D / 32)
         return fail(FQ_ERR_UNSUPPORTED, "V groups=%d must be 1 or D/32", c->v_groups);
+    if (bits == 8 && c->v_groups != 1) return fail(FQ_ERR_UNSUPPORTED, "INT8 V metadata is per token (v_groups=1)");
     if (!c->k_packed || !c->v_packed || !c->k_scale || !c->k_mn || !c->v_scale || !c->v_mn)
         return fail(FQ_ERR_INVALID, "NULL cache tensor");
     for (int i = 0; i < 4; ++i) {
-        if (c->k_strides[i] % 4 || c->v_strides[i] % 4)
-            return fail(FQ_ERR_UNSUPPORTED, "packed K/V strides must be multiples of 4 bytes");
+        if (c->k_strides[i] % bits || c->v_strides[i] % bits)
+            return fail(FQ_ERR_UNSUPPORTED, "K/V code strides must be multiples of %d bytes", bits);
         if (c->ks_strides[i] % 8 || c->km_strides[i] % 8)
             return fail(FQ_ERR_UNSUPPORTED, "K metadata strides must be multiples of 8 elements");
     }
     if (c->k_strides[4] != 1 || c->v_strides[4] != 1 || c->ks_strides[4] != 1 || c->km_strides[4] != 1 ||
         c->vs_strides[4] != 1 || c->vm_strides[4] != 1)
         return fail(FQ_ERR_UNSUPPORTED, "innermost cache axis must be contiguous");
-    if (((uintptr_t)c->k_packed | (uintptr_t)c->v_packed) & 3)
-        return fail(FQ_ERR_UNSUPPORTED, "packed K/V must be 4-byte aligned");
+    if (((uintptr_t)c->k_packed | (uintptr_t)c->v_packed) & (bits - 1))
+        return fail(FQ_ERR_UNSUPPORTED, "K/V codes must be %d-byte aligned", bits);
     if (((uintptr_t)c->k_scale | (uintptr_t)c->k_mn) & 15)
         return fail(FQ_ERR_UNSUPPORTED, "K metadata must be 16-byte aligned");
     Int4Cache& o = *out;
@@ -149,7 +152,7 @@ static int check_cache(const fq_int4_cache* c, Int4Cache* out) {
         o.vsc_s[i] = c->vs_strides[i]; o.vmn_s[i] = c->vm_strides[i];
     }
     o.L = c->L; o.B = c->B; o.Hkv = c->H_kv; o.S = c->S; o.P = c->P; o.D = c->D;
-    o.page = c->page_size; o.G = c->v_groups; o.meta_dtype = c->meta_dtype;
+    o.page = c->page_size; o.G = c->v_groups; o.meta_dtype = c->meta_dtype; o.bits = bits;
     return FQ_OK;
 }
 
@@ -172,6 +175,8 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
 }
 
 static std::atomic<int> g_split_request{0};
+// code width for fq_page_scores_int4's scoring constant (set by fq_page_scores_int8 for its call)
+static thread_local int g_score_bits = 4;
 int attention_splits_request() { return g_split_request.load(std::memory_order_relaxed); }
 
 void timer_before_launch(hipStream_t st) {
@@ -254,7 +259,7 @@ int fq_page_scores_int4(const void* q, int32_t q_dtype, const int64_t q_strides[
     c.ksc = k_scale; c.kmn = k_mn;
     c.ksc_s[0] = 0; c.kmn_s[0] = 0;
     for (int i = 0; i < 3; ++i) { c.ksc_s[i + 1] = ks_strides[i]; c.kmn_s[i + 1] = km_strides[i]; }
-    c.L = 1; c.B = B; c.Hkv = H_kv; c.P = P; c.D = D; c.meta_dtype = meta_dtype;
+    c.L = 1; c.B = B; c.Hkv = H_kv; c.P = P; c.D = D; c.meta_dtype = meta_dtype; c.bits = g_score_bits;
     QueryArgs qa{};
     qa.q = q; qa.q_dtype = q_dtype; qa.q_s[0] = 0; qa.Hq = H_q; qa.nrep = H_q / H_kv;
     return hip_status(launch_score(c, qa, S_q, q_strides, scores, sc_strides, nullptr, 0, nullptr, 0, 0, -1,
@@ -283,8 +288,8 @@ int fq_compact_ids(const uint8_t* mask, const int64_t mask_strides[4], int32_t B
 }
 
 static int attn_common(const fq_int4_cache* cache, const fq_query* query, void* workspace,
-                       size_t workspace_bytes_, Int4Cache* c, QueryArgs* q, Workspace* ws) {
-    int st = check_cache(cache, c);
+                       size_t workspace_bytes_, Int4Cache* c, QueryArgs* q, Workspace* ws, int bits = 4) {
+    int st = check_cache(cache, c, bits);
     if (st) return st;
     st = check_query(query, c->D, c->Hkv, q);
     if (st) return st;
@@ -298,20 +303,32 @@ static int attn_common(const fq_int4_cache* cache, const fq_query* query, void* 
     return FQ_OK;
 }
 
-int fq_sparse_int4_fwd_mask(const fq_int4_cache* cache, const fq_query* query, const uint8_t* mask,
-                            const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
-                            fq_stream_t stream) {
+static int sparse_fwd_mask(const fq_int4_cache* cache, const fq_query* query, const uint8_t* mask,
+                           const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
+                           fq_stream_t stream, int bits) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
-    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws, bits);
     if (st) return st;
     if (!mask) return fail(FQ_ERR_INVALID, "selection mask is NULL");
     hipStream_t s = (hipStream_t)stream;
     st = hip_status(launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, q.nrep, c.P, ws, s), "page union");
     if (st) return st;
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, c.P, ws.s_max);
-    return hip_status(launch_attn_int4(c, q, ws, al, s), "sparse int4 attention");
+    return hip_status(launch_attn_int4(c, q, ws, al, s), bits == 8 ? "sparse int8 attention" : "sparse int4 attention");
+}
+
+int fq_sparse_int4_fwd_mask(const fq_int4_cache* cache, const fq_query* query, const uint8_t* mask,
+                            const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
+                            fq_stream_t stream) {
+    return sparse_fwd_mask(cache, query, mask, mask_strides, workspace, workspace_bytes_, stream, 4);
+}
+
+int fq_sparse_int8_fwd_mask(const fq_int8_cache* cache, const fq_query* query, const uint8_t* mask,
+                            const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
+                            fq_stream_t stream) {
+    return sparse_fwd_mask(cache, query, mask, mask_strides, workspace, workspace_bytes_, stream, 8);
 }
 
 int fq_sparse_int4_fwd_ids(const fq_int4_cache* cache, const fq_query* query, const int32_t* ids,
@@ -354,14 +371,14 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
     return attn_selects_in_kernel(c, q, al);
 }
 
-int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
-                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
-                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
-                         fq_stream_t stream) {
+static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                        int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                        float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                        fq_stream_t stream, int bits) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
-    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws, bits);
     if (st) return st;
     if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
     if (select_mode != FQ_SELECT_PER_Q_HEAD && select_mode != FQ_SELECT_PER_KV_HEAD_SUM)
@@ -379,13 +396,21 @@ int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, cons
                       "score+select");
 }
 
+int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                         fq_stream_t stream) {
+    return quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out, mask_out,
+                        workspace, workspace_bytes_, stream, 4);
+}
+
 static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const float* retention, int32_t num_sinks,
                         int32_t window_pages, int32_t k_max, int32_t select_mode, const TailArgs* tail,
-                        void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+                        void* workspace, size_t workspace_bytes_, fq_stream_t stream, int bits = 4) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
-    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
+    int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws, bits);
     if (st) return st;
     if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
     if (num_sinks < 0) num_sinks = 0;
@@ -400,7 +425,8 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
     }
-    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail), "sparse int4 attention");
+    return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail),
+                      bits == 8 ? "sparse int8 attention" : "sparse int4 attention");
 }
 
 int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,
@@ -458,6 +484,53 @@ int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, cons
     if (st) return st;
     return fq_quest_attend_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, workspace,
                                 workspace_bytes_, stream);
+}
+
+int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                         fq_stream_t stream) {
+    int st = quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out, mask_out,
+                          workspace, workspace_bytes_, stream, 8);
+    if (st) return st;
+    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr, workspace,
+                        workspace_bytes_, stream, 8);
+}
+
+size_t fq_int8_workspace_bytes(const fq_int8_cache* cache, int32_t H_q) { return fq_workspace_bytes(cache, H_q); }
+
+int fq_page_scores_int8(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* k_scale,
+                        const int64_t ks_strides[4], const void* k_mn, const int64_t km_strides[4],
+                        int32_t meta_dtype, float* scores, const int64_t sc_strides[4], int32_t B,
+                        int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D, fq_stream_t stream) {
+    g_score_bits = 8;
+    const int st = fq_page_scores_int4(q, q_dtype, q_strides, k_scale, ks_strides, k_mn, km_strides, meta_dtype,
+                                       scores, sc_strides, B, H_q, S_q, H_kv, P, D, stream);
+    g_score_bits = 4;
+    return st;
+}
+
+int fq_quantize_k_int8(const void* k, int32_t in_dtype, const int64_t k_strides[4], int32_t B, int32_t H,
+                       int32_t S, int32_t D, int32_t page_size, uint8_t* codes, const int64_t c_strides[4],
+                       void* scale, const int64_t s_strides[4], void* mn, const int64_t m_strides[4],
+                       int32_t meta_dtype, fq_stream_t stream) {
+    if (D % 2) return fail(FQ_ERR_INVALID, "quantize_k requires even head_dim; got %d", D);
+    if (page_size < 1) return fail(FQ_ERR_INVALID, "page_size must be >= 1");
+    if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_quant_k(k, in_dtype, k_strides, B, H, S, D, page_size, codes, c_strides, scale,
+                                     s_strides, mn, m_strides, meta_dtype, (hipStream_t)stream, 8),
+                      "quantize k int8");
+}
+
+int fq_quantize_v_int8(const void* v, int32_t in_dtype, const int64_t v_strides[4], int32_t B, int32_t H,
+                       int32_t S, int32_t D, uint8_t* codes, const int64_t c_strides[4], void* scale,
+                       const int64_t s_strides[4], void* mn, const int64_t m_strides[4], int32_t meta_dtype,
+                       fq_stream_t stream) {
+    if (D % 2) return fail(FQ_ERR_INVALID, "quantize_v requires even head_dim; got %d", D);
+    if (!is_float_dtype(in_dtype) || !is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    return hip_status(launch_quant_v(v, in_dtype, v_strides, B, H, S, D, D, codes, c_strides, scale, s_strides, mn,
+                                     m_strides, meta_dtype, (hipStream_t)stream, 8),
+                      "quantize v int8");
 }
 
 int fq_merge_attn(const void* o_a, const float* lse_a, const void* o_b, const float* lse_b, int32_t dtype,

@@ -172,6 +172,7 @@ struct Int4Cache {
     const void* vmn;   int64_t vmn_s[4];
     int L, B, Hkv, S, P, D, page, G;
     int meta_dtype;                       // FQ_BF16 / FQ_F16
+    int bits;                             // code width: 4 (two codes per byte) or 8 (one byte per code); 0 = 4
 };
 
 struct QueryArgs {

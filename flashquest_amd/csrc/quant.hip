@@ -9,12 +9,15 @@ constexpr float kEps = 1e-6f;                 // kv_quant.py:14
 // Reciprocal torch's CUDA true-division uses for "tensor / 15.0"
 // (the divisor is a CPU scalar, so the kernel multiplies by fp32(1/15)).
 __device__ __constant__ float kInv15 = 1.0f / 15.0f;
+__device__ __constant__ float kInv255 = 1.0f / 255.0f;   // the INT8 quantisers' "/ 255.0"
 
 namespace {
 
 // -------------------------------------------------------------------------
-// quantize_k_int4 (kv_quant.py:131-171).  One thread per (b, h, page, channel
-// pair).  Scale arithmetic in the input dtype, codes by IEEE fp32 division.
+// quantize_k_int4 (kv_quant.py:131-171) and, BITS = 8, quantize_k
+// (kv_quant.py:18-61: "/ 255.0", codes 0..255 one per byte).  One thread per
+// (b, h, page, channel pair).  Scale arithmetic in the input dtype, codes by
+// IEEE fp32 division.
 // -------------------------------------------------------------------------
 struct QuantKParams {
     const void* k; int in_dtype; int64_t k_s[4];
@@ -25,7 +28,9 @@ struct QuantKParams {
     int meta_dtype;
 };
 
+template <int BITS>
 __global__ __launch_bounds__(kThreads) void quant_k_kernel(QuantKParams a) {
+    constexpr float kMaxCode = (1 << BITS) - 1;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     const int half_d = a.D / 2;
     const int64_t total = (int64_t)a.B * a.H * a.P * half_d;
@@ -49,7 +54,7 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(QuantKParams a) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const float diff = round_to(mx[u] - mn[u], a.in_dtype);
-        float s = round_to(diff * kInv15, a.in_dtype);
+        float s = round_to(diff * (BITS == 8 ? kInv255 : kInv15), a.in_dtype);
         s = round_to(fmaxf(s, kEps), a.in_dtype);
         sc[u] = s;
         const int64_t mo = b * a.s_s[0] + h * a.s_s[1] + p * a.s_s[2] + (2 * jp + u) * a.s_s[3];
@@ -63,16 +68,19 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(QuantKParams a) {
         for (int u = 0; u < 2; ++u) {
             const float v = load_any(a.k, a.in_dtype, base + t * a.k_s[2] + (2 * jp + u) * a.k_s[3]);
             float c = rintf(__fdiv_rn(v - mn[u], sc[u]));
-            c = fminf(fmaxf(c, 0.f), 15.f);
+            c = fminf(fmaxf(c, 0.f), kMaxCode);
+            if constexpr (BITS == 8)
+                a.packed[b * a.p_s[0] + h * a.p_s[1] + t * a.p_s[2] + (2 * jp + u) * a.p_s[3]] = (uint8_t)c;
             byte |= ((uint32_t)c) << (4 * u);
         }
-        a.packed[b * a.p_s[0] + h * a.p_s[1] + t * a.p_s[2] + jp * a.p_s[3]] = (uint8_t)byte;
+        if constexpr (BITS == 4) a.packed[b * a.p_s[0] + h * a.p_s[1] + t * a.p_s[2] + jp * a.p_s[3]] = (uint8_t)byte;
     }
 }
 
 // -------------------------------------------------------------------------
-// quantize_v_int4 (kv_quant.py:189-205), fp32 arithmetic.  One thread per
-// (b, h, token, channel group).
+// quantize_v_int4 (kv_quant.py:189-205) and, BITS = 8, quantize_v
+// (kv_quant.py:78-89), fp32 arithmetic.  One thread per (b, h, token,
+// channel group).
 // -------------------------------------------------------------------------
 struct QuantVParams {
     const void* v; int in_dtype; int64_t v_s[4];
@@ -83,7 +91,9 @@ struct QuantVParams {
     int meta_dtype;
 };
 
+template <int BITS>
 __global__ __launch_bounds__(kThreads) void quant_v_kernel(QuantVParams a) {
+    constexpr float kMaxCode = (1 << BITS) - 1;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     const int64_t total = (int64_t)a.B * a.H * a.S * a.G;
     if (idx >= total) return;
@@ -99,7 +109,7 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(QuantVParams a) {
         mn = fminf(mn, v);
         mx = fmaxf(mx, v);
     }
-    const float s = fmaxf((mx - mn) * kInv15, kEps);
+    const float s = fmaxf((mx - mn) * (BITS == 8 ? kInv255 : kInv15), kEps);
     store_any(a.scale, a.meta_dtype, b * a.s_s[0] + h * a.s_s[1] + t * a.s_s[2] + gi * a.s_s[3], s);
     store_any(a.mn, a.meta_dtype, b * a.m_s[0] + h * a.m_s[1] + t * a.m_s[2] + gi * a.m_s[3], mn);
     uint8_t* prow = a.packed + b * a.p_s[0] + h * a.p_s[1] + t * a.p_s[2];
@@ -109,10 +119,11 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(QuantVParams a) {
         for (int u = 0; u < 2; ++u) {
             const float v = load_any(a.v, a.in_dtype, base + (d + u) * a.v_s[3]);
             float c = rintf(__fdiv_rn(v - mn, s));
-            c = fminf(fmaxf(c, 0.f), 15.f);
+            c = fminf(fmaxf(c, 0.f), kMaxCode);
+            if constexpr (BITS == 8) prow[(d + u) * a.p_s[3]] = (uint8_t)c;
             byte |= ((uint32_t)c) << (4 * u);
         }
-        prow[(d / 2) * a.p_s[3]] = (uint8_t)byte;
+        if constexpr (BITS == 4) prow[(d / 2) * a.p_s[3]] = (uint8_t)byte;
     }
 }
 
@@ -332,7 +343,7 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + kThreads - 1) / k
 
 hipError_t launch_quant_k(const void* k, int in_dtype, const int64_t* k_s, int B, int H, int S, int D,
                           int page, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
-                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st) {
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st, int bits) {
     QuantKParams a{};
     a.k = k; a.in_dtype = in_dtype; a.B = B; a.H = H; a.S = S; a.D = D; a.page = page;
     a.P = (S + page - 1) / page;
@@ -340,13 +351,14 @@ hipError_t launch_quant_k(const void* k, int in_dtype, const int64_t* k_s, int B
     for (int i = 0; i < 4; ++i) { a.k_s[i] = k_s[i]; a.p_s[i] = p_s[i]; a.s_s[i] = s_s[i]; a.m_s[i] = m_s[i]; }
     const int64_t total = (int64_t)B * H * a.P * (D / 2);
     if (total == 0) return hipSuccess;
-    hipLaunchKernelGGL(quant_k_kernel, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    if (bits == 8) hipLaunchKernelGGL(quant_k_kernel<8>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL(quant_k_kernel<4>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_quant_v(const void* v, int in_dtype, const int64_t* v_s, int B, int H, int S, int D,
                           int group, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
-                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st) {
+                          void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st, int bits) {
     QuantVParams a{};
     a.v = v; a.in_dtype = in_dtype; a.B = B; a.H = H; a.S = S; a.D = D; a.group = group;
     a.G = D / group;
@@ -354,7 +366,8 @@ hipError_t launch_quant_v(const void* v, int in_dtype, const int64_t* v_s, int B
     for (int i = 0; i < 4; ++i) { a.v_s[i] = v_s[i]; a.p_s[i] = p_s[i]; a.s_s[i] = s_s[i]; a.m_s[i] = m_s[i]; }
     const int64_t total = (int64_t)B * H * S * a.G;
     if (total == 0) return hipSuccess;
-    hipLaunchKernelGGL(quant_v_kernel, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    if (bits == 8) hipLaunchKernelGGL(quant_v_kernel<8>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    else hipLaunchKernelGGL(quant_v_kernel<4>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 

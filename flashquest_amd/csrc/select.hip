@@ -74,7 +74,7 @@ struct ScoreParams {
 // Scores of one page for every query row (rows in LDS), computed by the NL lanes
 // of a page; emit(r, score) runs on all of them with the same value.
 template <int D, typename MT, typename Emit>
-FQ_DEV void score_page(const uint4& sv, const uint4& mv, const float (*s_q)[D], const float (*s_qp)[D], int rows,
+FQ_DEV void score_page(const uint4& sv, const uint4& mv, const float (*s_q)[D], const float (*s_qp)[D], int rows, float levels,
                        int lane_in_page, Emit emit) {
     constexpr int NL = D / 8;
     float sf[8], mf[8];
@@ -99,7 +99,7 @@ FQ_DEV void score_page(const uint4& sv, const uint4& mv, const float (*s_q)[D], 
         }
         t1 = row_sum<NL>(t1);
         t2 = row_sum<NL>(t2);
-        emit(r, __fadd_rn(t1, __fmul_rn(t2, 15.0f)));
+        emit(r, __fadd_rn(t1, __fmul_rn(t2, levels)));
     }
 }
 
@@ -192,6 +192,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     for (int u = 0; u < kPasses; ++u) fetch(u, u);
     load_q_rows<D>(a, l, b, h, s_q, s_qp);
     __syncthreads();
+    const float levels = c.bits == 8 ? 255.0f : 15.0f;     // INT8 / INT4 code range
     float qr[NR > 0 ? NR : 1][8], qp[NR > 0 ? NR : 1][8];
     if constexpr (NR > 0) {
 #pragma unroll
@@ -217,8 +218,8 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
                     }
                     acc_kv = r == 0 ? sc : __fadd_rn(acc_kv, sc);
                 };
-                if constexpr (NR > 0) score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, emit);
-                else score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.sum_rows ? 1 : a.rows, lane_in_page, emit);
+                if constexpr (NR > 0) score_page_regs<NR, MT>(sv[u], mv[u], qr, qp, emit, levels);
+                else score_page<D, MT>(sv[u], mv[u], s_q, s_qp, a.sum_rows ? 1 : a.rows, levels, lane_in_page, emit);
                 if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
                     ws_scores[p] = acc_kv;
             }

@@ -113,11 +113,12 @@ FQ_DEV int wave_select_group(const float* sc, int P, int nrep, int mode, const f
 // The fp32 order is fixed (and restated by the CPU oracle): a lane starts from
 // its first product (rounded) and adds the other 7 by fused multiply-adds, one
 // rounding each (fp16 metadata feeds v_fma_mix_f32 with no conversion); lanes
-// combine by the DPP butterfly in row_sum<16>, score = t1 + t2 * 15.
+// combine by the DPP butterfly in row_sum<16>, score = t1 + t2 * levels (15 for
+// INT4 metadata, criticality.py:161; 255 for INT8, criticality.py:123).
 // emit(r, score) runs on all 16 lanes with the same value.
 template <int NR, typename MT, typename Emit>
 FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[NR][8], const float (&qp)[NR][8],
-                            Emit emit) {
+                            Emit emit, float levels = 15.0f) {
     float sf[8], mf[8];
     const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
     const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
@@ -145,7 +146,7 @@ FQ_DEV void score_page_regs(const uint4& sv, const uint4& mv, const float (&qr)[
         t2[r] = row_sum<16>(t2[r]);
     }
 #pragma unroll
-    for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], 15.0f)));
+    for (int r = 0; r < NR; ++r) emit(r, __fadd_rn(t1[r], __fmul_rn(t2[r], levels)));
 }
 
 // The forced pages of a P-page row (selection.py:110-117): sinks [0, ns) and

@@ -140,6 +140,64 @@ def quest_decode_int4(
     return O, lse_out
 
 
+def quest_decode_int8(
+    Q: torch.Tensor,
+    K_uint8: torch.Tensor,
+    K_scale: torch.Tensor,
+    K_mn: torch.Tensor,
+    V_uint8: torch.Tensor,
+    V_scale: torch.Tensor,
+    V_mn: torch.Tensor,
+    *,
+    retention: float | torch.Tensor,
+    num_sinks: int = 4,
+    window_pages: int = 2,
+    k_max_static: int | None = None,
+    page_size: int = 64,
+    select_mode: str = "per_q_head",
+    sm_scale: float | None = None,
+    return_lse: bool = True,
+    return_selection: bool = False,
+):
+    """The INT8 decode step (llama_persistent_patch.py:143-160 with the
+    selection of 196-245): page_scores_int8_fast -> select_pages_vectorized ->
+    flash_attn_sparse_fwd over the completed pages, for one layer (Q
+    (B,H_q,1,D), 4D cache) or L layers at once (Q (L,B,H_q,1,D), 5D cache).
+    ``select_mode`` as quest_decode_int4.  Returns (O like Q, lse (..., H_q, 1)
+    fp32 or None[, mask (..., H_q, P) bool])."""
+    if select_mode not in L.SELECT_MODES:
+        raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
+    L.require_device(Q, K_uint8, K_scale)
+    if Q.shape[-2] != 1:
+        raise NotImplementedError(f"quest_decode_int8: decode-only (S_q={Q.shape[-2]})")
+    D = Q.shape[-1]
+    if D not in (64, 128):
+        raise NotImplementedError(f"head_dim={D} not in (64, 128)")
+    Q3 = Q[..., 0, :]
+    H_q = Q3.shape[-2]
+    P = K_scale.shape[-2]
+    O3 = torch.empty_like(Q3)
+    lse = torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device) if return_lse else None
+    cache, keep = _ops.int8_cache(K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, page_size)
+    if H_q % cache.H_kv:
+        raise ValueError(f"H_q={H_q} must be divisible by H_kv={cache.H_kv}")
+    query = _ops.query(Q3, O3, lse, sm_scale)
+    r = _ops.retention_tensor(retention, H_q, Q.device)
+    k_max = -1 if k_max_static is None else min(int(k_max_static), P)
+    mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device) if return_selection else None
+    ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q))
+    L.check(L.lib().fq_quest_decode_int8(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
+                                         L.SELECT_MODES[select_mode], None,
+                                         None if mask is None else mask.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+            "quest_decode_int8")
+    O = O3.unsqueeze(-2)
+    lse_out = lse.unsqueeze(-1) if lse is not None else None
+    if return_selection:
+        return O, lse_out, mask
+    return O, lse_out
+
+
 def quest_decode_turbo(
     Q: torch.Tensor,
     K_msb: torch.Tensor,

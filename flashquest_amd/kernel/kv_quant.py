@@ -1,7 +1,8 @@
 """KV quantisers on HIP kernels.
 
-Mirrors src/flashquest/kernel/kv_quant.py: INT4 (104-215) and TurboQuant
-K3-V3 (225-420).  Codes and metadata are bit-exact with the reference's CUDA
+Mirrors src/flashquest/kernel/kv_quant.py: INT8 (18-100: quantize_k /
+quantize_v, 255 levels, one code byte per channel), INT4 (104-215) and
+TurboQuant K3-V3 (225-420).  Codes and metadata are bit-exact with the reference's CUDA
 semantics: K scale arithmetic in the input dtype ((max - min) and "/ 15.0",
 the latter as a multiply by fp32(1/15) the way torch's CUDA division by a
 Python scalar does), codes by IEEE fp32 division, round-half-even, clamp
@@ -19,6 +20,62 @@ from .. import _lib as L
 K_TURBO_CODEBOOK = torch.tensor(
     [-2.1519, -1.3439, -0.7560, -0.2451, 0.2451, 0.7560, 1.3439, 2.1519], dtype=torch.float32)
 V_TURBO_CODEBOOK = K_TURBO_CODEBOOK.clone()
+
+
+def quantize_k(K: torch.Tensor, page_size: int, *, meta_dtype: torch.dtype = torch.bfloat16, out=None):
+    """kv_quant.py:43-61.  K (B, H, S, D) -> (K_uint8 (B,H,S,D) u8, scale
+    (B,H,P,D), mn (B,H,P,D)) with P = ceil(S / page_size); scale/min arithmetic
+    in K's dtype ("/ 255.0"), codes by fp32 division, round half even, clamp
+    0..255, metadata stored as ``meta_dtype`` (bf16 in the reference)."""
+    L.require_device(K)
+    B, H, S, D = K.shape
+    if D % 2 != 0:
+        raise ValueError(f"quantize_k requires even head_dim; got {D}")
+    P = (S + page_size - 1) // page_size
+    if out is None:
+        codes = torch.empty(B, H, S, D, dtype=torch.uint8, device=K.device)
+        scale = torch.empty(B, H, P, D, dtype=meta_dtype, device=K.device)
+        mn = torch.empty(B, H, P, D, dtype=meta_dtype, device=K.device)
+    else:
+        codes, scale, mn = out
+    L.check(L.lib().fq_quantize_k_int8(
+        K.data_ptr(), L.dtype_code(K.dtype), L.strides(K, 4), B, H, S, D, page_size,
+        codes.data_ptr(), L.strides(codes, 4), scale.data_ptr(), L.strides(scale, 4),
+        mn.data_ptr(), L.strides(mn, 4), L.dtype_code(scale.dtype), L.stream_handle(K.device)), "quantize_k")
+    return codes, scale, mn
+
+
+def quantize_v(V: torch.Tensor, *, meta_dtype: torch.dtype = torch.bfloat16, out=None):
+    """kv_quant.py:78-89.  V (B, H, S, D) -> (V_uint8 (B,H,S,D) u8, scale
+    (B,H,S,1), mn (B,H,S,1)), per token over all D in fp32."""
+    L.require_device(V)
+    B, H, S, D = V.shape
+    if D % 2 != 0:
+        raise ValueError(f"quantize_v requires even head_dim; got {D}")
+    if out is None:
+        codes = torch.empty(B, H, S, D, dtype=torch.uint8, device=V.device)
+        scale = torch.empty(B, H, S, 1, dtype=meta_dtype, device=V.device)
+        mn = torch.empty(B, H, S, 1, dtype=meta_dtype, device=V.device)
+    else:
+        codes, scale, mn = out
+    L.check(L.lib().fq_quantize_v_int8(
+        V.data_ptr(), L.dtype_code(V.dtype), L.strides(V, 4), B, H, S, D,
+        codes.data_ptr(), L.strides(codes, 4), scale.data_ptr(), L.strides(scale, 4),
+        mn.data_ptr(), L.strides(mn, 4), L.dtype_code(scale.dtype), L.stream_handle(V.device)), "quantize_v")
+    return codes, scale, mn
+
+
+def dequantize_k(K_uint8: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor, page_size: int) -> torch.Tensor:
+    """kv_quant.py:64-75 (tensor ops; prefill / test helper, not the decode path).  Returns bf16."""
+    S = K_uint8.shape[2]
+    s = scale.repeat_interleave(page_size, dim=2)[:, :, :S, :]
+    m = mn.repeat_interleave(page_size, dim=2)[:, :, :S, :]
+    return (K_uint8.to(torch.float32) * s.float() + m.float()).to(torch.bfloat16)
+
+
+def dequantize_v(V_uint8: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor) -> torch.Tensor:
+    """kv_quant.py:92-97 (tensor ops).  Returns bf16."""
+    return (V_uint8.to(torch.float32) * scale.float() + mn.float()).to(torch.bfloat16)
 
 
 def _pack_int4(x: torch.Tensor) -> torch.Tensor:

@@ -72,6 +72,12 @@ typedef struct fq_int4_cache {
     int32_t v_groups;        /* G: 1 (reference) or D/32 */
 } fq_int4_cache;
 
+/* INT8 cache view (cache/persistent_int8.py get_views): the same descriptor
+ * with one code byte per channel -- k_packed / v_packed hold K_uint8 / V_uint8
+ * (L, B, H_kv, S, D) -- K scale/min per (page, channel) and V scale/min per
+ * token (v_groups = 1).  Code strides are multiples of 8 bytes. */
+typedef fq_int4_cache fq_int8_cache;
+
 /* Decode query and outputs: Q (L, B, H_q, D), O (L, B, H_q, D), lse (L, B, H_q). */
 typedef struct fq_query {
     const void* q;   int32_t q_dtype;   int64_t q_strides[4];
@@ -312,6 +318,53 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache,
                           const fq_query* query, const float* retention,
                           int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                           uint8_t* mask_out, void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* ---- INT8 family (kv_bits = 8, the reference dispatcher's default) ---- */
+
+/* Workspace for the INT8 entry points (same sizing as fq_workspace_bytes). */
+size_t fq_int8_workspace_bytes(const fq_int8_cache* cache, int32_t H_q);
+
+/* Replaces page_scores_int8_fast (criticality.py:77-125): score = Q.K_mn +
+ * 255 * relu(Q).K_scale, fp32 in this library's fixed order; same arguments
+ * as fq_page_scores_int4. */
+int fq_page_scores_int8(const void* q, int32_t q_dtype, const int64_t q_strides[4],
+                        const void* k_scale, const int64_t ks_strides[4],
+                        const void* k_mn, const int64_t km_strides[4], int32_t meta_dtype,
+                        float* scores, const int64_t sc_strides[4],
+                        int32_t B, int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D,
+                        fq_stream_t stream);
+
+/* Replaces flash_attn_sparse_fwd (kernel/sparse_fwd.py:160-228, kernel
+ * 23-157): sparse GQA decode attention over the INT8 cache for a boolean page
+ * mask (L*B, H_q, P) (strides as fq_sparse_int4_fwd_mask). */
+int fq_sparse_int8_fwd_mask(const fq_int8_cache* cache, const fq_query* query,
+                            const uint8_t* mask, const int64_t mask_strides[4],
+                            void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* The INT8 decode step of llama_persistent_patch.py:143-160 with the selection
+ * of 196-245 (page_scores_int8_fast, select_pages_vectorized,
+ * flash_attn_sparse_fwd) for every (layer, batch, KV head) at once; arguments
+ * as fq_quest_decode_int4. */
+int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes,
+                         fq_stream_t stream);
+
+/* Replace quantize_k / quantize_v (kernel/kv_quant.py:43-61, 78-89): uint8
+ * codes, K scale/min per (page, channel) with the arithmetic in the input
+ * dtype ("/ 255.0"), V per token in fp32; metadata written as meta_dtype. */
+int fq_quantize_k_int8(const void* k, int32_t in_dtype, const int64_t k_strides[4],
+                       int32_t B, int32_t H, int32_t S, int32_t D, int32_t page_size,
+                       uint8_t* codes, const int64_t c_strides[4],
+                       void* scale, const int64_t s_strides[4],
+                       void* mn, const int64_t m_strides[4], int32_t meta_dtype,
+                       fq_stream_t stream);
+int fq_quantize_v_int8(const void* v, int32_t in_dtype, const int64_t v_strides[4],
+                       int32_t B, int32_t H, int32_t S, int32_t D,
+                       uint8_t* codes, const int64_t c_strides[4],
+                       void* scale, const int64_t s_strides[4],
+                       void* mn, const int64_t m_strides[4], int32_t meta_dtype,
+                       fq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -42,6 +42,7 @@ import numpy as np
 F32 = np.float32
 EPS = F32(1e-6)                       # kv_quant.py:14  _EPS = 1e-6
 INV15 = F32(1.0) / F32(15.0)          # fp32 reciprocal used by CUDA for "/ 15.0"
+INV255 = F32(1.0) / F32(255.0)        # likewise for the INT8 quantisers' "/ 255.0"
 LOG2E = 1.4426950408889634
 
 # kv_quant.py:225-229 (K_TURBO_CODEBOOK; V uses the same codebook, :230)
@@ -130,8 +131,8 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
 # Quantisers (kv_quant.py:131-215)
 # ----------------------------------------------------------------------------
 
-def scale_mn_per_page_channel_int4(K: np.ndarray, page_size: int, dtype: str = "bf16"):
-    """kv_quant.py:131-149.
+def scale_mn_per_page_channel_int4(K: np.ndarray, page_size: int, dtype: str = "bf16", inv=None):
+    """kv_quant.py:131-149 (INT4, "/ 15.0"); with inv=INV255 kv_quant.py:18-40 (INT8).
 
     K: (..., S, D) fp32 values exactly representable in ``dtype``.
     Arithmetic happens in the input dtype: (mx - mn) and "/ 15.0" are each
@@ -148,7 +149,7 @@ def scale_mn_per_page_channel_int4(K: np.ndarray, page_size: int, dtype: str = "
     mn = kmin.reshape(*lead, P, page_size, D).min(axis=-2)
     mx = kmax.reshape(*lead, P, page_size, D).max(axis=-2)
     diff = rnd(mx - mn)
-    scale = rnd(diff * INV15)
+    scale = rnd(diff * (INV15 if inv is None else inv))
     scale = rnd(np.maximum(scale, EPS))
     return scale, mn
 
@@ -213,6 +214,80 @@ def dequant_v(packed, scale, mn):
     G = scale.shape[-1]
     c = codes.reshape(*lead, S, G, D // G)
     return (c * scale[..., None] + mn[..., None]).reshape(*lead, S, D)
+
+
+# ----------------------------------------------------------------------------
+# INT8 KV (kernel/kv_quant.py:18-100, kernel/sparse_fwd.py:23-157)
+# ----------------------------------------------------------------------------
+
+def quantize_k_int8(K: np.ndarray, page_size: int, dtype: str = "bf16", meta: str = "bf16"):
+    """kv_quant.py:43-61: per-page, per-channel asymmetric uint8 for K.
+
+    scale/mn as kv_quant.py:18-40 in the input dtype ((mx - mn) and "/ 255.0"
+    each rounded to ``dtype``, clamp_min(1e-6)); codes by fp32 division with
+    those (dtype) values, round half even, clamp 0..255; the meta is returned
+    rounded to ``meta`` (the reference casts it to bf16 after the codes).
+    Returns (codes (..., S, D) u8, scale (..., P, D) f32, mn (..., P, D) f32).
+    """
+    K = np.asarray(K, dtype=F32)
+    *lead, S, D = K.shape
+    scale, mn = scale_mn_per_page_channel_int4(K, page_size, dtype, inv=INV255)
+    tok_scale = np.repeat(scale, page_size, axis=-2)[..., :S, :]
+    tok_mn = np.repeat(mn, page_size, axis=-2)[..., :S, :]
+    codes = np.clip(np.rint((K - tok_mn) / tok_scale), 0, 255).astype(np.uint8)
+    mrnd = rounder(meta)
+    return codes, mrnd(scale), mrnd(mn)
+
+
+def quantize_v_int8(V: np.ndarray, meta: str = "bf16"):
+    """kv_quant.py:78-89: per-token uint8 for V over all D channels, in fp32
+    (mn, mx, scale = max((mx - mn) * fp32(1/255), 1e-6), codes by fp32
+    division, round half even, clamp 0..255); meta rounded to ``meta`` after.
+    Returns (codes (..., S, D) u8, scale (..., S, 1), mn (..., S, 1))."""
+    V = np.asarray(V, dtype=F32)
+    mn = V.min(axis=-1, keepdims=True)
+    mx = V.max(axis=-1, keepdims=True)
+    scale = np.maximum((mx - mn) * INV255, EPS)
+    codes = np.clip(np.rint((V - mn) / scale), 0, 255).astype(np.uint8)
+    mrnd = rounder(meta)
+    return codes, mrnd(scale), mrnd(mn)
+
+
+def dequant_k_int8(codes, scale, mn, page_size):
+    """kv_quant.py:64-75 / sparse_fwd.py:95-96: codes*fp32(scale)+fp32(mn) (fp32, no final rounding)."""
+    c = np.asarray(codes).astype(F32)
+    S = c.shape[-2]
+    tok_scale = np.repeat(np.asarray(scale, F32), page_size, axis=-2)[..., :S, :]
+    tok_mn = np.repeat(np.asarray(mn, F32), page_size, axis=-2)[..., :S, :]
+    return c * tok_scale + tok_mn
+
+
+def dequant_v_int8(codes, scale, mn):
+    """kv_quant.py:92-97 / sparse_fwd.py:121-126: per-token codes*scale+mn in fp32."""
+    return np.asarray(codes).astype(F32) * np.asarray(scale, F32) + np.asarray(mn, F32)
+
+
+def page_scores_int8_exact(Q, K_scale, K_mn):
+    """criticality.py:77-125 in fp64: Q.mn + 255 * relu(Q).scale (GQA view)."""
+    Q = np.asarray(Q, np.float64)
+    B, Hq, D = Q.shape
+    Hkv = K_scale.shape[1]
+    rep = Hq // Hkv
+    qg = Q.reshape(B, Hkv, rep, D)
+    t1 = qg @ np.swapaxes(np.asarray(K_mn, np.float64), -1, -2)
+    t2 = np.maximum(qg, 0) @ np.swapaxes(np.asarray(K_scale, np.float64), -1, -2)
+    return (t1 + 255.0 * t2).reshape(B, Hq, -1)
+
+
+def sparse_int8_attention(Q, K_u8, K_scale, K_mn, V_u8, V_scale, V_mn, page_mask, page_size=64,
+                          sm_scale=None):
+    """flash_attn_sparse_fwd semantics (sparse_fwd.py:23-157, wrapper 160-228), exact.
+    Returns (O fp64, lse fp64)."""
+    keys = dequant_k_int8(K_u8, K_scale, K_mn, page_size)
+    vals = dequant_v_int8(V_u8, V_scale, V_mn)
+    S = keys.shape[-2]
+    tm = page_mask_to_token_mask(page_mask, S, page_size)
+    return exact_attention(Q, keys, vals, tm, sm_scale)
 
 
 # ----------------------------------------------------------------------------
@@ -304,7 +379,7 @@ def _lane_fma_butterfly(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return t[..., 0]
 
 
-def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head"):
+def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head", levels: float = 15.0):
     """criticality.py:128-163 with this build's fixed fp32 evaluation order.
 
     Per (query head r, page p): t1 = sum_d q_d*mn_d, t2 = sum_d relu(q_d)*scale_d
@@ -334,7 +409,7 @@ def page_scores_fixed(Q, K_scale, K_mn, mode: str = "per_q_head"):
     sc = np.asarray(K_scale, F32)[:, :, None, :, :]
     t1 = _lane_fma_butterfly(qg, mn)
     t2 = _lane_fma_butterfly(qpos, sc)
-    s = (t1 + (t2 * F32(15.0)).astype(F32)).astype(F32)      # (B, Hkv, rows, P)
+    s = (t1 + (t2 * F32(levels)).astype(F32)).astype(F32)    # (B, Hkv, rows, P); 255 for INT8
     if mode == "per_q_head":
         return s.reshape(B, Hq, P)
     return s[:, :, 0, :]
@@ -687,7 +762,7 @@ def unrotate_signed(y: np.ndarray, signs: np.ndarray) -> np.ndarray:
 
 def decode_step(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention,
                 num_sinks, window_pages, page_size=64, mode="per_q_head",
-                k_max_static=None):
+                k_max_static=None, bits=4):
     """Score -> select -> sparse attention for one layer.
 
     Returns dict(scores, mask (B,H_q,P), O fp64, lse fp64).  ``mode``
@@ -698,7 +773,7 @@ def decode_step(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retentio
     B, Hq, D = Q.shape
     Hkv, P = K_scale.shape[1], K_scale.shape[2]
     rep = Hq // Hkv
-    scores = page_scores_fixed(Q, K_scale, K_mn, mode)
+    scores = page_scores_fixed(Q, K_scale, K_mn, mode, 255.0 if bits == 8 else 15.0)
     if mode == "per_q_head":
         mask = select_pages_vectorized(scores[:, :, None, :], retention, num_sinks,
                                        window_pages, k_max_static)[:, :, 0, :]
@@ -707,6 +782,6 @@ def decode_step(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retentio
         m = select_pages_vectorized(scores[:, :, None, :], r, num_sinks, window_pages,
                                     k_max_static)[:, :, 0, :]
         mask = np.repeat(m, rep, axis=1)
-    O, lse = sparse_int4_attention(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
-                                   mask, page_size)
+    attn = sparse_int8_attention if bits == 8 else sparse_int4_attention
+    O, lse = attn(Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask, page_size)
     return {"scores": scores, "mask": mask, "O": O, "lse": lse}

@@ -66,3 +66,25 @@ def max_err(gpu: torch.Tensor, ref: np.ndarray) -> float:
     if not finite.any():
         return 0.0
     return float(np.abs(g[finite] - ref[finite]).max())
+
+
+class Int8Case:
+    """Oracle-quantised INT8 cache (kv_quant.py:43-89) + query, host and device."""
+
+    def __init__(self, seed, B=1, Hq=6, Hkv=2, S=1024, D=128, page=64, dtype="bf16", meta="bf16", outliers=True):
+        rng = np.random.default_rng(seed)
+        self.B, self.Hq, self.Hkv, self.S, self.D, self.page = B, Hq, Hkv, S, D, page
+        self.dtype, self.meta = dtype, meta
+        self.K, self.V = make_kv(rng, B, Hkv, S, D, dtype, outliers)
+        self.Q = O.rounder(dtype)(rng.standard_normal((B, Hq, D)).astype(np.float32))
+        self.ku, self.ks, self.km = O.quantize_k_int8(self.K, page, dtype, meta)
+        self.vu, self.vs, self.vm = O.quantize_v_int8(self.V, meta)
+        self.P = self.ks.shape[-2]
+
+    def device(self):
+        return dict(K_uint8=to_dev(self.ku), K_scale=to_dev_half(self.ks, self.meta),
+                    K_mn=to_dev_half(self.km, self.meta), V_uint8=to_dev(self.vu),
+                    V_scale=to_dev_half(self.vs, self.meta), V_mn=to_dev_half(self.vm, self.meta))
+
+    def q_dev(self):
+        return to_dev_half(self.Q, self.dtype)[:, :, None, :]
