@@ -274,6 +274,12 @@ bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q);
 hipError_t launch_attn_turbo_fused(const fq_turbo_cache& c, const Int4Cache* raw, const QueryArgs& q,
                                    const Workspace& ws, int max_entries, const SelectArgs* sel, hipStream_t st);
 bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+// INT8 cache on the matrix cores (attn_int8_mfma.hip): D = 128, 64-token pages,
+// per-token V metadata, dense rows, <= 4 query heads per KV head.
+bool int8_mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+bool int8_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
+                                 hipStream_t st, const SelectArgs* sel);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,

@@ -72,7 +72,8 @@ FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int
 }
 
 template <typename MT, int NREP, int NT, bool SUM>
-FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P) {
+FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P,
+                             float levels = 15.0f) {
     constexpr int PPP = NT / 16;
     const int lip = tid & 15, pip = tid >> 4;
     // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
@@ -105,7 +106,7 @@ FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128]
         const int p = u * PPP + pip;
         score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
             if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
-        });
+        }, levels);
     }
 }
 
