@@ -341,7 +341,10 @@ def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: i
                         page_size: int, k_max_static: int | None = None, select_mode: str = "per_q_head"):
     """The decode branch of llama_persistent_patch.py:202-245 for one layer.
 
-    ``views`` is PersistentInt4KVCache.get_views(layer) (persistent_int4.py:134-159).
+    ``views`` is get_views(layer) of a persistent INT4, INT8 or TurboQuant
+    cache (persistent_int4.py:134-159, persistent_int8.py:137-169,
+    persistent_turbo.py:149-176); the family follows from its keys, as the
+    reference's kv_bits dispatch (llama_persistent_patch.py:74-163).
     Returns attention output (B, H_q, 1, D) in q's dtype.
     """
     completed = views["completed_len"]
@@ -349,18 +352,26 @@ def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: i
     if completed == 0:
         o, _ = bf16_dense_attn_with_lse(q, views["K_partial"], views["V_partial"])
         return o.to(q.dtype)
-    args = (q, views["K_packed"], views["K_scale"], views["K_mn"], views["V_packed"], views["V_scale"],
-            views["V_mn"])
     kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
               page_size=page_size, select_mode=select_mode)
-    if partial > 0:
-        try:
-            # one fused call: the tail is attended in the split-merge launch
-            o, _ = quest_decode_int4(*args, K_tail=views["K_partial"], V_tail=views["V_partial"], **kw)
-            return o
-        except NotImplementedError:
-            pass                              # layouts the fused tail does not take: three operators
-    o_sparse, lse_sparse = quest_decode_int4(*args, **kw)
+    if "K_uint8" in views:                    # INT8 (kv_bits 8)
+        o_sparse, lse_sparse = quest_decode_int8(q, views["K_uint8"], views["K_scale"], views["K_mn"],
+                                                 views["V_uint8"], views["V_scale"], views["V_mn"], **kw)
+    elif "K_msb" in views:                    # TurboQuant K3-V3 (kv_bits 3)
+        o_sparse, lse_sparse = quest_decode_turbo(q, views["K_msb"], views["K_lsb"], views["K_scale_turbo"],
+                                                  views["V_msb"], views["V_lsb"], views["V_scale_turbo"],
+                                                  views["K_scale_raw"], views["K_mn_raw"], **kw)
+    else:                                     # INT4 (kv_bits 4)
+        args = (q, views["K_packed"], views["K_scale"], views["K_mn"], views["V_packed"], views["V_scale"],
+                views["V_mn"])
+        if partial > 0:
+            try:
+                # one fused call: the tail is attended with the selected pages
+                o, _ = quest_decode_int4(*args, K_tail=views["K_partial"], V_tail=views["V_partial"], **kw)
+                return o
+            except NotImplementedError:
+                pass                          # layouts the fused tail does not take: three operators
+        o_sparse, lse_sparse = quest_decode_int4(*args, **kw)
     if partial == 0:
         return o_sparse
     o_tail, lse_tail = bf16_dense_attn_with_lse(q.to(views["K_partial"].dtype), views["K_partial"],

@@ -74,7 +74,9 @@ def test_page_scores_int8_bit_exact(Hq, Hkv, D, meta):
 
 @pytest.mark.parametrize("Hq,Hkv,D,S,dtype,meta", [(24, 8, 128, 64 * 20 + 17, "bf16", "bf16"),
                                                    (8, 8, 64, 64 * 9, "f16", "f16"),
-                                                   (16, 2, 128, 64 * 12, "bf16", "bf16")])
+                                                   (16, 2, 128, 64 * 12, "bf16", "bf16"),
+                                                   (16, 4, 128, 64 * 7 + 1, "f16", "f16"),
+                                                   (8, 8, 128, 64 * 5, "bf16", "f16")])
 def test_flash_attn_sparse_fwd_matches_oracle(Hq, Hkv, D, S, dtype, meta):
     from flashquest_amd.kernel import flash_attn_sparse_fwd
     case = Int8Case(seed=S + Hq, B=2, Hq=Hq, Hkv=Hkv, S=S, D=D, dtype=dtype, meta=meta)
@@ -102,11 +104,15 @@ def test_flash_attn_sparse_fwd_errors():
         flash_attn_sparse_fwd(q, **d, selection_mask=m[..., :2])
 
 
-@pytest.mark.parametrize("layers,mode", [(1, "per_q_head"), (12, "per_kv_head_sum"), (12, "per_q_head")])
-def test_quest_decode_int8_matches_oracle_decode_step(layers, mode):
+@pytest.mark.parametrize("layers,mode,meta", [(1, "per_q_head", "bf16"), (12, "per_kv_head_sum", "bf16"),
+                                              (12, "per_q_head", "f16"), (24, "per_kv_head_sum", "f16")])
+def test_quest_decode_int8_matches_oracle_decode_step(layers, mode, meta):
+    # 1 and 12 layers: groups split over several workgroups, each selecting;
+    # 24 layers x 8 KV heads: one workgroup per group
     from flashquest_amd.eager import quest_decode_int8
     Hq, Hkv, P = 24, 8, 20
-    cases = [Int8Case(seed=60 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * (P - 1) + 30, D=128) for i in range(layers)]
+    cases = [Int8Case(seed=60 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * (P - 1) + 30, D=128, meta=meta)
+             for i in range(layers)]
     dev = [c.device() for c in cases]
     if layers > 1:
         stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
@@ -155,3 +161,31 @@ def test_persistent_int8_cache_appends_match_one_quantisation():
         cache.update_quantized(Kd[:, :, :100], Vd[:, :, :100], layer_idx=1)
     with pytest.raises(RuntimeError):
         cache.update(Kd, Vd, 0)
+
+
+@pytest.mark.parametrize("partial", [0, 29])
+def test_decode_layer_over_int8_cache_views(partial):
+    # the decode branch of the reference's attention patch with kv_bits = 8
+    # (llama_persistent_patch.py:143-160, 202-245): INT8 sparse attention on the
+    # completed pages, dense bf16 attention on the tail, LSE merge
+    from flashquest_amd.cache import PersistentInt8KVCache
+    from flashquest_amd.eager.decode import sparse_decode_layer
+    rng = np.random.default_rng(31 + partial)
+    B, Hq, H, D, P = 1, 6, 2, 128, 12
+    S = 64 * P + partial
+    K, V = make_kv(rng, B, H, S, D, "bf16")
+    Q = O.round_bf16(rng.standard_normal((B, Hq, D)).astype(np.float32))
+    cache = PersistentInt8KVCache(batch_size=B, num_layers=1, num_kv_heads=H, head_dim=D, max_seq_len=S)
+    cache.update_quantized(to_dev_half(K, "bf16"), to_dev_half(V, "bf16"), 0)
+    views = cache.get_views(0)
+    out = sparse_decode_layer(to_dev_half(Q, "bf16")[:, :, None, :], views, retention=0.3, num_sinks=1,
+                              window_pages=1, page_size=64)
+    comp = 64 * P
+    ku, ks, km = O.quantize_k_int8(K[:, :, :comp], 64)
+    vu, vs, vm = O.quantize_v_int8(V[:, :, :comp])
+    ref = O.decode_step(Q, ku, ks, km, vu, vs, vm, retention=0.3, num_sinks=1, window_pages=1, bits=8)
+    O_ref = ref["O"]
+    if partial:
+        ot, lt = O.dense_attn_with_lse(Q, K[:, :, comp:], V[:, :, comp:])
+        O_ref = O.merge_two_attentions(O.round_bf16(O_ref), ref["lse"], O.round_bf16(ot), lt)
+    assert max_err(out[:, :, 0], O_ref) <= 2e-2
