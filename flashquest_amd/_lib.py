@@ -59,6 +59,15 @@ class Tail(ctypes.Structure):
     ]
 
 
+class Prefill(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_strides", _I64x4),
+        ("out", ctypes.c_void_p), ("o_strides", _I64x4),
+        ("H_q", ctypes.c_int32), ("S_q", ctypes.c_int32),
+        ("causal_offset", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+    ]
+
+
 class TurboCache(ctypes.Structure):
     _fields_ = [
         ("k_msb", ctypes.c_void_p), ("kmsb_strides", _I64x5),
@@ -131,6 +140,9 @@ SIGNATURES = {
                                           _I, _P]),
     "fq_quantize_v_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
                                           _I, _P]),
+    # prefill over the packed cache
+    "fq_prefill_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill), _P]),
+    "fq_prefill_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill), _P]),
 }
 
 _lib = None

@@ -30,6 +30,8 @@ hipError_t launch_tail(const void* q, const int64_t* q_s, const void* k, const i
                        int Hq, int Hkv, int T, int D, hipStream_t st);
 hipError_t launch_attn_turbo(const fq_turbo_cache& c, const QueryArgs& q, const Workspace& ws,
                              const AttnLaunch& al, hipStream_t st);
+hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, const int64_t* q_s, void* out,
+                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, hipStream_t st);
 
 static thread_local std::string g_err;
 
@@ -117,11 +119,18 @@ static bool rows_aligned16(const void* p, const int64_t* strides, int n_outer, i
 
 // bits = 4: packed INT4 (two codes per byte); bits = 8: one code byte per
 // channel (the INT8 cache of flash_attn_sparse_fwd), V metadata per token.
-static int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits = 4) {
+static int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits = 4, bool allow_empty = false) {
     if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
     if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
     if (!is_half(c->meta_dtype)) return fail(FQ_ERR_UNSUPPORTED, "metadata dtype must be bf16 or fp16");
     if (c->L < 1 || c->B < 1 || c->H_kv < 1) return fail(FQ_ERR_INVALID, "empty L/B/H_kv");
+    if (allow_empty && c->S == 0) {   // no completed pages: nothing of the cache is read
+        Int4Cache& o = *out;
+        o = Int4Cache{};
+        o.L = c->L; o.B = c->B; o.Hkv = c->H_kv; o.D = c->D; o.page = c->page_size > 0 ? c->page_size : 1;
+        o.G = 1; o.meta_dtype = c->meta_dtype; o.bits = bits;
+        return FQ_OK;
+    }
     if (c->P < 1 || c->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d outside [1, %d]", c->P, kMaxPages);
     if (c->page_size < 1 || c->page_size > 4096) return fail(FQ_ERR_INVALID, "page_size=%d", c->page_size);
     if (c->S < 0) return fail(FQ_ERR_INVALID, "negative S");
@@ -736,6 +745,61 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     if (fusable) return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, nullptr, s), "quest turbo decode");
     const AttnLaunch al = choose_split(G, bound, ws.s_max);
     return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "quest turbo decode");
+}
+
+static bool aligned(const void* p, int bytes) { return ((uintptr_t)p & (uintptr_t)(bytes - 1)) == 0; }
+
+static int prefill(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* q, fq_stream_t stream, int bits) {
+    Int4Cache c{};
+    int st = check_cache(cache, &c, bits, true);
+    if (st) return st;
+    if (c.L != 1) return fail(FQ_ERR_INVALID, "prefill takes one layer's cache view (L=%d)", c.L);
+    if (c.D != 128) return fail(FQ_ERR_UNSUPPORTED, "prefill head_dim=%d (128 only)", c.D);
+    if (c.S > 0) {
+        if ((int64_t)c.P * c.page < c.S) return fail(FQ_ERR_INVALID, "%d pages of %d tokens < S=%d", c.P, c.page, c.S);
+        const int kal = bits == 4 ? 8 : 16;   // one thread loads 16 channels of codes
+        for (int i = 0; i < 4; ++i)
+            if (c.kp_s[i] % kal) return fail(FQ_ERR_UNSUPPORTED, "K code strides must be multiples of %d bytes", kal);
+        if (!aligned(c.kp, kal)) return fail(FQ_ERR_UNSUPPORTED, "K codes must be %d-byte aligned", kal);
+    }
+    TailArgs t{};
+    if (tail && tail->len > 0) {
+        if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
+        if (tail->dtype != FQ_BF16) return fail(FQ_ERR_UNSUPPORTED, "prefill tail must be bf16");
+        if (tail->D != c.D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, c.D);
+        if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
+            return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
+        for (int i = 1; i < 4; ++i)
+            if (tail->k_strides[i] % 8 || tail->v_strides[i] % 4)
+                return fail(FQ_ERR_UNSUPPORTED, "tail row strides must be multiples of 8 (K) / 4 (V) elements");
+        if (!aligned(tail->k, 16) || !aligned(tail->v, 8)) return fail(FQ_ERR_UNSUPPORTED, "tail K/V alignment");
+        t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
+        for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
+    }
+    if (!q || !q->q || !q->out) return fail(FQ_ERR_INVALID, "query/output is NULL");
+    if (q->H_q < 1 || q->H_q % c.Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, c.Hkv);
+    if (q->S_q < 1) return fail(FQ_ERR_INVALID, "S_q=%d", q->S_q);
+    if (q->causal_offset < 0) return fail(FQ_ERR_INVALID, "causal_offset=%d must be >= 0", q->causal_offset);
+    if ((int64_t)c.S + t.len < 1) return fail(FQ_ERR_INVALID, "no keys (S + tail = 0)");
+    if (q->q_strides[3] != 1 || q->o_strides[3] != 1) return fail(FQ_ERR_UNSUPPORTED, "Q/O channels must be contiguous");
+    for (int i = 0; i < 3; ++i)
+        if (q->q_strides[i] % 8 || q->o_strides[i] % 4)
+            return fail(FQ_ERR_UNSUPPORTED, "Q / O strides must be multiples of 8 / 4 elements");
+    if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
+    const int64_t rows = (int64_t)q->S_q * (q->H_q / c.Hkv);
+    if ((rows + 255) / 256 * c.Hkv * c.B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
+    const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)c.D);
+    return hip_status(launch_prefill(c, t, q->q, q->q_strides, q->out, q->o_strides, q->H_q / c.Hkv, q->S_q,
+                                     q->causal_offset, sm * kLog2e, (hipStream_t)stream),
+                      "prefill attention launch");
+}
+
+int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream) {
+    return prefill(cache, tail, query, stream, 4);
+}
+
+int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream) {
+    return prefill(cache, tail, query, stream, 8);
 }
 
 }  // extern "C"

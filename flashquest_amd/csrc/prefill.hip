@@ -1,0 +1,373 @@
+// Causal prefill attention over the packed KV cache on the gfx950 matrix cores.
+//
+// Semantics (S_q > 1 branch of the reference's attention patch,
+// src/flashquest/eager/llama_persistent_patch.py:196-201):
+//   K_full = cat(dequantize(K codes), K_partial)   (dequantize_k_int4 / dequantize_k,
+//   V_full = cat(dequantize(V codes), V_partial)    kv_quant.py:174-186, 208-215, 64-100)
+//   O = SDPA(q, K_full, V_full, is_causal=True, enable_gqa=True)
+// Each dequantised element is code * scale + mn in fp32 (the product of a code
+// and a half-precision scale is exact in fp32, so one FMA rounds the same as
+// the reference's multiply then add) rounded to bf16 -- the same bf16 K / V the
+// reference feeds SDPA.  Query row i attends keys j <= i + causal_off;
+// causal_off = 0 is torch's is_causal (upper-left aligned when S_q < S_kv).
+//
+// One 8-wave workgroup per (256 GQA-flattened query rows, KV head): row
+// m = pos * n_rep + r is query position pos of head kvh * n_rep + r, so every
+// K/V tile a workgroup dequantises serves all n_rep heads of the group.  Per
+// 64-key tile all 512 threads dequantise K into LDS as [key][channel] bf16 and
+// V transposed as [channel][key] bf16 (the tile after next is fetched into
+// registers while the current one is computed), then each wave runs
+//   S^T = K Q^T     v_mfma_f32_16x16x32_bf16, 4 key blocks x 2 query blocks
+//   online softmax  per query column (base 2, fp32), P rounded to bf16
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16, 8 channel blocks x 2 query blocks
+// Computing the transposed products keeps each lane on one query column, so
+// the softmax statistics are per lane and P leaves the S^T accumulator already
+// in the layout of the P^T operand (keys 4g..4g+3 and 16+4g..16+4g+3 of a
+// 32-key step; V^T is read with the same key order).
+#include "fq_common.h"
+
+namespace fq {
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kPD = 128;               // head dim
+constexpr int kPW = 8;                 // waves per workgroup
+constexpr int kPKT = 64;               // keys per tile
+constexpr int kPRW = 32;               // query rows per wave (two 16-column blocks)
+constexpr int kPRows = kPW * kPRW;     // query rows per workgroup
+constexpr int kKStr = kPD + 8;         // bf16 per K row in LDS (272 B: conflict-free 16-byte reads)
+constexpr int kVStr = kPKT + 8;        // bf16 per V^T row in LDS (144 B)
+
+struct PrefillParams {
+    Int4Cache c;
+    TailArgs t;            // bf16 tail rows (the partial page), keys S .. S + t.len - 1
+    const void* q; int64_t q_s[3];     // (b, h_q, pos) element strides, channels contiguous
+    void* out; int64_t o_s[3];
+    int nrep, Sq, Skv, causal_off;
+    float qk_scale;                    // sm_scale * log2(e)
+};
+
+// Raw bytes of one thread's K slice (one key, 16 channels) before dequantisation.
+struct KFetch {
+    uint4 c0, c1;          // codes (INT4: c0.xy, INT8: c0) or 16 bf16 tail values
+    uint4 s0, s1, m0, m1;  // 16 half scales / mins
+    int kind;              // 0 codes, 1 tail, 2 beyond the keys (zeros)
+};
+// One thread's V slice: 4 keys x 4 channels.
+struct VFetch {
+    uint2 raw[4];          // per key: codes (INT4: 16 bits, INT8: 32 bits) or 4 bf16 tail values
+    uint32_t sm[4];        // per key: scale | mn << 16 (half bits)
+    int kinds;             // 2 bits per key, as KFetch::kind
+};
+
+FQ_DEV float half_bits(uint32_t h, int meta_dtype) {
+    return meta_dtype == FQ_BF16 ? bf16_bits_to_f(h & 0xFFFFu) : f16_bits_to_f(h & 0xFFFFu);
+}
+FQ_DEV uint32_t word_of(const uint4& a, const uint4& b, int i) {   // dword i of the 8-dword pair
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    return w[i];
+}
+FQ_DEV uint32_t bf16_rne(float f) {    // fp32 -> bf16 bits, round to nearest even (finite inputs)
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+template <int BITS>
+FQ_DEV void fetch_k(KFetch& f, const PrefillParams& a, int b, int h, int key, int kc) {
+    const Int4Cache& c = a.c;
+    if (key < c.S) {
+        f.kind = 0;
+        const uint8_t* row = c.kp + b * c.kp_s[1] + h * c.kp_s[2] + (int64_t)key * c.kp_s[3];
+        if (BITS == 4) {
+            const uint2 v = *(const uint2*)(row + kc / 2);
+            f.c0 = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            f.c0 = *(const uint4*)(row + kc);
+        }
+        const int64_t page = key / c.page;
+        const uint16_t* ks = (const uint16_t*)c.ksc + b * c.ksc_s[1] + h * c.ksc_s[2] + page * c.ksc_s[3] + kc;
+        const uint16_t* km = (const uint16_t*)c.kmn + b * c.kmn_s[1] + h * c.kmn_s[2] + page * c.kmn_s[3] + kc;
+        f.s0 = *(const uint4*)ks; f.s1 = *(const uint4*)(ks + 8);
+        f.m0 = *(const uint4*)km; f.m1 = *(const uint4*)(km + 8);
+    } else if (key < a.Skv) {
+        f.kind = 1;
+        const uint16_t* row = (const uint16_t*)a.t.k + b * a.t.ks[1] + h * a.t.ks[2] + (int64_t)(key - c.S) * a.t.ks[3] + kc;
+        f.c0 = *(const uint4*)row; f.c1 = *(const uint4*)(row + 8);
+    } else {
+        f.kind = 2;
+    }
+}
+
+template <int BITS>
+FQ_DEV void store_k(const KFetch& f, uint16_t* dst, int meta_dtype) {
+    uint4 o0 = make_uint4(0u, 0u, 0u, 0u), o1 = o0;
+    if (f.kind == 1) {
+        o0 = f.c0; o1 = f.c1;
+    } else if (f.kind == 0) {
+        uint32_t packed[8];
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            uint32_t lo, hi;
+            if (BITS == 4) {
+                const uint32_t byte = (word_of(f.c0, f.c0, i >> 3) >> (8 * ((i >> 1) & 3))) & 0xFFu;
+                lo = byte & 15u; hi = byte >> 4;          // even channel in the low nibble
+            } else {
+                const uint32_t wd = word_of(f.c0, f.c0, i >> 2);
+                lo = (wd >> (8 * (i & 3))) & 0xFFu; hi = (wd >> (8 * (i & 3) + 8)) & 0xFFu;
+            }
+            const uint32_t sw = word_of(f.s0, f.s1, i >> 1), mw = word_of(f.m0, f.m1, i >> 1);
+            const float v0 = fmaf((float)lo, half_bits(sw, meta_dtype), half_bits(mw, meta_dtype));
+            const float v1 = fmaf((float)hi, half_bits(sw >> 16, meta_dtype), half_bits(mw >> 16, meta_dtype));
+            packed[i >> 1] = bf16_rne(v0) | (bf16_rne(v1) << 16);
+        }
+        o0 = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        o1 = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+    *(uint4*)dst = o0;
+    *(uint4*)(dst + 8) = o1;
+}
+
+template <int BITS>
+FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, int vd) {
+    const Int4Cache& c = a.c;
+    const int grp = vd / (kPD / c.G);
+    f.kinds = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int key = key0 + j;
+        f.raw[j] = make_uint2(0u, 0u);
+        f.sm[j] = 0u;
+        if (key < c.S) {
+            const uint8_t* row = c.vp + b * c.vp_s[1] + h * c.vp_s[2] + (int64_t)key * c.vp_s[3];
+            f.raw[j].x = BITS == 4 ? (uint32_t)*(const uint16_t*)(row + vd / 2) : *(const uint32_t*)(row + vd);
+            const uint16_t* vs = (const uint16_t*)c.vsc + b * c.vsc_s[1] + h * c.vsc_s[2] + (int64_t)key * c.vsc_s[3] + grp;
+            const uint16_t* vm = (const uint16_t*)c.vmn + b * c.vmn_s[1] + h * c.vmn_s[2] + (int64_t)key * c.vmn_s[3] + grp;
+            f.sm[j] = (uint32_t)*vs | ((uint32_t)*vm << 16);
+        } else if (key < a.Skv) {
+            f.kinds |= 1 << (2 * j);
+            const uint16_t* row = (const uint16_t*)a.t.v + b * a.t.vs[1] + h * a.t.vs[2] + (int64_t)(key - c.S) * a.t.vs[3] + vd;
+            f.raw[j] = *(const uint2*)row;
+        } else {
+            f.kinds |= 2 << (2 * j);
+        }
+    }
+}
+
+template <int BITS>
+FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */, int meta_dtype) {
+    uint32_t v[4][4];   // [key][channel] bf16 bits
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int kind = (f.kinds >> (2 * j)) & 3;
+        const float sc = half_bits(f.sm[j], meta_dtype), mn = half_bits(f.sm[j] >> 16, meta_dtype);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t code = BITS == 4 ? (f.raw[j].x >> (4 * i)) & 15u : (f.raw[j].x >> (8 * i)) & 0xFFu;
+            const uint32_t tail = ((i < 2 ? f.raw[j].x : f.raw[j].y) >> (16 * (i & 1))) & 0xFFFFu;
+            const uint32_t deq = bf16_rne(fmaf((float)code, sc, mn));
+            v[j][i] = kind == 0 ? deq : (kind == 1 ? tail : 0u);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *(uint2*)(dst + i * kVStr) = make_uint2(v[0][i] | (v[1][i] << 16), v[2][i] | (v[3][i] << 16));
+}
+
+template <int BITS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_attn_kernel(PrefillParams a) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPKT * kKStr];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * kVStr];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const Int4Cache& c = a.c;
+    // KV head in the low bits of the block index: consecutive blocks go to
+    // different XCDs, so with H_kv * B a multiple of 8 each XCD's L2 holds the
+    // K/V of its own heads.  Row blocks run last-first (the longest first).
+    const int HB = c.Hkv * c.B;
+    const int nblk = gridDim.x / HB;
+    const int hb = blockIdx.x % HB;
+    const int rb = nblk - 1 - (int)(blockIdx.x / HB);
+    const int h = hb % c.Hkv, b = hb / c.Hkv;
+    const int Mtot = a.Sq * a.nrep;
+    const int m0 = rb * kPRows;
+    const int last_wg = (min(m0 + kPRows, Mtot) - 1) / a.nrep;
+    const int nt = (min(a.Skv, last_wg + a.causal_off + 1) + kPKT - 1) / kPKT;
+
+    const int mw0 = m0 + w * kPRW;
+    const bool wave_on = mw0 < Mtot;
+    const int pmin = min(mw0, Mtot - 1) / a.nrep;
+    const int pmax = (min(mw0 + kPRW, Mtot) - 1) / a.nrep;
+    const int limit_w = min(a.Skv, pmax + a.causal_off + 1);
+
+    // this lane's two query columns: B operands of q.k (channels 32 ks + 8 g .. + 8)
+    int qpos[2];
+    bool qok[2];
+    const uint16_t* qrow[2];
+    v8bf qf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int m = mw0 + qb * 16 + n;
+        qok[qb] = m < Mtot;
+        const int mm = qok[qb] ? m : mw0;
+        qpos[qb] = qok[qb] ? mm / a.nrep : pmin;
+        const int hq = h * a.nrep + mm % a.nrep;
+        qrow[qb] = (const uint16_t*)a.q + b * a.q_s[0] + hq * a.q_s[1] + (int64_t)(mm / a.nrep) * a.q_s[2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (wave_on) qf[qb][ks] = *(const v8bf*)(qrow[qb] + 32 * ks + 8 * g);
+            else qf[qb][ks] = v8bf{};
+        }
+    }
+
+    v4f o[2][8];
+    float m_run[2], l_run[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        m_run[qb] = -INFINITY; l_run[qb] = 0.f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int kk = tid >> 3, kc = (tid & 7) * 16;      // K loader: one key, 16 channels
+    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4; // V loader: 4 keys, 4 channels
+    KFetch kf;
+    VFetch vf;
+    if (nt > 0) {
+        fetch_k<BITS>(kf, a, b, h, kk, kc);
+        fetch_v<BITS>(vf, a, b, h, vk, vd);
+        store_k<BITS>(kf, &s_k[0][kk * kKStr + kc], c.meta_dtype);
+        store_v<BITS>(vf, &s_v[0][vd * kVStr + vk], c.meta_dtype);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < nt; ++t) {
+        const int cur = t & 1;
+        const int key0 = t * kPKT;
+        if (t + 1 < nt) {
+            fetch_k<BITS>(kf, a, b, h, key0 + kPKT + kk, kc);
+            fetch_v<BITS>(vf, a, b, h, key0 + kPKT + vk, vd);
+        }
+        if (wave_on && key0 < limit_w) {
+            const uint16_t* sk = s_k[cur];
+            const uint16_t* sv = s_v[cur];
+            v4f s[2][4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                s[0][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+                s[1][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kKStr + 32 * ks + 8 * g);
+                    s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[0][ks], s[0][kb], 0, 0, 0);
+                    s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[1][ks], s[1][kb], 0, 0, 0);
+                }
+            }
+            const bool need_mask = key0 + kPKT - 1 > pmin + a.causal_off || key0 + kPKT > a.Skv;
+            v8bf pb[2][2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                if (need_mask) {
+                    const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1);
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc)
+                            if (key0 + kb * 16 + 4 * g + cc > lim) s[qb][kb][cc] = -INFINITY;
+                }
+                float mx = s[qb][0][0];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) mx = fmaxf(mx, s[qb][kb][cc]);
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m_run[qb], mx * a.qk_scale);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+                float sum = 0.f;
+                float p[4][4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
+                        p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], a.qk_scale, -m_use));
+                        sum += p[kb][cc];
+                    }
+                l_run[qb] = fmaf(l_run[qb], alpha, sum);
+                m_run[qb] = m_new;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) o[qb][db] *= alpha;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
+                        pb[qb][j][cc] = (__bf16)p[2 * j][cc];
+                        pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
+                    }
+            }
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const uint16_t* vrow = sv + (db * 16 + n) * kVStr + 4 * g;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint2 lo = *(const uint2*)(vrow + 32 * j);
+                    const uint2 hi = *(const uint2*)(vrow + 32 * j + 16);
+                    const v8bf av = __builtin_bit_cast(v8bf, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[0][j], o[0][db], 0, 0, 0);
+                    o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[1][j], o[1][db], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < nt) {
+            store_k<BITS>(kf, &s_k[cur ^ 1][kk * kKStr + kc], c.meta_dtype);
+            store_v<BITS>(vf, &s_v[cur ^ 1][vd * kVStr + vk], c.meta_dtype);
+        }
+        __syncthreads();
+    }
+
+    if (!wave_on) return;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float l = l_run[qb];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (!qok[qb]) continue;
+        const float inv = 1.0f / l;
+        const int m = mw0 + qb * 16 + n;
+        const int hq = h * a.nrep + m % a.nrep;
+        uint16_t* orow = (uint16_t*)a.out + b * a.o_s[0] + hq * a.o_s[1] + (int64_t)(m / a.nrep) * a.o_s[2];
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const v4f r = o[qb][db] * inv;
+            *(uint2*)(orow + db * 16 + 4 * g) =
+                make_uint2(bf16_rne(r[0]) | (bf16_rne(r[1]) << 16), bf16_rne(r[2]) | (bf16_rne(r[3]) << 16));
+        }
+    }
+}
+
+}  // namespace
+
+// Launch the prefill kernel.  The caller has checked shapes, strides and
+// alignment (capi.cpp: fq_prefill_int4 / fq_prefill_int8).
+hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, const int64_t* q_s, void* out,
+                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, hipStream_t st) {
+    PrefillParams a{};
+    a.c = c;
+    a.t = t;
+    a.q = q; a.out = out;
+    for (int i = 0; i < 3; ++i) { a.q_s[i] = q_s[i]; a.o_s[i] = o_s[i]; }
+    a.nrep = nrep; a.Sq = Sq; a.Skv = c.S + t.len; a.causal_off = causal_off; a.qk_scale = qk_scale;
+    const int64_t rows = (int64_t)Sq * nrep;
+    const int64_t nblk = (rows + kPRows - 1) / kPRows;
+    const dim3 grid((unsigned)(nblk * c.Hkv * c.B));
+    timer_before_launch(st);
+    if (c.bits == 8) hipLaunchKernelGGL(prefill_attn_kernel<8>, grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL(prefill_attn_kernel<4>, grid, dim3(512), 0, st, a);
+    timer_after_launch(st);
+    return hipGetLastError();
+}
+
+}  // namespace fq

@@ -386,7 +386,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             l_acc += pr[T];
         }
         if (lg < NREP) {
-            const int row = lg, kq = n16 & 3 ^ ((row >> 2) & 3);
+            const int row = lg, kq = (n16 & 3) ^ ((row >> 2) & 3);
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const float x0 = pr[2 * st] * vs_t[2 * st] * inv_s, x1 = pr[2 * st + 1] * vs_t[2 * st + 1] * inv_s;

@@ -5,4 +5,5 @@ from .decode import (  # noqa: F401
     quest_decode_turbo,
     sparse_decode_layer,
 )
+from .prefill import prefill_attention_layer  # noqa: F401
 from .selection import build_compact_selection, select_pages, select_pages_vectorized  # noqa: F401

@@ -366,6 +366,31 @@ int fq_quantize_v_int8(const void* v, int32_t in_dtype, const int64_t v_strides[
                        void* mn, const int64_t m_strides[4], int32_t meta_dtype,
                        fq_stream_t stream);
 
+/* Prefill query and output of fq_prefill_int4 / fq_prefill_int8:
+ * Q, O (B, H_q, S_q, D) bf16, element strides, channels contiguous. */
+typedef struct fq_prefill {
+    const void* q; int64_t q_strides[4];
+    void* out;     int64_t o_strides[4];
+    int32_t H_q, S_q;
+    int32_t causal_offset; /* query i attends keys j <= i + causal_offset (>= 0); 0 = torch is_causal */
+    float sm_scale;        /* <= 0 selects 1/sqrt(D) */
+} fq_prefill;
+
+/* The S_q > 1 (prefill) branch of the reference's attention patch,
+ * src/flashquest/eager/llama_persistent_patch.py:196-201:
+ *   SDPA(q, cat(dequantize_k_int4(cache), K_partial),
+ *           cat(dequantize_v_int4(cache), V_partial), is_causal=True, enable_gqa=True)
+ * with dequantize_k_int4 / dequantize_v_int4 of kernel/kv_quant.py:174-186,
+ * 208-215, fused: the packed codes are dequantised to bf16 tile by tile in the
+ * attention kernel.  cache: one layer (L == 1), S completed tokens (S may be 0),
+ * D == 128; tail: the bf16 partial-page rows (len >= 0, any length), keys S..
+ * S + len - 1.  FQ_ERR_UNSUPPORTED for layouts the kernel does not take. */
+int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream);
+
+/* The same over the INT8 cache (llama_persistent_patch.py:143-150:
+ * dequantize_k / dequantize_v, kernel/kv_quant.py:64-100). */
+int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

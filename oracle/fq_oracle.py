@@ -26,6 +26,10 @@ Pinning status (what checks each function; see tests/test_oracle_*.py):
                                       + fp64 closed form + upper-bound invariant
   select_pages_vectorized, compact    reference KATs + brute-force sort
   exact attention / merge / tail      closed forms (dense softmax, merge identity)
+  causal_prefill_attention            torch SDPA (is_causal, enable_gqa) on the CPU,
+                                      one-key and uniform-key closed forms
+  dequant_cache_bf16                  round trip within scale / 2, bf16 rounding
+                                      of the fp32 FMA checked elementwise
   wht128                              Sylvester Hadamard matrix, self-inverse
   quantize_*_turbo                    codebook KATs, bit-split round trip;
                                       rms reduction order: parity unpinned
@@ -531,6 +535,63 @@ def exact_attention(q, keys, values, token_mask, sm_scale=None):
     O = np.einsum("bhs,bhsd->bhd", p, v) / lsafe
     lse = np.where(l[..., 0] == 0, -np.inf, msafe[..., 0] + np.log(lsafe[..., 0]))
     return O, lse
+
+
+def dequant_cache_bf16(codes_or_packed, K_or_V: str, scale, mn, page_size: int = 64, bits: int = 4):
+    """The reference's prefill dequantisers, rounded to bf16 like them:
+    dequantize_k_int4 / dequantize_v_int4 (kernel/kv_quant.py:174-186, 208-215)
+    for bits 4 and dequantize_k / dequantize_v (64-75, 92-97) for bits 8:
+    fp32 code * scale + mn, then bf16.  Returns fp32 holding bf16 values."""
+    codes = unpack_int4(codes_or_packed) if bits == 4 else np.asarray(codes_or_packed)
+    codes = codes.astype(F32)
+    scale = np.asarray(scale, F32)
+    mn = np.asarray(mn, F32)
+    if K_or_V == "K":
+        S = codes.shape[-2]
+        s = np.repeat(scale, page_size, axis=-2)[..., :S, :]
+        m = np.repeat(mn, page_size, axis=-2)[..., :S, :]
+        out = (codes * s).astype(F32) + m
+    else:
+        *lead, S, D = codes.shape
+        G = scale.shape[-1]
+        c = codes.reshape(*lead, S, G, D // G)
+        out = ((c * scale[..., None]).astype(F32) + mn[..., None]).reshape(*lead, S, D)
+    return round_bf16(out.astype(F32))
+
+
+def causal_prefill_attention(q, keys, values, causal_offset: int = 0, sm_scale=None):
+    """F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)
+    as the reference's prefill calls it (llama_persistent_patch.py:196-201),
+    in fp64: query i attends keys j <= i + causal_offset, where torch's
+    is_causal is causal_offset = 0 (the upper-left aligned tril(ones(S_q, S_kv)))
+    and S_kv - S_q gives the lower-right alignment.  GQA: query head h uses KV
+    head h // (H_q / H_kv).  q (B,H_q,S_q,D); keys/values (B,H_kv,S_kv,D)."""
+    q = np.asarray(q, np.float64)
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = keys.shape[1], keys.shape[2]
+    rep = Hq // Hkv
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    k = np.repeat(np.asarray(keys, np.float64), rep, axis=1)
+    v = np.repeat(np.asarray(values, np.float64), rep, axis=1)
+    logits = np.einsum("bhid,bhjd->bhij", q, k) * sm_scale
+    allowed = np.arange(Skv)[None, :] <= np.arange(Sq)[:, None] + causal_offset
+    logits = np.where(allowed, logits, -np.inf)
+    m = logits.max(-1, keepdims=True)
+    p = np.exp(logits - m)
+    return np.einsum("bhij,bhjd->bhid", p, v) / p.sum(-1, keepdims=True)
+
+
+def prefill_packed(q, K_codes, K_scale, K_mn, V_codes, V_scale, V_mn, K_tail, V_tail, *, page_size: int = 64,
+                   bits: int = 4, causal_offset: int = 0, sm_scale=None):
+    """llama_persistent_patch.py:196-201: cat(dequant(cache), tail) then causal
+    SDPA (fp64 over the bf16 K/V the reference builds)."""
+    K = dequant_cache_bf16(K_codes, "K", K_scale, K_mn, page_size, bits)
+    V = dequant_cache_bf16(V_codes, "V", V_scale, V_mn, page_size, bits)
+    if K_tail is not None and K_tail.shape[-2] > 0:
+        K = np.concatenate([K, round_bf16(np.asarray(K_tail, F32))], axis=-2)
+        V = np.concatenate([V, round_bf16(np.asarray(V_tail, F32))], axis=-2)
+    return causal_prefill_attention(q, K, V, causal_offset, sm_scale)
 
 
 def page_mask_to_token_mask(page_mask, S: int, page_size: int):

@@ -1,0 +1,154 @@
+"""Prefill over the packed cache (llama_persistent_patch.py:196-201) on HIP vs
+the CPU oracle: causal GQA attention over cat(dequantised cache, bf16 tail),
+INT4 and INT8 codes, both causal alignments, and at a larger size vs torch's
+SDPA over the reference's own dequantise-then-concatenate tensors."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import fq_oracle as O
+from tests.cases import make_kv, to_dev, to_dev_half
+
+pytestmark = pytest.mark.gpu
+
+# bf16 Q/K/V, fp32 softmax, P and O rounded to bf16: |O| <= max|V|, so half a
+# bf16 ulp of O plus the P rounding stays well inside this bound
+ATOL = 1.5e-2
+
+
+class PrefillCase:
+    def __init__(self, seed, B=1, Hq=6, Hkv=2, S=256, T=0, Sq=None, D=128, page=64, bits=4, meta="bf16",
+                 vgroup=None, causal_offset=0):
+        rng = np.random.default_rng(seed)
+        self.S, self.T, self.page, self.bits, self.off = S, T, page, bits, causal_offset
+        self.Sq = S + T if Sq is None else Sq
+        K, V = make_kv(rng, B, Hkv, S + T, D, "bf16")
+        Kc, Vc = K[:, :, :S], V[:, :, :S]
+        self.Kt, self.Vt = K[:, :, S:], V[:, :, S:]
+        if bits == 4:
+            self.kc, self.ks, self.km = O.quantize_k_int4(Kc, page, "bf16", meta)
+            self.vc, self.vs, self.vm = O.quantize_v_int4(Vc, vgroup, meta)
+        else:
+            self.kc, self.ks, self.km = O.quantize_k_int8(Kc, page, "bf16", meta)
+            self.vc, self.vs, self.vm = O.quantize_v_int8(Vc, meta)
+        self.meta = meta
+        self.Q = O.round_bf16(rng.standard_normal((B, Hq, self.Sq, D)).astype(np.float32))
+
+    def run(self):
+        from flashquest_amd.kernel import flash_attn_prefill_int4, flash_attn_prefill_int8
+        fn = flash_attn_prefill_int4 if self.bits == 4 else flash_attn_prefill_int8
+        m = self.meta
+        return fn(to_dev_half(self.Q, "bf16"), to_dev(self.kc), to_dev_half(self.ks, m), to_dev_half(self.km, m),
+                  to_dev(self.vc), to_dev_half(self.vs, m), to_dev_half(self.vm, m),
+                  to_dev_half(self.Kt, "bf16"), to_dev_half(self.Vt, "bf16"), page_size=self.page,
+                  causal_offset=self.off)
+
+    def oracle(self):
+        return O.prefill_packed(self.Q, self.kc, self.ks, self.km, self.vc, self.vs, self.vm, self.Kt, self.Vt,
+                                page_size=self.page, bits=self.bits, causal_offset=self.off)
+
+
+def _check(case):
+    out = case.run()
+    torch.cuda.synchronize()
+    ref = case.oracle()
+    g = out.float().cpu().numpy()
+    assert g.shape == ref.shape
+    assert np.isfinite(g).all()
+    err = float(np.abs(g - ref).max())
+    assert err < ATOL, err
+    return err
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (2, 2), (8, 4), (8, 1), (24, 8)])
+def test_prefill_int4_whole_prompt(Hq, Hkv):
+    # the first prefill: the cache holds the prompt (completed pages + tail), S_q == S_kv
+    _check(PrefillCase(Hq + Hkv, Hq=Hq, Hkv=Hkv, S=320, T=23))
+
+
+@pytest.mark.parametrize("S,T,Sq,off", [(512, 0, 64, 0), (512, 40, 100, 0), (512, 40, 100, 452),
+                                        (1024, 63, 300, 787), (128, 5, 3, 0)])
+def test_prefill_int4_chunk(S, T, Sq, off):
+    # a later chunk: S_q < S_kv; off 0 is torch's is_causal (the reference's call), S_kv - S_q lower-right
+    _check(PrefillCase(S + T + Sq, S=S, T=T, Sq=Sq, causal_offset=off))
+
+
+@pytest.mark.parametrize("kw", [dict(meta="f16"), dict(vgroup=32), dict(page=32, S=256, T=31),
+                                dict(page=128, S=384, T=100), dict(S=0, T=77), dict(S=448, T=0),
+                                dict(B=2, S=192, T=9), dict(S=64, T=1, Sq=65)])
+def test_prefill_int4_layouts(kw):
+    _check(PrefillCase(7, **kw))
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(meta="f16"), dict(Sq=90, causal_offset=0, T=12),
+                                dict(Hq=8, Hkv=2, S=640, T=33), dict(S=0, T=50)])
+def test_prefill_int8(kw):
+    _check(PrefillCase(11, bits=8, **kw))
+
+
+def test_prefill_matches_sdpa_at_size():
+    """S_kv = 4096 + 37, 24 / 8 heads: vs F.scaled_dot_product_attention over
+    the reference's dequantise + concatenate tensors (llama_persistent_patch.py:196-201)."""
+    from flashquest_amd.kernel import dequantize_k_int4, dequantize_v_int4, flash_attn_prefill_int4, quantize_k_int4, \
+        quantize_v_int4
+    torch.manual_seed(0)
+    dev = torch.device("cuda:0")
+    S, T = 4096, 37
+    K = torch.randn(1, 8, S + T, 128, device=dev).to(torch.bfloat16)
+    V = torch.randn(1, 8, S + T, 128, device=dev).to(torch.bfloat16)
+    q = torch.randn(1, 24, S + T, 128, device=dev).to(torch.bfloat16)
+    kp, ks, km = quantize_k_int4(K[:, :, :S].contiguous(), 64)
+    vp, vs, vm = quantize_v_int4(V[:, :, :S].contiguous())
+    out = flash_attn_prefill_int4(q, kp, ks, km, vp, vs, vm, K[:, :, S:], V[:, :, S:], page_size=64)
+    Kf = torch.cat([dequantize_k_int4(kp, ks, km, 64), K[:, :, S:]], dim=2)
+    Vf = torch.cat([dequantize_v_int4(vp, vs, vm), V[:, :, S:]], dim=2)
+    ref = F.scaled_dot_product_attention(q.float(), Kf.float(), Vf.float(), is_causal=True, enable_gqa=True)
+    ref_bf16 = F.scaled_dot_product_attention(q, Kf, Vf, is_causal=True, enable_gqa=True)
+    err = (out.float() - ref).abs().max().item()
+    err_sdpa = (ref_bf16.float() - ref).abs().max().item()
+    assert err < max(2 * err_sdpa, 1e-2), (err, err_sdpa)
+
+
+def test_prefill_rejects_bad_arguments():
+    from flashquest_amd.kernel import flash_attn_prefill_int4
+    c = PrefillCase(1, S=128, T=0)
+    args = [to_dev(c.kc), to_dev_half(c.ks, "bf16"), to_dev_half(c.km, "bf16"), to_dev(c.vc),
+            to_dev_half(c.vs, "bf16"), to_dev_half(c.vm, "bf16")]
+    q = to_dev_half(c.Q, "bf16")
+    with pytest.raises(ValueError):
+        flash_attn_prefill_int4(q[:, :5], *args)                      # H_q not a multiple of H_kv
+    with pytest.raises(ValueError):
+        flash_attn_prefill_int4(q, *args, causal_offset=-1)
+    with pytest.raises(NotImplementedError):
+        flash_attn_prefill_int4(q[..., :64].contiguous(), *[a[..., :32] if i in (0, 3) else a[..., :64] if i in (1, 2)
+                                                           else a for i, a in enumerate(args)])
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prefill_over_persistent_cache_views(bits):
+    """The patch's prefill step: update_quantized(k, v) then attention over the
+    layer's views, for a first chunk and a second chunk (S_q < S_kv, is_causal)."""
+    from flashquest_amd.cache import PersistentInt4KVCache, PersistentInt8KVCache
+    from flashquest_amd.eager import prefill_attention_layer
+    rng = np.random.default_rng(40 + bits)
+    B, Hq, H, D = 1, 6, 2, 128
+    n1, n2 = 300, 77
+    K, V = make_kv(rng, B, H, n1 + n2, D, "bf16")
+    Q = O.round_bf16(rng.standard_normal((B, Hq, n1 + n2, D)).astype(np.float32))
+    cls = PersistentInt4KVCache if bits == 4 else PersistentInt8KVCache
+    cache = cls(batch_size=B, num_layers=1, num_kv_heads=H, head_dim=D, max_seq_len=512)
+    for lo, hi in ((0, n1), (n1, n1 + n2)):
+        cache.update_quantized(to_dev_half(K[:, :, lo:hi], "bf16"), to_dev_half(V[:, :, lo:hi], "bf16"), 0)
+        views = cache.get_views(0)
+        out = prefill_attention_layer(to_dev_half(Q[:, :, lo:hi], "bf16"), views, page_size=64)
+        comp = views["completed_len"]
+        if bits == 4:
+            kc, ks, km = O.quantize_k_int4(K[:, :, :comp], 64)
+            vc, vs, vm = O.quantize_v_int4(V[:, :, :comp])
+        else:
+            kc, ks, km = O.quantize_k_int8(K[:, :, :comp], 64)
+            vc, vs, vm = O.quantize_v_int8(V[:, :, :comp])
+        ref = O.prefill_packed(Q[:, :, lo:hi], kc, ks, km, vc, vs, vm, K[:, :, comp:hi], V[:, :, comp:hi],
+                               page_size=64, bits=bits)
+        assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
