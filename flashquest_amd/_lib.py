@@ -141,8 +141,12 @@ SIGNATURES = {
     "fq_quantize_v_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
                                           _I, _P]),
     # prefill over the packed cache
-    "fq_prefill_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill), _P]),
-    "fq_prefill_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill), _P]),
+    "fq_prefill_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill),
+                                       _P, ctypes.c_size_t, _P]),
+    "fq_prefill_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill),
+                                       _P, ctypes.c_size_t, _P]),
+    "fq_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail),
+                                                     ctypes.POINTER(Prefill), _I]),
 }
 
 _lib = None

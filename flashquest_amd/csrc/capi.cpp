@@ -31,7 +31,9 @@ hipError_t launch_tail(const void* q, const int64_t* q_s, const void* k, const i
 hipError_t launch_attn_turbo(const fq_turbo_cache& c, const QueryArgs& q, const Workspace& ws,
                              const AttnLaunch& al, hipStream_t st);
 hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, const int64_t* q_s, void* out,
-                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, hipStream_t st);
+                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, void* ws,
+                          hipStream_t st);
+size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep);
 
 static thread_local std::string g_err;
 
@@ -749,8 +751,9 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p & (uintptr_t)(bytes - 1)) == 0; }
 
-static int prefill(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* q, fq_stream_t stream, int bits) {
-    Int4Cache c{};
+// Validates a prefill call; on success fills c, t and the needed workspace size.
+static int prefill_check(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* q, int bits, Int4Cache& c,
+                         TailArgs& t, size_t* ws_bytes) {
     int st = check_cache(cache, &c, bits, true);
     if (st) return st;
     if (c.L != 1) return fail(FQ_ERR_INVALID, "prefill takes one layer's cache view (L=%d)", c.L);
@@ -762,7 +765,7 @@ static int prefill(const fq_int4_cache* cache, const fq_tail* tail, const fq_pre
             if (c.kp_s[i] % kal) return fail(FQ_ERR_UNSUPPORTED, "K code strides must be multiples of %d bytes", kal);
         if (!aligned(c.kp, kal)) return fail(FQ_ERR_UNSUPPORTED, "K codes must be %d-byte aligned", kal);
     }
-    TailArgs t{};
+    t = TailArgs{};
     if (tail && tail->len > 0) {
         if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
         if (tail->dtype != FQ_BF16) return fail(FQ_ERR_UNSUPPORTED, "prefill tail must be bf16");
@@ -788,18 +791,44 @@ static int prefill(const fq_int4_cache* cache, const fq_tail* tail, const fq_pre
     if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
     const int64_t rows = (int64_t)q->S_q * (q->H_q / c.Hkv);
     if ((rows + 255) / 256 * c.Hkv * c.B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
+    *ws_bytes = prefill_workspace_bytes(c, c.S + t.len, q->S_q, q->H_q / c.Hkv);
+    return FQ_OK;
+}
+
+static int prefill(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* q, void* workspace,
+                   size_t workspace_bytes_, fq_stream_t stream, int bits) {
+    Int4Cache c{};
+    TailArgs t{};
+    size_t need = 0;
+    int st = prefill_check(cache, tail, q, bits, c, t, &need);
+    if (st) return st;
+    if (need > 0 && (!workspace || workspace_bytes_ < need))
+        return fail(FQ_ERR_WORKSPACE, "prefill workspace of %zu bytes needed (got %zu)", need, workspace_bytes_);
+    if (need > 0 && !aligned(workspace, 16)) return fail(FQ_ERR_INVALID, "workspace must be 16-byte aligned");
     const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)c.D);
     return hip_status(launch_prefill(c, t, q->q, q->q_strides, q->out, q->o_strides, q->H_q / c.Hkv, q->S_q,
-                                     q->causal_offset, sm * kLog2e, (hipStream_t)stream),
+                                     q->causal_offset, sm * kLog2e, workspace, (hipStream_t)stream),
                       "prefill attention launch");
 }
 
-int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream) {
-    return prefill(cache, tail, query, stream, 4);
+size_t fq_prefill_workspace_bytes(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query,
+                                  int32_t bits) {
+    Int4Cache c{};
+    TailArgs t{};
+    size_t need = 0;
+    if (bits != 4 && bits != 8) return 0;
+    if (prefill_check(cache, tail, query, bits, c, t, &need)) return 0;
+    return need;
 }
 
-int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream) {
-    return prefill(cache, tail, query, stream, 8);
+int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, void* workspace,
+                    size_t workspace_bytes, fq_stream_t stream) {
+    return prefill(cache, tail, query, workspace, workspace_bytes, stream, 4);
+}
+
+int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, void* workspace,
+                    size_t workspace_bytes, fq_stream_t stream) {
+    return prefill(cache, tail, query, workspace, workspace_bytes, stream, 8);
 }
 
 }  // extern "C"

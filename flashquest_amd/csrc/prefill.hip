@@ -45,105 +45,126 @@ struct PrefillParams {
     TailArgs t;            // bf16 tail rows (the partial page), keys S .. S + t.len - 1
     const void* q; int64_t q_s[3];     // (b, h_q, pos) element strides, channels contiguous
     void* out; int64_t o_s[3];
+    uint16_t* kd;          // dense bf16 K   [b][h][S_pad][128]   (two-pass path)
+    uint16_t* vtd;         // dense bf16 V^T [b][h][128][S_pad]
+    int s_pad;             // keys in the dense arrays, a multiple of 64 (zeros beyond S_kv)
     int nrep, Sq, Skv, causal_off;
     float qk_scale;                    // sm_scale * log2(e)
 };
 
-// Raw bytes of one thread's K slice (one key, 16 channels) before dequantisation.
+template <int META>
+FQ_DEV float meta_lo(uint32_t w) {   // low half of a dword of half-precision metadata
+    return META == FQ_BF16 ? __uint_as_float(w << 16) : f16_bits_to_f(w & 0xFFFFu);
+}
+template <int META>
+FQ_DEV float meta_hi(uint32_t w) {
+    return META == FQ_BF16 ? __uint_as_float(w & 0xFFFF0000u) : f16_bits_to_f(w >> 16);
+}
+FQ_DEV uint32_t bf16_rne(float f) {    // fp32 -> bf16 bits, round to nearest even (finite inputs)
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+FQ_DEV uint32_t pack_bf16(float lo, float hi) { return bf16_rne(lo) | (bf16_rne(hi) << 16); }
+
+// ---- K: one thread = one key x 16 channels --------------------------------
+// Raw bytes before dequantisation.
 struct KFetch {
     uint4 c0, c1;          // codes (INT4: c0.xy, INT8: c0) or 16 bf16 tail values
     uint4 s0, s1, m0, m1;  // 16 half scales / mins
     int kind;              // 0 codes, 1 tail, 2 beyond the keys (zeros)
 };
-// One thread's V slice: 4 keys x 4 channels.
-struct VFetch {
-    uint2 raw[4];          // per key: codes (INT4: 16 bits, INT8: 32 bits) or 4 bf16 tail values
-    uint32_t sm[4];        // per key: scale | mn << 16 (half bits)
-    int kinds;             // 2 bits per key, as KFetch::kind
-};
-
-FQ_DEV float half_bits(uint32_t h, int meta_dtype) {
-    return meta_dtype == FQ_BF16 ? bf16_bits_to_f(h & 0xFFFFu) : f16_bits_to_f(h & 0xFFFFu);
-}
-FQ_DEV uint32_t word_of(const uint4& a, const uint4& b, int i) {   // dword i of the 8-dword pair
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    return w[i];
-}
-FQ_DEV uint32_t bf16_rne(float f) {    // fp32 -> bf16 bits, round to nearest even (finite inputs)
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
-}
 
 template <int BITS>
-FQ_DEV void fetch_k(KFetch& f, const PrefillParams& a, int b, int h, int key, int kc) {
-    const Int4Cache& c = a.c;
-    if (key < c.S) {
-        f.kind = 0;
-        const uint8_t* row = c.kp + b * c.kp_s[1] + h * c.kp_s[2] + (int64_t)key * c.kp_s[3];
-        if (BITS == 4) {
-            const uint2 v = *(const uint2*)(row + kc / 2);
-            f.c0 = make_uint4(v.x, v.y, 0u, 0u);
-        } else {
-            f.c0 = *(const uint4*)(row + kc);
-        }
-        const int64_t page = key / c.page;
-        const uint16_t* ks = (const uint16_t*)c.ksc + b * c.ksc_s[1] + h * c.ksc_s[2] + page * c.ksc_s[3] + kc;
-        const uint16_t* km = (const uint16_t*)c.kmn + b * c.kmn_s[1] + h * c.kmn_s[2] + page * c.kmn_s[3] + kc;
-        f.s0 = *(const uint4*)ks; f.s1 = *(const uint4*)(ks + 8);
-        f.m0 = *(const uint4*)km; f.m1 = *(const uint4*)(km + 8);
+FQ_DEV void fetch_k_codes(KFetch& f, const Int4Cache& c, int b, int h, int key, int kc) {
+    const uint8_t* row = c.kp + b * c.kp_s[1] + h * c.kp_s[2] + (int64_t)key * c.kp_s[3];
+    if (BITS == 4) {
+        const uint2 v = *(const uint2*)(row + kc / 2);
+        f.c0 = make_uint4(v.x, v.y, 0u, 0u);
+    } else {
+        f.c0 = *(const uint4*)(row + kc);
+    }
+    const int64_t page = key / c.page;
+    const uint16_t* ks = (const uint16_t*)c.ksc + b * c.ksc_s[1] + h * c.ksc_s[2] + page * c.ksc_s[3] + kc;
+    const uint16_t* km = (const uint16_t*)c.kmn + b * c.kmn_s[1] + h * c.kmn_s[2] + page * c.kmn_s[3] + kc;
+    f.s0 = *(const uint4*)ks; f.s1 = *(const uint4*)(ks + 8);
+    f.m0 = *(const uint4*)km; f.m1 = *(const uint4*)(km + 8);
+    f.kind = 0;
+}
+
+// `whole`: the tile lies inside the completed pages (no tail or padding keys).
+template <int BITS>
+FQ_DEV void fetch_k(KFetch& f, const PrefillParams& a, int b, int h, int key, int kc, bool whole) {
+    if (whole || key < a.c.S) {
+        fetch_k_codes<BITS>(f, a.c, b, h, key, kc);
     } else if (key < a.Skv) {
         f.kind = 1;
-        const uint16_t* row = (const uint16_t*)a.t.k + b * a.t.ks[1] + h * a.t.ks[2] + (int64_t)(key - c.S) * a.t.ks[3] + kc;
+        const uint16_t* row = (const uint16_t*)a.t.k + b * a.t.ks[1] + h * a.t.ks[2] + (int64_t)(key - a.c.S) * a.t.ks[3] + kc;
         f.c0 = *(const uint4*)row; f.c1 = *(const uint4*)(row + 8);
     } else {
         f.kind = 2;
     }
 }
 
-template <int BITS>
-FQ_DEV void store_k(const KFetch& f, uint16_t* dst, int meta_dtype) {
-    uint4 o0 = make_uint4(0u, 0u, 0u, 0u), o1 = o0;
-    if (f.kind == 1) {
-        o0 = f.c0; o1 = f.c1;
-    } else if (f.kind == 0) {
-        uint32_t packed[8];
+FQ_DEV uint32_t dw(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// Dequantise 16 channels: code * scale + mn in fp32 (exact product, one rounding), then bf16.
+template <int BITS, int META>
+FQ_DEV void dequant_k16(const KFetch& f, uint4& o0, uint4& o1) {
+    uint32_t out[8];
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            uint32_t lo, hi;
-            if (BITS == 4) {
-                const uint32_t byte = (word_of(f.c0, f.c0, i >> 3) >> (8 * ((i >> 1) & 3))) & 0xFFu;
-                lo = byte & 15u; hi = byte >> 4;          // even channel in the low nibble
-            } else {
-                const uint32_t wd = word_of(f.c0, f.c0, i >> 2);
-                lo = (wd >> (8 * (i & 3))) & 0xFFu; hi = (wd >> (8 * (i & 3) + 8)) & 0xFFu;
-            }
-            const uint32_t sw = word_of(f.s0, f.s1, i >> 1), mw = word_of(f.m0, f.m1, i >> 1);
-            const float v0 = fmaf((float)lo, half_bits(sw, meta_dtype), half_bits(mw, meta_dtype));
-            const float v1 = fmaf((float)hi, half_bits(sw >> 16, meta_dtype), half_bits(mw >> 16, meta_dtype));
-            packed[i >> 1] = bf16_rne(v0) | (bf16_rne(v1) << 16);
+    for (int i = 0; i < 16; i += 2) {
+        float c0, c1;
+        if (BITS == 4) {
+            const uint32_t wd = dw(f.c0, i >> 3);
+            const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+            const int by = (i >> 1) & 3;
+            c0 = (float)((lo >> (8 * by)) & 0xFFu);
+            c1 = (float)((hi >> (8 * by)) & 0xFFu);
+        } else {
+            const uint32_t wd = dw(f.c0, i >> 2);
+            c0 = (float)((wd >> (8 * (i & 3))) & 0xFFu);
+            c1 = (float)((wd >> (8 * (i & 3) + 8)) & 0xFFu);
         }
-        o0 = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        o1 = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+        const uint32_t sw = i < 8 ? dw(f.s0, i >> 1) : dw(f.s1, (i >> 1) - 4);
+        const uint32_t mw = i < 8 ? dw(f.m0, i >> 1) : dw(f.m1, (i >> 1) - 4);
+        out[i >> 1] = pack_bf16(fmaf(c0, meta_lo<META>(sw), meta_lo<META>(mw)),
+                                fmaf(c1, meta_hi<META>(sw), meta_hi<META>(mw)));
     }
+    o0 = make_uint4(out[0], out[1], out[2], out[3]);
+    o1 = make_uint4(out[4], out[5], out[6], out[7]);
+}
+
+template <int BITS, int META>
+FQ_DEV void store_k(const KFetch& f, uint16_t* dst) {
+    uint4 o0 = make_uint4(0u, 0u, 0u, 0u), o1 = o0;
+    if (f.kind == 0) dequant_k16<BITS, META>(f, o0, o1);
+    else if (f.kind == 1) { o0 = f.c0; o1 = f.c1; }
     *(uint4*)dst = o0;
     *(uint4*)(dst + 8) = o1;
 }
 
+// ---- V: one thread = 4 keys x 4 channels, stored transposed -----------------
+struct VFetch {
+    uint2 raw[4];          // per key: codes (INT4: 16 bits, INT8: 32 bits) or 4 bf16 tail values
+    uint32_t sc[4], mn[4]; // per key: half bits of scale / mn
+    int kinds;             // 2 bits per key, as KFetch::kind
+};
+
 template <int BITS>
-FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, int vd) {
+FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, int vd, bool whole) {
     const Int4Cache& c = a.c;
     const int grp = vd / (kPD / c.G);
     f.kinds = 0;
+    const uint8_t* rows = c.vp + b * c.vp_s[1] + h * c.vp_s[2] + (int64_t)key0 * c.vp_s[3] + (BITS == 4 ? vd / 2 : vd);
+    const uint16_t* vs = (const uint16_t*)c.vsc + b * c.vsc_s[1] + h * c.vsc_s[2] + (int64_t)key0 * c.vsc_s[3] + grp;
+    const uint16_t* vm = (const uint16_t*)c.vmn + b * c.vmn_s[1] + h * c.vmn_s[2] + (int64_t)key0 * c.vmn_s[3] + grp;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = key0 + j;
-        f.raw[j] = make_uint2(0u, 0u);
-        f.sm[j] = 0u;
-        if (key < c.S) {
-            const uint8_t* row = c.vp + b * c.vp_s[1] + h * c.vp_s[2] + (int64_t)key * c.vp_s[3];
-            f.raw[j].x = BITS == 4 ? (uint32_t)*(const uint16_t*)(row + vd / 2) : *(const uint32_t*)(row + vd);
-            const uint16_t* vs = (const uint16_t*)c.vsc + b * c.vsc_s[1] + h * c.vsc_s[2] + (int64_t)key * c.vsc_s[3] + grp;
-            const uint16_t* vm = (const uint16_t*)c.vmn + b * c.vmn_s[1] + h * c.vmn_s[2] + (int64_t)key * c.vmn_s[3] + grp;
-            f.sm[j] = (uint32_t)*vs | ((uint32_t)*vm << 16);
+        if (whole || key < c.S) {
+            f.raw[j].x = BITS == 4 ? (uint32_t)*(const uint16_t*)(rows + j * c.vp_s[3])
+                                   : *(const uint32_t*)(rows + j * c.vp_s[3]);
+            f.sc[j] = vs[j * c.vsc_s[3]];
+            f.mn[j] = vm[j * c.vmn_s[3]];
         } else if (key < a.Skv) {
             f.kinds |= 1 << (2 * j);
             const uint16_t* row = (const uint16_t*)a.t.v + b * a.t.vs[1] + h * a.t.vs[2] + (int64_t)(key - c.S) * a.t.vs[3] + vd;
@@ -154,31 +175,66 @@ FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, i
     }
 }
 
-template <int BITS>
-FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */, int meta_dtype) {
-    uint32_t v[4][4];   // [key][channel] bf16 bits
+// v[key][i] as bf16 bits for channels vd + i
+template <int BITS, int META>
+FQ_DEV void dequant_v44(const VFetch& f, uint32_t (&v)[4][4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int kind = (f.kinds >> (2 * j)) & 3;
-        const float sc = half_bits(f.sm[j], meta_dtype), mn = half_bits(f.sm[j] >> 16, meta_dtype);
+        const float sc = meta_lo<META>(f.sc[j]), mn = meta_lo<META>(f.mn[j]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t code = BITS == 4 ? (f.raw[j].x >> (4 * i)) & 15u : (f.raw[j].x >> (8 * i)) & 0xFFu;
             const uint32_t tail = ((i < 2 ? f.raw[j].x : f.raw[j].y) >> (16 * (i & 1))) & 0xFFFFu;
-            const uint32_t deq = bf16_rne(fmaf((float)code, sc, mn));
-            v[j][i] = kind == 0 ? deq : (kind == 1 ? tail : 0u);
+            v[j][i] = kind == 0 ? bf16_rne(fmaf((float)code, sc, mn)) : (kind == 1 ? tail : 0u);
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *(uint2*)(dst + i * kVStr) = make_uint2(v[0][i] | (v[1][i] << 16), v[2][i] | (v[3][i] << 16));
 }
 
-template <int BITS>
+template <int BITS, int META>
+FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */, int row_stride) {
+    uint32_t v[4][4];
+    dequant_v44<BITS, META>(f, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *(uint2*)(dst + i * row_stride) = make_uint2(v[0][i] | (v[1][i] << 16), v[2][i] | (v[3][i] << 16));
+}
+
+// ---- dense bf16 source (two-pass path) --------------------------------------
+struct DFetch { uint4 k0, k1, v0, v1; };
+
+// The first pass: dequantise the cache and the tail once into dense bf16 K and
+// V^T (keys padded with zeros to a multiple of 64).  One 512-thread block per
+// (64-key tile, b, h); V goes through LDS to be written transposed.
+template <int BITS, int META>
+__global__ __launch_bounds__(512) void prefill_dequant_kernel(PrefillParams a) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kPD * kVStr];
+    const int tid = threadIdx.x;
+    const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int key0 = tile * kPKT;
+    const bool whole = key0 + kPKT <= a.c.S;
+    const int kk = tid >> 3, kc = (tid & 7) * 16;
+    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4;
+    KFetch kf;
+    VFetch vf;
+    fetch_k<BITS>(kf, a, b, h, key0 + kk, kc, whole);
+    fetch_v<BITS>(vf, a, b, h, key0 + vk, vd, whole);
+    const int64_t bh = (int64_t)b * a.c.Hkv + h;
+    store_k<BITS, META>(kf, a.kd + (bh * a.s_pad + key0 + kk) * kPD + kc);
+    store_v<BITS, META>(vf, &s_v[vd * kVStr + vk], kVStr);
+    __syncthreads();
+    const int d = tid >> 2, q = (tid & 3) * 16;
+    uint16_t* dst = a.vtd + (bh * kPD + d) * a.s_pad + key0 + q;
+    *(uint4*)dst = *(const uint4*)&s_v[d * kVStr + q];
+    *(uint4*)(dst + 8) = *(const uint4*)&s_v[d * kVStr + q + 8];
+}
+
+template <int SRC, int META>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_kernel(PrefillParams a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPKT * kKStr];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * kVStr];
+    constexpr int BITS = SRC == 16 ? 4 : SRC;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -205,7 +261,6 @@ void prefill_attn_kernel(PrefillParams a) {
     // this lane's two query columns: B operands of q.k (channels 32 ks + 8 g .. + 8)
     int qpos[2];
     bool qok[2];
-    const uint16_t* qrow[2];
     v8bf qf[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -214,10 +269,10 @@ void prefill_attn_kernel(PrefillParams a) {
         const int mm = qok[qb] ? m : mw0;
         qpos[qb] = qok[qb] ? mm / a.nrep : pmin;
         const int hq = h * a.nrep + mm % a.nrep;
-        qrow[qb] = (const uint16_t*)a.q + b * a.q_s[0] + hq * a.q_s[1] + (int64_t)(mm / a.nrep) * a.q_s[2];
+        const uint16_t* qrow = (const uint16_t*)a.q + b * a.q_s[0] + hq * a.q_s[1] + (int64_t)(mm / a.nrep) * a.q_s[2];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            if (wave_on) qf[qb][ks] = *(const v8bf*)(qrow[qb] + 32 * ks + 8 * g);
+            if (wave_on) qf[qb][ks] = *(const v8bf*)(qrow + 32 * ks + 8 * g);
             else qf[qb][ks] = v8bf{};
         }
     }
@@ -232,24 +287,49 @@ void prefill_attn_kernel(PrefillParams a) {
     }
 
     const int kk = tid >> 3, kc = (tid & 7) * 16;      // K loader: one key, 16 channels
-    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4; // V loader: 4 keys, 4 channels
+    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4; // V loader (packed): 4 keys, 4 channels
+    const int td = tid >> 2, tq = (tid & 3) * 16;       // V^T loader (dense): one channel, 16 keys
+    const int64_t bh = (int64_t)b * c.Hkv + h;
+    const uint16_t* kd_base = SRC == 16 ? a.kd + (bh * a.s_pad + kk) * kPD + kc : nullptr;
+    const uint16_t* vd_base = SRC == 16 ? a.vtd + (bh * kPD + td) * a.s_pad + tq : nullptr;
+
     KFetch kf;
     VFetch vf;
-    if (nt > 0) {
-        fetch_k<BITS>(kf, a, b, h, kk, kc);
-        fetch_v<BITS>(vf, a, b, h, vk, vd);
-        store_k<BITS>(kf, &s_k[0][kk * kKStr + kc], c.meta_dtype);
-        store_v<BITS>(vf, &s_v[0][vd * kVStr + vk], c.meta_dtype);
-    }
+    DFetch df;
+    auto fetch = [&](int key0) {
+        if constexpr (SRC == 16) {
+            const uint16_t* kp = kd_base + (int64_t)key0 * kPD;
+            df.k0 = *(const uint4*)kp; df.k1 = *(const uint4*)(kp + 8);
+            const uint16_t* vp = vd_base + key0;
+            df.v0 = *(const uint4*)vp; df.v1 = *(const uint4*)(vp + 8);
+        } else {
+            const bool whole = key0 + kPKT <= c.S;
+            fetch_k<BITS>(kf, a, b, h, key0 + kk, kc, whole);
+            fetch_v<BITS>(vf, a, b, h, key0 + vk, vd, whole);
+        }
+    };
+    auto stage = [&](int buf) {
+        if constexpr (SRC == 16) {
+            uint16_t* kdst = &s_k[buf][kk * kKStr + kc];
+            *(uint4*)kdst = df.k0; *(uint4*)(kdst + 8) = df.k1;
+            uint16_t* vdst = &s_v[buf][td * kVStr + tq];
+            *(uint4*)vdst = df.v0; *(uint4*)(vdst + 8) = df.v1;
+        } else if (c.meta_dtype == FQ_BF16) {
+            store_k<BITS, FQ_BF16>(kf, &s_k[buf][kk * kKStr + kc]);
+            store_v<BITS, FQ_BF16>(vf, &s_v[buf][vd * kVStr + vk], kVStr);
+        } else {
+            store_k<BITS, FQ_F16>(kf, &s_k[buf][kk * kKStr + kc]);
+            store_v<BITS, FQ_F16>(vf, &s_v[buf][vd * kVStr + vk], kVStr);
+        }
+    };
+
+    if (nt > 0) { fetch(0); stage(0); }
     __syncthreads();
 
     for (int t = 0; t < nt; ++t) {
         const int cur = t & 1;
         const int key0 = t * kPKT;
-        if (t + 1 < nt) {
-            fetch_k<BITS>(kf, a, b, h, key0 + kPKT + kk, kc);
-            fetch_v<BITS>(vf, a, b, h, key0 + kPKT + vk, vd);
-        }
+        if (t + 1 < nt) fetch(key0 + kPKT);
         if (wave_on && key0 < limit_w) {
             const uint16_t* sk = s_k[cur];
             const uint16_t* sv = s_v[cur];
@@ -267,26 +347,28 @@ void prefill_attn_kernel(PrefillParams a) {
             }
             const bool need_mask = key0 + kPKT - 1 > pmin + a.causal_off || key0 + kPKT > a.Skv;
             v8bf pb[2][2];
+            bool rescale = false;
+            float alpha[2];
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 if (need_mask) {
-                    const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1);
+                    const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1) - key0 - 4 * g;
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int cc = 0; cc < 4; ++cc)
-                            if (key0 + kb * 16 + 4 * g + cc > lim) s[qb][kb][cc] = -INFINITY;
+                            if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
                 }
-                float mx = s[qb][0][0];
+                float mx = fmaxf(fmaxf(s[qb][0][0], s[qb][0][1]), fmaxf(s[qb][0][2], s[qb][0][3]));
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) mx = fmaxf(mx, s[qb][kb][cc]);
+                for (int kb = 1; kb < 4; ++kb)
+                    mx = fmaxf(mx, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
                 mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
                 const float m_new = fmaxf(m_run[qb], mx * a.qk_scale);
                 const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+                alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+                rescale |= m_new != m_run[qb];
                 float sum = 0.f;
                 float p[4][4];
 #pragma unroll
@@ -296,10 +378,8 @@ void prefill_attn_kernel(PrefillParams a) {
                         p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], a.qk_scale, -m_use));
                         sum += p[kb][cc];
                     }
-                l_run[qb] = fmaf(l_run[qb], alpha, sum);
+                l_run[qb] = fmaf(l_run[qb], alpha[qb], sum);
                 m_run[qb] = m_new;
-#pragma unroll
-                for (int db = 0; db < 8; ++db) o[qb][db] *= alpha;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -307,6 +387,12 @@ void prefill_attn_kernel(PrefillParams a) {
                         pb[qb][j][cc] = (__bf16)p[2 * j][cc];
                         pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
                     }
+            }
+            if (__builtin_amdgcn_ballot_w64(rescale)) {   // the running max moved for some column
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                    for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
             }
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
@@ -321,10 +407,7 @@ void prefill_attn_kernel(PrefillParams a) {
                 }
             }
         }
-        if (t + 1 < nt) {
-            store_k<BITS>(kf, &s_k[cur ^ 1][kk * kKStr + kc], c.meta_dtype);
-            store_v<BITS>(vf, &s_v[cur ^ 1][vd * kVStr + vk], c.meta_dtype);
-        }
+        if (t + 1 < nt) stage(cur ^ 1);
         __syncthreads();
     }
 
@@ -342,30 +425,61 @@ void prefill_attn_kernel(PrefillParams a) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
             const v4f r = o[qb][db] * inv;
-            *(uint2*)(orow + db * 16 + 4 * g) =
-                make_uint2(bf16_rne(r[0]) | (bf16_rne(r[1]) << 16), bf16_rne(r[2]) | (bf16_rne(r[3]) << 16));
+            *(uint2*)(orow + db * 16 + 4 * g) = make_uint2(pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3]));
         }
     }
 }
 
 }  // namespace
 
-// Launch the prefill kernel.  The caller has checked shapes, strides and
-// alignment (capi.cpp: fq_prefill_int4 / fq_prefill_int8).
+// Rows of 256 GQA-flattened queries per KV head at or above which the
+// two-pass path (dequantise once to dense bf16, then attend) beats
+// dequantising every K/V tile in every row block.
+constexpr int kTwoPassBlocks = 3;
+
+int64_t prefill_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kPRows - 1) / kPRows; }
+
+size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep) {
+    if (prefill_row_blocks(Sq, nrep) < kTwoPassBlocks) return 0;
+    const int64_t s_pad = ((int64_t)Skv + kPKT - 1) / kPKT * kPKT;
+    return (size_t)(2 * s_pad * kPD * 2) * c.Hkv * c.B;
+}
+
+// Launch the prefill.  The caller has checked shapes, strides and alignment
+// (capi.cpp: fq_prefill_int4 / fq_prefill_int8) and provides a workspace of
+// prefill_workspace_bytes (the dense K and V^T of the two-pass path).
 hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, const int64_t* q_s, void* out,
-                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, hipStream_t st) {
+                          const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, void* ws,
+                          hipStream_t st) {
     PrefillParams a{};
     a.c = c;
     a.t = t;
     a.q = q; a.out = out;
     for (int i = 0; i < 3; ++i) { a.q_s[i] = q_s[i]; a.o_s[i] = o_s[i]; }
     a.nrep = nrep; a.Sq = Sq; a.Skv = c.S + t.len; a.causal_off = causal_off; a.qk_scale = qk_scale;
-    const int64_t rows = (int64_t)Sq * nrep;
-    const int64_t nblk = (rows + kPRows - 1) / kPRows;
+    const int64_t nblk = prefill_row_blocks(Sq, nrep);
     const dim3 grid((unsigned)(nblk * c.Hkv * c.B));
+    const bool bf = c.meta_dtype == FQ_BF16;
+    if (prefill_workspace_bytes(c, a.Skv, Sq, nrep) > 0) {
+        a.s_pad = (a.Skv + kPKT - 1) / kPKT * kPKT;
+        a.kd = (uint16_t*)ws;
+        a.vtd = a.kd + (int64_t)a.s_pad * kPD * c.Hkv * c.B;
+        const dim3 dgrid(a.s_pad / kPKT, c.Hkv, c.B);
+        if (c.bits == 8) {
+            if (bf) hipLaunchKernelGGL((prefill_dequant_kernel<8, FQ_BF16>), dgrid, dim3(512), 0, st, a);
+            else hipLaunchKernelGGL((prefill_dequant_kernel<8, FQ_F16>), dgrid, dim3(512), 0, st, a);
+        } else {
+            if (bf) hipLaunchKernelGGL((prefill_dequant_kernel<4, FQ_BF16>), dgrid, dim3(512), 0, st, a);
+            else hipLaunchKernelGGL((prefill_dequant_kernel<4, FQ_F16>), dgrid, dim3(512), 0, st, a);
+        }
+        timer_before_launch(st);
+        hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), grid, dim3(512), 0, st, a);
+        timer_after_launch(st);
+        return hipGetLastError();
+    }
     timer_before_launch(st);
-    if (c.bits == 8) hipLaunchKernelGGL(prefill_attn_kernel<8>, grid, dim3(512), 0, st, a);
-    else hipLaunchKernelGGL(prefill_attn_kernel<4>, grid, dim3(512), 0, st, a);
+    if (c.bits == 8) hipLaunchKernelGGL((prefill_attn_kernel<8, FQ_BF16>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((prefill_attn_kernel<4, FQ_BF16>), grid, dim3(512), 0, st, a);
     timer_after_launch(st);
     return hipGetLastError();
 }

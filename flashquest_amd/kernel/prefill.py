@@ -39,7 +39,11 @@ def _prefill_call(fn_name: str, cache_desc, keep, q, K_tail, V_tail, causal_offs
     out = torch.empty(B, H_q, S_q, D, dtype=torch.bfloat16, device=q.device)
     pq = L.Prefill(qb.data_ptr(), L.strides(qb, 4), out.data_ptr(), L.strides(out, 4), H_q, S_q,
                    int(causal_offset), float(sm_scale) if sm_scale is not None else 0.0)
-    L.check(getattr(L.lib(), fn_name)(cache_desc, tail, pq, L.stream_handle(q.device)), fn_name)
+    bits = 4 if fn_name.endswith("int4") else 8
+    nbytes = L.lib().fq_prefill_workspace_bytes(cache_desc, tail, pq, bits)
+    # the dense bf16 K / V^T of the two-pass path: written in full before it is read
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    L.check(getattr(L.lib(), fn_name)(cache_desc, tail, pq, L.ptr(ws), nbytes, L.stream_handle(q.device)), fn_name)
     del tails
     return out
 

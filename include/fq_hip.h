@@ -385,11 +385,21 @@ typedef struct fq_prefill {
  * attention kernel.  cache: one layer (L == 1), S completed tokens (S may be 0),
  * D == 128; tail: the bf16 partial-page rows (len >= 0, any length), keys S..
  * S + len - 1.  FQ_ERR_UNSUPPORTED for layouts the kernel does not take. */
-int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream);
+int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query,
+                    void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
 /* The same over the INT8 cache (llama_persistent_patch.py:143-150:
  * dequantize_k / dequantize_v, kernel/kv_quant.py:64-100). */
-int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, fq_stream_t stream);
+int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query,
+                    void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
+/* Workspace bytes fq_prefill_int4 (bits 4) / fq_prefill_int8 (bits 8) needs for
+ * these arguments: 0 when every workgroup dequantises its own K/V tiles (few
+ * query rows), else room for the dense bf16 K and V^T of the two-pass path
+ * (dequantised once, 2 * 2 * 128 B per key and KV head).  0 also for invalid
+ * arguments (the call then reports the error).  No reference counterpart. */
+size_t fq_prefill_workspace_bytes(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query,
+                                  int32_t bits);
 
 #ifdef __cplusplus
 }
