@@ -31,6 +31,10 @@ namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+// native vectors (not HIP's u32x4 / u32x2 wrapper structs) keep the fetch
+// registers out of private memory
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPD = 128;               // head dim
 constexpr int kPW = 8;                 // waves per workgroup
@@ -68,8 +72,8 @@ FQ_DEV uint32_t pack_bf16(float lo, float hi) { return bf16_rne(lo) | (bf16_rne(
 // ---- K: one thread = one key x 16 channels --------------------------------
 // Raw bytes before dequantisation.
 struct KFetch {
-    uint4 c0, c1;          // codes (INT4: c0.xy, INT8: c0) or 16 bf16 tail values
-    uint4 s0, s1, m0, m1;  // 16 half scales / mins
+    u32x4 c0, c1;          // codes (INT4: c0.xy, INT8: c0) or 16 bf16 tail values
+    u32x4 s0, s1, m0, m1;  // 16 half scales / mins
     int kind;              // 0 codes, 1 tail, 2 beyond the keys (zeros)
 };
 
@@ -77,16 +81,16 @@ template <int BITS>
 FQ_DEV void fetch_k_codes(KFetch& f, const Int4Cache& c, int b, int h, int key, int kc) {
     const uint8_t* row = c.kp + b * c.kp_s[1] + h * c.kp_s[2] + (int64_t)key * c.kp_s[3];
     if (BITS == 4) {
-        const uint2 v = *(const uint2*)(row + kc / 2);
-        f.c0 = make_uint4(v.x, v.y, 0u, 0u);
+        const u32x2 v = *(const u32x2*)(row + kc / 2);
+        f.c0 = u32x4{v.x, v.y, 0u, 0u};
     } else {
-        f.c0 = *(const uint4*)(row + kc);
+        f.c0 = *(const u32x4*)(row + kc);
     }
     const int64_t page = key / c.page;
     const uint16_t* ks = (const uint16_t*)c.ksc + b * c.ksc_s[1] + h * c.ksc_s[2] + page * c.ksc_s[3] + kc;
     const uint16_t* km = (const uint16_t*)c.kmn + b * c.kmn_s[1] + h * c.kmn_s[2] + page * c.kmn_s[3] + kc;
-    f.s0 = *(const uint4*)ks; f.s1 = *(const uint4*)(ks + 8);
-    f.m0 = *(const uint4*)km; f.m1 = *(const uint4*)(km + 8);
+    f.s0 = *(const u32x4*)ks; f.s1 = *(const u32x4*)(ks + 8);
+    f.m0 = *(const u32x4*)km; f.m1 = *(const u32x4*)(km + 8);
     f.kind = 0;
 }
 
@@ -98,17 +102,17 @@ FQ_DEV void fetch_k(KFetch& f, const PrefillParams& a, int b, int h, int key, in
     } else if (key < a.Skv) {
         f.kind = 1;
         const uint16_t* row = (const uint16_t*)a.t.k + b * a.t.ks[1] + h * a.t.ks[2] + (int64_t)(key - a.c.S) * a.t.ks[3] + kc;
-        f.c0 = *(const uint4*)row; f.c1 = *(const uint4*)(row + 8);
+        f.c0 = *(const u32x4*)row; f.c1 = *(const u32x4*)(row + 8);
     } else {
         f.kind = 2;
     }
 }
 
-FQ_DEV uint32_t dw(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+FQ_DEV uint32_t dw(const u32x4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // Dequantise 16 channels: code * scale + mn in fp32 (exact product, one rounding), then bf16.
 template <int BITS, int META>
-FQ_DEV void dequant_k16(const KFetch& f, uint4& o0, uint4& o1) {
+FQ_DEV void dequant_k16(const KFetch& f, u32x4& o0, u32x4& o1) {
     uint32_t out[8];
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
@@ -129,22 +133,22 @@ FQ_DEV void dequant_k16(const KFetch& f, uint4& o0, uint4& o1) {
         out[i >> 1] = pack_bf16(fmaf(c0, meta_lo<META>(sw), meta_lo<META>(mw)),
                                 fmaf(c1, meta_hi<META>(sw), meta_hi<META>(mw)));
     }
-    o0 = make_uint4(out[0], out[1], out[2], out[3]);
-    o1 = make_uint4(out[4], out[5], out[6], out[7]);
+    o0 = u32x4{out[0], out[1], out[2], out[3]};
+    o1 = u32x4{out[4], out[5], out[6], out[7]};
 }
 
 template <int BITS, int META>
 FQ_DEV void store_k(const KFetch& f, uint16_t* dst) {
-    uint4 o0 = make_uint4(0u, 0u, 0u, 0u), o1 = o0;
+    u32x4 o0 = u32x4{0u, 0u, 0u, 0u}, o1 = o0;
     if (f.kind == 0) dequant_k16<BITS, META>(f, o0, o1);
     else if (f.kind == 1) { o0 = f.c0; o1 = f.c1; }
-    *(uint4*)dst = o0;
-    *(uint4*)(dst + 8) = o1;
+    *(u32x4*)dst = o0;
+    *(u32x4*)(dst + 8) = o1;
 }
 
 // ---- V: one thread = 4 keys x 4 channels, stored transposed -----------------
 struct VFetch {
-    uint2 raw[4];          // per key: codes (INT4: 16 bits, INT8: 32 bits) or 4 bf16 tail values
+    u32x2 raw[4];          // per key: codes (INT4: 16 bits, INT8: 32 bits) or 4 bf16 tail values
     uint32_t sc[4], mn[4]; // per key: half bits of scale / mn
     int kinds;             // 2 bits per key, as KFetch::kind
 };
@@ -168,7 +172,7 @@ FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, i
         } else if (key < a.Skv) {
             f.kinds |= 1 << (2 * j);
             const uint16_t* row = (const uint16_t*)a.t.v + b * a.t.vs[1] + h * a.t.vs[2] + (int64_t)(key - c.S) * a.t.vs[3] + vd;
-            f.raw[j] = *(const uint2*)row;
+            f.raw[j] = *(const u32x2*)row;
         } else {
             f.kinds |= 2 << (2 * j);
         }
@@ -197,11 +201,11 @@ FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */
     dequant_v44<BITS, META>(f, v);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        *(uint2*)(dst + i * row_stride) = make_uint2(v[0][i] | (v[1][i] << 16), v[2][i] | (v[3][i] << 16));
+        *(u32x2*)(dst + i * row_stride) = u32x2{v[0][i] | (v[1][i] << 16), v[2][i] | (v[3][i] << 16)};
 }
 
 // ---- dense bf16 source (two-pass path) --------------------------------------
-struct DFetch { uint4 k0, k1, v0, v1; };
+struct DFetch { u32x4 k0, k1, v0, v1; };
 
 // The first pass: dequantise the cache and the tail once into dense bf16 K and
 // V^T (keys padded with zeros to a multiple of 64).  One 512-thread block per
@@ -225,8 +229,40 @@ __global__ __launch_bounds__(512) void prefill_dequant_kernel(PrefillParams a) {
     __syncthreads();
     const int d = tid >> 2, q = (tid & 3) * 16;
     uint16_t* dst = a.vtd + (bh * kPD + d) * a.s_pad + key0 + q;
-    *(uint4*)dst = *(const uint4*)&s_v[d * kVStr + q];
-    *(uint4*)(dst + 8) = *(const uint4*)&s_v[d * kVStr + q + 8];
+    *(u32x4*)dst = *(const u32x4*)&s_v[d * kVStr + q];
+    *(u32x4*)(dst + 8) = *(const u32x4*)&s_v[d * kVStr + q + 8];
+}
+
+template <int SRC>
+FQ_DEV void prefill_fetch(const PrefillParams& a, KFetch& kf, VFetch& vf, DFetch& df, const uint16_t* kd_base,
+                          const uint16_t* vd_base, int key0, int b, int h, int kk, int kc, int vk, int vd) {
+    if constexpr (SRC == 16) {
+        const uint16_t* kp = kd_base + (int64_t)key0 * kPD;
+        df.k0 = *(const u32x4*)kp; df.k1 = *(const u32x4*)(kp + 8);
+        const uint16_t* vp = vd_base + key0;
+        df.v0 = *(const u32x4*)vp; df.v1 = *(const u32x4*)(vp + 8);
+    } else {
+        const bool whole = key0 + kPKT <= a.c.S;
+        fetch_k<SRC>(kf, a, b, h, key0 + kk, kc, whole);
+        fetch_v<SRC>(vf, a, b, h, key0 + vk, vd, whole);
+    }
+}
+
+template <int SRC>
+FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch& vf, const DFetch& df, uint16_t* sk,
+                          uint16_t* sv, int kk, int kc, int vd, int vk, int td, int tq) {
+    if constexpr (SRC == 16) {
+        uint16_t* kdst = sk + kk * kKStr + kc;
+        *(u32x4*)kdst = df.k0; *(u32x4*)(kdst + 8) = df.k1;
+        uint16_t* vdst = sv + td * kVStr + tq;
+        *(u32x4*)vdst = df.v0; *(u32x4*)(vdst + 8) = df.v1;
+    } else if (a.c.meta_dtype == FQ_BF16) {
+        store_k<SRC, FQ_BF16>(kf, sk + kk * kKStr + kc);
+        store_v<SRC, FQ_BF16>(vf, sv + vd * kVStr + vk, kVStr);
+    } else {
+        store_k<SRC, FQ_F16>(kf, sk + kk * kKStr + kc);
+        store_v<SRC, FQ_F16>(vf, sv + vd * kVStr + vk, kVStr);
+    }
 }
 
 template <int SRC, int META>
@@ -234,7 +270,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_kernel(PrefillParams a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPKT * kKStr];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * kVStr];
-    constexpr int BITS = SRC == 16 ? 4 : SRC;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -266,15 +301,14 @@ void prefill_attn_kernel(PrefillParams a) {
     for (int qb = 0; qb < 2; ++qb) {
         const int m = mw0 + qb * 16 + n;
         qok[qb] = m < Mtot;
-        const int mm = qok[qb] ? m : mw0;
+        const int mm = qok[qb] ? m : (wave_on ? mw0 : 0);
         qpos[qb] = qok[qb] ? mm / a.nrep : pmin;
         const int hq = h * a.nrep + mm % a.nrep;
         const uint16_t* qrow = (const uint16_t*)a.q + b * a.q_s[0] + hq * a.q_s[1] + (int64_t)(mm / a.nrep) * a.q_s[2];
+        // unconditional loads (an idle wave reads a valid row it never uses):
+        // no branch leaves these loads pending at the tile loop
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            if (wave_on) qf[qb][ks] = *(const v8bf*)(qrow + 32 * ks + 8 * g);
-            else qf[qb][ks] = v8bf{};
-        }
+        for (int ks = 0; ks < 4; ++ks) qf[qb][ks] = *(const v8bf*)(qrow + 32 * ks + 8 * g);
     }
 
     v4f o[2][8];
@@ -296,40 +330,19 @@ void prefill_attn_kernel(PrefillParams a) {
     KFetch kf;
     VFetch vf;
     DFetch df;
-    auto fetch = [&](int key0) {
-        if constexpr (SRC == 16) {
-            const uint16_t* kp = kd_base + (int64_t)key0 * kPD;
-            df.k0 = *(const uint4*)kp; df.k1 = *(const uint4*)(kp + 8);
-            const uint16_t* vp = vd_base + key0;
-            df.v0 = *(const uint4*)vp; df.v1 = *(const uint4*)(vp + 8);
-        } else {
-            const bool whole = key0 + kPKT <= c.S;
-            fetch_k<BITS>(kf, a, b, h, key0 + kk, kc, whole);
-            fetch_v<BITS>(vf, a, b, h, key0 + vk, vd, whole);
-        }
-    };
-    auto stage = [&](int buf) {
-        if constexpr (SRC == 16) {
-            uint16_t* kdst = &s_k[buf][kk * kKStr + kc];
-            *(uint4*)kdst = df.k0; *(uint4*)(kdst + 8) = df.k1;
-            uint16_t* vdst = &s_v[buf][td * kVStr + tq];
-            *(uint4*)vdst = df.v0; *(uint4*)(vdst + 8) = df.v1;
-        } else if (c.meta_dtype == FQ_BF16) {
-            store_k<BITS, FQ_BF16>(kf, &s_k[buf][kk * kKStr + kc]);
-            store_v<BITS, FQ_BF16>(vf, &s_v[buf][vd * kVStr + vk], kVStr);
-        } else {
-            store_k<BITS, FQ_F16>(kf, &s_k[buf][kk * kKStr + kc]);
-            store_v<BITS, FQ_F16>(vf, &s_v[buf][vd * kVStr + vk], kVStr);
-        }
-    };
-
-    if (nt > 0) { fetch(0); stage(0); }
+    // nt >= 1: key 0 is always attended (causal_off >= 0, S_kv >= 1)
+    prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, 0, b, h, kk, kc, vk, vd);
+    prefill_stage<SRC>(a, kf, vf, df, s_k[0], s_v[0], kk, kc, vd, vk, td, tq);
+    // every prologue load (Q included) lands before the loop: the loop's own
+    // waits then only cover the tile prefetched inside it
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
 
     for (int t = 0; t < nt; ++t) {
         const int cur = t & 1;
         const int key0 = t * kPKT;
-        if (t + 1 < nt) fetch(key0 + kPKT);
+        if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, key0 + kPKT, b, h, kk, kc, vk, vd);
+        __builtin_amdgcn_sched_barrier(0);
         if (wave_on && key0 < limit_w) {
             const uint16_t* sk = s_k[cur];
             const uint16_t* sv = s_v[cur];
@@ -338,13 +351,16 @@ void prefill_attn_kernel(PrefillParams a) {
             for (int kb = 0; kb < 4; ++kb) {
                 s[0][kb] = v4f{0.f, 0.f, 0.f, 0.f};
                 s[1][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+            // k-step outer: eight independent accumulators between dependent MFMAs
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
                     const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kKStr + 32 * ks + 8 * g);
                     s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[0][ks], s[0][kb], 0, 0, 0);
                     s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[1][ks], s[1][kb], 0, 0, 0);
                 }
-            }
             const bool need_mask = key0 + kPKT - 1 > pmin + a.causal_off || key0 + kPKT > a.Skv;
             v8bf pb[2][2];
             bool rescale = false;
@@ -395,19 +411,21 @@ void prefill_attn_kernel(PrefillParams a) {
                     for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
             }
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                const uint16_t* vrow = sv + (db * 16 + n) * kVStr + 4 * g;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint2 lo = *(const uint2*)(vrow + 32 * j);
-                    const uint2 hi = *(const uint2*)(vrow + 32 * j + 16);
-                    const v8bf av = __builtin_bit_cast(v8bf, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                for (int db = 0; db < 8; ++db) {
+                    const uint16_t* vrow = sv + (db * 16 + n) * kVStr + 4 * g + 32 * j;
+                    const u32x2 lo = *(const u32x2*)vrow;
+                    const u32x2 hi = *(const u32x2*)(vrow + 16);
+                    const v8bf av = __builtin_bit_cast(v8bf, u32x4{lo.x, lo.y, hi.x, hi.y});
                     o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[0][j], o[0][db], 0, 0, 0);
                     o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[1][j], o[1][db], 0, 0, 0);
                 }
-            }
         }
-        if (t + 1 < nt) stage(cur ^ 1);
+        // keep the LDS writes of the next tile after this tile's math, so the
+        // global loads issued above have the whole tile to arrive
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < nt) prefill_stage<SRC>(a, kf, vf, df, s_k[cur ^ 1], s_v[cur ^ 1], kk, kc, vd, vk, td, tq);
         __syncthreads();
     }
 
@@ -425,7 +443,7 @@ void prefill_attn_kernel(PrefillParams a) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
             const v4f r = o[qb][db] * inv;
-            *(uint2*)(orow + db * 16 + 4 * g) = make_uint2(pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3]));
+            *(u32x2*)(orow + db * 16 + 4 * g) = u32x2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
         }
     }
 }
