@@ -43,6 +43,7 @@ constexpr int kPRW = 32;               // query rows per wave (two 16-column blo
 constexpr int kPRows = kPW * kPRW;     // query rows per workgroup
 constexpr int kKStr = kPD + 8;         // bf16 per K row in LDS (272 B: conflict-free 16-byte reads)
 constexpr int kVStr = kPKT + 8;        // bf16 per V^T row in LDS (144 B)
+constexpr int kDenseKT = 128;          // keys per LDS stage of the dense (two-pass) source
 
 struct PrefillParams {
     Int4Cache c;
@@ -51,7 +52,7 @@ struct PrefillParams {
     void* out; int64_t o_s[3];
     uint16_t* kd;          // dense bf16 K   [b][h][S_pad][128]   (two-pass path)
     uint16_t* vtd;         // dense bf16 V^T [b][h][128][S_pad]
-    int s_pad;             // keys in the dense arrays, a multiple of 64 (zeros beyond S_kv)
+    int s_pad;             // keys in the dense arrays, a multiple of 128 (zeros beyond S_kv)
     int nrep, Sq, Skv, causal_off;
     float qk_scale;                    // sm_scale * log2(e)
 };
@@ -68,6 +69,22 @@ FQ_DEV uint32_t bf16_rne(float f) {    // fp32 -> bf16 bits, round to nearest ev
     return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 FQ_DEV uint32_t pack_bf16(float lo, float hi) { return bf16_rne(lo) | (bf16_rne(hi) << 16); }
+
+// Across the four 16-lane rows of a wave (lanes n, n + 16, n + 32, n + 48):
+// v_permlane16_swap / v_permlane32_swap exchange rows in VALU, no LDS trip.
+// Both partners of each swap combine the same two values in the same order.
+FQ_DEV float rows_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+FQ_DEV float rows_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
 
 // ---- K: one thread = one key x 16 channels --------------------------------
 // Raw bytes before dequantisation.
@@ -205,7 +222,7 @@ FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */
 }
 
 // ---- dense bf16 source (two-pass path) --------------------------------------
-struct DFetch { u32x4 k0, k1, v0, v1; };
+struct DFetch { u32x4 k[4], v[4]; };   // 32 bf16 of one K row, 32 of one V^T row
 
 // The first pass: dequantise the cache and the tail once into dense bf16 K and
 // V^T (keys padded with zeros to a multiple of 64).  One 512-thread block per
@@ -233,14 +250,123 @@ __global__ __launch_bounds__(512) void prefill_dequant_kernel(PrefillParams a) {
     *(u32x4*)(dst + 8) = *(const u32x4*)&s_v[d * kVStr + q + 8];
 }
 
+// S^T (64 keys x 32 query columns of this wave) = K Q^T for one LDS K tile.
+// k-step outer: eight independent accumulators between dependent MFMAs.
+FQ_DEV void qk_tile(const uint16_t* sk, const v8bf (&qf)[2][4], v4f (&s)[2][4], int n, int g) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        s[0][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+        s[1][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kKStr + 32 * ks + 8 * g);
+            s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[0][ks], s[0][kb], 0, 0, 0);
+            s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[1][ks], s[1][kb], 0, 0, 0);
+        }
+}
+
+// Online softmax of one S^T tile in three steps (mask, running max, exp and
+// pack P as the bf16 P^T operand), then O^T += V^T P^T from the LDS V^T tile.
+FQ_DEV void mask_tile(v4f (&s)[2][4], const int (&qpos)[2], int key0, int causal_off, int Skv, int g) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int lim = min(qpos[qb] + causal_off, Skv - 1) - key0 - 4 * g;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
+    }
+}
+
+// New running max per query column; returns whether it moved for any lane's column.
+FQ_DEV bool tile_max(const v4f (&s)[2][4], float (&m_run)[2], float (&m_use)[2], float (&alpha)[2], float qk_scale) {
+    bool moved = false;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float mx = fmaxf(fmaxf(s[qb][0][0], s[qb][0][1]), fmaxf(s[qb][0][2], s[qb][0][3]));
+#pragma unroll
+        for (int kb = 1; kb < 4; ++kb)
+            mx = fmaxf(mx, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
+        mx = rows_max(mx);
+        const float m_new = fmaxf(m_run[qb], mx * qk_scale);
+        m_use[qb] = m_new == -INFINITY ? 0.f : m_new;
+        alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use[qb]);
+        moved |= m_new != m_run[qb];
+        m_run[qb] = m_new;
+    }
+    return moved;
+}
+
+FQ_DEV void tile_exp(const v4f (&s)[2][4], const float (&m_use)[2], const float (&alpha)[2], float (&l_run)[2],
+                     v8bf (&pb)[2][2], float qk_scale) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float sum = 0.f;
+        float p[4][4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], qk_scale, -m_use[qb]));
+                sum += p[kb][cc];
+            }
+        l_run[qb] = fmaf(l_run[qb], alpha[qb], sum);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                pb[qb][j][cc] = (__bf16)p[2 * j][cc];
+                pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
+            }
+    }
+}
+
+FQ_DEV void tile_pv(v4f (&o)[2][8], const v8bf (&pb)[2][2], const uint16_t* sv, int vstr, int n, int g) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const uint16_t* vrow = sv + (db * 16 + n) * vstr + 4 * g + 32 * j;
+            const u32x2 lo = *(const u32x2*)vrow;
+            const u32x2 hi = *(const u32x2*)(vrow + 16);
+            const v8bf av = __builtin_bit_cast(v8bf, u32x4{lo.x, lo.y, hi.x, hi.y});
+            o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[0][j], o[0][db], 0, 0, 0);
+            o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[1][j], o[1][db], 0, 0, 0);
+        }
+}
+
+FQ_DEV void softmax_pv(v4f (&s)[2][4], v4f (&o)[2][8], float (&m_run)[2], float (&l_run)[2], const uint16_t* sv,
+                       int vstr, const int (&qpos)[2], int key0, int pmin, int causal_off, int Skv, float qk_scale, int n,
+                       int g) {
+    if (key0 + kPKT - 1 > pmin + causal_off || key0 + kPKT > Skv) mask_tile(s, qpos, key0, causal_off, Skv, g);
+    float m_use[2], alpha[2];
+    const bool moved = tile_max(s, m_run, m_use, alpha, qk_scale);
+    v8bf pb[2][2];
+    tile_exp(s, m_use, alpha, l_run, pb, qk_scale);
+    if (__builtin_amdgcn_ballot_w64(moved)) {   // the running max moved for some column
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
+    }
+    tile_pv(o, pb, sv, vstr, n, g);
+}
+
 template <int SRC>
 FQ_DEV void prefill_fetch(const PrefillParams& a, KFetch& kf, VFetch& vf, DFetch& df, const uint16_t* kd_base,
                           const uint16_t* vd_base, int key0, int b, int h, int kk, int kc, int vk, int vd) {
     if constexpr (SRC == 16) {
         const uint16_t* kp = kd_base + (int64_t)key0 * kPD;
-        df.k0 = *(const u32x4*)kp; df.k1 = *(const u32x4*)(kp + 8);
         const uint16_t* vp = vd_base + key0;
-        df.v0 = *(const u32x4*)vp; df.v1 = *(const u32x4*)(vp + 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            df.k[i] = *(const u32x4*)(kp + 8 * i);
+            df.v[i] = *(const u32x4*)(vp + 8 * i);
+        }
     } else {
         const bool whole = key0 + kPKT <= a.c.S;
         fetch_k<SRC>(kf, a, b, h, key0 + kk, kc, whole);
@@ -253,9 +379,12 @@ FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch
                           uint16_t* sv, int kk, int kc, int vd, int vk, int td, int tq) {
     if constexpr (SRC == 16) {
         uint16_t* kdst = sk + kk * kKStr + kc;
-        *(u32x4*)kdst = df.k0; *(u32x4*)(kdst + 8) = df.k1;
-        uint16_t* vdst = sv + td * kVStr + tq;
-        *(u32x4*)vdst = df.v0; *(u32x4*)(vdst + 8) = df.v1;
+        uint16_t* vdst = sv + td * (kDenseKT + 8) + tq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *(u32x4*)(kdst + 8 * i) = df.k[i];
+            *(u32x4*)(vdst + 8 * i) = df.v[i];
+        }
     } else if (a.c.meta_dtype == FQ_BF16) {
         store_k<SRC, FQ_BF16>(kf, sk + kk * kKStr + kc);
         store_v<SRC, FQ_BF16>(vf, sv + vd * kVStr + vk, kVStr);
@@ -268,8 +397,12 @@ FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch
 template <int SRC, int META>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_kernel(PrefillParams a) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kPKT * kKStr];
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * kVStr];
+    // One LDS stage holds ST keys: 128 for the dense source (two 64-key
+    // sub-tiles per barrier, 136 KB double-buffered), 64 for the packed source.
+    constexpr int ST = SRC == 16 ? kDenseKT : kPKT;
+    constexpr int VSTR = ST + 8;   // bf16 per V^T row (row stride = 4 banks mod 64: conflict-free reads)
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][ST * kKStr];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * VSTR];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
@@ -285,7 +418,7 @@ void prefill_attn_kernel(PrefillParams a) {
     const int Mtot = a.Sq * a.nrep;
     const int m0 = rb * kPRows;
     const int last_wg = (min(m0 + kPRows, Mtot) - 1) / a.nrep;
-    const int nt = (min(a.Skv, last_wg + a.causal_off + 1) + kPKT - 1) / kPKT;
+    const int nt = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;
 
     const int mw0 = m0 + w * kPRW;
     const bool wave_on = mw0 < Mtot;
@@ -320,9 +453,10 @@ void prefill_attn_kernel(PrefillParams a) {
         for (int db = 0; db < 8; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int kk = tid >> 3, kc = (tid & 7) * 16;      // K loader: one key, 16 channels
+    // K loader: one key, 16 channels (packed) or 32 channels (dense, 128 keys)
+    const int kk = SRC == 16 ? tid >> 2 : tid >> 3, kc = SRC == 16 ? (tid & 3) * 32 : (tid & 7) * 16;
     const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4; // V loader (packed): 4 keys, 4 channels
-    const int td = tid >> 2, tq = (tid & 3) * 16;       // V^T loader (dense): one channel, 16 keys
+    const int td = tid >> 2, tq = (tid & 3) * 32;       // V^T loader (dense): one channel, 32 keys
     const int64_t bh = (int64_t)b * c.Hkv + h;
     const uint16_t* kd_base = SRC == 16 ? a.kd + (bh * a.s_pad + kk) * kPD + kc : nullptr;
     const uint16_t* vd_base = SRC == 16 ? a.vtd + (bh * kPD + td) * a.s_pad + tq : nullptr;
@@ -333,97 +467,24 @@ void prefill_attn_kernel(PrefillParams a) {
     // nt >= 1: key 0 is always attended (causal_off >= 0, S_kv >= 1)
     prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, 0, b, h, kk, kc, vk, vd);
     prefill_stage<SRC>(a, kf, vf, df, s_k[0], s_v[0], kk, kc, vd, vk, td, tq);
-    // every prologue load (Q included) lands before the loop: the loop's own
-    // waits then only cover the tile prefetched inside it
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): prologue loads (Q included) land before the loop
     __syncthreads();
-
     for (int t = 0; t < nt; ++t) {
         const int cur = t & 1;
-        const int key0 = t * kPKT;
-        if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, key0 + kPKT, b, h, kk, kc, vk, vd);
+        const int key0 = t * ST;
+        if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, key0 + ST, b, h, kk, kc, vk, vd);
         __builtin_amdgcn_sched_barrier(0);
-        if (wave_on && key0 < limit_w) {
-            const uint16_t* sk = s_k[cur];
-            const uint16_t* sv = s_v[cur];
-            v4f s[2][4];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                s[0][kb] = v4f{0.f, 0.f, 0.f, 0.f};
-                s[1][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int sub = 0; sub < ST / kPKT; ++sub) {
+            const int k0 = key0 + sub * kPKT;
+            if (wave_on && k0 < limit_w) {
+                v4f s[2][4];
+                qk_tile(s_k[cur] + sub * kPKT * kKStr, qf, s, n, g);
+                softmax_pv(s, o, m_run, l_run, s_v[cur] + sub * kPKT, VSTR, qpos, k0, pmin, a.causal_off, a.Skv,
+                           a.qk_scale, n, g);
             }
-            // k-step outer: eight independent accumulators between dependent MFMAs
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kKStr + 32 * ks + 8 * g);
-                    s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[0][ks], s[0][kb], 0, 0, 0);
-                    s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[1][ks], s[1][kb], 0, 0, 0);
-                }
-            const bool need_mask = key0 + kPKT - 1 > pmin + a.causal_off || key0 + kPKT > a.Skv;
-            v8bf pb[2][2];
-            bool rescale = false;
-            float alpha[2];
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                if (need_mask) {
-                    const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1) - key0 - 4 * g;
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int cc = 0; cc < 4; ++cc)
-                            if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
-                }
-                float mx = fmaxf(fmaxf(s[qb][0][0], s[qb][0][1]), fmaxf(s[qb][0][2], s[qb][0][3]));
-#pragma unroll
-                for (int kb = 1; kb < 4; ++kb)
-                    mx = fmaxf(mx, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float m_new = fmaxf(m_run[qb], mx * a.qk_scale);
-                const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
-                rescale |= m_new != m_run[qb];
-                float sum = 0.f;
-                float p[4][4];
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) {
-                        p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], a.qk_scale, -m_use));
-                        sum += p[kb][cc];
-                    }
-                l_run[qb] = fmaf(l_run[qb], alpha[qb], sum);
-                m_run[qb] = m_new;
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) {
-                        pb[qb][j][cc] = (__bf16)p[2 * j][cc];
-                        pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
-                    }
-            }
-            if (__builtin_amdgcn_ballot_w64(rescale)) {   // the running max moved for some column
-#pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-                    for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    const uint16_t* vrow = sv + (db * 16 + n) * kVStr + 4 * g + 32 * j;
-                    const u32x2 lo = *(const u32x2*)vrow;
-                    const u32x2 hi = *(const u32x2*)(vrow + 16);
-                    const v8bf av = __builtin_bit_cast(v8bf, u32x4{lo.x, lo.y, hi.x, hi.y});
-                    o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[0][j], o[0][db], 0, 0, 0);
-                    o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[1][j], o[1][db], 0, 0, 0);
-                }
         }
-        // keep the LDS writes of the next tile after this tile's math, so the
-        // global loads issued above have the whole tile to arrive
+        // the dequantising LDS writes of the next tile after this tile's math
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < nt) prefill_stage<SRC>(a, kf, vf, df, s_k[cur ^ 1], s_v[cur ^ 1], kk, kc, vd, vk, td, tq);
         __syncthreads();
@@ -432,9 +493,7 @@ void prefill_attn_kernel(PrefillParams a) {
     if (!wave_on) return;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-        float l = l_run[qb];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        const float l = rows_sum(l_run[qb]);
         if (!qok[qb]) continue;
         const float inv = 1.0f / l;
         const int m = mw0 + qb * 16 + n;
@@ -459,7 +518,7 @@ int64_t prefill_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kPRo
 
 size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep) {
     if (prefill_row_blocks(Sq, nrep) < kTwoPassBlocks) return 0;
-    const int64_t s_pad = ((int64_t)Skv + kPKT - 1) / kPKT * kPKT;
+    const int64_t s_pad = ((int64_t)Skv + kDenseKT - 1) / kDenseKT * kDenseKT;
     return (size_t)(2 * s_pad * kPD * 2) * c.Hkv * c.B;
 }
 
@@ -479,7 +538,7 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
     const dim3 grid((unsigned)(nblk * c.Hkv * c.B));
     const bool bf = c.meta_dtype == FQ_BF16;
     if (prefill_workspace_bytes(c, a.Skv, Sq, nrep) > 0) {
-        a.s_pad = (a.Skv + kPKT - 1) / kPKT * kPKT;
+        a.s_pad = (a.Skv + kDenseKT - 1) / kDenseKT * kDenseKT;
         a.kd = (uint16_t*)ws;
         a.vtd = a.kd + (int64_t)a.s_pad * kPD * c.Hkv * c.B;
         const dim3 dgrid(a.s_pad / kPKT, c.Hkv, c.B);
