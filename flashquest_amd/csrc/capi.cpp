@@ -33,7 +33,7 @@ hipError_t launch_attn_turbo(const fq_turbo_cache& c, const QueryArgs& q, const 
 hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, const int64_t* q_s, void* out,
                           const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, void* ws,
                           hipStream_t st);
-size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep);
+size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, int causal_off);
 
 static thread_local std::string g_err;
 
@@ -791,7 +791,7 @@ static int prefill_check(const fq_int4_cache* cache, const fq_tail* tail, const 
     if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
     const int64_t rows = (int64_t)q->S_q * (q->H_q / c.Hkv);
     if ((rows + 255) / 256 * c.Hkv * c.B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
-    *ws_bytes = prefill_workspace_bytes(c, c.S + t.len, q->S_q, q->H_q / c.Hkv);
+    *ws_bytes = prefill_workspace_bytes(c, c.S + t.len, q->S_q, q->H_q / c.Hkv, q->causal_offset);
     return FQ_OK;
 }
 

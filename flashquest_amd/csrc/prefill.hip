@@ -24,6 +24,8 @@
 // the softmax statistics are per lane and P leaves the S^T accumulator already
 // in the layout of the P^T operand (keys 4g..4g+3 and 16+4g..16+4g+3 of a
 // 32-key step; V^T is read with the same key order).
+#include <algorithm>
+
 #include "fq_common.h"
 
 namespace fq {
@@ -509,16 +511,19 @@ void prefill_attn_kernel(PrefillParams a) {
 
 }  // namespace
 
-// Rows of 256 GQA-flattened queries per KV head at or above which the
-// two-pass path (dequantise once to dense bf16, then attend) beats
-// dequantising every K/V tile in every row block.
-constexpr int kTwoPassBlocks = 3;
+// The keys any query can attend: min(S_kv, S_q + causal_off).
+int64_t prefill_keys_needed(int Skv, int Sq, int causal_off) { return std::min<int64_t>(Skv, (int64_t)Sq + causal_off); }
 
 int64_t prefill_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kPRows - 1) / kPRows; }
 
-size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep) {
-    if (prefill_row_blocks(Sq, nrep) < kTwoPassBlocks) return 0;
-    const int64_t s_pad = ((int64_t)Skv + kDenseKT - 1) / kDenseKT * kDenseKT;
+// The fused path (each workgroup dequantises the K/V tiles it attends) only
+// for one row block per KV head over at most 1024 keys; otherwise the
+// two-pass path (dequantise the needed keys once, in parallel, into dense
+// bf16 K and V^T, then attend plain bf16 tiles) is faster.
+size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, int causal_off) {
+    const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
+    if (prefill_row_blocks(Sq, nrep) == 1 && keys <= 1024) return 0;
+    const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
     return (size_t)(2 * s_pad * kPD * 2) * c.Hkv * c.B;
 }
 
@@ -537,8 +542,8 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
     const int64_t nblk = prefill_row_blocks(Sq, nrep);
     const dim3 grid((unsigned)(nblk * c.Hkv * c.B));
     const bool bf = c.meta_dtype == FQ_BF16;
-    if (prefill_workspace_bytes(c, a.Skv, Sq, nrep) > 0) {
-        a.s_pad = (a.Skv + kDenseKT - 1) / kDenseKT * kDenseKT;
+    if (prefill_workspace_bytes(c, a.Skv, Sq, nrep, causal_off) > 0) {
+        a.s_pad = (int)((prefill_keys_needed(a.Skv, Sq, causal_off) + kDenseKT - 1) / kDenseKT * kDenseKT);
         a.kd = (uint16_t*)ws;
         a.vtd = a.kd + (int64_t)a.s_pad * kPD * c.Hkv * c.B;
         const dim3 dgrid(a.s_pad / kPKT, c.Hkv, c.B);

@@ -394,9 +394,10 @@ int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_pr
                     void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
 /* Workspace bytes fq_prefill_int4 (bits 4) / fq_prefill_int8 (bits 8) needs for
- * these arguments: 0 when every workgroup dequantises its own K/V tiles (few
- * query rows), else room for the dense bf16 K and V^T of the two-pass path
- * (dequantised once, 2 * 2 * 128 B per key and KV head).  0 also for invalid
+ * these arguments: 0 when the attention kernel dequantises its own K/V tiles
+ * (at most 256 / n_rep query rows over at most 1024 attended keys), else room
+ * for the dense bf16 K and V^T of the two-pass path (the attended keys
+ * dequantised once, 2 * 2 * 128 B per key and KV head, keys rounded up to 128).  0 also for invalid
  * arguments (the call then reports the error).  No reference counterpart. */
 size_t fq_prefill_workspace_bytes(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query,
                                   int32_t bits);

@@ -152,3 +152,11 @@ def test_prefill_over_persistent_cache_views(bits):
         ref = O.prefill_packed(Q[:, :, lo:hi], kc, ks, km, vc, vs, vm, K[:, :, comp:hi], V[:, :, comp:hi],
                                page_size=64, bits=bits)
         assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
+
+
+@pytest.mark.parametrize("kw", [dict(S=512, T=40, Sq=80, causal_offset=472), dict(S=512, T=40, Sq=80, meta="f16"),
+                                dict(S=256, T=9, Sq=60, vgroup=32, causal_offset=205), dict(S=960, T=63, Sq=20),
+                                dict(S=384, T=7, Sq=33, bits=8, causal_offset=358), dict(S=0, T=40, Sq=40, bits=8)])
+def test_prefill_single_pass_path(kw):
+    # one row block over at most 1024 attended keys: the kernel dequantises its own tiles
+    _check(PrefillCase(5, **kw))
