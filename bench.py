@@ -34,6 +34,7 @@ from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402
 
 METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 matrix peak (no sparsity)
 
 
 def parse():
@@ -53,6 +54,8 @@ def parse():
                     help="skip the batch-16 line (BASELINE config 4) among the extras")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="for rocprofv3 runs: 5 prefills of a 32k-token prompt over one INT4 layer only")
     ap.add_argument("--profile-turbo", action="store_true",
                     help="for rocprofv3 runs: 10 flushed fused TurboQuant decode steps (--select mode) only")
     return ap.parse_args()
@@ -200,6 +203,18 @@ class Flusher:
             torch.sum(self.buf)             # one read pass, a 4-byte result
 
 
+def prefill_inputs(S, Hq, dev, Hkv=8, D=128):
+    """A prompt of S tokens written to one layer's INT4 cache (K/V N(0,1) in
+    bf16, quantised by this build's quantisers), the bf16 queries, and the
+    empty partial-page tail (S is a whole number of pages)."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    K = torch.randn(1, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    V = torch.randn(1, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(1, Hq, S, D, device=dev, generator=g).to(torch.bfloat16)
+    planes = quantize_k_int4(K, 64) + quantize_v_int4(V)
+    return q, planes, K[:, :, :0], V[:, :, :0]
+
+
 def time_steps(fn_pre, fn_timed, steps, warmup, flush, kernel_timer=False):
     """Mean ms of fn_timed over `steps` runs (events on torch's current stream,
     which is the stream the library launches on), each after flush() and the
@@ -288,6 +303,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L, B, P = args.layers, args.batch, args.pages
+    if args.profile_prefill:
+        from flashquest_amd.kernel import flash_attn_prefill_int4
+        qp, pk, kt, vt = prefill_inputs(P * 64, 24, dev)   # config 1 shape: 24 query / 8 KV heads
+        for _ in range(5):
+            flash_attn_prefill_int4(qp, *pk, kt, vt, page_size=64)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_prefill": "done", "tokens": P * 64}))
+        return
     if args.profile_turbo:
         from flashquest_amd.eager.decode import quest_decode_turbo
         tc = make_turbo_cache(L, P=P, dev=dev)
@@ -483,6 +506,31 @@ def main():
                       "int8_step_GBps": i_bytes / (i_ms * 1e-3) / 1e9,
                       "int8_roofline_frac": i_bytes / (i_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
         del ic, iplanes
+
+        # Prefill over the packed cache (the reference's S_q > 1 branch,
+        # llama_persistent_patch.py:196-201) for one layer and a 32k-token
+        # prompt already written to the INT4 cache: this build's kernel
+        # (dequantise once, causal bf16 flash attention on the matrix cores) vs
+        # the reference's operator sequence (dequantise with tensor ops,
+        # concatenate, SDPA is_causal) timed on the same GPU.
+        from flashquest_amd.kernel import dequantize_k_int4, dequantize_v_int4, flash_attn_prefill_int4
+        import torch.nn.functional as F
+        Sp = P * 64
+        qp, pk, kt, vt = prefill_inputs(Sp, Hq, dev)
+        pf_steps = max(3, args.steps // 4)
+        pf_ms, _, _ = time_steps(noop, lambda: flash_attn_prefill_int4(qp, *pk, kt, vt, page_size=64),
+                                 pf_steps, 1, noop)
+
+        def ref_prefill():
+            Kf = torch.cat([dequantize_k_int4(pk[0], pk[1], pk[2], 64), kt], dim=2)
+            Vf = torch.cat([dequantize_v_int4(pk[3], pk[4], pk[5]), vt], dim=2)
+            return F.scaled_dot_product_attention(qp, Kf, Vf, is_causal=True, enable_gqa=True)
+        pr_ms, _, _ = time_steps(noop, ref_prefill, pf_steps, 1, noop)
+        pf_flops = 2.0 * Sp * Sp * 128 * Hq          # causal: 4 S^2 D H_q / 2
+        extra.update({"prefill_32k_layer_ms": pf_ms, "prefill_TFLOPs": pf_flops / (pf_ms * 1e-3) / 1e12,
+                      "prefill_mfma_frac": pf_flops / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                      "prefill_reference_sequence_ms": pr_ms, "prefill_speedup_vs_reference_sequence": pr_ms / pf_ms})
+        del qp, pk
 
         # batch 16 independent sequences, 28 layers, 32k each
         if B == 1 and args.batch16:
