@@ -147,6 +147,10 @@ SIGNATURES = {
                                        _P, ctypes.c_size_t, _P]),
     "fq_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Tail),
                                                      ctypes.POINTER(Prefill), _I]),
+    "fq_prefill_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), ctypes.POINTER(Tail), ctypes.POINTER(Prefill),
+                                        _P, ctypes.c_size_t, _P]),
+    "fq_prefill_turbo_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TurboCache), ctypes.POINTER(Tail),
+                                                           ctypes.POINTER(Prefill)]),
 }
 
 _lib = None

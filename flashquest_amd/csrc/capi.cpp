@@ -34,6 +34,10 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
                           const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, void* ws,
                           hipStream_t st);
 size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, int causal_off);
+size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int causal_off);
+hipError_t launch_prefill_turbo(const fq_turbo_cache& tc, const TailArgs& t, const void* q, const int64_t* q_s,
+                                void* out, const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale,
+                                void* ws, hipStream_t st);
 
 static thread_local std::string g_err;
 
@@ -752,6 +756,37 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p & (uintptr_t)(bytes - 1)) == 0; }
 
 // Validates a prefill call; on success fills c, t and the needed workspace size.
+static int prefill_check_tail_query(const fq_tail* tail, const fq_prefill* q, int D, int Hkv, int B, int S,
+                                    TailArgs& t) {
+    t = TailArgs{};
+    if (tail && tail->len > 0) {
+        if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
+        if (tail->dtype != FQ_BF16) return fail(FQ_ERR_UNSUPPORTED, "prefill tail must be bf16");
+        if (tail->D != D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, D);
+        if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
+            return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
+        for (int i = 1; i < 4; ++i)
+            if (tail->k_strides[i] % 8 || tail->v_strides[i] % 4)
+                return fail(FQ_ERR_UNSUPPORTED, "tail row strides must be multiples of 8 (K) / 4 (V) elements");
+        if (!aligned(tail->k, 16) || !aligned(tail->v, 8)) return fail(FQ_ERR_UNSUPPORTED, "tail K/V alignment");
+        t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
+        for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
+    }
+    if (!q || !q->q || !q->out) return fail(FQ_ERR_INVALID, "query/output is NULL");
+    if (q->H_q < 1 || q->H_q % Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, Hkv);
+    if (q->S_q < 1) return fail(FQ_ERR_INVALID, "S_q=%d", q->S_q);
+    if (q->causal_offset < 0) return fail(FQ_ERR_INVALID, "causal_offset=%d must be >= 0", q->causal_offset);
+    if ((int64_t)S + t.len < 1) return fail(FQ_ERR_INVALID, "no keys (S + tail = 0)");
+    if (q->q_strides[3] != 1 || q->o_strides[3] != 1) return fail(FQ_ERR_UNSUPPORTED, "Q/O channels must be contiguous");
+    for (int i = 0; i < 3; ++i)
+        if (q->q_strides[i] % 8 || q->o_strides[i] % 4)
+            return fail(FQ_ERR_UNSUPPORTED, "Q / O strides must be multiples of 8 / 4 elements");
+    if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
+    const int64_t rows = (int64_t)q->S_q * (q->H_q / Hkv);
+    if ((rows + 255) / 256 * Hkv * B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
+    return FQ_OK;
+}
+
 static int prefill_check(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* q, int bits, Int4Cache& c,
                          TailArgs& t, size_t* ws_bytes) {
     int st = check_cache(cache, &c, bits, true);
@@ -765,32 +800,8 @@ static int prefill_check(const fq_int4_cache* cache, const fq_tail* tail, const 
             if (c.kp_s[i] % kal) return fail(FQ_ERR_UNSUPPORTED, "K code strides must be multiples of %d bytes", kal);
         if (!aligned(c.kp, kal)) return fail(FQ_ERR_UNSUPPORTED, "K codes must be %d-byte aligned", kal);
     }
-    t = TailArgs{};
-    if (tail && tail->len > 0) {
-        if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
-        if (tail->dtype != FQ_BF16) return fail(FQ_ERR_UNSUPPORTED, "prefill tail must be bf16");
-        if (tail->D != c.D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, c.D);
-        if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
-            return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
-        for (int i = 1; i < 4; ++i)
-            if (tail->k_strides[i] % 8 || tail->v_strides[i] % 4)
-                return fail(FQ_ERR_UNSUPPORTED, "tail row strides must be multiples of 8 (K) / 4 (V) elements");
-        if (!aligned(tail->k, 16) || !aligned(tail->v, 8)) return fail(FQ_ERR_UNSUPPORTED, "tail K/V alignment");
-        t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
-        for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
-    }
-    if (!q || !q->q || !q->out) return fail(FQ_ERR_INVALID, "query/output is NULL");
-    if (q->H_q < 1 || q->H_q % c.Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, c.Hkv);
-    if (q->S_q < 1) return fail(FQ_ERR_INVALID, "S_q=%d", q->S_q);
-    if (q->causal_offset < 0) return fail(FQ_ERR_INVALID, "causal_offset=%d must be >= 0", q->causal_offset);
-    if ((int64_t)c.S + t.len < 1) return fail(FQ_ERR_INVALID, "no keys (S + tail = 0)");
-    if (q->q_strides[3] != 1 || q->o_strides[3] != 1) return fail(FQ_ERR_UNSUPPORTED, "Q/O channels must be contiguous");
-    for (int i = 0; i < 3; ++i)
-        if (q->q_strides[i] % 8 || q->o_strides[i] % 4)
-            return fail(FQ_ERR_UNSUPPORTED, "Q / O strides must be multiples of 8 / 4 elements");
-    if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
-    const int64_t rows = (int64_t)q->S_q * (q->H_q / c.Hkv);
-    if ((rows + 255) / 256 * c.Hkv * c.B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
+    st = prefill_check_tail_query(tail, q, c.D, c.Hkv, c.B, c.S, t);
+    if (st) return st;
     *ws_bytes = prefill_workspace_bytes(c, c.S + t.len, q->S_q, q->H_q / c.Hkv, q->causal_offset);
     return FQ_OK;
 }
@@ -819,6 +830,46 @@ size_t fq_prefill_workspace_bytes(const fq_int4_cache* cache, const fq_tail* tai
     if (bits != 4 && bits != 8) return 0;
     if (prefill_check(cache, tail, query, bits, c, t, &need)) return 0;
     return need;
+}
+
+static int prefill_turbo_check(const fq_turbo_cache* c, const fq_tail* tail, const fq_prefill* q, TailArgs& t,
+                               size_t* ws_bytes) {
+    if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    if (c->L != 1) return fail(FQ_ERR_INVALID, "prefill takes one layer's cache view (L=%d)", c->L);
+    if (c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "prefill head_dim=%d (128 only)", c->D);
+    if (c->B < 1 || c->H_kv < 1 || c->S < 0) return fail(FQ_ERR_INVALID, "empty B/H_kv or negative S");
+    if (c->S > 0) {
+        if (!c->k_msb || !c->k_lsb || !c->k_scale || !c->v_msb || !c->v_lsb || !c->v_scale)
+            return fail(FQ_ERR_INVALID, "NULL cache tensor");
+        if (c->kmsb_strides[4] != 1 || c->klsb_strides[4] != 1 || c->vmsb_strides[4] != 1 || c->vlsb_strides[4] != 1)
+            return fail(FQ_ERR_UNSUPPORTED, "innermost plane axis must be contiguous");
+    }
+    int st = prefill_check_tail_query(tail, q, c->D, c->H_kv, c->B, c->S, t);
+    if (st) return st;
+    *ws_bytes = prefill_turbo_workspace_bytes(c->H_kv, c->B, c->S + t.len, q->S_q, q->causal_offset);
+    return FQ_OK;
+}
+
+size_t fq_prefill_turbo_workspace_bytes(const fq_turbo_cache* cache, const fq_tail* tail, const fq_prefill* query) {
+    TailArgs t{};
+    size_t need = 0;
+    if (prefill_turbo_check(cache, tail, query, t, &need)) return 0;
+    return need;
+}
+
+int fq_prefill_turbo(const fq_turbo_cache* cache, const fq_tail* tail, const fq_prefill* q, void* workspace,
+                     size_t workspace_bytes_, fq_stream_t stream) {
+    TailArgs t{};
+    size_t need = 0;
+    int st = prefill_turbo_check(cache, tail, q, t, &need);
+    if (st) return st;
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "prefill workspace of %zu bytes needed (got %zu)", need, workspace_bytes_);
+    if (!aligned(workspace, 16)) return fail(FQ_ERR_INVALID, "workspace must be 16-byte aligned");
+    const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)cache->D);
+    return hip_status(launch_prefill_turbo(*cache, t, q->q, q->q_strides, q->out, q->o_strides, q->H_q / cache->H_kv,
+                                           q->S_q, q->causal_offset, sm * kLog2e, workspace, (hipStream_t)stream),
+                      "turbo prefill launch");
 }
 
 int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_prefill* query, void* workspace,

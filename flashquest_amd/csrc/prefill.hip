@@ -358,6 +358,91 @@ FQ_DEV void softmax_pv(v4f (&s)[2][4], v4f (&o)[2][8], float (&m_run)[2], float 
     tile_pv(o, pb, sv, vstr, n, g);
 }
 
+// ---- TurboQuant source: dequantise the rotated codes and rotate back ---------
+// dequantize_k_turbo / dequantize_v_turbo (kv_quant.py:366-420): index
+// idx = (msb bit << 2) | lsb field (msb byte j bit i = channel 8j + i, lsb
+// byte j field i = channel 4j + i), value = codebook[idx] * fp32(scale), then
+// the normalised WHT (wht.py:17-41: stages h = 1, 2, ..., 64 of (a + b, a - b)
+// in fp32, then times fp32(1 / sqrt(128))), then bf16.
+struct TurboPrefill {
+    const uint8_t* k_msb; int64_t kmsb_s[3];   // (b, h, token) byte strides
+    const uint8_t* k_lsb; int64_t klsb_s[3];
+    const uint16_t* k_sc; int64_t ksc_s[3];     // bf16 per-token scale
+    const uint8_t* v_msb; int64_t vmsb_s[3];
+    const uint8_t* v_lsb; int64_t vlsb_s[3];
+    const uint16_t* v_sc; int64_t vsc_s[3];
+};
+
+FQ_DEV float turbo_value(uint32_t idx) {   // kv_quant.py:225-229
+    const uint32_t pos = idx & 4u;
+    const uint32_t t = pos ? (idx & 3u) : ((idx & 3u) ^ 3u);
+    const float m01 = (t & 1u) ? 0.7560f : 0.2451f;
+    const float m23 = (t & 1u) ? 2.1519f : 1.3439f;
+    const float mag = (t & 2u) ? m23 : m01;
+    return pos ? mag : -mag;
+}
+
+// One wave per token: lane l holds channels l and l + 64.
+FQ_DEV void turbo_token(const uint8_t* msb, const uint8_t* lsb, const uint16_t* sc, int lane, float& v0, float& v1) {
+    const float scale = bf16_bits_to_f(*sc);
+    const uint32_t m0 = msb[lane >> 3], m1 = msb[(lane + 64) >> 3];
+    const uint32_t l0 = lsb[lane >> 2], l1 = lsb[(lane + 64) >> 2];
+    v0 = turbo_value((((m0 >> (lane & 7)) & 1u) << 2) | ((l0 >> (2 * (lane & 3))) & 3u)) * scale;
+    v1 = turbo_value((((m1 >> (lane & 7)) & 1u) << 2) | ((l1 >> (2 * (lane & 3))) & 3u)) * scale;
+#pragma unroll
+    for (int hh = 1; hh < 64; hh <<= 1) {
+        const float y0 = __shfl_xor(v0, hh, 64), y1 = __shfl_xor(v1, hh, 64);
+        v0 = (lane & hh) ? y0 - v0 : v0 + y0;
+        v1 = (lane & hh) ? y1 - v1 : v1 + y1;
+    }
+    const float x = v0, y = v1;
+    const float inv = 1.0f / sqrtf(128.0f);
+    v0 = (x + y) * inv;
+    v1 = (x - y) * inv;
+}
+
+// The first pass for the TurboQuant cache: dense bf16 K and V^T of the
+// attended keys (tail rows copied, zeros beyond S_kv).  One 512-thread block
+// per (64-key tile, b, h), one wave per token, V through LDS to be written
+// transposed.
+__global__ __launch_bounds__(512) void prefill_dequant_turbo_kernel(PrefillParams a, TurboPrefill tq) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kPD * kVStr];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int key0 = blockIdx.x * kPKT, h = blockIdx.y, b = blockIdx.z;
+    const int64_t bh = (int64_t)b * a.c.Hkv + h;
+    for (int j = w; j < kPKT; j += kPW) {
+        const int key = key0 + j;
+        float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+        uint32_t kb0, kb1, vb0, vb1;
+        if (key < a.c.S) {
+            turbo_token(tq.k_msb + b * tq.kmsb_s[0] + h * tq.kmsb_s[1] + (int64_t)key * tq.kmsb_s[2],
+                        tq.k_lsb + b * tq.klsb_s[0] + h * tq.klsb_s[1] + (int64_t)key * tq.klsb_s[2],
+                        tq.k_sc + b * tq.ksc_s[0] + h * tq.ksc_s[1] + (int64_t)key * tq.ksc_s[2], lane, k0, k1);
+            turbo_token(tq.v_msb + b * tq.vmsb_s[0] + h * tq.vmsb_s[1] + (int64_t)key * tq.vmsb_s[2],
+                        tq.v_lsb + b * tq.vlsb_s[0] + h * tq.vlsb_s[1] + (int64_t)key * tq.vlsb_s[2],
+                        tq.v_sc + b * tq.vsc_s[0] + h * tq.vsc_s[1] + (int64_t)key * tq.vsc_s[2], lane, v0, v1);
+            kb0 = bf16_rne(k0); kb1 = bf16_rne(k1); vb0 = bf16_rne(v0); vb1 = bf16_rne(v1);
+        } else if (key < a.Skv) {
+            const uint16_t* kr = (const uint16_t*)a.t.k + b * a.t.ks[1] + h * a.t.ks[2] + (int64_t)(key - a.c.S) * a.t.ks[3];
+            const uint16_t* vr = (const uint16_t*)a.t.v + b * a.t.vs[1] + h * a.t.vs[2] + (int64_t)(key - a.c.S) * a.t.vs[3];
+            kb0 = kr[lane]; kb1 = kr[lane + 64]; vb0 = vr[lane]; vb1 = vr[lane + 64];
+        } else {
+            kb0 = kb1 = vb0 = vb1 = 0u;
+        }
+        uint16_t* krow = a.kd + (bh * a.s_pad + key) * kPD;
+        krow[lane] = (uint16_t)kb0;
+        krow[lane + 64] = (uint16_t)kb1;
+        s_v[lane * kVStr + j] = (uint16_t)vb0;
+        s_v[(lane + 64) * kVStr + j] = (uint16_t)vb1;
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    const int d = tid >> 2, q = (tid & 3) * 16;
+    uint16_t* dst = a.vtd + (bh * kPD + d) * a.s_pad + key0 + q;
+    *(u32x4*)dst = *(const u32x4*)&s_v[d * kVStr + q];
+    *(u32x4*)(dst + 8) = *(const u32x4*)&s_v[d * kVStr + q + 8];
+}
+
 template <int SRC>
 FQ_DEV void prefill_fetch(const PrefillParams& a, KFetch& kf, VFetch& vf, DFetch& df, const uint16_t* kd_base,
                           const uint16_t* vd_base, int key0, int b, int h, int kk, int kc, int vk, int vd) {
@@ -562,6 +647,45 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
     timer_before_launch(st);
     if (c.bits == 8) hipLaunchKernelGGL((prefill_attn_kernel<8, FQ_BF16>), grid, dim3(512), 0, st, a);
     else hipLaunchKernelGGL((prefill_attn_kernel<4, FQ_BF16>), grid, dim3(512), 0, st, a);
+    timer_after_launch(st);
+    return hipGetLastError();
+}
+
+size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int causal_off) {
+    const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
+    const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
+    return (size_t)(2 * s_pad * kPD * 2) * Hkv * B;
+}
+
+// Prefill over the TurboQuant cache: always the two-pass path (the first pass
+// dequantises and rotates back every attended key).
+hipError_t launch_prefill_turbo(const fq_turbo_cache& tc, const TailArgs& t, const void* q, const int64_t* q_s,
+                                void* out, const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale,
+                                void* ws, hipStream_t st) {
+    PrefillParams a{};
+    a.c.B = tc.B; a.c.Hkv = tc.H_kv; a.c.S = tc.S; a.c.D = tc.D; a.c.page = tc.page_size; a.c.G = 1;
+    a.c.meta_dtype = FQ_BF16;
+    a.t = t;
+    a.q = q; a.out = out;
+    for (int i = 0; i < 3; ++i) { a.q_s[i] = q_s[i]; a.o_s[i] = o_s[i]; }
+    a.nrep = nrep; a.Sq = Sq; a.Skv = tc.S + t.len; a.causal_off = causal_off; a.qk_scale = qk_scale;
+    a.s_pad = (int)((prefill_keys_needed(a.Skv, Sq, causal_off) + kDenseKT - 1) / kDenseKT * kDenseKT);
+    a.kd = (uint16_t*)ws;
+    a.vtd = a.kd + (int64_t)a.s_pad * kPD * tc.H_kv * tc.B;
+    TurboPrefill tp{};
+    tp.k_msb = tc.k_msb; tp.k_lsb = tc.k_lsb; tp.k_sc = (const uint16_t*)tc.k_scale;
+    tp.v_msb = tc.v_msb; tp.v_lsb = tc.v_lsb; tp.v_sc = (const uint16_t*)tc.v_scale;
+    for (int i = 0; i < 3; ++i) {   // layer 0: (l, b, h, token) -> (b, h, token)
+        tp.kmsb_s[i] = tc.kmsb_strides[i + 1]; tp.klsb_s[i] = tc.klsb_strides[i + 1];
+        tp.ksc_s[i] = tc.kst_strides[i + 1];
+        tp.vmsb_s[i] = tc.vmsb_strides[i + 1]; tp.vlsb_s[i] = tc.vlsb_strides[i + 1];
+        tp.vsc_s[i] = tc.vst_strides[i + 1];
+    }
+    hipLaunchKernelGGL(prefill_dequant_turbo_kernel, dim3(a.s_pad / kPKT, tc.H_kv, tc.B), dim3(512), 0, st, a, tp);
+    const int64_t nblk = prefill_row_blocks(Sq, nrep);
+    timer_before_launch(st);
+    hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), dim3((unsigned)(nblk * tc.H_kv * tc.B)), dim3(512), 0,
+                       st, a);
     timer_after_launch(st);
     return hipGetLastError();
 }

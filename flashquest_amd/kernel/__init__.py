@@ -3,7 +3,7 @@ from .kv_quant import (  # noqa: F401
     dequantize_k, dequantize_k_int4, dequantize_v, dequantize_v_int4, quantize_k, quantize_k_int4,
     quantize_k_turbo, quantize_v, quantize_v_int4, quantize_v_turbo,
 )
-from .prefill import flash_attn_prefill_int4, flash_attn_prefill_int8  # noqa: F401
+from .prefill import flash_attn_prefill_int4, flash_attn_prefill_int8, flash_attn_prefill_turbo  # noqa: F401
 from .sparse_fwd import flash_attn_sparse_fwd  # noqa: F401
 from .sparse_int4_fwd import flash_attn_sparse_int4_fwd  # noqa: F401
 from .sparse_int4_fwd_compact import flash_attn_sparse_int4_fwd_compact  # noqa: F401

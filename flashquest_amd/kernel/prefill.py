@@ -39,8 +39,10 @@ def _prefill_call(fn_name: str, cache_desc, keep, q, K_tail, V_tail, causal_offs
     out = torch.empty(B, H_q, S_q, D, dtype=torch.bfloat16, device=q.device)
     pq = L.Prefill(qb.data_ptr(), L.strides(qb, 4), out.data_ptr(), L.strides(out, 4), H_q, S_q,
                    int(causal_offset), float(sm_scale) if sm_scale is not None else 0.0)
-    bits = 4 if fn_name.endswith("int4") else 8
-    nbytes = L.lib().fq_prefill_workspace_bytes(cache_desc, tail, pq, bits)
+    if fn_name == "fq_prefill_turbo":
+        nbytes = L.lib().fq_prefill_turbo_workspace_bytes(cache_desc, tail, pq)
+    else:
+        nbytes = L.lib().fq_prefill_workspace_bytes(cache_desc, tail, pq, 4 if fn_name.endswith("int4") else 8)
     # the dense bf16 K / V^T of the two-pass path: written in full before it is read
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
     L.check(getattr(L.lib(), fn_name)(cache_desc, tail, pq, L.ptr(ws), nbytes, L.stream_handle(q.device)), fn_name)
@@ -66,3 +68,15 @@ def flash_attn_prefill_int8(q, K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, K
     K_uint8 = _ops._ensure_inner_contiguous(K_uint8, 16)
     c, keep = _ops.int8_cache(K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, page_size)
     return _prefill_call("fq_prefill_int8", c, keep, q, K_tail, V_tail, causal_offset, sm_scale)
+
+
+def flash_attn_prefill_turbo(q, K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo, K_tail=None, V_tail=None,
+                             *, page_size: int = 64, causal_offset: int = 0, sm_scale: float | None = None):
+    """flash_attn_prefill_int4 over the TurboQuant K3-V3 cache: the planes are
+    dequantised as dequantize_k_turbo / dequantize_v_turbo
+    (kernel/kv_quant.py:366-420: codebook * scale, inverse WHT, bf16) once
+    into dense bf16 K / V^T, then attended like the INT4 two-pass path."""
+    S = K_msb.shape[-2]
+    c, keep = _ops.turbo_cache(K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo,
+                               (S + page_size - 1) // page_size, page_size)
+    return _prefill_call("fq_prefill_turbo", c, keep, q, K_tail, V_tail, causal_offset, sm_scale)

@@ -393,6 +393,17 @@ int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_pr
 int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query,
                     void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* The prefill branch over the TurboQuant cache (llama_persistent_patch.py:
+ * 93-102, 196-201: dequantize_k_turbo / dequantize_v_turbo, kernel/kv_quant.py:
+ * 366-420, i.e. codebook * scale, inverse WHT, bf16; then causal SDPA over
+ * cat(dequantised, K_partial / V_partial)).  cache: one layer (L == 1),
+ * D == 128, S completed tokens (may be 0).  Always needs the workspace of
+ * fq_prefill_turbo_workspace_bytes (dense bf16 K and V^T of the attended keys). */
+int fq_prefill_turbo(const fq_turbo_cache* cache, const fq_tail* tail, const fq_prefill* query,
+                     void* workspace, size_t workspace_bytes, fq_stream_t stream);
+/* No reference counterpart: workspace bytes of fq_prefill_turbo (0 for invalid arguments). */
+size_t fq_prefill_turbo_workspace_bytes(const fq_turbo_cache* cache, const fq_tail* tail, const fq_prefill* query);
+
 /* Workspace bytes fq_prefill_int4 (bits 4) / fq_prefill_int8 (bits 8) needs for
  * these arguments: 0 when the attention kernel dequantises its own K/V tiles
  * (at most 256 / n_rep query rows over at most 1024 attended keys), else room

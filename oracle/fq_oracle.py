@@ -783,6 +783,12 @@ def dequant_turbo_rot(msb, lsb, scale, D: int):
     return TURBO_CODEBOOK[idx.astype(np.int64)] * np.asarray(scale, F32)
 
 
+def dequant_turbo_bf16(msb, lsb, scale, D: int = 128):
+    """dequantize_k_turbo / dequantize_v_turbo (kernel/kv_quant.py:366-420):
+    codebook[idx] * fp32(scale), the fp32 WHT (wht.py:17-41), then bf16."""
+    return round_bf16(wht(dequant_turbo_rot(msb, lsb, scale, D), "f32"))
+
+
 def sparse_turbo_attention(Q, K_msb, K_lsb, K_st, V_msb, V_lsb, V_st, page_mask,
                            page_size=64, sm_scale=None):
     """flash_attn_sparse_turbo_fwd semantics (sparse_turbo_fwd.py:254-346), exact:

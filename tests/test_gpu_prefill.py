@@ -160,3 +160,51 @@ def test_prefill_over_persistent_cache_views(bits):
 def test_prefill_single_pass_path(kw):
     # one row block over at most 1024 attended keys: the kernel dequantises its own tiles
     _check(PrefillCase(5, **kw))
+
+
+def _turbo_case(seed, B=1, Hq=6, Hkv=2, S=256, T=17, Sq=None):
+    rng = np.random.default_rng(seed)
+    K, V = make_kv(rng, B, Hkv, S + T, 128, "bf16")
+    km, kl, ks = O.quantize_turbo(K[:, :, :S])
+    vm, vl, vs = O.quantize_turbo(V[:, :, :S])
+    Sq = S + T if Sq is None else Sq
+    Q = O.round_bf16(rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32))
+    return K, V, Q, (km, kl, ks, vm, vl, vs)
+
+
+@pytest.mark.parametrize("S,T,Sq,off,Hq,Hkv", [(256, 17, None, 0, 6, 2), (512, 0, None, 0, 8, 2),
+                                               (384, 40, 100, 0, 24, 8), (384, 40, 100, 324, 6, 2),
+                                               (0, 50, None, 0, 4, 4)])
+def test_prefill_turbo(S, T, Sq, off, Hq, Hkv):
+    """The TurboQuant prefill: dequantize_k_turbo / dequantize_v_turbo (codebook x scale, inverse WHT,
+    bf16; kv_quant.py:366-420), the bf16 tail, causal SDPA."""
+    from flashquest_amd.kernel import flash_attn_prefill_turbo
+    K, V, Q, (km, kl, ks, vm, vl, vs) = _turbo_case(S + T + Hq, Hq=Hq, Hkv=Hkv, S=S, T=T, Sq=Sq)
+    out = flash_attn_prefill_turbo(to_dev_half(Q, "bf16"), to_dev(km), to_dev(kl), to_dev_half(ks, "bf16"),
+                                   to_dev(vm), to_dev(vl), to_dev_half(vs, "bf16"),
+                                   to_dev_half(K[:, :, S:], "bf16"), to_dev_half(V[:, :, S:], "bf16"),
+                                   page_size=64, causal_offset=off)
+    Kf = np.concatenate([O.dequant_turbo_bf16(km, kl, ks), K[:, :, S:]], axis=2)
+    Vf = np.concatenate([O.dequant_turbo_bf16(vm, vl, vs), V[:, :, S:]], axis=2)
+    ref = O.causal_prefill_attention(Q, Kf, Vf, causal_offset=off)
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
+
+
+def test_prefill_over_persistent_turbo_views():
+    from flashquest_amd.cache import PersistentTurboKVCache
+    from flashquest_amd.eager import prefill_attention_layer
+    rng = np.random.default_rng(77)
+    B, Hq, H, n = 1, 6, 2, 333
+    K, V = make_kv(rng, B, H, n, 128, "bf16")
+    Q = O.round_bf16(rng.standard_normal((B, Hq, n, 128)).astype(np.float32))
+    cache = PersistentTurboKVCache(batch_size=B, num_layers=1, num_kv_heads=H, head_dim=128, max_seq_len=512)
+    cache.update_quantized(to_dev_half(K, "bf16"), to_dev_half(V, "bf16"), 0)
+    views = cache.get_views(0)
+    out = prefill_attention_layer(to_dev_half(Q, "bf16"), views, page_size=64)
+    comp = views["completed_len"]
+    km, kl, ks = O.quantize_turbo(K[:, :, :comp])
+    vm, vl, vs = O.quantize_turbo(V[:, :, :comp])
+    Kf = np.concatenate([O.dequant_turbo_bf16(km, kl, ks), K[:, :, comp:]], axis=2)
+    Vf = np.concatenate([O.dequant_turbo_bf16(vm, vl, vs), V[:, :, comp:]], axis=2)
+    ref = O.causal_prefill_attention(Q, Kf, Vf)
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL

@@ -65,3 +65,18 @@ def test_dequant_bf16_matches_reference_expression(bits, meta, group):
     # round trip: within half a quantisation step (+ bf16 rounding)
     step_k = np.repeat(ks, 32, axis=-2)[..., :S, :]
     assert np.all(np.abs(kd - K) <= step_k * 0.5 + np.abs(K) * 2 ** -8 + 1e-6)
+
+
+def test_dequant_turbo_bf16_closed_form():
+    # codebook * scale then the normalised Hadamard transform (Sylvester matrix, fp64) -> within one bf16 ulp
+    rng = np.random.default_rng(9)
+    X = O.round_bf16(rng.standard_normal((1, 2, 40, 128)).astype(np.float32))
+    msb, lsb, st = O.quantize_turbo(X)
+    got = O.dequant_turbo_bf16(msb, lsb, st)
+    rot = O.dequant_turbo_rot(msb, lsb, st, 128).astype(np.float64)
+    ref = rot @ O.hadamard_matrix(128).T          # hadamard_matrix is already normalised
+    # one bf16 ulp, plus the fp32 butterflies' cancellation on near-zero outputs
+    ulp = np.abs(O.round_bf16(ref.astype(np.float32))) * 2 ** -7 + 1e-5
+    assert np.all(np.abs(got - ref) <= ulp)
+    # and the transform undoes the quantiser's rotation: close to the input
+    assert np.abs(got - X).mean() < 0.25
