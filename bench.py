@@ -54,6 +54,8 @@ def parse():
                     help="skip the batch-16 line (BASELINE config 4) among the extras")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
+    ap.add_argument("--profile-int8", action="store_true",
+                    help="for rocprofv3 runs: 10 flushed fused INT8 decode steps (--select mode) only")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for rocprofv3 runs: 5 prefills of a 32k-token prompt over one INT4 layer only")
     ap.add_argument("--profile-turbo", action="store_true",
@@ -303,6 +305,19 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L, B, P = args.layers, args.batch, args.pages
+    if args.profile_int8:
+        from flashquest_amd.eager.decode import quest_decode_int8
+        ic = make_int8_cache(L, P=P, dev=dev)
+        iplanes = [ic[x] for x in ("K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")]
+        flush = Flusher(dev)
+        k = math.ceil(args.retention * P)
+        for _ in range(10):
+            flush()
+            quest_decode_int8(ic["Q"], *iplanes, retention=args.retention, num_sinks=4, window_pages=2,
+                              k_max_static=k, select_mode=args.select)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_int8": "done", "select": args.select}))
+        return
     if args.profile_prefill:
         from flashquest_amd.kernel import flash_attn_prefill_int4
         qp, pk, kt, vt = prefill_inputs(P * 64, 24, dev)   # config 1 shape: 24 query / 8 KV heads

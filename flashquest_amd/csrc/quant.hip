@@ -127,6 +127,51 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(QuantVParams a) {
     }
 }
 
+// The same quantiser with a lane per channel pair (channels 2p, 2p + 1): a
+// token's row is read by consecutive lanes (coalesced), the group's min / max
+// come from lane shuffles over group / 2 lanes, and each lane writes its two
+// codes.  For D in {64, 128} and power-of-two groups (the cache layouts); the
+// arithmetic per element is the one-thread kernel's.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void quant_v_wave_kernel(QuantVParams a) {
+    constexpr float kMaxCode = (1 << BITS) - 1;
+    const int64_t p = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int half = a.D / 2;
+    const int64_t total = (int64_t)a.B * a.H * a.S * half;
+    const bool live = p < total;
+    const int64_t pp = live ? p : 0;
+    const int pair = pp % half;
+    const int64_t tok = pp / half;
+    const int t = tok % a.S;
+    const int h = (tok / a.S) % a.H;
+    const int b = tok / ((int64_t)a.S * a.H);
+    const int64_t base = b * a.v_s[0] + h * a.v_s[1] + t * a.v_s[2];
+    const int d = 2 * pair;
+    const float v0 = load_any(a.v, a.in_dtype, base + d * a.v_s[3]);
+    const float v1 = load_any(a.v, a.in_dtype, base + (d + 1) * a.v_s[3]);
+    float mn = fminf(v0, v1), mx = fmaxf(v0, v1);
+    for (int off = 1; off < a.group / 2; off <<= 1) {   // lanes of one group: aligned, power-of-two span
+        mn = fminf(mn, __shfl_xor(mn, off, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    if (!live) return;
+    const float s = fmaxf((mx - mn) * (BITS == 8 ? kInv255 : kInv15), kEps);
+    const int gi = d / a.group;
+    if (d % a.group == 0) {
+        store_any(a.scale, a.meta_dtype, b * a.s_s[0] + h * a.s_s[1] + t * a.s_s[2] + gi * a.s_s[3], s);
+        store_any(a.mn, a.meta_dtype, b * a.m_s[0] + h * a.m_s[1] + t * a.m_s[2] + gi * a.m_s[3], mn);
+    }
+    const float c0 = fminf(fmaxf(rintf(__fdiv_rn(v0 - mn, s)), 0.f), kMaxCode);
+    const float c1 = fminf(fmaxf(rintf(__fdiv_rn(v1 - mn, s)), 0.f), kMaxCode);
+    uint8_t* prow = a.packed + b * a.p_s[0] + h * a.p_s[1] + t * a.p_s[2];
+    if constexpr (BITS == 8) {
+        prow[d * a.p_s[3]] = (uint8_t)c0;
+        prow[(d + 1) * a.p_s[3]] = (uint8_t)c1;
+    } else {
+        prow[pair * a.p_s[3]] = (uint8_t)((uint32_t)c0 | ((uint32_t)c1 << 4));
+    }
+}
+
 // -------------------------------------------------------------------------
 // WHT along the last axis (wht.py:17-41): stages h = 1, 2, ..., D/2 of
 // (a + b, a - b), each rounded to arith_dtype, then * fp32(1/sqrt(D)).
@@ -366,8 +411,16 @@ hipError_t launch_quant_v(const void* v, int in_dtype, const int64_t* v_s, int B
     for (int i = 0; i < 4; ++i) { a.v_s[i] = v_s[i]; a.p_s[i] = p_s[i]; a.s_s[i] = s_s[i]; a.m_s[i] = m_s[i]; }
     const int64_t total = (int64_t)B * H * S * a.G;
     if (total == 0) return hipSuccess;
-    if (bits == 8) hipLaunchKernelGGL(quant_v_kernel<8>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL(quant_v_kernel<4>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    const bool pow2 = group >= 2 && (group & (group - 1)) == 0;
+    if ((D == 64 || D == 128) && pow2) {
+        const int64_t pairs = (int64_t)B * H * S * (D / 2);
+        if (bits == 8) hipLaunchKernelGGL(quant_v_wave_kernel<8>, dim3(blocks_for(pairs)), dim3(kThreads), 0, st, a);
+        else hipLaunchKernelGGL(quant_v_wave_kernel<4>, dim3(blocks_for(pairs)), dim3(kThreads), 0, st, a);
+    } else if (bits == 8) {
+        hipLaunchKernelGGL(quant_v_kernel<8>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(quant_v_kernel<4>, dim3(blocks_for(total)), dim3(kThreads), 0, st, a);
+    }
     return hipGetLastError();
 }
 
