@@ -236,9 +236,10 @@ _ws: dict = {}
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per-(device, stream) scratch buffer, zero-initialised when (re)allocated.
 
-    The kernels leave its arrival counters at zero, so the buffer is reused
-    across calls without clearing.  Calls that overlap on one stream are
-    serialised by the stream; distinct streams get distinct buffers.
+    Every region a call reads (selection lists, counts, split partials) is
+    written earlier in the same call, so the buffer is reused across calls
+    without clearing.  Calls that overlap on one stream are serialised by the
+    stream; distinct streams get distinct buffers.
     """
     key = (device.index, stream_handle(device))
     buf = _ws.get(key)
