@@ -34,7 +34,7 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
                           const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale, void* ws,
                           hipStream_t st);
 size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, int causal_off);
-size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int causal_off);
+size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int nrep, int causal_off);
 hipError_t launch_prefill_turbo(const fq_turbo_cache& tc, const TailArgs& t, const void* q, const int64_t* q_s,
                                 void* out, const int64_t* o_s, int nrep, int Sq, int causal_off, float qk_scale,
                                 void* ws, hipStream_t st);
@@ -846,7 +846,7 @@ static int prefill_turbo_check(const fq_turbo_cache* c, const fq_tail* tail, con
     }
     int st = prefill_check_tail_query(tail, q, c->D, c->H_kv, c->B, c->S, t);
     if (st) return st;
-    *ws_bytes = prefill_turbo_workspace_bytes(c->H_kv, c->B, c->S + t.len, q->S_q, q->causal_offset);
+    *ws_bytes = prefill_turbo_workspace_bytes(c->H_kv, c->B, c->S + t.len, q->S_q, q->H_q / c->H_kv, q->causal_offset);
     return FQ_OK;
 }
 

@@ -55,6 +55,8 @@ struct PrefillParams {
     uint16_t* kd;          // dense bf16 K   [b][h][S_pad][128]   (two-pass path)
     uint16_t* vtd;         // dense bf16 V^T [b][h][128][S_pad]
     int s_pad;             // keys in the dense arrays, a multiple of 128 (zeros beyond S_kv)
+    int kv_splits;         // > 1: workgroups take slices of the key stages and store partials
+    float* part;           // [split][b][h][row][128] unnormalised O, then [split][b][h][row][2] (m, l)
     int nrep, Sq, Skv, causal_off;
     float qk_scale;                    // sm_scale * log2(e)
 };
@@ -498,14 +500,20 @@ void prefill_attn_kernel(PrefillParams a) {
     // different XCDs, so with H_kv * B a multiple of 8 each XCD's L2 holds the
     // K/V of its own heads.  Row blocks run last-first (the longest first).
     const int HB = c.Hkv * c.B;
-    const int nblk = gridDim.x / HB;
+    const int KS = a.kv_splits > 1 ? a.kv_splits : 1;
+    const int nblk = gridDim.x / (HB * KS);
     const int hb = blockIdx.x % HB;
-    const int rb = nblk - 1 - (int)(blockIdx.x / HB);
+    const int rb = nblk - 1 - (int)((blockIdx.x / HB) % nblk);
+    const int split = (int)(blockIdx.x / (HB * nblk));
     const int h = hb % c.Hkv, b = hb / c.Hkv;
     const int Mtot = a.Sq * a.nrep;
     const int m0 = rb * kPRows;
     const int last_wg = (min(m0 + kPRows, Mtot) - 1) / a.nrep;
-    const int nt = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;
+    const int nt_all = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;
+    // this workgroup's key stages [t_begin, nt) (all of them without splits)
+    const int per = (nt_all + KS - 1) / KS;
+    const int t_begin = min(nt_all, split * per);
+    const int nt = min(nt_all, t_begin + per);
 
     const int mw0 = m0 + w * kPRW;
     const bool wave_on = mw0 < Mtot;
@@ -552,12 +560,15 @@ void prefill_attn_kernel(PrefillParams a) {
     VFetch vf;
     DFetch df;
     // nt >= 1: key 0 is always attended (causal_off >= 0, S_kv >= 1)
-    prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, 0, b, h, kk, kc, vk, vd);
-    prefill_stage<SRC>(a, kf, vf, df, s_k[0], s_v[0], kk, kc, vd, vk, td, tq);
+    // a workgroup with no stages (a split past the causal limit) stores an empty partial
+    if (t_begin < nt) {
+        prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, t_begin * ST, b, h, kk, kc, vk, vd);
+        prefill_stage<SRC>(a, kf, vf, df, s_k[0], s_v[0], kk, kc, vd, vk, td, tq);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): prologue loads (Q included) land before the loop
     __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-        const int cur = t & 1;
+    for (int t = t_begin; t < nt; ++t) {
+        const int cur = (t - t_begin) & 1;
         const int key0 = t * ST;
         if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, key0 + ST, b, h, kk, kc, vk, vd);
         __builtin_amdgcn_sched_barrier(0);
@@ -578,6 +589,24 @@ void prefill_attn_kernel(PrefillParams a) {
     }
 
     if (!wave_on) return;
+    if (KS > 1) {   // unnormalised partial + (m, l) per row for prefill_merge_kernel
+        const int64_t rows = (int64_t)c.B * c.Hkv * Mtot;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const float l = rows_sum(l_run[qb]);
+            if (!qok[qb]) continue;
+            const int64_t row = ((int64_t)split * c.B * c.Hkv + hb) * Mtot + mw0 + qb * 16 + n;
+            float* prow = a.part + row * kPD;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) *(v4f*)(prow + db * 16 + 4 * g) = o[qb][db];
+            if (g == 0) {
+                float* ml = a.part + (int64_t)KS * rows * kPD + row * 2;
+                ml[0] = m_run[qb];
+                ml[1] = l;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
         const float l = rows_sum(l_run[qb]);
@@ -596,6 +625,37 @@ void prefill_attn_kernel(PrefillParams a) {
 
 }  // namespace
 
+// Combines the key-range partials of the split path: per row (b, h, m)
+// M = max m_i, L = sum 2^(m_i - M) l_i, O = sum 2^(m_i - M) O_i / L, in split
+// order; one wave per row, lane = two channels.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams a) {
+    const int64_t rows = (int64_t)a.c.B * a.c.Hkv * a.Sq * a.nrep;
+    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int KS = a.kv_splits;
+    const float* ml = a.part + (int64_t)KS * rows * kPD;
+    float M = -INFINITY;
+    for (int sp = 0; sp < KS; ++sp) M = fmaxf(M, ml[(sp * rows + row) * 2]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int sp = 0; sp < KS; ++sp) {
+        const float m = ml[(sp * rows + row) * 2];
+        const float wt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        L = fmaf(wt, ml[(sp * rows + row) * 2 + 1], L);
+        const float* po = a.part + (sp * rows + row) * kPD;
+        o0 = fmaf(wt, po[2 * lane], o0);
+        o1 = fmaf(wt, po[2 * lane + 1], o1);
+    }
+    const int Mtot = a.Sq * a.nrep;
+    const int m = (int)(row % Mtot);
+    const int hb = (int)(row / Mtot);
+    const int h = hb % a.c.Hkv, b = hb / a.c.Hkv;
+    const int hq = h * a.nrep + m % a.nrep;
+    uint16_t* orow = (uint16_t*)a.out + b * a.o_s[0] + hq * a.o_s[1] + (int64_t)(m / a.nrep) * a.o_s[2];
+    const float inv = 1.0f / L;
+    *(uint32_t*)(orow + 2 * lane) = pack_bf16(o0 * inv, o1 * inv);
+}
+
 // The keys any query can attend: min(S_kv, S_q + causal_off).
 int64_t prefill_keys_needed(int Skv, int Sq, int causal_off) { return std::min<int64_t>(Skv, (int64_t)Sq + causal_off); }
 
@@ -605,11 +665,50 @@ int64_t prefill_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kPRo
 // for one row block per KV head over at most 1024 keys; otherwise the
 // two-pass path (dequantise the needed keys once, in parallel, into dense
 // bf16 K and V^T, then attend plain bf16 tiles) is faster.
+// Key-range splits of the dense path: when the row blocks leave most CUs idle
+// (few query rows over many keys, e.g. a chunk with causal_off = S_kv - S_q),
+// workgroups take slices of at least 4 key stages and a merge launch combines
+// their partials.
+int prefill_kv_splits(int64_t nblk, int64_t heads, int64_t keys) {
+    const int64_t wgs = nblk * heads;
+    const int64_t stages = (keys + kDenseKT - 1) / kDenseKT;
+    if (wgs >= 128 || stages < 8) return 1;
+    const int64_t ks = std::min<int64_t>((256 + wgs - 1) / wgs, stages / 4);
+    return (int)std::max<int64_t>(1, ks);
+}
+
+// Dense K / V^T of the attended keys, then (with key-range splits) the partials.
+size_t prefill_dense_bytes(int Hkv, int B, int Skv, int Sq, int nrep, int causal_off) {
+    const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
+    const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
+    size_t n = (size_t)(2 * s_pad * kPD * 2) * Hkv * B;
+    const int ks = prefill_kv_splits(prefill_row_blocks(Sq, nrep), (int64_t)Hkv * B, keys);
+    if (ks > 1) n += (size_t)ks * B * Hkv * Sq * nrep * (kPD + 2) * sizeof(float);
+    return n;
+}
+
 size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, int causal_off) {
     const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
     if (prefill_row_blocks(Sq, nrep) == 1 && keys <= 1024) return 0;
-    const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
-    return (size_t)(2 * s_pad * kPD * 2) * c.Hkv * c.B;
+    return prefill_dense_bytes(c.Hkv, c.B, Skv, Sq, nrep, causal_off);
+}
+
+// The attention launch of the dense path (a.kd / a.vtd / a.s_pad set), with
+// key-range splits and their merge when the row blocks are few.
+hipError_t launch_dense_attn(PrefillParams& a, int Sq, int nrep, hipStream_t st) {
+    const int64_t nblk = prefill_row_blocks(Sq, nrep);
+    const int64_t heads = (int64_t)a.c.Hkv * a.c.B;
+    const int ks = prefill_kv_splits(nblk, heads, prefill_keys_needed(a.Skv, Sq, a.causal_off));
+    a.kv_splits = ks;
+    a.part = ks > 1 ? (float*)(a.vtd + (int64_t)a.s_pad * kPD * heads) : nullptr;
+    timer_before_launch(st);
+    hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), dim3((unsigned)(nblk * heads * ks)), dim3(512), 0, st, a);
+    timer_after_launch(st);
+    if (ks > 1) {
+        const int64_t rows = heads * Sq * nrep;
+        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((rows * 64 + 255) / 256)), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
 }
 
 // Launch the prefill.  The caller has checked shapes, strides and alignment
@@ -639,10 +738,7 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
             if (bf) hipLaunchKernelGGL((prefill_dequant_kernel<4, FQ_BF16>), dgrid, dim3(512), 0, st, a);
             else hipLaunchKernelGGL((prefill_dequant_kernel<4, FQ_F16>), dgrid, dim3(512), 0, st, a);
         }
-        timer_before_launch(st);
-        hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), grid, dim3(512), 0, st, a);
-        timer_after_launch(st);
-        return hipGetLastError();
+        return launch_dense_attn(a, Sq, nrep, st);
     }
     timer_before_launch(st);
     if (c.bits == 8) hipLaunchKernelGGL((prefill_attn_kernel<8, FQ_BF16>), grid, dim3(512), 0, st, a);
@@ -651,10 +747,8 @@ hipError_t launch_prefill(const Int4Cache& c, const TailArgs& t, const void* q, 
     return hipGetLastError();
 }
 
-size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int causal_off) {
-    const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
-    const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
-    return (size_t)(2 * s_pad * kPD * 2) * Hkv * B;
+size_t prefill_turbo_workspace_bytes(int Hkv, int B, int Skv, int Sq, int nrep, int causal_off) {
+    return prefill_dense_bytes(Hkv, B, Skv, Sq, nrep, causal_off);
 }
 
 // Prefill over the TurboQuant cache: always the two-pass path (the first pass
@@ -682,12 +776,7 @@ hipError_t launch_prefill_turbo(const fq_turbo_cache& tc, const TailArgs& t, con
         tp.vsc_s[i] = tc.vst_strides[i + 1];
     }
     hipLaunchKernelGGL(prefill_dequant_turbo_kernel, dim3(a.s_pad / kPKT, tc.H_kv, tc.B), dim3(512), 0, st, a, tp);
-    const int64_t nblk = prefill_row_blocks(Sq, nrep);
-    timer_before_launch(st);
-    hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), dim3((unsigned)(nblk * tc.H_kv * tc.B)), dim3(512), 0,
-                       st, a);
-    timer_after_launch(st);
-    return hipGetLastError();
+    return launch_dense_attn(a, Sq, nrep, st);
 }
 
 }  // namespace fq

@@ -208,3 +208,26 @@ def test_prefill_over_persistent_turbo_views():
     Vf = np.concatenate([O.dequant_turbo_bf16(vm, vl, vs), V[:, :, comp:]], axis=2)
     ref = O.causal_prefill_attention(Q, Kf, Vf)
     assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
+
+
+@pytest.mark.parametrize("kw", [dict(S=8192, T=30, Sq=64, causal_offset=8158), dict(S=4096, T=0, Sq=16, causal_offset=4080),
+                                dict(S=4096, T=5, Sq=200, causal_offset=3901, bits=8),
+                                dict(S=2048, T=64, Sq=300, Hq=8, Hkv=2, causal_offset=1812)])
+def test_prefill_key_range_splits(kw):
+    # few query rows over many keys: workgroups take slices of the key range, a merge launch combines them
+    _check(PrefillCase(13, **kw))
+
+
+def test_prefill_turbo_key_range_splits():
+    from flashquest_amd.kernel import flash_attn_prefill_turbo
+    S, T, Sq = 4096, 20, 48
+    K, V, Q, (km, kl, ks, vm, vl, vs) = _turbo_case(3, S=S, T=T, Sq=Sq)
+    off = S + T - Sq
+    out = flash_attn_prefill_turbo(to_dev_half(Q, "bf16"), to_dev(km), to_dev(kl), to_dev_half(ks, "bf16"),
+                                   to_dev(vm), to_dev(vl), to_dev_half(vs, "bf16"),
+                                   to_dev_half(K[:, :, S:], "bf16"), to_dev_half(V[:, :, S:], "bf16"),
+                                   page_size=64, causal_offset=off)
+    Kf = np.concatenate([O.dequant_turbo_bf16(km, kl, ks), K[:, :, S:]], axis=2)
+    Vf = np.concatenate([O.dequant_turbo_bf16(vm, vl, vs), V[:, :, S:]], axis=2)
+    ref = O.causal_prefill_attention(Q, Kf, Vf, causal_offset=off)
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
