@@ -541,6 +541,11 @@ def main():
             Vf = torch.cat([dequantize_v_int4(pk[3], pk[4], pk[5]), vt], dim=2)
             return F.scaled_dot_product_attention(qp, Kf, Vf, is_causal=True, enable_gqa=True)
         pr_ms, _, _ = time_steps(noop, ref_prefill, pf_steps, 1, noop)
+        # a 128-token chunk over the same cache, lower-right aligned (key-range splits)
+        qc = qp[:, :, -128:].contiguous()
+        pc_ms, _, _ = time_steps(noop, lambda: flash_attn_prefill_int4(qc, *pk, kt, vt, page_size=64,
+                                                                       causal_offset=Sp - 128), pf_steps, 1, noop)
+        extra["prefill_chunk128_over_32k_us"] = pc_ms * 1e3
         pf_flops = 2.0 * Sp * Sp * 128 * Hq          # causal: 4 S^2 D H_q / 2
         extra.update({"prefill_32k_layer_ms": pf_ms, "prefill_TFLOPs": pf_flops / (pf_ms * 1e-3) / 1e12,
                       "prefill_mfma_frac": pf_flops / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
