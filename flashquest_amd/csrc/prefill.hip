@@ -15,8 +15,8 @@
 // m = pos * n_rep + r is query position pos of head kvh * n_rep + r, so every
 // K/V tile a workgroup dequantises serves all n_rep heads of the group.  Per
 // 64-key tile all 512 threads dequantise K into LDS as [key][channel] bf16 and
-// V transposed as [channel][key] bf16 (the tile after next is fetched into
-// registers while the current one is computed), then each wave runs
+// V transposed as [channel][key] bf16 (keys in vt_pos order; the next tile is
+// fetched into registers while the current one is computed), then each wave runs
 //   S^T = K Q^T     v_mfma_f32_16x16x32_bf16, 4 key blocks x 2 query blocks
 //   online softmax  per query column (base 2, fp32), P rounded to bf16
 //   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16, 8 channel blocks x 2 query blocks
@@ -73,6 +73,15 @@ FQ_DEV uint32_t bf16_rne(float f) {    // fp32 -> bf16 bits, round to nearest ev
     return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 FQ_DEV uint32_t pack_bf16(float lo, float hi) { return bf16_rne(lo) | (bf16_rne(hi) << 16); }
+
+// Key order of V^T rows (LDS and the dense array): inside each 32-key block,
+// keys 4g..4g+3 and 16+4g..16+4g+3 sit together at 8g..8g+7 -- the eight keys
+// one lane of the p.v operand needs -- so the operand is one 16-byte read.
+// Groups of 4 consecutive keys stay consecutive.
+FQ_DEV int vt_pos(int k) {
+    const int r = k & 31;
+    return (k & ~31) + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+}
 
 // Across the four 16-lane rows of a wave (lanes n, n + 16, n + 32, n + 48):
 // v_permlane16_swap / v_permlane32_swap exchange rows in VALU, no LDS trip.
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(512) void prefill_dequant_kernel(PrefillParams a) {
     fetch_v<BITS>(vf, a, b, h, key0 + vk, vd, whole);
     const int64_t bh = (int64_t)b * a.c.Hkv + h;
     store_k<BITS, META>(kf, a.kd + (bh * a.s_pad + key0 + kk) * kPD + kc);
-    store_v<BITS, META>(vf, &s_v[vd * kVStr + vk], kVStr);
+    store_v<BITS, META>(vf, &s_v[vd * kVStr + vt_pos(vk)], kVStr);
     __syncthreads();
     const int d = tid >> 2, q = (tid & 3) * 16;
     uint16_t* dst = a.vtd + (bh * kPD + d) * a.s_pad + key0 + q;
@@ -334,10 +343,7 @@ FQ_DEV void tile_pv(v4f (&o)[2][8], const v8bf (&pb)[2][2], const uint16_t* sv, 
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            const uint16_t* vrow = sv + (db * 16 + n) * vstr + 4 * g + 32 * j;
-            const u32x2 lo = *(const u32x2*)vrow;
-            const u32x2 hi = *(const u32x2*)(vrow + 16);
-            const v8bf av = __builtin_bit_cast(v8bf, u32x4{lo.x, lo.y, hi.x, hi.y});
+            const v8bf av = *(const v8bf*)(sv + (db * 16 + n) * vstr + 32 * j + 8 * g);   // keys in vt_pos order
             o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[0][j], o[0][db], 0, 0, 0);
             o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[1][j], o[1][db], 0, 0, 0);
         }
@@ -434,8 +440,8 @@ __global__ __launch_bounds__(512) void prefill_dequant_turbo_kernel(PrefillParam
         uint16_t* krow = a.kd + (bh * a.s_pad + key) * kPD;
         krow[lane] = (uint16_t)kb0;
         krow[lane + 64] = (uint16_t)kb1;
-        s_v[lane * kVStr + j] = (uint16_t)vb0;
-        s_v[(lane + 64) * kVStr + j] = (uint16_t)vb1;
+        s_v[lane * kVStr + vt_pos(j)] = (uint16_t)vb0;
+        s_v[(lane + 64) * kVStr + vt_pos(j)] = (uint16_t)vb1;
     }
     __syncthreads();
     const int tid = threadIdx.x;
@@ -476,10 +482,10 @@ FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch
         }
     } else if (a.c.meta_dtype == FQ_BF16) {
         store_k<SRC, FQ_BF16>(kf, sk + kk * kKStr + kc);
-        store_v<SRC, FQ_BF16>(vf, sv + vd * kVStr + vk, kVStr);
+        store_v<SRC, FQ_BF16>(vf, sv + vd * kVStr + vt_pos(vk), kVStr);
     } else {
         store_k<SRC, FQ_F16>(kf, sk + kk * kKStr + kc);
-        store_v<SRC, FQ_F16>(vf, sv + vd * kVStr + vk, kVStr);
+        store_v<SRC, FQ_F16>(vf, sv + vd * kVStr + vt_pos(vk), kVStr);
     }
 }
 
