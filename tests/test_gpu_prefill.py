@@ -231,3 +231,24 @@ def test_prefill_turbo_key_range_splits():
     Vf = np.concatenate([O.dequant_turbo_bf16(vm, vl, vs), V[:, :, S:]], axis=2)
     ref = O.causal_prefill_attention(Q, Kf, Vf, causal_offset=off)
     assert float(np.abs(out.float().cpu().numpy() - ref).max()) < ATOL
+
+
+@pytest.mark.parametrize("kw", [dict(B=2, S=2048, T=11, Sq=40, causal_offset=2019), dict(B=2, S=640, T=0, Sq=None),
+                                dict(page=32, S=2048, T=20, Sq=70, causal_offset=1998, meta="f16", vgroup=32)])
+def test_prefill_batch_and_layout_mixes(kw):
+    _check(PrefillCase(17, **kw))
+
+
+def test_prefill_fp16_query_is_cast_like_the_reference():
+    # the reference casts q (and the new K/V) to bf16 before the cache and SDPA (llama_persistent_patch.py:183-190)
+    c = PrefillCase(19, S=320, T=9)
+    from flashquest_amd.kernel import flash_attn_prefill_int4
+    m = c.meta
+    args = (to_dev(c.kc), to_dev_half(c.ks, m), to_dev_half(c.km, m), to_dev(c.vc), to_dev_half(c.vs, m),
+            to_dev_half(c.vm, m), to_dev_half(c.Kt, "bf16"), to_dev_half(c.Vt, "bf16"))
+    qb = to_dev_half(c.Q, "bf16")
+    o16 = flash_attn_prefill_int4(qb.to(torch.float16), *args, page_size=c.page)
+    o = flash_attn_prefill_int4(qb, *args, page_size=c.page)
+    # Q holds bf16 values; fp16 holds most of them exactly, so the outputs agree to bf16 rounding
+    assert o16.dtype == torch.bfloat16
+    assert float((o16.float() - o.float()).abs().max()) < 2e-2
