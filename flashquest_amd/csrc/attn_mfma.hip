@@ -287,6 +287,9 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             // the balanced slice [e0, e1) of it
             const int total = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max,
                                                                   a.sel.num_sinks, a.sel.window, s_ent, s_bsel);
+            if (a.sel.mask_out && split == 0)        // uniform: the caller asked for the selection
+                block_write_mask<NT, NREP>(s_ent, total, c.P, (uint8_t*)s_key,
+                                           a.sel.mask_out + (int64_t)g * NREP * c.P, tid);
             e0 = (int)((int64_t)total * split / a.splits);
             e1 = (int)((int64_t)total * (split + 1) / a.splits);
             ent_base = e0;

@@ -389,7 +389,7 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
 static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
-                        fq_stream_t stream, int bits) {
+                        fq_stream_t stream, int bits, bool mask_from_attention = false) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
@@ -404,7 +404,10 @@ static int quest_select(const fq_int4_cache* cache, const fq_query* query, const
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};   // (L*B, H_q, 1, P) contiguous
     float* sc_user = (scores_out && select_mode == FQ_SELECT_PER_Q_HEAD) ? scores_out : nullptr;
-    if (!mask_out && !sc_user && decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws))
+    // the fused attention kernel selects for itself (and, when the whole step
+    // is one call, writes the mask too)
+    if ((!mask_out || mask_from_attention) && !sc_user &&
+        decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws))
         return FQ_OK;
     return hip_status(launch_score(c, q, 1, q4, sc_user, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                    k_max, mask_out, (hipStream_t)stream),
@@ -421,7 +424,8 @@ int fq_quest_select_int4(const fq_int4_cache* cache, const fq_query* query, cons
 
 static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const float* retention, int32_t num_sinks,
                         int32_t window_pages, int32_t k_max, int32_t select_mode, const TailArgs* tail,
-                        void* workspace, size_t workspace_bytes_, fq_stream_t stream, int bits = 4) {
+                        void* workspace, size_t workspace_bytes_, fq_stream_t stream, int bits = 4,
+                        uint8_t* mask_out = nullptr) {
     Int4Cache c{};
     QueryArgs q{};
     Workspace ws{};
@@ -438,7 +442,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     SelectArgs sel{};
     if (attn_selects_in_kernel(c, q, al)) {
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
-        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
+        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
     }
     return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail),
                       bits == 8 ? "sparse int8 attention" : "sparse int4 attention");
@@ -494,11 +498,11 @@ int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, cons
                          int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                          float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
                          fq_stream_t stream) {
-    int st = fq_quest_select_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out,
-                                  mask_out, workspace, workspace_bytes_, stream);
+    int st = quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out, mask_out,
+                          workspace, workspace_bytes_, stream, 4, true);
     if (st) return st;
-    return fq_quest_attend_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, workspace,
-                                workspace_bytes_, stream);
+    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr, workspace,
+                        workspace_bytes_, stream, 4, mask_out);
 }
 
 int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, const float* retention,
@@ -506,10 +510,10 @@ int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, cons
                          float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
                          fq_stream_t stream) {
     int st = quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out, mask_out,
-                          workspace, workspace_bytes_, stream, 8);
+                          workspace, workspace_bytes_, stream, 8, true);
     if (st) return st;
     return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr, workspace,
-                        workspace_bytes_, stream, 8);
+                        workspace_bytes_, stream, 8, mask_out);
 }
 
 size_t fq_int8_workspace_bytes(const fq_int8_cache* cache, int32_t H_q) { return fq_workspace_bytes(cache, H_q); }
@@ -736,10 +740,10 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     hipStream_t s = (hipStream_t)stream;
     const int bound = quest_bound(c, q, num_sinks, window_pages, k_max, select_mode);
     const bool fusable = turbo_fused_supported(*cache, q);
-    if (fusable && !mask_out && G >= 192 && c.P <= 64 * 8) {
+    if (fusable && G >= 192 && c.P <= 64 * 8 && attention_splits_request() <= 0) {
         SelectArgs sel{};
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
-        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect;
+        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
         return hip_status(launch_attn_turbo_fused(*cache, &c, q, ws, bound, &sel, s), "quest turbo decode");
     }
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};

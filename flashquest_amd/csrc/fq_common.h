@@ -213,6 +213,7 @@ struct SelectArgs {
     const float* retention;
     int num_sinks, window, k_max, mode;
     int enabled;
+    uint8_t* mask_out;      // fused kernels: the selection as (L, B, H_q, P) bool rows, or null
 };
 
 struct AttnLaunch {

@@ -301,6 +301,22 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
     return n;
 }
 
+// The group's selection as boolean rows mask[r * P + i] (query head r of the
+// group, page i), from the entry list (page | selecting-heads << 16) of
+// block_select_rows.  scratch: >= P bytes of LDS that nothing else uses any
+// more; every thread of the NT-thread workgroup calls this (two barriers).
+template <int NT, int NREP>
+FQ_DEV void block_write_mask(const int* entries, int n, int P, uint8_t* scratch, uint8_t* mask, int tid) {
+    for (int i = tid; i < P; i += NT) scratch[i] = 0;
+    __syncthreads();
+    for (int e = tid; e < n; e += NT) scratch[entries[e] & 0xFFFF] = (uint8_t)(entries[e] >> 16);
+    __syncthreads();
+    for (int i = tid; i < NREP * P; i += NT) {
+        const int r = i / P, p = i - r * P;
+        mask[i] = (scratch[p] >> r) & 1;
+    }
+}
+
 template <int C, int NW, int NREP>
 FQ_DEV int block_select_group(const uint32_t* keys, int P, int mode, float ret_l, int k_max, int num_sinks, int window,
                               int* entries, BlockSelectLds& sl) {

@@ -248,6 +248,9 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         e0 = 0;
         e1 = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
                                                  a.sel.window, s_ent, s_bsel);
+        if (a.sel.mask_out)                          // uniform: the caller asked for the selection
+            block_write_mask<NT, NREP>(s_ent, e1, c.P, (uint8_t*)s_key, a.sel.mask_out + (int64_t)g * NREP * c.P,
+                                       tid);
     } else {
         const int n_sel = a.ws.n_sel[g];
         e0 = (int)((int64_t)n_sel * split / a.splits);

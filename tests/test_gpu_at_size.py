@@ -1,0 +1,260 @@
+"""The benchmarked decode at the BASELINE geometries, against the CPU oracle.
+
+The whole-step decode over all layers is one kernel launch when the KV groups
+fill the GPU (L*B*H_kv >= 192): every workgroup scores its group's 512 pages,
+selects them in LDS (8 keys per lane) and attends.  These tests run exactly
+that launch on the bench's own synthetic caches (bench.make_cache: lognormal K
+channels, planted pages, fp16 metadata, V in 32-channel groups) and check
+
+* the in-kernel selection of every (layer, sequence, KV head) bit-exact
+  against the oracle's score -> top-k -> forced pages, and against the split
+  path's separate selection kernel;
+* O and lse of sampled layers against the oracle's fp64 attention over the
+  same selection (north-star bar 2e-3 max-abs, plus half an fp16 ulp of |O|);
+* that asking for the mask does not change O (same kernel, bitwise);
+* the split path (several workgroups per group, merge launch) against the
+  fused one within the same tolerance (their fp32 orders differ).
+
+Configs: 1 (28 layers, r = 0.25, k = 128 of 512), 2 (r = 1: k = P), 3
+(rotated INT4: Q rotated, decode, O rotated back) and 4 (batch 16, 3584
+groups), in both selection modes where the reference has them.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from flashquest_amd import _lib as L
+from flashquest_amd.eager.decode import QuestDecoder, quest_decode_int4
+from oracle import fq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_O = 2e-3
+TOL_LSE = 1e-4
+PLANES = ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")
+LAYERS, P = 28, 512
+
+
+def _tol(ref_o):
+    return TOL_O + 2.0 ** -11 * float(np.abs(ref_o).max())
+
+
+@pytest.fixture(scope="module")
+def cfg1():
+    return bench.make_cache(LAYERS, 1, P=P, dev=torch.device("cuda:0"))
+
+
+def _host(c, l, b):
+    """(Q (1,H_q,D), planes) of (layer l, sequence b) as numpy for the oracle."""
+    q = c["Q"][l, b:b + 1, :, 0].float().cpu().numpy()
+    planes = []
+    for k in PLANES:
+        t = c[k][l, b:b + 1].cpu()
+        planes.append(t.numpy() if t.dtype == torch.uint8 else t.float().numpy())
+    return q, planes
+
+
+def _oracle_mask(q, planes, retention, mode):
+    ks, km = planes[1], planes[2]
+    scores = O.page_scores_fixed(q, ks, km, mode)
+    Hq, Hkv = q.shape[1], ks.shape[1]
+    rep = Hq // Hkv
+    if mode == "per_q_head":
+        return O.select_pages_vectorized(scores[:, :, None, :], retention, 4, 2)[:, :, 0, :]
+    m = O.select_pages_vectorized(scores[:, :, None, :], retention, 4, 2)[:, :, 0, :]
+    return np.repeat(m, rep, axis=1)
+
+
+def _kmax(retention):
+    return min(math.ceil(float(np.max(np.asarray(retention))) * P), P)
+
+
+def _run(c, retention, mode, splits=None, with_mask=True):
+    k = _kmax(retention)
+    if not np.isscalar(retention):
+        retention = torch.as_tensor(np.asarray(retention, np.float32))
+    args = [c["Q"]] + [c[x] for x in PLANES]
+    kw = dict(retention=retention, num_sinks=4, window_pages=2, k_max_static=k, select_mode=mode,
+              return_selection=with_mask)
+    if splits is None:
+        res = quest_decode_int4(*args, **kw)
+    else:
+        with L.attention_splits(splits):
+            res = quest_decode_int4(*args, **kw)
+    torch.cuda.synchronize()
+    return res
+
+
+def _is_fused(c, retention, mode):
+    k = _kmax(retention)
+    if not np.isscalar(retention):
+        retention = torch.as_tensor(np.asarray(retention, np.float32))
+    d = QuestDecoder(c["Q"], *[c[x] for x in PLANES], retention=retention, num_sinks=4, window_pages=2,
+                     k_max_static=k, select_mode=mode)
+    return d.fused
+
+
+def _check_step(c, retention, mode, sample, mask_sample=None):
+    """Fused step vs oracle (selection on mask_sample or every (l, b), O/lse on
+    `sample`), vs the split path, and mask-on vs mask-off bitwise."""
+    assert _is_fused(c, retention, mode), "the benchmarked configuration must take the single-launch kernel"
+    Lc, B = c["Q"].shape[0], c["Q"].shape[1]
+    o, lse, mask = _run(c, retention, mode)
+    o2, lse2 = _run(c, retention, mode, with_mask=False)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2), "mask output changed the fused result"
+    os_, lses, masks = _run(c, retention, mode, splits=4)
+    assert torch.equal(mask, masks), "fused in-kernel selection differs from the selection kernel"
+    m_host = mask.cpu().numpy()
+    pairs = mask_sample if mask_sample is not None else [(l, b) for l in range(Lc) for b in range(B)]
+    for l, b in pairs:
+        q, planes = _host(c, l, b)
+        ref = _oracle_mask(q, planes, retention, mode)
+        assert np.array_equal(m_host[l, b:b + 1], ref), f"selection differs from the oracle at layer {l}, seq {b}"
+    tol_split = 0.0
+    for l, b in sample:
+        q, planes = _host(c, l, b)
+        ref_o, ref_l = O.sparse_int4_attention(q, *planes, m_host[l, b:b + 1], 64)
+        got_o = o[l, b:b + 1, :, 0].float().cpu().numpy()
+        got_l = lse[l, b:b + 1, :, 0].cpu().numpy()
+        err_o = np.abs(got_o - ref_o).max()
+        assert err_o <= _tol(ref_o), f"layer {l} seq {b}: max|O - oracle| = {err_o}"
+        assert np.abs(got_l - ref_l).max() <= TOL_LSE, f"layer {l} seq {b}: lse"
+        tol_split = max(tol_split, 2 * _tol(ref_o))
+    d = (o.float() - os_.float()).abs().max().item()
+    assert d <= tol_split, f"fused vs split O differ by {d}"
+    assert (lse - lses).abs().max().item() <= 2 * TOL_LSE
+    return mask
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_config1_fused_step(cfg1, mode):
+    mask = _check_step(cfg1, 0.25, mode, sample=[(0, 0), (13, 0), (27, 0)])
+    # top-128 plus the 6 forced pages, which the top-k may already hold
+    per_head = mask.view(LAYERS, 1, 8, 3, P).sum(-1)
+    assert int(per_head.min()) >= 128 and int(per_head.max()) <= 134
+
+
+def test_config2_all_pages(cfg1):
+    mask = _check_step(cfg1, 1.0, "per_kv_head_sum", sample=[(5, 0)])
+    assert bool(mask.all()), "retention 1 selects every page"
+
+
+def test_config1_retention_per_head(cfg1):
+    """Different retention per query head (DuoAttention-style vectors), k of
+    each head from fp32 ceil(r * P), through the fused kernel."""
+    r = np.array([0.25, 0.1, 0.4] * 8, np.float32)
+    _check_step(cfg1, r, "per_q_head", sample=[(3, 0)], mask_sample=[(l, 0) for l in range(0, LAYERS, 3)])
+
+
+def test_config3_rotated_step():
+    """Config 3: K, V rotated by WHT(s * x) before quantisation; the step
+    rotates Q, decodes and rotates O back.  Against the oracle: the oracle's
+    fp64 rotation of the raw Q, selection and attention over the GPU's rotated
+    query, and the fp64 inverse rotation of the oracle's O."""
+    dev = torch.device("cuda:0")
+    signs = bench.rotation_signs(dev=dev)
+    rc = bench.make_cache(LAYERS, 1, P=P, dev=dev, signs=signs)
+    q_raw = rc["Q"].clone()
+    from flashquest_amd.kernel.wht import wht_along_head_dim
+    wht_along_head_dim(q_raw, signs=signs, out=rc["Q"])
+    o_rot, lse, mask = _run(rc, 0.25, "per_kv_head_sum")
+    o_raw = wht_along_head_dim(o_rot, signs=signs, inverse=True)
+    torch.cuda.synchronize()
+    s_host = signs.cpu().numpy()
+    m_host = mask.cpu().numpy()
+    for l in (0, 27):
+        q, planes = _host(rc, l, 0)
+        qr = q_raw[l, 0:1, :, 0].float().cpu().numpy()
+        # the GPU's rotated query: WHT of s * q with every butterfly stage
+        # rounded to fp16 (the reference's wht in the input dtype), bit-exact
+        assert np.array_equal(q, O.wht(qr * s_host, "f16"))
+        assert np.abs(q - O.rotate_signed(qr, s_host)).max() <= 8 * 2.0 ** -11 * np.abs(q).max()
+        assert np.array_equal(m_host[l, 0:1], _oracle_mask(q, planes, 0.25, "per_kv_head_sum"))
+        ref_rot, ref_l = O.sparse_int4_attention(q, *planes, m_host[l, 0:1], 64)
+        ref_raw = O.unrotate_signed(ref_rot, s_host)
+        got = o_raw[l, 0:1, :, 0].float().cpu().numpy()
+        # + the inverse rotation's fp16 stage roundings (7 stages)
+        assert np.abs(got - ref_raw).max() <= _tol(ref_raw) + 4 * 2.0 ** -11 * np.abs(ref_raw).max()
+        assert np.abs(lse[l, 0:1, :, 0].cpu().numpy() - ref_l).max() <= TOL_LSE
+
+
+def test_config4_batch16():
+    dev = torch.device("cuda:0")
+    bc = bench.make_cache(LAYERS, 16, P=P, dev=dev)
+    rng = np.random.default_rng(4)
+    pairs = sorted({(int(l), int(b)) for l, b in zip(rng.integers(0, LAYERS, 48), rng.integers(0, 16, 48))})
+    _check_step(bc, 0.25, "per_kv_head_sum", sample=[(0, 15), (27, 7)], mask_sample=pairs)
+
+
+def _host4(c, keys, l):
+    """Layer l of a cache whose layers are folded into the batch axis."""
+    out = []
+    for k in keys:
+        t = c[k][l:l + 1].cpu()
+        out.append(t.numpy() if t.dtype == torch.uint8 else t.float().numpy())
+    return out
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_int8_fused_step_at_size(mode):
+    """The INT8 family (kv_bits 8) at config 1's geometry: 28 layers x 8 KV
+    heads x 512 pages, bf16 metadata, through the single-launch kernel."""
+    from flashquest_amd.eager.decode import quest_decode_int8
+    ic = bench.make_int8_cache(LAYERS, P=P, dev=torch.device("cuda:0"))
+    keys = ("K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, k_max_static=128, select_mode=mode)
+    o, lse, mask = quest_decode_int8(ic["Q"], *[ic[k] for k in keys], return_selection=True, **kw)
+    o2, lse2 = quest_decode_int8(ic["Q"], *[ic[k] for k in keys], **kw)
+    with L.attention_splits(4):
+        os_, lses, masks = quest_decode_int8(ic["Q"], *[ic[k] for k in keys], return_selection=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(mask, masks)
+    m_host = mask.cpu().numpy()
+    for l in range(LAYERS):
+        q = ic["Q"][l:l + 1, :, 0].float().cpu().numpy()
+        planes = _host4(ic, keys, l)
+        scores = O.page_scores_fixed(q, planes[1], planes[2], mode, 255.0)
+        ref_mask = O.select_pages_vectorized(scores[:, :, None, :], 0.25, 4, 2, 128)[:, :, 0, :]
+        if mode == "per_kv_head_sum":
+            ref_mask = np.repeat(ref_mask, 3, axis=1)
+        assert np.array_equal(m_host[l:l + 1], ref_mask), l
+        if l in (0, 27):
+            ref_o, ref_l = O.sparse_int8_attention(q, *planes, ref_mask, 64)
+            assert np.abs(o[l:l + 1, :, 0].float().cpu().numpy() - ref_o).max() <= TOL_O + 2.0 ** -8 * np.abs(ref_o).max()
+            assert np.abs(lse[l:l + 1, :, 0].cpu().numpy() - ref_l).max() <= TOL_LSE
+    assert (o.float() - os_.float()).abs().max().item() <= 2 * (TOL_O + 2.0 ** -8)
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_turbo_fused_step_at_size(mode):
+    """TurboQuant K3-V3 at config 1's geometry through the single-launch kernel."""
+    from flashquest_amd.eager.decode import quest_decode_turbo
+    tc = bench.make_turbo_cache(LAYERS, P=P, dev=torch.device("cuda:0"))
+    keys = ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, k_max_static=128, select_mode=mode)
+    args = [tc["Q"]] + [tc[k] for k in keys] + [tc["K_scale_raw"], tc["K_mn_raw"]]
+    o, lse, mask = quest_decode_turbo(*args, return_selection=True, **kw)
+    o2, lse2 = quest_decode_turbo(*args, **kw)
+    with L.attention_splits(4):
+        os_, lses, masks = quest_decode_turbo(*args, return_selection=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(mask, masks)
+    m_host = mask.cpu().numpy()
+    for l in range(LAYERS):
+        q = tc["Q"][l:l + 1, :, 0].float().cpu().numpy()
+        ksr, kmr = _host4(tc, ("K_scale_raw", "K_mn_raw"), l)
+        scores = O.page_scores_fixed(q, ksr, kmr, mode)
+        ref_mask = O.select_pages_vectorized(scores[:, :, None, :], 0.25, 4, 2, 128)[:, :, 0, :]
+        if mode == "per_kv_head_sum":
+            ref_mask = np.repeat(ref_mask, 3, axis=1)
+        assert np.array_equal(m_host[l:l + 1], ref_mask), l
+        if l in (0, 27):
+            ref_o, ref_l = O.sparse_turbo_attention(q, *_host4(tc, keys, l), ref_mask, 64)
+            assert np.abs(o[l:l + 1, :, 0].float().cpu().numpy() - ref_o).max() <= TOL_O + 2.0 ** -8 * np.abs(ref_o).max()
+            assert np.abs(lse[l:l + 1, :, 0].cpu().numpy() - ref_l).max() <= TOL_LSE
+    assert (o.float() - os_.float()).abs().max().item() <= 2 * (TOL_O + 2.0 ** -8)

@@ -49,8 +49,8 @@ def test_turbo_mask_attention_matches_oracle(B, Hq, Hkv):
 @pytest.mark.parametrize("Hq,sinks,window,P", [(24, 3, 2, 20), (24, 0, 0, 20), (16, 9, 1, 12), (8, 4, 2, 6)])
 def test_fused_turbo_decode_matches_oracle(mode, Hq, sinks, window, P):
     # 24 layers x 8 KV heads = 192 KV groups: one workgroup per group, which
-    # scores and selects its pages; a second call asks for the mask (the
-    # scoring-kernel path), which must give the oracle's selection bit for bit
+    # scores and selects its pages; a second call also writes the kernel's
+    # selection as a mask, which must be the oracle's bit for bit
     from flashquest_amd.eager import quest_decode_turbo
     rng = np.random.default_rng(7 + Hq + P)
     Lyr, Hkv = 24, 8
