@@ -12,7 +12,8 @@ def _ensure_inner_contiguous(t: torch.Tensor, align_elems: int = 1) -> torch.Ten
     """Kernels need a unit-stride innermost axis and aligned rows; copy otherwise."""
     if t.stride(-1) != 1 or any(s % align_elems for s in t.stride()[:-1]) or \
             t.data_ptr() % (align_elems * t.element_size()):
-        return t.contiguous()
+        # a fresh copy: contiguous() would return a contiguous but misaligned view unchanged
+        return t.clone(memory_format=torch.contiguous_format)
     return t
 
 
