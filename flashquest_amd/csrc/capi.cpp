@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -206,6 +207,32 @@ void timer_after_launch(hipStream_t st) {
 }  // namespace fq
 
 using namespace fq;
+
+// Scratch of fq_quest_decode_int4_noalloc: one array per GPU (each device holds
+// its own copy at its own address), held until the process ends.  Its host-side
+// name is only a stand-in: kernels get the device address that
+// hipGetSymbolAddress returns, looked up once per device and kept here.
+static __device__ __align__(256) unsigned char scratch[FQ_NOALLOC_SCRATCH_BYTES];
+static constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+static int noalloc_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxScratchDevices) return fail(FQ_ERR_UNSUPPORTED, "device %d: scratch table holds %d devices", dev, kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+        if (!p || ((uintptr_t)p & 255)) return fail(FQ_ERR_HIP, "scratch address %p is not 256-byte aligned", p);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FQ_OK;
+}
 
 extern "C" {
 
@@ -884,6 +911,23 @@ int fq_prefill_int4(const fq_int4_cache* cache, const fq_tail* tail, const fq_pr
 int fq_prefill_int8(const fq_int8_cache* cache, const fq_tail* tail, const fq_prefill* query, void* workspace,
                     size_t workspace_bytes, fq_stream_t stream) {
     return prefill(cache, tail, query, workspace, workspace_bytes, stream, 8);
+}
+
+int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* query, const float* retention,
+                                 int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                                 float* scores_out, uint8_t* mask_out, fq_stream_t stream) {
+    if (!cache || !query) return fail(FQ_ERR_INVALID, "cache or query descriptor is NULL");
+    const size_t need = fq_workspace_bytes(cache, query->H_q);
+    if (need == 0) return fail(FQ_ERR_INVALID, "H_q=%d must be a positive multiple of H_kv=%d", query->H_q, cache->H_kv);
+    if (need > (size_t)FQ_NOALLOC_SCRATCH_BYTES)
+        return fail(FQ_ERR_UNSUPPORTED,
+                    "fq_quest_decode_int4_noalloc: this step needs %zu bytes of scratch, the static buffer holds %zu "
+                    "(call fq_quest_decode_int4 with a workspace)", need, (size_t)FQ_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    const int st = noalloc_scratch(&ws);
+    if (st) return st;
+    return fq_quest_decode_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out,
+                                mask_out, ws, (size_t)FQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

@@ -182,6 +182,23 @@ int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query,
                          float* scores_out, uint8_t* mask_out,
                          void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* fq_quest_decode_int4 for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments and results without the
+ * workspace: the split-path lists and partials live in a static device array
+ * of FQ_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), whose
+ * address is looked up on the first call on each device (the current device).
+ * Allocates nothing.  A step whose workspace (fq_workspace_bytes) exceeds the
+ * array returns FQ_ERR_UNSUPPORTED before touching any pointer.  All calls on
+ * one GPU share the array: calls that overlap on one GPU (different streams,
+ * or host threads) race and must be serialised by the caller.  Nothing in the
+ * array needs clearing: every region a call reads it writes first. */
+#define FQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* query,
+                                 const float* retention, int32_t num_sinks, int32_t window_pages,
+                                 int32_t k_max, int32_t select_mode,
+                                 float* scores_out, uint8_t* mask_out, fq_stream_t stream);
+
 /* The two halves of fq_quest_decode_int4, for callers that time or overlap
  * them separately; call both with the same cache, query, retention, k_max,
  * num_sinks, window_pages, select_mode and workspace.  fq_quest_select_int4
