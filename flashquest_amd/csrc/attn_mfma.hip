@@ -183,6 +183,19 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         l1 = *(const uint16_t*)(qc + o1);
         h1 = *(const uint16_t*)(qc + o1 + esz - 2);
     }
+    // Scoring's q in registers: channels 8 * (tid & 15) .. + 7 of every query
+    // head of the group, one 16-byte load per head, so that each wave scores
+    // its pages as its own loads land, with no barrier on the other waves' q.
+    // Needs 16-bit q with unit channel stride and 16-byte aligned rows; other
+    // layouts (q_fast false: an empty buffer, the loads read 0) go through LDS.
+    uint4 qsr[NREP];
+    const bool q_fast = FUSED && !q32 && q.q_s[3] == 1 && (q.q_s[2] & 7) == 0 &&
+                        (((uintptr_t)q.q + 2 * (uint64_t)qb) & 15) == 0;
+    if constexpr (FUSED) {
+        const auto rq = make_rsrc((const char*)q.q + 2 * qb, q_fast ? 2 * ((int64_t)(NREP - 1) * q.q_s[2] + D) : 0);
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) qsr[r] = ld128(rq, (int)(2 * (r * q.q_s[2] + 8 * (tid & 15))));
+    }
     __builtin_amdgcn_sched_barrier(0);      // q's loads go out before the metadata loads
     // retention of query head L of the group (lanes past NREP repeat the last)
     float ret_l = 0.f;
@@ -274,9 +287,25 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 *(uint4*)&s_tk[i >> 4][8 * (i & 15)] = tkr[u];
                 *(uint4*)&s_tv[i >> 4][8 * (i & 15)] = tvr[u];
             }
-            __syncthreads();
-            if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
-            else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
+            const bool sum = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM;
+            if (q_fast) {      // uniform
+                float qin[NREP][8];
+#pragma unroll
+                for (int r = 0; r < NREP; ++r) {
+                    const uint32_t wv[4] = {qsr[r].x, qsr[r].y, qsr[r].z, qsr[r].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        qin[r][2 * j] = qbf ? bf16_bits_to_f(wv[j] & 0xFFFFu) : f16_bits_to_f(wv[j] & 0xFFFFu);
+                        qin[r][2 * j + 1] = qbf ? bf16_bits_to_f(wv[j] >> 16) : f16_bits_to_f(wv[j] >> 16);
+                    }
+                }
+                if (sum) score_group_regs_q<MT, NREP, NT, true>(sr, qin, s_key, tid, c.P);
+                else score_group_regs_q<MT, NREP, NT, false>(sr, qin, s_key, tid, c.P);
+            } else {
+                __syncthreads();
+                if (sum) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+                else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
+            }
             const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
             if (S > 0 && split == 0 && w < fp.count) {       // split 0's first entries are the forced pages
                 issue_page(b0, fp.page(w));

@@ -71,9 +71,10 @@ FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int
     }
 }
 
+// qin[r][j]: query head r's raw value at channel 8 * (tid & 15) + j.
 template <typename MT, int NREP, int NT, bool SUM>
-FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P,
-                             float levels = 15.0f) {
+FQ_DEV void score_group_regs_q(const ScoreRegs<NT>& sr, const float (&qin)[NREP][8], uint32_t* s_key, int tid, int P,
+                               float levels = 15.0f) {
     constexpr int PPP = NT / 16;
     const int lip = tid & 15, pip = tid >> 4;
     // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
@@ -83,11 +84,11 @@ FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128]
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         if constexpr (SUM) {
-            float qs = s_qraw[0][lip * 8 + j];
+            float qs = qin[0][j];
             float ps = qs > 0.f ? qs : 0.f;
 #pragma unroll
             for (int r = 1; r < NREP; ++r) {
-                const float v = s_qraw[r][lip * 8 + j];
+                const float v = qin[r][j];
                 qs = __fadd_rn(qs, v);
                 ps = __fadd_rn(ps, v > 0.f ? v : 0.f);
             }
@@ -96,7 +97,7 @@ FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128]
         } else {
 #pragma unroll
             for (int r = 0; r < NREP; ++r) {
-                qr[r][j] = s_qraw[r][lip * 8 + j];
+                qr[r][j] = qin[r][j];
                 qp[r][j] = qr[r][j] > 0.f ? qr[r][j] : 0.f;
             }
         }
@@ -108,6 +109,18 @@ FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128]
             if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
         }, levels);
     }
+}
+
+template <typename MT, int NREP, int NT, bool SUM>
+FQ_DEV void score_group_regs(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P,
+                             float levels = 15.0f) {
+    const int lip = tid & 15;
+    float qin[NREP][8];
+#pragma unroll
+    for (int r = 0; r < NREP; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qin[r][j] = s_qraw[r][lip * 8 + j];
+    score_group_regs_q<MT, NREP, NT, SUM>(sr, qin, s_key, tid, P, levels);
 }
 
 }  // namespace fq
