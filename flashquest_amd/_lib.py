@@ -65,6 +65,7 @@ class Prefill(ctypes.Structure):
         ("out", ctypes.c_void_p), ("o_strides", _I64x4),
         ("H_q", ctypes.c_int32), ("S_q", ctypes.c_int32),
         ("causal_offset", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+        ("D", ctypes.c_int32),
     ]
 
 
@@ -111,6 +112,10 @@ SIGNATURES = {
                                             _P, _P, _P, ctypes.c_size_t, _P]),
     "fq_int4_cache_append": (ctypes.c_int, [ctypes.POINTER(Int4Cache), _I, _P, _I64P, _P, _I64P, _I, _P, _I64P,
                                             _P, _I64P, _I, _I, _P]),
+    "fq_int8_cache_append": (ctypes.c_int, [ctypes.POINTER(Int4Cache), _I, _P, _I64P, _P, _I64P, _I, _P, _I64P,
+                                            _P, _I64P, _I, _I, _P]),
+    "fq_turbo_cache_append": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, _I, _P, _I64P, _P,
+                                             _I64P, _I, _P, _I64P, _P, _I64P, _I, _I, _P]),
     "fq_quest_decode_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, ctypes.POINTER(Query),
                                              _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int4_tail": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), ctypes.POINTER(Tail),

@@ -13,11 +13,13 @@
 // per-group min/max over the group's lanes, fp32 arithmetic (as
 // quant_v_kernel).  Codes are stored 4 bytes (8 channels) per thread and token.
 #include "fq_common.h"
+#include "turbo_quant.h"
 
 namespace fq {
 
 constexpr float kCacheEps = 1e-6f;                      // kv_quant.py:14
 __device__ __constant__ float kCacheInv15 = 1.0f / 15.0f;
+__device__ __constant__ float kCacheInv255 = 1.0f / 255.0f;    // the INT8 quantisers' "/ 255.0"
 
 namespace {
 
@@ -69,17 +71,33 @@ FQ_DEV void load8(const TokSrc& s, int b, int h, int pos, int c8, float (&x)[8])
     }
 }
 
-FQ_DEV uint32_t code4(float v, float mn, float s) {
+template <int BITS>
+FQ_DEV uint32_t codeq(float v, float mn, float s) {
     float c = rintf(__fdiv_rn(v - mn, s));
-    c = fminf(fmaxf(c, 0.f), 15.f);
+    c = fminf(fmaxf(c, 0.f), (float)((1 << BITS) - 1));
     return (uint32_t)c;
+}
+
+// The 8 codes of a thread's channels: BITS 4 packs two per byte (4 bytes),
+// BITS 8 one per byte (8 bytes), at byte 8 * c8 * BITS / 8 of the row.
+template <int BITS>
+FQ_DEV void store_codes(uint8_t* row, int c8, const uint32_t (&c)[8]) {
+    if constexpr (BITS == 4) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= c[i] << (4 * i);
+        *(uint32_t*)(row + 4 * c8) = word;
+    } else {
+        *(uint2*)(row + 8 * c8) = make_uint2(c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24,
+                                             c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24);
+    }
 }
 
 FQ_DEV uint32_t meta_bits(float f, int dtype) {
     return dtype == FQ_BF16 ? f_to_bf16_bits(f) : f_to_f16_bits(f);
 }
 
-template <int D>
+template <int D, int BITS>
 __global__ __launch_bounds__(kThreads) void page_quant_kernel(PageQuantParams a) {
     constexpr int CPR = D / 8;                  // threads per token row
     constexpr int RPP = kThreads / CPR;         // token rows per pass
@@ -139,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void page_quant_kernel(PageQuantParams a)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float diff = round_to(mx[i] - mn[i], dt);
-            float s = round_to(diff * kCacheInv15, dt);
+            float s = round_to(diff * (BITS == 8 ? kCacheInv255 : kCacheInv15), dt);
             sc[i] = round_to(fmaxf(s, kCacheEps), dt);
         }
         if (r == 0) {
@@ -159,11 +177,11 @@ __global__ __launch_bounds__(kThreads) void page_quant_kernel(PageQuantParams a)
 #pragma unroll
             for (int u = 0; u < TPT; ++u) {
                 if (!ok[u]) continue;
-                uint32_t word = 0;
+                uint32_t cd[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) word |= code4(x[u][i], mn[i], sc[i]) << (4 * i);
-                *(uint32_t*)(a.kp + b * a.kp_s[0] + h * a.kp_s[1] + (int64_t)(a.tok_dst0 + pos[u]) * a.kp_s[2] +
-                             4 * c8) = word;
+                for (int i = 0; i < 8; ++i) cd[i] = codeq<BITS>(x[u][i], mn[i], sc[i]);
+                store_codes<BITS>(a.kp + b * a.kp_s[0] + h * a.kp_s[1] + (int64_t)(a.tok_dst0 + pos[u]) * a.kp_s[2],
+                                  c8, cd);
             }
         }
     }
@@ -187,17 +205,18 @@ __global__ __launch_bounds__(kThreads) void page_quant_kernel(PageQuantParams a)
                 mn = fminf(mn, __shfl_xor(mn, off, 64));
                 mx = fmaxf(mx, __shfl_xor(mx, off, 64));
             }
-            const float s = fmaxf((mx - mn) * kCacheInv15, kCacheEps);      // fp32 (kv_quant.py:189-205)
+            // fp32 (kv_quant.py:189-205; INT8: 78-89)
+            const float s = fmaxf((mx - mn) * (BITS == 8 ? kCacheInv255 : kCacheInv15), kCacheEps);
             if (!ok[u]) continue;
             const int64_t t = a.tok_dst0 + pos[u];
             if (c8 % lpg == 0) {
                 store_any(a.vs, a.meta_dtype, b * a.vs_s[0] + h * a.vs_s[1] + t * a.vs_s[2] + g, s);
                 store_any(a.vm, a.meta_dtype, b * a.vm_s[0] + h * a.vm_s[1] + t * a.vm_s[2] + g, mn);
             }
-            uint32_t word = 0;
+            uint32_t cd[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) word |= code4(x[i], mn, s) << (4 * i);
-            *(uint32_t*)(a.vp + b * a.vp_s[0] + h * a.vp_s[1] + t * a.vp_s[2] + 4 * c8) = word;
+            for (int i = 0; i < 8; ++i) cd[i] = codeq<BITS>(x[i], mn, s);
+            store_codes<BITS>(a.vp + b * a.vp_s[0] + h * a.vp_s[1] + t * a.vp_s[2], c8, cd);
         }
     }
 }
@@ -208,23 +227,62 @@ struct TailCopyParams {
     const void* src[2]; int64_t ss[2][3];
     void* dst[2]; int64_t ds[2][3];
     int src_t0, dst_t0, n, B, H, row_bytes, esize;
+    int zero_rows;          // after the copy range, dst rows [dst_t0 + n, dst_t0 + n + zero_rows) are zeroed
 };
 
 __global__ __launch_bounds__(kThreads) void tail_copy_kernel(TailCopyParams a) {
     const int kv = blockIdx.y;
     const int chunks = a.row_bytes / 16;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t total = (int64_t)a.B * a.H * a.n * chunks;
+    const int rows = a.n + a.zero_rows;
+    const int64_t total = (int64_t)a.B * a.H * rows * chunks;
     if (idx >= total) return;
     const int ch = idx % chunks;
-    const int t = (idx / chunks) % a.n;
-    const int bh = idx / ((int64_t)chunks * a.n);
+    const int t = (idx / chunks) % rows;
+    const int bh = idx / ((int64_t)chunks * rows);
     const int b = bh / a.H, h = bh % a.H;
-    const char* s = (const char*)a.src[kv] +
-                    (b * a.ss[kv][0] + h * a.ss[kv][1] + (int64_t)(a.src_t0 + t) * a.ss[kv][2]) * a.esize + 16 * ch;
     char* d = (char*)a.dst[kv] +
               (b * a.ds[kv][0] + h * a.ds[kv][1] + (int64_t)(a.dst_t0 + t) * a.ds[kv][2]) * a.esize + 16 * ch;
+    if (t >= a.n) {
+        *(uint4*)d = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
+    const char* s = (const char*)a.src[kv] +
+                    (b * a.ss[kv][0] + h * a.ss[kv][1] + (int64_t)(a.src_t0 + t) * a.ss[kv][2]) * a.esize + 16 * ch;
     *(uint4*)d = *(const uint4*)s;
+}
+
+// TurboQuant rows of positions [0, n_tok) of a two-source token stream into
+// the planes / per-token scale at token tok_dst0 + position; one thread per
+// (b, h, token), the arithmetic of turbo_quant_row.
+struct TurboAppendParams {
+    TokSrc src;
+    int B, H, n_tok, tok_dst0;
+    uint8_t* msb; int64_t msb_s[3];     // (b, h, t) byte strides; bytes of a row contiguous
+    uint8_t* lsb; int64_t lsb_s[3];
+    void* scale; int64_t s_s[3];        // (b, h, t) element strides (bf16)
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void turbo_append_kernel(TurboAppendParams a) {
+    const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t total = (int64_t)a.B * a.H * a.n_tok;
+    if (idx >= total) return;
+    const int pos = idx % a.n_tok;
+    const int h = (idx / a.n_tok) % a.H;
+    const int b = idx / ((int64_t)a.n_tok * a.H);
+    float v[D];
+#pragma unroll
+    for (int c8 = 0; c8 < D / 8; ++c8) {
+        float x[8];
+        load8(a.src, b, h, pos, c8, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[8 * c8 + i] = x[i];
+    }
+    const int64_t t = a.tok_dst0 + pos;
+    turbo_quant_row<D>(v, a.src.dtype, a.msb + b * a.msb_s[0] + h * a.msb_s[1] + t * a.msb_s[2], 1,
+                       a.lsb + b * a.lsb_s[0] + h * a.lsb_s[1] + t * a.lsb_s[2], 1, a.scale,
+                       b * a.s_s[0] + h * a.s_s[1] + t * a.s_s[2]);
 }
 
 bool rows16(const void* p, const int64_t* s, int n, int esize) {
@@ -259,11 +317,13 @@ bool page_quant_v_ok(int D, int group, int in_dtype, const void* v, const int64_
 
 // Quantise positions [0, n_tok) of (k, v) sources into the outputs at token
 // tok_dst0 (K: whole pages, tok_dst0 a multiple of 64).
-hipError_t launch_page_quant(const PageQuantParams& a, int D, hipStream_t st) {
+hipError_t launch_page_quant(const PageQuantParams& a, int D, hipStream_t st, int bits = 4) {
     if (a.n_tok <= 0 || a.B * a.H == 0) return hipSuccess;
     dim3 grid((a.n_tok + kPage - 1) / kPage, a.B * a.H);
-    if (D == 128) hipLaunchKernelGGL(page_quant_kernel<128>, grid, dim3(kThreads), 0, st, a);
-    else if (D == 64) hipLaunchKernelGGL(page_quant_kernel<64>, grid, dim3(kThreads), 0, st, a);
+    if (D == 128 && bits == 4) hipLaunchKernelGGL((page_quant_kernel<128, 4>), grid, dim3(kThreads), 0, st, a);
+    else if (D == 64 && bits == 4) hipLaunchKernelGGL((page_quant_kernel<64, 4>), grid, dim3(kThreads), 0, st, a);
+    else if (D == 128 && bits == 8) hipLaunchKernelGGL((page_quant_kernel<128, 8>), grid, dim3(kThreads), 0, st, a);
+    else if (D == 64 && bits == 8) hipLaunchKernelGGL((page_quant_kernel<64, 8>), grid, dim3(kThreads), 0, st, a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
@@ -292,30 +352,71 @@ hipError_t launch_quant_v_pages(const void* v, int in_dtype, const int64_t* v_s,
     return launch_page_quant(a, D, st);
 }
 
-// update_quantized (persistent_int4.py:69-132) for one layer: pages completed
-// by the append are quantised from (partial tail, new tokens) into the cache,
-// then the remaining tokens are staged in the tail.  The page kernel reads the
-// old tail before the copy (stream order) overwrites it.
-hipError_t launch_int4_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
-                              const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
-                              const void* vnew, const int64_t* vn_s, int seen, int S_new, hipStream_t st) {
-    const int page = c.page;
-    const int partial_len = seen % page;
-    const int total = partial_len + S_new;
-    const int n_complete = total / page;
-    const int complete_len = n_complete * page;
-    const int new_partial = total - complete_len;
+// Stage the tokens that remain after the completed pages in the partial-page
+// tail: tokens [src_t0, src_t0 + n) of the new tokens -> tail rows
+// [dst_t0, dst_t0 + n); zero_tail also clears the tail rows after them (the
+// INT8 cache's convention, persistent_int8.py:129-132).
+hipError_t stage_tail(int B, int H, int D, int page, void* kpart, const int64_t* kpart_s, void* vpart,
+                      const int64_t* vpart_s, int64_t layer, const void* knew, const int64_t* kn_s, const void* vnew,
+                      const int64_t* vn_s, int src_t0, int dst_t0, int n, bool zero_tail, hipStream_t st) {
+    const int zero_rows = zero_tail ? page - (dst_t0 + n) : 0;
+    if (n + zero_rows == 0 || B * H == 0) return hipSuccess;
+    TailCopyParams t{};
+    t.src[0] = knew; t.src[1] = vnew;
+    t.dst[0] = (char*)kpart + layer * kpart_s[0] * 2;
+    t.dst[1] = (char*)vpart + layer * vpart_s[0] * 2;
+    for (int i = 0; i < 3; ++i) {
+        t.ss[0][i] = kn_s[i]; t.ss[1][i] = vn_s[i];
+        t.ds[0][i] = kpart_s[i + 1]; t.ds[1][i] = vpart_s[i + 1];
+    }
+    t.src_t0 = src_t0; t.dst_t0 = dst_t0; t.n = n; t.zero_rows = zero_rows;
+    t.B = B; t.H = H; t.esize = 2; t.row_bytes = D * 2;
+    const int64_t threads = (int64_t)B * H * (n + zero_rows) * (t.row_bytes / 16);
+    hipLaunchKernelGGL(tail_copy_kernel, dim3((unsigned)((threads + kThreads - 1) / kThreads), 2), dim3(kThreads), 0,
+                       st, t);
+    return hipGetLastError();
+}
+
+// The page arithmetic of an append: `seen` tokens were in the layer, S_new
+// arrive; the stream (old tail, new tokens) completes n_complete pages
+// starting at token page_tok0, and `rest` tokens stay in the tail.
+struct AppendPlan {
+    int partial_len, n_complete, complete_len, page_tok0, rest;
+};
+AppendPlan plan_append(int seen, int S_new, int page) {
+    AppendPlan p{};
+    p.partial_len = seen % page;
+    p.n_complete = (p.partial_len + S_new) / page;
+    p.complete_len = p.n_complete * page;
+    p.page_tok0 = seen - p.partial_len;
+    p.rest = p.partial_len + S_new - p.complete_len;
+    return p;
+}
+
+// Token sources of the stream: the layer's tail rows, then the new tokens.
+TokSrc stream_src(const void* part, const int64_t* part_s, int64_t layer, const void* fresh, const int64_t* fresh_s,
+                  int partial_len, int dtype) {
+    return TokSrc{(const char*)part + layer * part_s[0] * 2, {part_s[1], part_s[2], part_s[3]}, fresh,
+                  {fresh_s[0], fresh_s[1], fresh_s[2]}, partial_len, dtype};
+}
+
+// update_quantized of the INT4 cache (persistent_int4.py:69-132; bits 4) and
+// of the INT8 cache (persistent_int8.py:72-135; bits 8, tail rows after the
+// staged ones zeroed) for one layer: pages completed by the append are
+// quantised from (partial tail, new tokens) into the cache, then the remaining
+// tokens are staged in the tail.  The page kernel reads the old tail before
+// the copy (stream order) overwrites it.
+hipError_t launch_kv_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
+                            const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
+                            const void* vnew, const int64_t* vn_s, int seen, int S_new, int bits, hipStream_t st) {
+    const AppendPlan pl = plan_append(seen, S_new, c.page);
     const int64_t l = layer;
-    if (n_complete > 0) {
+    if (pl.n_complete > 0) {
         PageQuantParams a{};
-        const char* kp0 = (const char*)kpart + l * kpart_s[0] * 2;
-        const char* vp0 = (const char*)vpart + l * vpart_s[0] * 2;
-        a.k = TokSrc{kp0, {kpart_s[1], kpart_s[2], kpart_s[3]}, knew, {kn_s[0], kn_s[1], kn_s[2]}, partial_len,
-                     part_dtype};
-        a.v = TokSrc{vp0, {vpart_s[1], vpart_s[2], vpart_s[3]}, vnew, {vn_s[0], vn_s[1], vn_s[2]}, partial_len,
-                     part_dtype};
+        a.k = stream_src(kpart, kpart_s, l, knew, kn_s, pl.partial_len, part_dtype);
+        a.v = stream_src(vpart, vpart_s, l, vnew, vn_s, pl.partial_len, part_dtype);
         a.do_k = true; a.k_codes = true; a.do_v = true;
-        a.B = c.B; a.H = c.Hkv; a.n_tok = complete_len; a.tok_dst0 = seen - partial_len;
+        a.B = c.B; a.H = c.Hkv; a.n_tok = pl.complete_len; a.tok_dst0 = pl.page_tok0;
         a.kp = (uint8_t*)c.kp + l * c.kp_s[0];
         a.vp = (uint8_t*)c.vp + l * c.vp_s[0];
         a.ks = (uint16_t*)c.ksc + l * c.ksc_s[0];
@@ -329,26 +430,63 @@ hipError_t launch_int4_append(const Int4Cache& c, int layer, void* kpart, const 
         }
         a.v_group = c.D / c.G;
         a.meta_dtype = c.meta_dtype;
-        const hipError_t e = launch_page_quant(a, c.D, st);
+        const hipError_t e = launch_page_quant(a, c.D, st, bits);
         if (e != hipSuccess) return e;
     }
-    const int n = n_complete > 0 ? new_partial : S_new;
-    if (n == 0 || c.B * c.Hkv == 0) return hipSuccess;
-    TailCopyParams t{};
-    t.src[0] = knew; t.src[1] = vnew;
-    t.dst[0] = (char*)kpart + l * kpart_s[0] * 2;
-    t.dst[1] = (char*)vpart + l * vpart_s[0] * 2;
-    for (int i = 0; i < 3; ++i) {
-        t.ss[0][i] = kn_s[i]; t.ss[1][i] = vn_s[i];
-        t.ds[0][i] = kpart_s[i + 1]; t.ds[1][i] = vpart_s[i + 1];
+    // without a completed page the new tokens extend the tail in place
+    const bool done = pl.n_complete > 0;
+    return stage_tail(c.B, c.Hkv, c.D, c.page, kpart, kpart_s, vpart, vpart_s, l, knew, kn_s, vnew, vn_s,
+                      done ? S_new - pl.rest : 0, done ? 0 : pl.partial_len, done ? pl.rest : S_new, bits == 8, st);
+}
+
+// update_quantized of the TurboQuant cache (persistent_turbo.py:83-147) for
+// one layer: for the completed pages, the un-rotated K's bf16 page scale/min
+// (the INT4 metadata, no codes) and the K and V rotated 3-bit planes with
+// their per-token scales; then the remaining tokens go to the tail.  raw:
+// descriptor of K_scale_raw / K_mn_raw (ksc / kmn, element strides).
+hipError_t launch_turbo_append(const fq_turbo_cache& tc, const Int4Cache& raw, int layer, void* kpart,
+                               const int64_t* kpart_s, void* vpart, const int64_t* vpart_s, int part_dtype,
+                               const void* knew, const int64_t* kn_s, const void* vnew, const int64_t* vn_s, int seen,
+                               int S_new, hipStream_t st) {
+    const AppendPlan pl = plan_append(seen, S_new, tc.page_size);
+    const int64_t l = layer;
+    if (pl.n_complete > 0) {
+        PageQuantParams a{};
+        a.k = stream_src(kpart, kpart_s, l, knew, kn_s, pl.partial_len, part_dtype);
+        a.do_k = true; a.k_codes = false;
+        a.B = tc.B; a.H = tc.H_kv; a.n_tok = pl.complete_len; a.tok_dst0 = pl.page_tok0;
+        a.ks = (uint16_t*)raw.ksc + l * raw.ksc_s[0];
+        a.km = (uint16_t*)raw.kmn + l * raw.kmn_s[0];
+        for (int i = 0; i < 3; ++i) { a.ks_s[i] = raw.ksc_s[i + 1]; a.km_s[i] = raw.kmn_s[i + 1]; }
+        a.meta_dtype = FQ_BF16;
+        hipError_t e = launch_page_quant(a, tc.D, st, 4);
+        if (e != hipSuccess) return e;
+        for (int kv = 0; kv < 2; ++kv) {
+            TurboAppendParams t{};
+            t.src = kv == 0 ? a.k : stream_src(vpart, vpart_s, l, vnew, vn_s, pl.partial_len, part_dtype);
+            t.B = tc.B; t.H = tc.H_kv; t.n_tok = pl.complete_len; t.tok_dst0 = pl.page_tok0;
+            const uint8_t* msb = kv == 0 ? tc.k_msb : tc.v_msb;
+            const uint8_t* lsb = kv == 0 ? tc.k_lsb : tc.v_lsb;
+            const void* sc = kv == 0 ? tc.k_scale : tc.v_scale;
+            const int64_t* ms = kv == 0 ? tc.kmsb_strides : tc.vmsb_strides;
+            const int64_t* ls = kv == 0 ? tc.klsb_strides : tc.vlsb_strides;
+            const int64_t* ss = kv == 0 ? tc.kst_strides : tc.vst_strides;
+            t.msb = (uint8_t*)msb + l * ms[0];
+            t.lsb = (uint8_t*)lsb + l * ls[0];
+            t.scale = (uint16_t*)sc + l * ss[0];
+            for (int i = 0; i < 3; ++i) { t.msb_s[i] = ms[i + 1]; t.lsb_s[i] = ls[i + 1]; t.s_s[i] = ss[i + 1]; }
+            const int64_t n = (int64_t)t.B * t.H * t.n_tok;
+            const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+            if (tc.D == 128) hipLaunchKernelGGL(turbo_append_kernel<128>, grid, dim3(kThreads), 0, st, t);
+            else if (tc.D == 64) hipLaunchKernelGGL(turbo_append_kernel<64>, grid, dim3(kThreads), 0, st, t);
+            else return hipErrorInvalidValue;
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
-    t.src_t0 = n_complete > 0 ? S_new - new_partial : 0;
-    t.dst_t0 = n_complete > 0 ? 0 : partial_len;
-    t.n = n; t.B = c.B; t.H = c.Hkv; t.esize = 2; t.row_bytes = c.D * 2;
-    const int64_t threads = (int64_t)c.B * c.Hkv * n * (t.row_bytes / 16);
-    hipLaunchKernelGGL(tail_copy_kernel, dim3((unsigned)((threads + kThreads - 1) / kThreads), 2), dim3(kThreads), 0,
-                       st, t);
-    return hipGetLastError();
+    const bool done = pl.n_complete > 0;
+    return stage_tail(tc.B, tc.H_kv, tc.D, tc.page_size, kpart, kpart_s, vpart, vpart_s, l, knew, kn_s, vnew, vn_s,
+                      done ? S_new - pl.rest : 0, done ? 0 : pl.partial_len, done ? pl.rest : S_new, false, st);
 }
 
 }  // namespace fq

@@ -634,34 +634,91 @@ int fq_quantize_v_int4(const void* v, int32_t in_dtype, const int64_t v_strides[
                       "quantize v");
 }
 
-int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer, void* k_partial, const int64_t kpart_strides[5],
-                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype, const void* k_new,
-                         const int64_t kn_strides[4], const void* v_new, const int64_t vn_strides[4], int32_t seen,
-                         int32_t S_new, fq_stream_t stream) {
-    Int4Cache c{};
-    int st = check_cache(cache, &c);
-    if (st) return st;
-    if (layer < 0 || layer >= c.L) return fail(FQ_ERR_INVALID, "layer_idx %d out of range [0, %d)", layer, c.L);
-    if (seen < 0 || S_new < 0) return fail(FQ_ERR_INVALID, "negative seen / S_new");
-    if ((int64_t)seen + S_new > c.S)
-        return fail(FQ_ERR_INVALID, "seen+new=%lld exceeds max_seq_len=%d", (long long)seen + S_new, c.S);
-    if (c.page != 64) return fail(FQ_ERR_UNSUPPORTED, "page_size=%d (the append kernel takes 64)", c.page);
-    if ((int64_t)(seen + S_new + c.page - 1) / c.page > c.P) return fail(FQ_ERR_INVALID, "page metadata too short");
+// Checks shared by the three cache appends: bounds of the append, the tail
+// dtype, 16-byte aligned contiguous rows of the tails and the new tokens.
+static int check_append(int L, int S, int P, int page, int layer, void* k_partial, const int64_t kpart_strides[5],
+                        void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype, const void* k_new,
+                        const int64_t kn_strides[4], const void* v_new, const int64_t vn_strides[4], int32_t seen,
+                        int32_t S_new) {
+    if (layer < 0 || layer >= L) return fail(FQ_ERR_INVALID, "layer %d is not one of the cache's %d layers", layer, L);
+    if (seen < 0 || S_new < 0) return fail(FQ_ERR_INVALID, "negative token count (seen %d, new %d)", seen, S_new);
+    if ((int64_t)seen + S_new > S)
+        return fail(FQ_ERR_INVALID, "%lld tokens do not fit the cache's %d token slots", (long long)seen + S_new, S);
+    if (page != 64) return fail(FQ_ERR_UNSUPPORTED, "page_size=%d (the append kernel takes 64)", page);
+    if ((int64_t)(seen + S_new + page - 1) / page > P) return fail(FQ_ERR_INVALID, "page metadata holds %d pages", P);
     if (partial_dtype != FQ_BF16 && partial_dtype != FQ_F16)
         return fail(FQ_ERR_UNSUPPORTED, "partial tail dtype must be bf16 or fp16");
     if (!k_partial || !v_partial || (!k_new && S_new) || (!v_new && S_new)) return fail(FQ_ERR_INVALID, "NULL tensor");
-    const int64_t pk3[4] = {kpart_strides[1], kpart_strides[2], kpart_strides[3], kpart_strides[4]};
-    const int64_t pv3[4] = {vpart_strides[1], vpart_strides[2], vpart_strides[3], vpart_strides[4]};
     if (!rows_aligned16(k_partial, kpart_strides, 4, 2) || !rows_aligned16(v_partial, vpart_strides, 4, 2) ||
-        kpart_strides[4] != 1 || vpart_strides[4] != 1 || pk3[3] != 1 || pv3[3] != 1)
+        kpart_strides[4] != 1 || vpart_strides[4] != 1)
         return fail(FQ_ERR_UNSUPPORTED, "partial tails need 16-byte aligned contiguous rows");
     if (S_new > 0 && (!rows_aligned16(k_new, kn_strides, 3, 2) || !rows_aligned16(v_new, vn_strides, 3, 2) ||
                       kn_strides[3] != 1 || vn_strides[3] != 1))
         return fail(FQ_ERR_UNSUPPORTED, "new K/V need 16-byte aligned contiguous rows");
+    return FQ_OK;
+}
+
+static int kv_cache_append(const fq_int4_cache* cache, int bits, int32_t layer, void* k_partial,
+                           const int64_t kpart_strides[5], void* v_partial, const int64_t vpart_strides[5],
+                           int32_t partial_dtype, const void* k_new, const int64_t kn_strides[4], const void* v_new,
+                           const int64_t vn_strides[4], int32_t seen, int32_t S_new, fq_stream_t stream) {
+    Int4Cache c{};
+    int st = check_cache(cache, &c, bits);
+    if (st) return st;
+    st = check_append(c.L, c.S, c.P, c.page, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype,
+                      k_new, kn_strides, v_new, vn_strides, seen, S_new);
+    if (st) return st;
+    if (c.D != 64 && c.D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d (the append kernel takes 64, 128)", c.D);
     if (((uintptr_t)c.vsc | (uintptr_t)c.vmn) & 1) return fail(FQ_ERR_UNSUPPORTED, "V metadata must be 2-byte aligned");
-    return hip_status(launch_int4_append(c, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype,
-                                         k_new, kn_strides, v_new, vn_strides, seen, S_new, (hipStream_t)stream),
-                      "int4 cache append");
+    return hip_status(launch_kv_append(c, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype,
+                                       k_new, kn_strides, v_new, vn_strides, seen, S_new, bits, (hipStream_t)stream),
+                      bits == 8 ? "int8 cache append" : "int4 cache append");
+}
+
+int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer, void* k_partial, const int64_t kpart_strides[5],
+                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype, const void* k_new,
+                         const int64_t kn_strides[4], const void* v_new, const int64_t vn_strides[4], int32_t seen,
+                         int32_t S_new, fq_stream_t stream) {
+    return kv_cache_append(cache, 4, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype, k_new,
+                           kn_strides, v_new, vn_strides, seen, S_new, stream);
+}
+
+int fq_int8_cache_append(const fq_int8_cache* cache, int32_t layer, void* k_partial, const int64_t kpart_strides[5],
+                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype, const void* k_new,
+                         const int64_t kn_strides[4], const void* v_new, const int64_t vn_strides[4], int32_t seen,
+                         int32_t S_new, fq_stream_t stream) {
+    if (cache && cache->v_groups != 1) return fail(FQ_ERR_UNSUPPORTED, "INT8 V metadata is per token (v_groups=1)");
+    return kv_cache_append(cache, 8, layer, k_partial, kpart_strides, v_partial, vpart_strides, partial_dtype, k_new,
+                           kn_strides, v_new, vn_strides, seen, S_new, stream);
+}
+
+int fq_turbo_cache_append(const fq_turbo_cache* cache, void* k_scale_raw, const int64_t ksr_strides[5],
+                          void* k_mn_raw, const int64_t kmr_strides[5], int32_t layer, void* k_partial,
+                          const int64_t kpart_strides[5], void* v_partial, const int64_t vpart_strides[5],
+                          int32_t partial_dtype, const void* k_new, const int64_t kn_strides[4], const void* v_new,
+                          const int64_t vn_strides[4], int32_t seen, int32_t S_new, fq_stream_t stream) {
+    if (!cache) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    const fq_turbo_cache& tc = *cache;
+    if (tc.D != 64 && tc.D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d (the append kernel takes 64, 128)", tc.D);
+    if (tc.L < 1 || tc.B < 1 || tc.H_kv < 1) return fail(FQ_ERR_INVALID, "empty L/B/H_kv");
+    int st = check_append(tc.L, tc.S, tc.P, tc.page_size, layer, k_partial, kpart_strides, v_partial, vpart_strides,
+                          partial_dtype, k_new, kn_strides, v_new, vn_strides, seen, S_new);
+    if (st) return st;
+    if (!tc.k_msb || !tc.k_lsb || !tc.k_scale || !tc.v_msb || !tc.v_lsb || !tc.v_scale || !k_scale_raw || !k_mn_raw)
+        return fail(FQ_ERR_INVALID, "NULL cache tensor");
+    if (tc.kmsb_strides[4] != 1 || tc.klsb_strides[4] != 1 || tc.vmsb_strides[4] != 1 || tc.vlsb_strides[4] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "code planes need contiguous rows");
+    if (((uintptr_t)tc.k_scale | (uintptr_t)tc.v_scale) & 1) return fail(FQ_ERR_UNSUPPORTED, "scales must be 2-byte aligned");
+    if (ksr_strides[4] != 1 || kmr_strides[4] != 1 || !rows_aligned16(k_scale_raw, ksr_strides, 4, 2) ||
+        !rows_aligned16(k_mn_raw, kmr_strides, 4, 2))
+        return fail(FQ_ERR_UNSUPPORTED, "raw K page metadata needs 16-byte aligned contiguous rows");
+    Int4Cache raw{};
+    raw.ksc = k_scale_raw; raw.kmn = k_mn_raw;
+    for (int i = 0; i < 4; ++i) { raw.ksc_s[i] = ksr_strides[i]; raw.kmn_s[i] = kmr_strides[i]; }
+    return hip_status(launch_turbo_append(tc, raw, layer, k_partial, kpart_strides, v_partial, vpart_strides,
+                                          partial_dtype, k_new, kn_strides, v_new, vn_strides, seen, S_new,
+                                          (hipStream_t)stream),
+                      "turbo cache append");
 }
 
 int fq_wht(const void* x, int32_t x_dtype, int64_t x_row_stride, void* out, int32_t out_dtype,
@@ -804,6 +861,7 @@ static int prefill_check_tail_query(const fq_tail* tail, const fq_prefill* q, in
         for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
     }
     if (!q || !q->q || !q->out) return fail(FQ_ERR_INVALID, "query/output is NULL");
+    if (q->D != D) return fail(FQ_ERR_INVALID, "query head_dim %d != cache head_dim %d", q->D, D);
     if (q->H_q < 1 || q->H_q % Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, Hkv);
     if (q->S_q < 1) return fail(FQ_ERR_INVALID, "S_q=%d", q->S_q);
     if (q->causal_offset < 0) return fail(FQ_ERR_INVALID, "causal_offset=%d must be >= 0", q->causal_offset);

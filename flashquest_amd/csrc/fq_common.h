@@ -266,9 +266,13 @@ hipError_t launch_quant_k_pages(const void* k, int in_dtype, const int64_t* k_s,
 hipError_t launch_quant_v_pages(const void* v, int in_dtype, const int64_t* v_s, int B, int H, int S, int D,
                                 int group, uint8_t* packed, const int64_t* p_s, void* scale, const int64_t* s_s,
                                 void* mn, const int64_t* m_s, int meta_dtype, hipStream_t st);
-hipError_t launch_int4_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
-                              const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
-                              const void* vnew, const int64_t* vn_s, int seen, int S_new, hipStream_t st);
+hipError_t launch_kv_append(const Int4Cache& c, int layer, void* kpart, const int64_t* kpart_s, void* vpart,
+                            const int64_t* vpart_s, int part_dtype, const void* knew, const int64_t* kn_s,
+                            const void* vnew, const int64_t* vn_s, int seen, int S_new, int bits, hipStream_t st);
+hipError_t launch_turbo_append(const fq_turbo_cache& tc, const Int4Cache& raw, int layer, void* kpart,
+                               const int64_t* kpart_s, void* vpart, const int64_t* vpart_s, int part_dtype,
+                               const void* knew, const int64_t* kn_s, const void* vnew, const int64_t* vn_s, int seen,
+                               int S_new, hipStream_t st);
 // Fused-layout TurboQuant attention (turbo_fused.hip): D = 128, 64-token pages,
 // <= 3 query heads per KV head.  raw + sel: score and select in the kernel.
 bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q);

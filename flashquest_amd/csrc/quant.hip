@@ -2,6 +2,7 @@
 // bf16 tail attention (gfx950).  These are the operators on either side of the
 // sparse decode kernel in the reference's decode path.
 #include "fq_common.h"
+#include "turbo_quant.h"
 
 namespace fq {
 
@@ -238,9 +239,6 @@ __global__ __launch_bounds__(kThreads) void wht_kernel(WhtParams a) {
 // nearest of 8 codepoints (first on ties) -> bit-split planes.  One thread
 // per token.
 // -------------------------------------------------------------------------
-__device__ __constant__ float kTurboCodebook[8] = {-2.1519f, -1.3439f, -0.7560f, -0.2451f,
-                                                   0.2451f, 0.7560f, 1.3439f, 2.1519f};
-
 struct TurboQParams {
     const void* x; int in_dtype; int64_t x_s[4];
     int B, H, S;
@@ -261,44 +259,9 @@ __global__ __launch_bounds__(kThreads) void turbo_quant_kernel(TurboQParams a) {
     const int64_t base = b * a.x_s[0] + h * a.x_s[1] + t * a.x_s[2];
 #pragma unroll
     for (int d = 0; d < D; ++d) v[d] = load_any(a.x, a.in_dtype, base + d * a.x_s[3]);
-#pragma unroll
-    for (int hh = 1; hh < D; hh <<= 1) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
-            if ((i & hh) == 0) {
-                const float x = v[i], y = v[i + hh];
-                v[i] = round_to(x + y, a.in_dtype);
-                v[i + hh] = round_to(x - y, a.in_dtype);
-            }
-        }
-    }
-    const float inv = 1.0f / sqrtf((float)D);
-    float ss = 0.f;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        v[d] = round_to(v[d] * inv, a.in_dtype);
-        ss = __fadd_rn(ss, __fmul_rn(v[d], v[d]));
-    }
-    const float rms = fmaxf(__fsqrt_rn(__fdiv_rn(ss, (float)D)), kEps);
-    store_any(a.scale, FQ_BF16, b * a.s_s[0] + h * a.s_s[1] + t * a.s_s[2], rms);
-    uint8_t* mrow = a.msb + b * a.msb_s[0] + h * a.msb_s[1] + t * a.msb_s[2];
-    uint8_t* lrow = a.lsb + b * a.lsb_s[0] + h * a.lsb_s[1] + t * a.lsb_s[2];
-    uint32_t mbyte = 0, lbyte = 0;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        const float x = __fdiv_rn(v[d], rms);
-        int best = 0;
-        float bd = fabsf(x - kTurboCodebook[0]);
-#pragma unroll
-        for (int k = 1; k < 8; ++k) {
-            const float dd = fabsf(x - kTurboCodebook[k]);
-            if (dd < bd) { bd = dd; best = k; }
-        }
-        mbyte |= (uint32_t)((best >> 2) & 1) << (d % 8);
-        lbyte |= (uint32_t)(best & 3) << (2 * (d % 4));
-        if (d % 4 == 3) { lrow[(d / 4) * a.lsb_s[3]] = (uint8_t)lbyte; lbyte = 0; }
-        if (d % 8 == 7) { mrow[(d / 8) * a.msb_s[3]] = (uint8_t)mbyte; mbyte = 0; }
-    }
+    turbo_quant_row<D>(v, a.in_dtype, a.msb + b * a.msb_s[0] + h * a.msb_s[1] + t * a.msb_s[2], a.msb_s[3],
+                       a.lsb + b * a.lsb_s[0] + h * a.lsb_s[1] + t * a.lsb_s[2], a.lsb_s[3],
+                       a.scale, b * a.s_s[0] + h * a.s_s[1] + t * a.s_s[2]);
 }
 
 // -------------------------------------------------------------------------

@@ -233,6 +233,34 @@ int fq_int4_cache_append(const fq_int4_cache* cache, int32_t layer,
                          const void* v_new, const int64_t vn_strides[4],
                          int32_t seen, int32_t S_new, fq_stream_t stream);
 
+/* PersistentInt8KVCache.update_quantized (src/flashquest/cache/persistent_int8.py:72-135)
+ * for one layer, with the arguments of fq_int4_cache_append over the INT8
+ * descriptor (codes one byte per channel, v_groups = 1): completed pages get
+ * fq_quantize_k_int8 / fq_quantize_v_int8's codes and metadata, the remaining
+ * tokens go to the tail and the tail rows after them are zeroed, as the
+ * reference's cache does. */
+int fq_int8_cache_append(const fq_int8_cache* cache, int32_t layer,
+                         void* k_partial, const int64_t kpart_strides[5],
+                         void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype,
+                         const void* k_new, const int64_t kn_strides[4],
+                         const void* v_new, const int64_t vn_strides[4],
+                         int32_t seen, int32_t S_new, fq_stream_t stream);
+
+/* PersistentTurboKVCache.update_quantized (src/flashquest/cache/persistent_turbo.py:83-147)
+ * for one layer of the preallocated TurboQuant cache (`cache`: the full
+ * planes and per-token scales, S = max_seq_len, P = max_pages), plus the
+ * un-rotated K's bf16 page scale/min K_scale_raw / K_mn_raw (L, B, H_kv, P, D).
+ * Completed pages: the page metadata of fq_quantize_k_int4 (no codes) and the
+ * planes and scales of fq_quantize_turbo for K and V, bit-identical to
+ * quantising the whole stream; the remaining tokens go to the tail. */
+int fq_turbo_cache_append(const fq_turbo_cache* cache, void* k_scale_raw, const int64_t ksr_strides[5],
+                          void* k_mn_raw, const int64_t kmr_strides[5], int32_t layer,
+                          void* k_partial, const int64_t kpart_strides[5],
+                          void* v_partial, const int64_t vpart_strides[5], int32_t partial_dtype,
+                          const void* k_new, const int64_t kn_strides[4],
+                          const void* v_new, const int64_t vn_strides[4],
+                          int32_t seen, int32_t S_new, fq_stream_t stream);
+
 /* The whole decode branch of the reference's attention patch for a step with
  * a partial page (llama_persistent_patch.py:202-240): score, select and
  * attend the completed pages, attend the tail densely
@@ -391,6 +419,7 @@ typedef struct fq_prefill {
     int32_t H_q, S_q;
     int32_t causal_offset; /* query i attends keys j <= i + causal_offset (>= 0); 0 = torch is_causal */
     float sm_scale;        /* <= 0 selects 1/sqrt(D) */
+    int32_t D;             /* head_dim of Q and O: must equal the cache's */
 } fq_prefill;
 
 /* The S_q > 1 (prefill) branch of the reference's attention patch,

@@ -1,4 +1,4 @@
-"""Persistent INT4 / turbo caches (src/flashquest/cache/persistent_{int4,turbo}.py):
+"""Persistent INT4 / INT8 / turbo caches (src/flashquest/cache/persistent_{int4,int8,turbo}.py):
 a stream appended in chunks of every shape (single decode tokens, chunks that
 end inside a page, exactly on a page, or span several pages) leaves exactly
 what quantising the whole stream at once gives (bit-exact codes and metadata,
@@ -36,7 +36,7 @@ def test_int4_appends_equal_whole_stream_quantisation(D, meta, vgroup):
     K, V = _stream(rng, B, H, total, D)
     cache = PersistentInt4KVCache(batch_size=B, num_layers=layers, num_kv_heads=H, head_dim=D,
                                   max_seq_len=total + 7, meta_dtype=TORCH_HALF[meta], v_group=vgroup)
-    assert cache._desc is not None            # the fused append path
+    assert cache._kernel_append               # the HIP append path
     pos = 0
     for n in CHUNKS:
         cache.update_quantized(to_dev_half(K[:, :, pos:pos + n], "bf16"), to_dev_half(V[:, :, pos:pos + n], "bf16"),
@@ -64,7 +64,7 @@ def test_int4_concat_path_and_errors():
     K, V = _stream(rng, B, H, 75, D)
     cache = PersistentInt4KVCache(batch_size=B, num_layers=1, num_kv_heads=H, head_dim=D, max_seq_len=80,
                                   page_size=page)
-    assert cache._desc is None
+    assert not cache._kernel_append
     pos = 0
     for n in (3, 20, 1, 51):
         cache.update_quantized(torch.from_numpy(K[:, :, pos:pos + n]).cuda(), torch.from_numpy(V[:, :, pos:pos + n]).cuda(), 0)
@@ -77,39 +77,80 @@ def test_int4_concat_path_and_errors():
     # scale arithmetic runs in fp32 on bf16-exact values: the same codes and metadata
     assert np.array_equal(_np(v["K_packed"]), kp) and np.array_equal(_np(v["V_packed"]), vp)
     assert np.array_equal(_np(v["K_scale"]), ks) and np.array_equal(_np(v["V_mn"]), vm)
-    with pytest.raises(IndexError):
+    # the exception types and message keys the reference's tests match on
+    # (tests/test_persistent_cache.py:96-107, test_persistent_int4.py:36-74)
+    with pytest.raises(IndexError, match="layer_idx"):
         cache.get_views(1)
-    with pytest.raises(IndexError):
+    with pytest.raises(IndexError, match="layer_idx"):
         cache.update_quantized(torch.zeros(1, 2, 1, D, device="cuda"), torch.zeros(1, 2, 1, D, device="cuda"), -1)
-    with pytest.raises(RuntimeError):
+    with pytest.raises(RuntimeError, match="exceeds max_seq_len"):
         cache.update_quantized(torch.zeros(1, 2, 6, D, device="cuda"), torch.zeros(1, 2, 6, D, device="cuda"), 0)
     with pytest.raises(NotImplementedError):
         cache.update(None, None, 0)
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="even head_dim"):
         PersistentInt4KVCache(batch_size=1, num_layers=1, num_kv_heads=1, head_dim=7, max_seq_len=8)
 
 
-def test_turbo_appends_equal_whole_stream_quantisation():
+@pytest.mark.parametrize("D", [128, 64])
+def test_turbo_appends_equal_whole_stream_quantisation(D):
+    # fq_turbo_cache_append: after every chunk the completed pages equal the
+    # oracle's quantisation of the whole stream so far, bit for bit
     from flashquest_amd.cache import PersistentTurboKVCache
-    rng = np.random.default_rng(5)
-    B, H, D = 1, 2, 128
+    rng = np.random.default_rng(5 + D)
+    B, H = 2, 2
     total = sum(CHUNKS)
     K, V = _stream(rng, B, H, total, D)
     cache = PersistentTurboKVCache(batch_size=B, num_layers=2, num_kv_heads=H, head_dim=D, max_seq_len=total)
+    assert cache._kernel_append
     pos = 0
     for n in CHUNKS:
         cache.update_quantized(to_dev_half(K[:, :, pos:pos + n], "bf16"), to_dev_half(V[:, :, pos:pos + n], "bf16"), 1)
         pos += n
-    v = cache.get_views(1)
-    comp = pos - pos % 64
-    km, kl, kst, ksr, kmr = O.quantize_k_turbo(K[:, :, :comp], 64, "bf16")
-    vm_, vl, vst = O.quantize_turbo(V[:, :, :comp], "bf16")
-    for name, ref in (("K_msb", km), ("K_lsb", kl), ("K_scale_turbo", kst), ("K_scale_raw", ksr), ("K_mn_raw", kmr),
-                      ("V_msb", vm_), ("V_lsb", vl), ("V_scale_turbo", vst)):
-        assert np.array_equal(_np(v[name]), ref), name
-    assert np.array_equal(_np(v["K_partial"]), K[:, :, comp:pos])
-    with pytest.raises(ValueError):
+        v = cache.get_views(1)
+        comp = pos - pos % 64
+        assert (v["seq_len"], v["completed_len"], v["partial_len"]) == (pos, comp, pos % 64)
+        km, kl, kst, ksr, kmr = O.quantize_k_turbo(K[:, :, :comp], 64, "bf16")
+        vm_, vl, vst = O.quantize_turbo(V[:, :, :comp], "bf16")
+        for name, ref in (("K_msb", km), ("K_lsb", kl), ("K_scale_turbo", kst), ("K_scale_raw", ksr),
+                          ("K_mn_raw", kmr), ("V_msb", vm_), ("V_lsb", vl), ("V_scale_turbo", vst)):
+            assert np.array_equal(_np(v[name]), ref), (n, pos, name)
+        assert np.array_equal(_np(v["K_partial"]), K[:, :, comp:pos])
+        assert np.array_equal(_np(v["V_partial"]), V[:, :, comp:pos])
+    assert not cache.K_msb[0].any() and not cache.K_scale_raw[0].any()      # other layer untouched
+    with pytest.raises(ValueError, match="multiple of 8"):
+        PersistentTurboKVCache(batch_size=1, num_layers=1, num_kv_heads=1, head_dim=12, max_seq_len=8)
+    with pytest.raises(ValueError, match="power of two"):
         PersistentTurboKVCache(batch_size=1, num_layers=1, num_kv_heads=1, head_dim=24, max_seq_len=8)
+
+
+@pytest.mark.parametrize("meta", ["bf16", "f16"])
+def test_int8_appends_equal_whole_stream_quantisation(meta):
+    # fq_int8_cache_append: codes and metadata equal the oracle's INT8
+    # quantisation of the whole stream after every chunk; the tail holds the
+    # incomplete page and zeros after it (persistent_int8.py:129-132)
+    from flashquest_amd.cache import PersistentInt8KVCache
+    rng = np.random.default_rng(17)
+    B, H, D = 1, 3, 128
+    total = sum(CHUNKS)
+    K, V = _stream(rng, B, H, total, D)
+    cache = PersistentInt8KVCache(batch_size=B, num_layers=2, num_kv_heads=H, head_dim=D, max_seq_len=total + 3,
+                                  meta_dtype=TORCH_HALF[meta])
+    assert cache._kernel_append
+    pos = 0
+    for n in CHUNKS:
+        cache.update_quantized(to_dev_half(K[:, :, pos:pos + n], "bf16"), to_dev_half(V[:, :, pos:pos + n], "bf16"), 0)
+        pos += n
+        v = cache.get_views(0)
+        comp = pos - pos % 64
+        ku, ks, km = O.quantize_k_int8(K[:, :, :comp], 64, "bf16", meta)
+        vu, vs, vm = O.quantize_v_int8(V[:, :, :comp], meta)
+        for name, ref in (("K_uint8", ku), ("K_scale", ks), ("K_mn", km), ("V_uint8", vu), ("V_scale", vs),
+                          ("V_mn", vm)):
+            assert np.array_equal(_np(v[name]), ref), (n, pos, name)
+        assert np.array_equal(_np(v["K_partial"]), K[:, :, comp:pos])
+        assert not cache.K_partial[0, :, :, pos - comp:].any() and not cache.V_partial[0, :, :, pos - comp:].any()
+    with pytest.raises(RuntimeError):
+        cache.update(None, None, 0)
 
 
 @pytest.mark.parametrize("partial", [0, 1, 37])
