@@ -70,6 +70,12 @@ def int8_cache(K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, page_size: int):
 
 
 def turbo_cache(K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale, num_pages: int, page_size: int):
+    D = K_msb.shape[-1] * 8
+    if (V_msb.shape[-1] * 8, K_lsb.shape[-1] * 4, V_lsb.shape[-1] * 4) != (D, D, D):
+        raise AssertionError(f"TurboQuant planes disagree on head_dim: MSB rows {K_msb.shape[-1]}/{V_msb.shape[-1]} "
+                             f"bytes (D/8), LSB rows {K_lsb.shape[-1]}/{V_lsb.shape[-1]} bytes (D/4)")
+    if K_scale.shape[-1] != 1 or V_scale.shape[-1] != 1:
+        raise AssertionError("TurboQuant scales must be per token: (..., S, 1)")
     ts = [_ensure_inner_contiguous(t) for t in (K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale)]
     lead = _lead(ts[0], 5)
     c = L.TurboCache()

@@ -25,6 +25,8 @@ def _prefill_call(fn_name: str, cache_desc, keep, q, K_tail, V_tail, causal_offs
     qb = _ops._ensure_inner_contiguous(q.to(torch.bfloat16), 8)
     if cache_desc.B != B:
         raise ValueError(f"batch mismatch: q has {B}, cache has {cache_desc.B}")
+    if D != cache_desc.D:
+        raise ValueError(f"head_dim mismatch: q has {D}, the cache has {cache_desc.D}")
     tail = L.Tail()
     tails = ()
     if K_tail is not None and K_tail.shape[-2] > 0:
@@ -38,7 +40,7 @@ def _prefill_call(fn_name: str, cache_desc, keep, q, K_tail, V_tail, causal_offs
         tails = (kt, vt)
     out = torch.empty(B, H_q, S_q, D, dtype=torch.bfloat16, device=q.device)
     pq = L.Prefill(qb.data_ptr(), L.strides(qb, 4), out.data_ptr(), L.strides(out, 4), H_q, S_q,
-                   int(causal_offset), float(sm_scale) if sm_scale is not None else 0.0)
+                   int(causal_offset), float(sm_scale) if sm_scale is not None else 0.0, D)
     if fn_name == "fq_prefill_turbo":
         nbytes = L.lib().fq_prefill_turbo_workspace_bytes(cache_desc, tail, pq)
     else:

@@ -25,7 +25,7 @@ def _query(Sq, Hq=6, off=0, D=128):
     q = L.Prefill()
     q.q = q.out = 8192
     q.q_strides = q.o_strides = L.i64([Hq * Sq * D, Sq * D, D, 1], 4)
-    q.H_q, q.S_q, q.causal_offset, q.sm_scale = Hq, Sq, off, 0.0
+    q.H_q, q.S_q, q.causal_offset, q.sm_scale, q.D = Hq, Sq, off, 0.0, D
     return q
 
 
@@ -58,7 +58,8 @@ def test_prefill_argument_errors():
              (_cache(D=64), _query(Sq=8, D=64), L.FQ_ERR_UNSUPPORTED),  # head_dim 64
              (_cache(), _query(Sq=8, Hq=5), L.FQ_ERR_INVALID),          # H_q not a multiple of H_kv
              (_cache(), _query(Sq=8, off=-1), L.FQ_ERR_INVALID),        # negative causal offset
-             (_cache(), _query(Sq=0), L.FQ_ERR_INVALID)]                # no queries
+             (_cache(), _query(Sq=0), L.FQ_ERR_INVALID),                # no queries
+             (_cache(), _query(Sq=8, D=64), L.FQ_ERR_INVALID)]          # q head_dim != the cache's
     for c, q, want in cases:
         assert lib.fq_prefill_int4(c, tail, q, None, 0, None) == want
     # a long prompt without its workspace
