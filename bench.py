@@ -268,6 +268,66 @@ def measured_traffic(L, B, P, retention, select, fused):
     return t.get("hbm_bytes_per_launch")
 
 
+def self_check(cache, dec, mask, k, args):
+    """The timed kernel computes the right thing: its in-kernel selection equals
+    the selection kernel's (split path) bit for bit on every group, and O of
+    every layer agrees with the split path (several workgroups per KV group and
+    a merge launch, a different fp32 order) within the north-star 2e-3."""
+    from flashquest_amd import _lib as L
+    o_fused = dec.O3.clone()
+    smask = torch.zeros_like(mask)
+    with L.attention_splits(4):
+        ref = QuestDecoder(cache["Q"], cache["K_packed"], cache["K_scale"], cache["K_mn"], cache["V_packed"],
+                           cache["V_scale"], cache["V_mn"], retention=args.retention, num_sinks=4, window_pages=2,
+                           k_max_static=k, select_mode=args.select, mask_out=smask)
+        ref()
+    torch.cuda.synchronize()
+    err = (o_fused.float() - ref.O3.float()).abs().max().item()
+    same_sel = bool(torch.equal(mask, smask))
+    if not same_sel or not err <= 2e-3 or not torch.isfinite(o_fused).all():
+        raise RuntimeError(f"bench self-check failed: selection equal={same_sel}, max|O_fused - O_split|={err}")
+    return {"selection_equal_to_split_path": same_sel, "max_abs_O_vs_split_path": err}
+
+
+def config0(args, dev, flush, noop):
+    """one layer, 8k context (128 pages), r = 0.20, the
+    BASELINE layout (fp16 metadata, V in 32-channel groups), batch 1: the
+    whole decode step of one layer (8 KV groups: split over workgroups, the
+    split merge), and the CPU baseline on the same layer."""
+    from oracle import torch_eager as TE
+    c0 = make_cache(1, 1, P=128, dev=dev)
+    k0 = math.ceil(0.2 * 128)
+    m0 = torch.zeros(1, 1, 24, 128, dtype=torch.bool, device=dev)
+    d0 = QuestDecoder(c0["Q"], c0["K_packed"], c0["K_scale"], c0["K_mn"], c0["V_packed"], c0["V_scale"], c0["V_mn"],
+                      retention=0.2, num_sinks=4, window_pages=2, k_max_static=k0, select_mode=args.select,
+                      mask_out=m0)
+    d0()
+    torch.cuda.synchronize()
+    sb, ab, _, _ = step_bytes(c0, m0)
+    d0.mask_out = None
+    ms, _, _ = time_steps(noop, d0, args.steps, args.warmup, flush)
+    out = {"config0_step_us": ms * 1e3, "config0_step_bytes": sb + ab,
+           "config0_step_GBps": (sb + ab) / (ms * 1e-3) / 1e9}
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        prev = torch.get_num_threads()
+        torch.set_num_threads(threads)
+        host = {key: v[0, 0].cpu() for key, v in c0.items()}
+        times = []
+        try:
+            for rep in range(12):
+                t0 = time.perf_counter()
+                TE.decode_layer(host["Q"][:, 0].float(), host["K_packed"], host["K_scale"], host["K_mn"],
+                                host["V_packed"], host["V_scale"], host["V_mn"], retention=0.2, select=args.select)
+                if rep >= 2:
+                    times.append(time.perf_counter() - t0)
+        finally:
+            torch.set_num_threads(prev)
+        out["config0_cpu_baseline_us"] = sorted(times)[len(times) // 2] * 1e6
+        out["config0_cpu_threads"] = threads
+    return out
+
+
 def cpu_baseline(cache, args, n_layers):
     """The reference's eager CPU path restated in PyTorch (oracle/torch_eager.py:
     two fp32 matmuls for the scores, topk + forced pages, fp32 dequant of the
@@ -369,15 +429,17 @@ def main():
     scoring_b, attn_b, attn_kernel_b, union = step_bytes(cache, mask)
     dec.mask_out = None
     noop = lambda: None
+    check = self_check(cache, dec, mask, k, args)
     step_ms, wall, _ = time_steps(noop, dec, args.steps, args.warmup, flush)
     attend_ms, _, attn_ms = time_steps(dec.select, dec.attend, args.steps, args.warmup, flush, kernel_timer=True)
     total_b = scoring_b + attn_b
-    extra = {"union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
+    extra = {"self_check": check, "union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
              "step_GBps": total_b / (step_ms * 1e-3) / 1e9,
              "step_roofline_frac": total_b / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
              "attention_kernel_us": attn_ms * 1e3, "attend_with_split_merge_us": attend_ms * 1e3,
              "select_us": None, "select_mode": args.select}
     if not args.no_extra:
+        extra.update(config0(args, dev, flush, noop))
         ctl = decoder(1.0, P, args.select)
         ctl_ms, _, _ = time_steps(noop, ctl, args.steps, args.warmup, flush)
         full_mask = torch.ones(L, B, Hq, P, dtype=torch.bool, device=dev)
@@ -587,7 +649,10 @@ def main():
     line = {
         "metric": METRIC, "value": step_ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8 MFMA (exact digit split) + fp32", "data": "synthetic",
+        "vs_baseline": None,
+        "dtype": "int4 KV; q.k on int8 MFMA (exact 3-digit split of q*K_scale, int32 accumulate); p.v on fp16 MFMA "
+                 "(p*V_scale rounded to fp16, fp32 accumulate); fp32 softmax",
+        "data": "synthetic",
         "config": {"workload": f"BASELINE config 1: {L} independent layers x batch {B}, {Hq}/8 heads, D=128, "
                                f"{P} pages x 64 tokens, retention {args.retention} ({args.select} top-{k} + 4 sink "
                                "+ 2 window pages), INT4 K/V with fp16 metadata (V per 32 channels), "
