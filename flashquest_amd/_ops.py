@@ -108,6 +108,30 @@ def query(Q3: torch.Tensor, O3: torch.Tensor, lse: torch.Tensor | None, sm_scale
     return q
 
 
+def retention_rows(retention, head_pattern, H_q: int, H_kv: int, layers: int, device):
+    """The retention array of a decode call and its layer stride.
+
+    Without ``head_pattern``: retention_tensor's (H_q,) vector, stride 0.
+    With ``head_pattern`` (H_kv,) or (layers, H_kv) bool (True = retrieval,
+    False = streaming): query heads of streaming KV heads get retention 0, so
+    they keep only the sink and window pages, the others the given retention
+    (llama_persistent_patch.py:214-220, duo/fused_dispatch.py:56-62).  A
+    per-layer pattern gives an (layers, H_q) array with stride H_q.
+    """
+    r = retention_tensor(retention, H_q, device)
+    if head_pattern is None:
+        return r, 0
+    pat = torch.as_tensor(head_pattern)
+    if pat.dtype != torch.bool:
+        raise ValueError(f"head_pattern must be a bool tensor; got {pat.dtype}")
+    if pat.shape not in ((H_kv,), (layers, H_kv)):
+        raise ValueError(f"head_pattern must be ({H_kv},) or ({layers}, {H_kv}) (KV heads, per layer); "
+                         f"got {tuple(pat.shape)}")
+    per_q = pat.to(device).repeat_interleave(H_q // H_kv, dim=-1)
+    rows = torch.where(per_q, r, torch.zeros_like(r)).contiguous()
+    return rows, (H_q if rows.dim() == 2 else 0)
+
+
 def retention_tensor(retention, H: int, device) -> torch.Tensor:
     """selection.py:92-101: scalar in [0, 1] or a (H,) tensor -> device fp32 (H,)."""
     if isinstance(retention, torch.Tensor):

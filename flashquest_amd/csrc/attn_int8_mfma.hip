@@ -133,7 +133,7 @@ void attn_int8_mfma_kernel(Int8Params a) {
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
+        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         score_group_load<MT, NT>(sr, c, tid, l, b, h);
     }
     float qv_raw;

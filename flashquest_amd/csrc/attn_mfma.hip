@@ -208,7 +208,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     uint4 tkr[2], tvr[2];
     const int tail_T = FUSED && a.tail.in_kernel ? a.tail.len : 0;
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
+        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         const TailArgs& t = a.tail;
         const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + h * t.ks[2]) : nullptr;
         const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + h * t.vs[2]) : nullptr;

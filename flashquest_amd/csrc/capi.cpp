@@ -185,6 +185,8 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
     for (int i = 0; i < 4; ++i) { o.q_s[i] = q->q_strides[i]; o.o_s[i] = q->o_strides[i]; }
     for (int i = 0; i < 3; ++i) o.lse_s[i] = q->lse_strides[i];
     o.Hq = q->H_q; o.nrep = nrep;
+    if (q->retention_layer_stride < 0) return fail(FQ_ERR_INVALID, "negative retention layer stride");
+    o.ret_ls = q->retention_layer_stride;
     const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)D);
     o.qk_scale = sm * kLog2e;
     return FQ_OK;

@@ -181,6 +181,7 @@ struct QueryArgs {
     float* lse; int64_t lse_s[3];
     int Hq, nrep;
     float qk_scale;                                 // sm_scale * log2(e)
+    int64_t ret_ls;                                 // retention (L, H_q): layer stride (0: one row for all layers)
 };
 
 // Workspace regions (device pointers) for one decode / attention call.

@@ -237,6 +237,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
 struct GroupSelectParams {
     Workspace ws; int mode, nrep, Hkv, P;
     const float* retention; int num_sinks, window, k_max;
+    int B; int64_t ret_ls;                        // retention row of group g: layer g / (B * Hkv), stride ret_ls
     uint8_t* mask_out;                            // (l, b, h_q, p) contiguous or null
 };
 
@@ -259,16 +260,23 @@ FQ_DEV void finish_group(SelectLds& s, const GroupSelectParams& a, int g) {
     if (tid == 0) a.ws.n_sel[g] = n;
 }
 
+// The retention of group g's query heads: (H_q,) for every layer, or row
+// g / (B * Hkv) of an (L, H_q) array.
+FQ_DEV const float* group_retention(const GroupSelectParams& a, int g) {
+    return a.retention + (int64_t)(g / (a.B * a.Hkv)) * a.ret_ls + (g % a.Hkv) * a.nrep;
+}
+
 // Top-k per query head (row r's keys at keys + r * P) or once per KV head from
 // the summed scores (keys[0..P)), into a cleared s.qmask; then the group tail.
 FQ_DEV void select_group(SelectLds& s, const GroupSelectParams& a, int g, const uint32_t* keys) {
-    const int h = g % a.Hkv, P = a.P;
+    const int P = a.P;
+    const float* ret = group_retention(a, g);
     if (a.mode == FQ_SELECT_PER_Q_HEAD) {
         for (int r = 0; r < a.nrep; ++r)
-            topk_into_qmask(s, keys + r * P, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
+            topk_into_qmask(s, keys + r * P, P, k_for(ret[r], P, a.k_max), (uint8_t)(1u << r));
     } else {
         float rmax = 0.f;
-        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, a.retention[h * a.nrep + r]);
+        for (int r = 0; r < a.nrep; ++r) rmax = fmaxf(rmax, ret[r]);
         topk_into_qmask(s, keys, P, k_for(rmax, P, a.k_max), (uint8_t)((1u << a.nrep) - 1u));
     }
     finish_group(s, a, g);
@@ -282,11 +290,11 @@ __global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectPara
     if (a.mode == FQ_SELECT_PER_Q_HEAD) {
         // one row at a time through s.keys
         __syncthreads();
-        const int h = g % a.Hkv;
+        const float* ret = group_retention(a, g);
         for (int r = 0; r < a.nrep; ++r) {
             for (int i = tid; i < P; i += kThreads) s.keys[i] = sortable_key(sc[r * P + i]);
             __syncthreads();
-            topk_into_qmask(s, s.keys, P, k_for(a.retention[h * a.nrep + r], P, a.k_max), (uint8_t)(1u << r));
+            topk_into_qmask(s, s.keys, P, k_for(ret[r], P, a.k_max), (uint8_t)(1u << r));
         }
         finish_group(s, a, g);
     } else {
@@ -304,11 +312,11 @@ template <int C>
 __global__ __launch_bounds__(kThreads) void select_groups_wave_kernel(GroupSelectParams a, int G) {
     const int g = blockIdx.x * (kThreads / 64) + wave_id();
     if (g >= G) return;                      // whole wave
-    const int h = g % a.Hkv, P = a.P;
+    const int P = a.P;
     int* entries = a.ws.entries + (int64_t)g * P;
     uint8_t* mo = a.mask_out ? a.mask_out + ((int64_t)g * a.nrep) * P : nullptr;
     const int n = wave_select_group<C>(a.ws.scores + (int64_t)g * a.nrep * P, P, a.nrep, a.mode,
-                                       a.retention + h * a.nrep, a.k_max, a.num_sinks, a.window, entries, mo);
+                                       group_retention(a, g), a.k_max, a.num_sinks, a.window, entries, mo);
     if (lane_id() == 0) a.ws.n_sel[g] = n;
 }
 
@@ -442,7 +450,7 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     if (ws) {
         sp.ws = *ws; sp.mode = select_mode; sp.nrep = q.nrep; sp.Hkv = c.Hkv; sp.P = c.P;
         sp.retention = retention; sp.num_sinks = num_sinks; sp.window = window; sp.k_max = k_max;
-        sp.mask_out = mask_out;
+        sp.mask_out = mask_out; sp.B = c.B; sp.ret_ls = q.ret_ls;
     }
     dim3 grid(a.nchunks, G);
 #define FQ_SCORE(D_, MT_, NR_) hipLaunchKernelGGL((score_kernel<D_, MT_, NR_>), grid, dim3(kThreads), 0, st, a)

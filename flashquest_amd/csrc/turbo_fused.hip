@@ -149,7 +149,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[h * NREP + min(L, NREP - 1)];
+        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
     }
     float qv_raw;

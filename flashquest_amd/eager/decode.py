@@ -72,6 +72,7 @@ def quest_decode_int4(
     out: torch.Tensor | None = None,
     K_tail: torch.Tensor | None = None,
     V_tail: torch.Tensor | None = None,
+    head_pattern: torch.Tensor | None = None,
 ):
     """Fused score -> select -> sparse attention over completed pages.
 
@@ -84,6 +85,9 @@ def quest_decode_int4(
     attended with the selected pages (llama_persistent_patch.py:229-240); O and
     lse are then those of the merged attention.  Raises NotImplementedError for
     shapes the fused tail does not take (``sparse_decode_layer`` falls back).
+    ``head_pattern`` (H_kv,) or (L, H_kv) bool: DuoAttention's per-KV-head
+    retrieval (True) / streaming (False) pattern; streaming heads keep only
+    the sink and window pages (llama_persistent_patch.py:214-220).
     Returns (O like Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
     """
     if select_mode not in L.SELECT_MODES:
@@ -104,7 +108,8 @@ def quest_decode_int4(
     if H_q % cache.H_kv:
         raise ValueError(f"H_q={H_q} must be divisible by H_kv={cache.H_kv}")
     query = _ops.query(Q3, O3, lse, sm_scale)
-    r = _ops.retention_tensor(retention, H_q, Q.device)
+    r, query.retention_layer_stride = _ops.retention_rows(retention, head_pattern, H_q, cache.H_kv,
+                                                          Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = None
     if return_selection:
@@ -158,13 +163,14 @@ def quest_decode_int8(
     sm_scale: float | None = None,
     return_lse: bool = True,
     return_selection: bool = False,
+    head_pattern: torch.Tensor | None = None,
 ):
     """The INT8 decode step (llama_persistent_patch.py:143-160 with the
     selection of 196-245): page_scores_int8_fast -> select_pages_vectorized ->
     flash_attn_sparse_fwd over the completed pages, for one layer (Q
     (B,H_q,1,D), 4D cache) or L layers at once (Q (L,B,H_q,1,D), 5D cache).
-    ``select_mode`` as quest_decode_int4.  Returns (O like Q, lse (..., H_q, 1)
-    fp32 or None[, mask (..., H_q, P) bool])."""
+    ``select_mode`` and ``head_pattern`` as quest_decode_int4.  Returns (O like
+    Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool])."""
     if select_mode not in L.SELECT_MODES:
         raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
     L.require_device(Q, K_uint8, K_scale)
@@ -182,7 +188,8 @@ def quest_decode_int8(
     if H_q % cache.H_kv:
         raise ValueError(f"H_q={H_q} must be divisible by H_kv={cache.H_kv}")
     query = _ops.query(Q3, O3, lse, sm_scale)
-    r = _ops.retention_tensor(retention, H_q, Q.device)
+    r, query.retention_layer_stride = _ops.retention_rows(retention, head_pattern, H_q, cache.H_kv,
+                                                          Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device) if return_selection else None
     ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q))
@@ -218,14 +225,16 @@ def quest_decode_turbo(
     sm_scale: float | None = None,
     return_lse: bool = True,
     return_selection: bool = False,
+    head_pattern: torch.Tensor | None = None,
 ):
     """The reference's TurboQuant decode over completed pages, fused: page scores
     from the un-rotated K page metadata (criticality.py:128-163), selection
     (selection.py:65-126), flash_attn_sparse_turbo_fwd (sparse_turbo_fwd.py:254-346).
 
     One layer: Q (B,H_q,1,D) raw basis, cache tensors 4D (B,H_kv,...).  L layers
-    at once: Q (L,B,H_q,1,D), cache tensors 5D.  Returns (O like Q in the raw
-    basis, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
+    at once: Q (L,B,H_q,1,D), cache tensors 5D.  ``head_pattern`` as
+    quest_decode_int4.  Returns (O like Q in the raw basis, lse (..., H_q, 1)
+    fp32 or None[, mask (..., H_q, P) bool]).
     """
     if select_mode not in L.SELECT_MODES:
         raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
@@ -249,7 +258,8 @@ def quest_decode_turbo(
     ksr = K_scale_raw if K_scale_raw.stride(-1) == 1 else K_scale_raw.contiguous()
     kmr = K_mn_raw if K_mn_raw.stride(-1) == 1 else K_mn_raw.contiguous()
     query = _ops.query(Q3, O3, lse, sm_scale)
-    r = _ops.retention_tensor(retention, H_q, Q.device)
+    r, query.retention_layer_stride = _ops.retention_rows(retention, head_pattern, H_q, cache.H_kv,
+                                                          Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = None
     if return_selection:
@@ -280,7 +290,7 @@ class QuestDecoder:
 
     def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
                  window_pages=2, k_max_static=None, page_size=64, select_mode="per_q_head", sm_scale=None,
-                 out=None, lse=None, mask_out=None, K_tail=None, V_tail=None):
+                 out=None, lse=None, mask_out=None, K_tail=None, V_tail=None, head_pattern=None):
         if select_mode not in L.SELECT_MODES:
             raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
         self.Q3 = Q[..., 0, :]
@@ -290,7 +300,8 @@ class QuestDecoder:
         self.query = _ops.query(self.Q3, self.O3, lse, sm_scale)
         H_q = self.Q3.shape[-2]
         P = K_scale.shape[-2]
-        self.r = _ops.retention_tensor(retention, H_q, Q.device)
+        self.r, self.query.retention_layer_stride = _ops.retention_rows(
+            retention, head_pattern, H_q, self.cache.H_kv, self.Q3.shape[0] if self.Q3.dim() == 4 else 1, Q.device)
         self.k_max = -1 if k_max_static is None else min(int(k_max_static), P)
         self.sinks, self.window = int(num_sinks), int(window_pages)
         self.mode = L.SELECT_MODES[select_mode]
@@ -338,13 +349,16 @@ class QuestDecoder:
 
 
 def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: int, window_pages: int,
-                        page_size: int, k_max_static: int | None = None, select_mode: str = "per_q_head"):
+                        page_size: int, k_max_static: int | None = None, select_mode: str = "per_q_head",
+                        head_pattern: torch.Tensor | None = None):
     """The decode branch of llama_persistent_patch.py:202-245 for one layer.
 
     ``views`` is get_views(layer) of a persistent INT4, INT8 or TurboQuant
     cache (persistent_int4.py:134-159, persistent_int8.py:137-169,
     persistent_turbo.py:149-176); the family follows from its keys, as the
     reference's kv_bits dispatch (llama_persistent_patch.py:74-163).
+    ``head_pattern`` (H_kv,) bool: the layer's DuoAttention pattern
+    (head_pattern_layer, llama_persistent_patch.py:214-220).
     Returns attention output (B, H_q, 1, D) in q's dtype.
     """
     completed = views["completed_len"]
@@ -353,7 +367,7 @@ def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: i
         o, _ = bf16_dense_attn_with_lse(q, views["K_partial"], views["V_partial"])
         return o.to(q.dtype)
     kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
-              page_size=page_size, select_mode=select_mode)
+              page_size=page_size, select_mode=select_mode, head_pattern=head_pattern)
     if "K_uint8" in views:                    # INT8 (kv_bits 8)
         o_sparse, lse_sparse = quest_decode_int8(q, views["K_uint8"], views["K_scale"], views["K_mn"],
                                                  views["V_uint8"], views["V_scale"], views["V_mn"], **kw)

@@ -85,6 +85,10 @@ typedef struct fq_query {
     float* lse;      int64_t lse_strides[3];  /* may be NULL (return_lse=False) */
     int32_t H_q;
     float sm_scale;  /* <= 0 selects 1/sqrt(D) (sparse_int4_fwd.py:206-207) */
+    /* Decode entries that select pages: the retention array is (H_q,) for
+     * every layer (0), or (L, H_q) with this layer stride (H_q or more), e.g.
+     * a DuoAttention head pattern per layer (llama_persistent_patch.py:214-220). */
+    int64_t retention_layer_stride;
 } fq_query;
 
 /* TurboQuant K3-V3 cache (persistent_turbo.py:55-73):
