@@ -30,7 +30,7 @@ from flashquest_amd._lib import KernelTimer  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import (quantize_k, quantize_k_int4, quantize_k_turbo, quantize_v,  # noqa: E402
                                             quantize_v_int4, quantize_v_turbo)
-from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402
+from flashquest_amd.kernel.wht import wht_along_head_dim  # noqa: E402  (rotated caches, config 3)
 
 METRIC = "decode-attn µs/step (28 layers, 32k, sparse INT4) + achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
@@ -505,29 +505,26 @@ def main():
         extra["step_us_after_write_flush"] = wf_ms * 1e3
         del wflush
 
-        # rotated INT4 (K, V rotated by WHT(signs * x) before
-        # quantisation).  The step rotates Q, decodes, and rotates O back.
+        # rotated INT4 (K, V rotated by x -> WHT(s x) / sqrt(128)
+        # before quantisation).  The single launch rotates Q in its prologue and
+        # O back in its store.
         signs = rotation_signs(dev=dev)
         rc = make_cache(L, B, P=P, dev=dev, signs=signs)
-        q_raw = rc["Q"].clone()
-        rmask = torch.zeros(L, B, Hq, P, dtype=torch.bool, device=dev)
-        wht_along_head_dim(q_raw, signs=signs, out=rc["Q"])
-        rdec = decoder(args.retention, k, args.select, c=rc, mask=rmask)
-        rdec()
+        from flashquest_amd.eager.decode import quest_decode_int4
+        rplanes = [rc[x] for x in ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")]
+        _, _, rmask = quest_decode_int4(rc["Q"], *rplanes, retention=args.retention, num_sinks=4, window_pages=2,
+                                        k_max_static=k, select_mode=args.select, return_selection=True,
+                                        rotation_signs=signs)      # the kernel's own selection, as a mask
+        rdec = QuestDecoder(rc["Q"], *rplanes, retention=args.retention, num_sinks=4, window_pages=2,
+                            k_max_static=k, select_mode=args.select, rotation_signs=signs)
         torch.cuda.synchronize()
         rs_b, ra_b, _, _ = step_bytes(rc, rmask)
-        rdec.mask_out = None
-        o_raw = torch.empty_like(rdec.O3)
-
-        def rot_step():
-            wht_along_head_dim(q_raw, signs=signs, out=rc["Q"])                  # Q_rot = WHT(s * Q)
-            rdec()
-            wht_along_head_dim(rdec.O3, signs=signs, inverse=True, out=o_raw)    # O = s * WHT(O_rot)
-
-        r_ms, _, _ = time_steps(noop, rot_step, args.steps, args.warmup, flush)
-        extra.update({"config3_rotated_us": r_ms * 1e3, "config3_step_GBps": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9,
-                      "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
-        del rc, rdec, q_raw, o_raw, rmask
+        r_ms, _, _ = time_steps(noop, rdec, args.steps, args.warmup, flush)
+        extra.update({"config3_rotated_us": r_ms * 1e3, "config3_fused": rdec.fused,
+                      "config3_step_GBps": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9,
+                      "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                      "config3_over_config1": r_ms / step_ms})
+        del rc, rdec, rmask
 
         # TurboQuant K3-V3 (the reference's kv_bits == 3 path) over all layers:
         # the fused decode (scores from the raw K page metadata, selection,

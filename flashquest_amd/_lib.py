@@ -48,7 +48,7 @@ class Query(ctypes.Structure):
         ("out", ctypes.c_void_p), ("out_dtype", ctypes.c_int32), ("o_strides", _I64x4),
         ("lse", ctypes.c_void_p), ("lse_strides", _I64x3),
         ("H_q", ctypes.c_int32), ("sm_scale", ctypes.c_float),
-        ("retention_layer_stride", ctypes.c_int64),
+        ("retention_layer_stride", ctypes.c_int64), ("rotation_signs", ctypes.c_void_p),
     ]
 
 

@@ -60,14 +60,15 @@ FQ_DEV void store_outputs(const QueryArgs& q, int l, int b, int h, const float (
                           const float* Ms) {
     const int tid = threadIdx.x;
     const float inv = 1.0f / sqrtf((float)D);
-    if constexpr (ROT && D == 128) {        // one wave per head
+    if (D == 128 && (ROT || q.rot)) {       // one wave per head; q.rot: then times the signs, s WHT(O) / sqrt(D)
         const int lane = lane_id();
+        const float s0 = q.rot ? q.rot[lane] : 1.f, s1 = q.rot ? q.rot[lane + 64] : 1.f;
         for (int r = wave_id(); r < NREP; r += NT / 64) {
             float v0 = vals[r][lane], v1 = vals[r][lane + 64];
             wave_hadamard128(v0, v1);
             const int64_t ob = l * q.o_s[0] + b * q.o_s[1] + (h * NREP + r) * q.o_s[2];
-            store_any(q.out, q.out_dtype, ob + lane * q.o_s[3], v0 * inv);
-            store_any(q.out, q.out_dtype, ob + (lane + 64) * q.o_s[3], v1 * inv);
+            store_any(q.out, q.out_dtype, ob + lane * q.o_s[3], v0 * inv * s0);
+            store_any(q.out, q.out_dtype, ob + (lane + 64) * q.o_s[3], v1 * inv * s1);
         }
     } else
     for (int i = tid; i < NREP * D; i += NT) {

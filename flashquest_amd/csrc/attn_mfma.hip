@@ -189,7 +189,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // Needs 16-bit q with unit channel stride and 16-byte aligned rows; other
     // layouts (q_fast false: an empty buffer, the loads read 0) go through LDS.
     uint4 qsr[NREP];
-    const bool q_fast = FUSED && !q32 && q.q_s[3] == 1 && (q.q_s[2] & 7) == 0 &&
+    const bool q_fast = FUSED && !q32 && !q.rot && q.q_s[3] == 1 && (q.q_s[2] & 7) == 0 &&
                         (((uintptr_t)q.q + 2 * (uint64_t)qb) & 15) == 0;
     if constexpr (FUSED) {
         const auto rq = make_rsrc((const char*)q.q + 2 * qb, q_fast ? 2 * ((int64_t)(NREP - 1) * q.q_s[2] + D) : 0);
@@ -303,6 +303,20 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 else score_group_regs_q<MT, NREP, NT, false>(sr, qin, s_key, tid, c.P);
             } else {
                 __syncthreads();
+                if (q.rot) {       // uniform: wave r rotates head r, q -> WHT(s q) / sqrt(D), in fp32
+                    if (w < NREP) {
+                        float x0 = s_qraw[w][L] * q.rot[L], x1 = s_qraw[w][L + 64] * q.rot[L + 64];
+                        wave_hadamard128(x0, x1);
+                        const float inv = 1.0f / sqrtf((float)D);
+                        x0 *= inv;
+                        x1 *= inv;
+                        s_qraw[w][L] = x0;
+                        s_qraw[w][L + 64] = x1;
+                        s_q[w][L] = x0 * q.qk_scale;
+                        s_q[w][L + 64] = x1 * q.qk_scale;
+                    }
+                    __syncthreads();
+                }
                 if (sum) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
                 else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
             }

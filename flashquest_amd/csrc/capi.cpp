@@ -187,6 +187,8 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
     o.Hq = q->H_q; o.nrep = nrep;
     if (q->retention_layer_stride < 0) return fail(FQ_ERR_INVALID, "negative retention layer stride");
     o.ret_ls = q->retention_layer_stride;
+    o.rot = q->rotation_signs;
+    if (o.rot && D != 128) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode takes head_dim 128");
     const float sm = q->sm_scale > 0.f ? q->sm_scale : 1.0f / sqrtf((float)D);
     o.qk_scale = sm * kLog2e;
     return FQ_OK;
@@ -338,6 +340,7 @@ static int attn_common(const fq_int4_cache* cache, const fq_query* query, void* 
     st = check_query(query, c->D, c->Hkv, q);
     if (st) return st;
     if (((uintptr_t)q->q) & 1) return fail(FQ_ERR_UNSUPPORTED, "query must be 2-byte aligned");
+    if (q->rot && bits == 8) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode is INT4 only");
     const int G = c->L * c->B * c->Hkv;
     const size_t need = workspace_bytes(G, c->P, q->nrep, q->nrep, c->D);
     if (!workspace || workspace_bytes_ < need)
@@ -356,6 +359,7 @@ static int sparse_fwd_mask(const fq_int4_cache* cache, const fq_query* query, co
     int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws, bits);
     if (st) return st;
     if (!mask) return fail(FQ_ERR_INVALID, "selection mask is NULL");
+    if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "rotation is a decode-step option (fq_quest_decode_int4)");
     hipStream_t s = (hipStream_t)stream;
     st = hip_status(launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, q.nrep, c.P, ws, s), "page union");
     if (st) return st;
@@ -384,6 +388,7 @@ int fq_sparse_int4_fwd_ids(const fq_int4_cache* cache, const fq_query* query, co
     int st = attn_common(cache, query, workspace, workspace_bytes_, &c, &q, &ws);
     if (st) return st;
     if (!ids || bucket < 1) return fail(FQ_ERR_INVALID, "page id list is NULL or empty");
+    if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "rotation is a decode-step option (fq_quest_decode_int4)");
     hipStream_t s = (hipStream_t)stream;
     st = hip_status(launch_union_from_ids(ids, id_strides, bucket, c.L, c.B, c.Hkv, q.nrep, c.P, ws, s),
                     "page union");
@@ -438,6 +443,9 @@ static int quest_select(const fq_int4_cache* cache, const fq_query* query, const
     if ((!mask_out || mask_from_attention) && !sc_user &&
         decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws))
         return FQ_OK;
+    if (q.rot)
+        return fail(FQ_ERR_UNSUPPORTED, "the rotated decode runs as the single-launch kernel only (enough KV groups to "
+                                        "fill the GPU, no score output)");
     return hip_status(launch_score(c, q, 1, q4, sc_user, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                    k_max, mask_out, (hipStream_t)stream),
                       "score+select");
@@ -469,6 +477,8 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     if (tail && tail->len > 0 && !mfma_supported(c, q, al))
         return fail(FQ_ERR_UNSUPPORTED, "the fused tail needs the matrix-core attention layout");
     SelectArgs sel{};
+    if (q.rot && !attn_selects_in_kernel(c, q, al))
+        return fail(FQ_ERR_UNSUPPORTED, "the rotated decode runs as the single-launch kernel only");
     if (attn_selects_in_kernel(c, q, al)) {
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
@@ -766,6 +776,7 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
     QueryArgs q{};
     int st = check_query(query, cache->D, cache->H_kv, &q);
     if (st) return st;
+    if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode is INT4 only");
     const int G = cache->L * cache->B * cache->H_kv;
     const size_t need = workspace_bytes(G, cache->P, q.nrep, q.nrep, cache->D);
     if (!workspace || workspace_bytes_ < need)
@@ -800,6 +811,7 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     QueryArgs q{};
     int st = check_query(query, cache->D, cache->H_kv, &q);
     if (st) return st;
+    if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode is INT4 only");
     if (((uintptr_t)q.q) & 1) return fail(FQ_ERR_UNSUPPORTED, "query must be 2-byte aligned");
     // the raw page metadata as an INT4 cache descriptor (scoring reads only K scale/min)
     if (!k_scale_raw || !k_mn_raw) return fail(FQ_ERR_INVALID, "NULL raw K metadata");

@@ -182,6 +182,7 @@ struct QueryArgs {
     int Hq, nrep;
     float qk_scale;                                 // sm_scale * log2(e)
     int64_t ret_ls;                                 // retention (L, H_q): layer stride (0: one row for all layers)
+    const float* rot;                               // (D,) signs s: q -> WHT(s q) / sqrt(D), O -> s WHT(O) / sqrt(D); or null
 };
 
 // Workspace regions (device pointers) for one decode / attention call.

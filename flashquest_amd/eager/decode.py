@@ -73,6 +73,8 @@ def quest_decode_int4(
     K_tail: torch.Tensor | None = None,
     V_tail: torch.Tensor | None = None,
     head_pattern: torch.Tensor | None = None,
+    rotation_signs: torch.Tensor | None = None,
+    _rotation: torch.Tensor | None = None,
 ):
     """Fused score -> select -> sparse attention over completed pages.
 
@@ -88,6 +90,12 @@ def quest_decode_int4(
     ``head_pattern`` (H_kv,) or (L, H_kv) bool: DuoAttention's per-KV-head
     retrieval (True) / streaming (False) pattern; streaming heads keep only
     the sink and window pages (llama_persistent_patch.py:214-220).
+    ``rotation_signs`` (D,) +-1 (no reference function): the
+    cache holds K and V rotated by x -> WHT(s x) / sqrt(D); Q is rotated the
+    same way (fp32) before scoring and attention and O rotated back,
+    O = s WHT(O_rot) / sqrt(D), lse unchanged (the rotation is orthogonal).
+    The single-launch kernel does both in its prologue and epilogue; calls
+    that take the split path rotate with fq_wht (fp32) around the step.
     Returns (O like Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool]).
     """
     if select_mode not in L.SELECT_MODES:
@@ -95,6 +103,12 @@ def quest_decode_int4(
     L.require_device(Q, K_packed, K_scale)
     if Q.shape[-2] != 1:
         raise NotImplementedError(f"quest_decode_int4: decode-only (S_q={Q.shape[-2]})")
+    if rotation_signs is not None:
+        return _rotated_decode(Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), rotation_signs, out,
+                               dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
+                                    k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
+                                    sm_scale=sm_scale, return_lse=return_lse, return_selection=return_selection,
+                                    K_tail=K_tail, V_tail=V_tail, head_pattern=head_pattern))
     D = Q.shape[-1]
     if D not in (64, 128):
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
@@ -110,6 +124,7 @@ def quest_decode_int4(
     query = _ops.query(Q3, O3, lse, sm_scale)
     r, query.retention_layer_stride = _ops.retention_rows(retention, head_pattern, H_q, cache.H_kv,
                                                           Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
+    query.rotation_signs = None if _rotation is None else _rotation.data_ptr()
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = None
     if return_selection:
@@ -143,6 +158,38 @@ def quest_decode_int4(
     if return_selection:
         return O, lse_out, mask
     return O, lse_out
+
+
+def _signs(rotation_signs, D, device):
+    s = rotation_signs.to(device=device, dtype=torch.float32).contiguous()
+    if s.shape != (D,) or not bool(((s == 1) | (s == -1)).all()):
+        raise ValueError(f"rotation_signs must be a ({D},) vector of +-1")
+    return s
+
+
+def _rotated_decode(Q, planes, rotation_signs, out, kw):
+    """quest_decode_int4 with rotation_signs: the kernel's own rotation when
+    the step is one launch, else fq_wht in fp32 around the split-path step."""
+    from ..kernel.wht import wht_along_head_dim
+    D = Q.shape[-1]
+    if D != 128:
+        raise NotImplementedError("the rotated decode takes head_dim 128")
+    signs = _signs(rotation_signs, D, Q.device)
+    Q3 = Q[..., 0, :]
+    cache, keep = _ops.int4_cache(*planes, kw["page_size"])
+    probe = _ops.query(Q3, Q3, None, None)
+    k_max = -1 if kw["k_max_static"] is None else min(int(kw["k_max_static"]), planes[1].shape[-2])
+    fused = L.lib().fq_quest_fused_int4(cache, probe, int(kw["num_sinks"]), int(kw["window_pages"]), k_max,
+                                        L.SELECT_MODES[kw["select_mode"]]) == 1
+    if fused:
+        return quest_decode_int4(Q, *planes, out=out, _rotation=signs, **kw)
+    q_rot = wht_along_head_dim(Q.float(), signs=signs)            # fp32 in, fp32 butterflies
+    res = quest_decode_int4(q_rot, *planes, **kw)
+    o = wht_along_head_dim(res[0], signs=signs, inverse=True).to(Q.dtype)
+    if out is not None:
+        out.copy_(o)
+        o = out
+    return (o,) + tuple(res[1:])
 
 
 def quest_decode_int8(
@@ -290,7 +337,8 @@ class QuestDecoder:
 
     def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
                  window_pages=2, k_max_static=None, page_size=64, select_mode="per_q_head", sm_scale=None,
-                 out=None, lse=None, mask_out=None, K_tail=None, V_tail=None, head_pattern=None):
+                 out=None, lse=None, mask_out=None, K_tail=None, V_tail=None, head_pattern=None,
+                 rotation_signs=None):
         if select_mode not in L.SELECT_MODES:
             raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
         self.Q3 = Q[..., 0, :]
@@ -300,6 +348,8 @@ class QuestDecoder:
         self.query = _ops.query(self.Q3, self.O3, lse, sm_scale)
         H_q = self.Q3.shape[-2]
         P = K_scale.shape[-2]
+        self._signs = None if rotation_signs is None else _signs(rotation_signs, self.Q3.shape[-1], Q.device)
+        self.query.rotation_signs = None if self._signs is None else self._signs.data_ptr()
         self.r, self.query.retention_layer_stride = _ops.retention_rows(
             retention, head_pattern, H_q, self.cache.H_kv, self.Q3.shape[0] if self.Q3.dim() == 4 else 1, Q.device)
         self.k_max = -1 if k_max_static is None else min(int(k_max_static), P)

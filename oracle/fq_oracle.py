@@ -817,6 +817,13 @@ def rotate_signed(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
     return (np.asarray(x, np.float64) * signs) @ hadamard_matrix(D).T
 
 
+def rotate_signed_f32(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """The rotated decode's fp32 rotation of Q (config 3): WHT(s * x) with every
+    butterfly rounded to fp32 (h = 1, 2, ..., D/2), then times fp32(1/sqrt(D)).
+    s * x is exact; ``wht`` restates the butterflies."""
+    return wht(np.asarray(x, F32) * np.asarray(signs, F32), "f32")
+
+
 def unrotate_signed(y: np.ndarray, signs: np.ndarray) -> np.ndarray:
     """Inverse of ``rotate_signed``: s * WHT(y)."""
     D = y.shape[-1]

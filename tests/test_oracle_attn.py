@@ -185,3 +185,20 @@ def test_torch_eager_baseline_matches_oracle():
         out = TE.decode_layer(t(Q[0]), t(kp[0]), t(ks[0]).half(), t(km[0]).half(), t(vp[0]), t(vs[0]).half(),
                               t(vm[0]).half(), retention=0.25, select=mode)
         assert float((out - t(ref[0])).abs().max()) < 1e-5
+
+
+def test_fp32_rotation_of_the_rotated_decode():
+    # rotate_signed_f32 (the kernel's fp32 butterflies) agrees with the exact
+    # rotation to fp32 rounding, is exact on a signed basis vector (one
+    # Hadamard column / sqrt(128)), and its inverse recovers the input
+    rng = np.random.default_rng(9)
+    s = O.random_signs(3)
+    x = rng.standard_normal((5, 128)).astype(np.float32)
+    r = O.rotate_signed_f32(x, s)
+    assert r.dtype == np.float32
+    assert np.abs(r - O.rotate_signed(x, s)).max() <= 1e-5 * np.abs(x).sum(-1).max()
+    e = np.zeros(128, np.float32)
+    e[37] = 1.0
+    col = O.rotate_signed_f32(e, s)
+    assert np.array_equal(np.abs(col), np.full(128, np.float32(1.0) / np.float32(np.sqrt(128)), np.float32))
+    assert np.allclose(O.unrotate_signed(r, s), x, atol=1e-5)
