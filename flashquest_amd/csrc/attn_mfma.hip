@@ -200,6 +200,9 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // retention of query head L of the group (lanes past NREP repeat the last)
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
+    ScoreRowRegs<NREP, NT> srow;        // kSelectOnly: the group's precomputed scores
+    const bool from_scores = FUSED && a.sel.enabled == kSelectOnly;
+    const int score_rows = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
     // Partial-page tail (fused kernel, tail.in_kernel): its <= 64 raw 16-bit
     // K / V rows go to LDS with q, before scoring needs the metadata.  The
     // loads are unconditional: without a tail the buffer is empty and they read 0.
@@ -220,7 +223,8 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             tkr[u] = ld128(rk, (int)(2 * tt * t.ks[3]) + 16 * j);
             tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
         }
-        score_group_load<MT, NT>(sr, c, tid, l, b, h);
+        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        else score_group_load<MT, NT>(sr, c, tid, l, b, h);
     }
     const bool qbf = q.q_dtype == FQ_BF16;
     auto q_float = [&](uint32_t u) {
@@ -288,7 +292,9 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 *(uint4*)&s_tv[i >> 4][8 * (i & 15)] = tvr[u];
             }
             const bool sum = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM;
-            if (q_fast) {      // uniform
+            if (from_scores) {     // uniform: a scoring launch wrote the group's scores (never with q.rot)
+                scores_to_keys<NREP, NT>(srow, s_key, score_rows, c.P, tid);
+            } else if (q_fast) {      // uniform
                 float qin[NREP][8];
 #pragma unroll
                 for (int r = 0; r < NREP; ++r) {

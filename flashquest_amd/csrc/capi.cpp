@@ -420,6 +420,14 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
     return attn_selects_in_kernel(c, q, al);
 }
 
+// Decode steps that split KV groups over several workgroups (too few groups
+// to fill the GPU) score each group once in a scoring launch over all CUs; the
+// attention workgroups then select from those scores (kSelectOnly) instead of
+// each re-scoring the group's pages.  INT4, unrotated.
+static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q) {
+    return c.L * c.B * c.Hkv < 192 && !q.rot && c.bits != 8;
+}
+
 static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
@@ -441,8 +449,12 @@ static int quest_select(const fq_int4_cache* cache, const fq_query* query, const
     // the fused attention kernel selects for itself (and, when the whole step
     // is one call, writes the mask too)
     if ((!mask_out || mask_from_attention) && !sc_user &&
-        decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws))
-        return FQ_OK;
+        decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws)) {
+        if (!attend_from_scores(c, q)) return FQ_OK;      // the attention kernel scores too
+        return hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks,
+                                       window_pages, k_max, nullptr, (hipStream_t)stream, false),
+                          "page scores");
+    }
     if (q.rot)
         return fail(FQ_ERR_UNSUPPORTED, "the rotated decode runs as the single-launch kernel only (enough KV groups to "
                                         "fill the GPU, no score output)");
@@ -481,7 +493,8 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
         return fail(FQ_ERR_UNSUPPORTED, "the rotated decode runs as the single-launch kernel only");
     if (attn_selects_in_kernel(c, q, al)) {
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
-        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
+        sel.k_max = k_max; sel.mode = select_mode; sel.mask_out = mask_out;
+        sel.enabled = attend_from_scores(c, q) ? kSelectOnly : kScoreSelect;
     }
     return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail),
                       bits == 8 ? "sparse int8 attention" : "sparse int4 attention");

@@ -211,6 +211,7 @@ struct Workspace {
 // enabled: 0 = pages from the workspace lists, kScoreSelect = the attention
 // kernel scores and selects the pages itself (one launch per decode step).
 constexpr int kScoreSelect = 2;
+constexpr int kSelectOnly = 1;        // the attention kernel selects from scores a scoring launch wrote to the workspace
 struct SelectArgs {
     const float* retention;
     int num_sinks, window, k_max, mode;
@@ -241,7 +242,7 @@ AttnLaunch choose_split(int G, int max_entries, int s_max);
 hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const int64_t* q4_s,
                         float* scores, const int64_t* sc4_s, const Workspace* ws, int select_mode,
                         const float* retention, int num_sinks, int window, int k_max,
-                        uint8_t* mask_out, hipStream_t st);
+                        uint8_t* mask_out, hipStream_t st, bool select_groups = true);
 hipError_t launch_select_rows(const float* scores, const int64_t* sc_s, int B, int H, int S_q, int P,
                               const float* retention, int num_sinks, int window, int k_max,
                               uint8_t* mask, const int64_t* m_s, hipStream_t st);

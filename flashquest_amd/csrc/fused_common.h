@@ -71,6 +71,32 @@ FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int
     }
 }
 
+// Precomputed scores of one KV group (the workspace rows of score_kernel:
+// `rows` rows of P fp32 scores) as the sortable keys of the in-kernel
+// selection: s_key[r * 64 kSelC + p], 0 (below every score) for p >= P.
+// scores_load issues the loads; scores_to_keys converts after they land.
+template <int NREP, int NT>
+struct ScoreRowRegs {
+    static constexpr int kN = (NREP * 64 * kSelC + NT - 1) / NT;
+    float v[kN];
+};
+template <int NREP, int NT>
+FQ_DEV void scores_load(ScoreRowRegs<NREP, NT>& sr, const float* g_scores, int rows, int P, int tid) {
+#pragma unroll
+    for (int u = 0; u < ScoreRowRegs<NREP, NT>::kN; ++u) {
+        const int i = tid + u * NT, r = i / (64 * kSelC), p = i % (64 * kSelC);
+        sr.v[u] = g_scores[min(r, rows - 1) * P + min(p, P - 1)];
+    }
+}
+template <int NREP, int NT>
+FQ_DEV void scores_to_keys(const ScoreRowRegs<NREP, NT>& sr, uint32_t* s_key, int rows, int P, int tid) {
+#pragma unroll
+    for (int u = 0; u < ScoreRowRegs<NREP, NT>::kN; ++u) {
+        const int i = tid + u * NT, r = i / (64 * kSelC), p = i % (64 * kSelC);
+        if (r < rows) s_key[i] = p < P ? sortable_key(sr.v[u]) : 0u;
+    }
+}
+
 // qin[r][j]: query head r's raw value at channel 8 * (tid & 15) + j.
 template <typename MT, int NREP, int NT, bool SUM>
 FQ_DEV void score_group_regs_q(const ScoreRegs<NT>& sr, const float (&qin)[NREP][8], uint32_t* s_key, int tid, int P,

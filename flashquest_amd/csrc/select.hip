@@ -423,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void union_from_ids_kernel(UnionParams a)
 hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const int64_t* q4_s,
                         float* scores, const int64_t* sc4_s, const Workspace* ws, int select_mode,
                         const float* retention, int num_sinks, int window, int k_max,
-                        uint8_t* mask_out, hipStream_t st) {
+                        uint8_t* mask_out, hipStream_t st, bool select_groups) {
     ScoreParams a{};
     a.c = c;
     a.q = q.q; a.q_dtype = q.q_dtype;
@@ -470,7 +470,7 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
 #undef FQ_SCORE_NR
 #undef FQ_SCORE
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !ws) return e;
+    if (e != hipSuccess || !ws || !select_groups) return e;
     const dim3 wgrid((G + kThreads / 64 - 1) / (kThreads / 64));
     if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, wgrid, dim3(kThreads), 0, st, sp, G);
     else if (c.P <= 64 * 32) hipLaunchKernelGGL(select_groups_wave_kernel<32>, wgrid, dim3(kThreads), 0, st, sp, G);
