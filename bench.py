@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from flashquest_amd._lib import KernelTimer  # noqa: E402
+from flashquest_amd._ops import read_decode_pages  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import (quantize_k, quantize_k_int4, quantize_k_turbo, quantize_v,  # noqa: E402
                                             quantize_v_int4, quantize_v_turbo)
@@ -433,11 +434,16 @@ def main():
     step_ms, wall, _ = time_steps(noop, dec, args.steps, args.warmup, flush)
     attend_ms, _, attn_ms = time_steps(dec.select, dec.attend, args.steps, args.warmup, flush, kernel_timer=True)
     total_b = scoring_b + attn_b
+    # the access pattern's ceiling: the same bytes read in the same order with no compute
+    planes = [cache[x] for x in ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")]
+    rd_ms, _, _ = time_steps(noop, lambda: read_decode_pages(*planes, mask), args.steps, args.warmup, flush)
     extra = {"self_check": check, "union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
              "step_GBps": total_b / (step_ms * 1e-3) / 1e9,
              "step_roofline_frac": total_b / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
              "attention_kernel_us": attn_ms * 1e3, "attend_with_split_merge_us": attend_ms * 1e3,
-             "select_us": None, "select_mode": args.select}
+             "select_us": None, "select_mode": args.select,
+             # event time of the probe call: the union-list launch plus the read-only kernel
+             "read_only_pass_with_union_us": rd_ms * 1e3, "step_over_read_only_pass": step_ms / rd_ms}
     if not args.no_extra:
         extra.update(config0(args, dev, flush, noop))
         ctl = decoder(1.0, P, args.select)

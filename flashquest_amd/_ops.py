@@ -141,3 +141,21 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
     if not (0.0 <= float(retention) <= 1.0):
         raise ValueError(f"scalar retention must be in [0, 1]; got {retention}")
     return torch.full((H,), float(retention), dtype=torch.float32, device=device)
+
+
+def read_decode_pages(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask: torch.Tensor,
+                      page_size: int = 64) -> None:
+    """Measurement only (no counterpart in the reference): read exactly the
+    bytes a single-launch INT4 decode step reads for the selection ``mask``
+    (L, B, H_q, P), in the same order, and compute nothing.  Its time is the
+    memory system's ceiling for the step's access pattern."""
+    c, keep = int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size)
+    L.require_device(mask, *keep)
+    if mask.dtype != torch.bool or mask.dim() != 4:
+        raise ValueError(f"mask must be a 4D (L, B, H_q, P) bool tensor, got {mask.dtype} {tuple(mask.shape)}")
+    H_q = mask.shape[2]
+    ws = L.workspace(mask.device, L.lib().fq_workspace_bytes(c, H_q))
+    sink = torch.zeros(1, dtype=torch.int32, device=mask.device)
+    L.check(L.lib().fq_read_decode_pages(c, mask.data_ptr(), L.strides(mask, 4), H_q, sink.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), L.stream_handle(mask.device)),
+            "read_decode_pages")

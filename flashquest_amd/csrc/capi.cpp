@@ -1015,4 +1015,27 @@ int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* que
                                 mask_out, ws, (size_t)FQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
+int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
+                         int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+    Int4Cache c{};
+    int st = check_cache(cache, &c);
+    if (st) return st;
+    if (H_q < 1 || H_q % c.Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, c.Hkv);
+    if (c.D != 128 || c.page != 64 || (c.G != 1 && c.G != 4))
+        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes the matrix-core decode's layout");
+    if (c.kp_s[3] != 64 || c.vp_s[3] != 64 || c.ksc_s[3] != 128 || c.kmn_s[3] != 128 || c.vsc_s[3] != c.G ||
+        c.vmn_s[3] != c.G)
+        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes packed token / page rows");
+    if (!mask || !sink) return fail(FQ_ERR_INVALID, "NULL mask or sink");
+    const int G = c.L * c.B * c.Hkv, nrep = H_q / c.Hkv;
+    const size_t need = workspace_bytes(G, c.P, nrep, nrep, c.D);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
+    Workspace ws = carve_workspace(workspace, G, c.P, nrep, nrep, c.D);
+    hipStream_t s = (hipStream_t)stream;
+    st = hip_status(launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, nrep, c.P, ws, s), "page union");
+    if (st) return st;
+    return hip_status(launch_read_step(c, ws, sink, s), "read decode pages");
+}
+
 }  // extern "C"

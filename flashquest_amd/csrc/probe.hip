@@ -1,0 +1,79 @@
+// The memory-system ceiling of the decode step's access pattern: a kernel
+// that reads exactly the bytes the single-launch INT4 decode reads, in the
+// same order and granularity, and computes nothing.  One workgroup of 8 waves
+// per KV group streams the K scale / min of every page (the scoring
+// metadata, 16 bytes per lane and load), then its waves take the group's
+// selected pages w, w + 8, ... and read each page's K and V codes, V scale /
+// min and K scale / min.  Measurement only: bench.py times it beside the
+// decode, so the gap between the two is what scoring, selection and the
+// attention math add.  Every loaded word is folded into a value that is
+// stored only if it hits an unlikely constant, so no load is dead.
+#include "fused_common.h"
+
+namespace fq {
+namespace {
+
+template <int G>
+__global__ __launch_bounds__(512) void read_step_kernel(Int4Cache c, Workspace ws, unsigned* sink) {
+    constexpr int NT = 512, NW = 8;
+    const int g = blockIdx.x, tid = threadIdx.x, lane = lane_id(), w = wave_id();
+    const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
+    const char* ks = (const char*)((const uint16_t*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2]);
+    const char* km = (const char*)((const uint16_t*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2]);
+    uint32_t acc = 0;
+    // scoring metadata: P pages x 256 bytes of K scale and of K min
+    {
+        const int n16 = c.P * 16;                  // 16-byte chunks per tensor
+        for (int i = tid; i < n16; i += 4 * NT) {
+            uint4 x[8];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = min(i + u * NT, n16 - 1);
+                x[2 * u] = *(const uint4*)(ks + (int64_t)j * 16);
+                x[2 * u + 1] = *(const uint4*)(km + (int64_t)j * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc ^= x[u].x ^ x[u].w;
+        }
+    }
+    __syncthreads();
+    const uint8_t* kp = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
+    const uint8_t* vp = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
+    const char* vs = (const char*)((const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2]);
+    const char* vm = (const char*)((const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2]);
+    const int n = ws.n_sel[g];
+    for (int i = w; i < n; i += NW) {
+        const int p = ws.entries[(int64_t)g * c.P + i] & 0xFFFF;
+        const int64_t t0 = (int64_t)p * 64;
+        uint4 a[4], v[4];
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            a[T] = *(const uint4*)(kp + t0 * 64 + T * 1024 + lane * 16);
+            v[T] = *(const uint4*)(vp + t0 * 64 + T * 1024 + lane * 16);
+        }
+        uint32_t x = 0;
+        if constexpr (G == 4) {
+            const uint2 s = *(const uint2*)(vs + (t0 + lane) * 8), m = *(const uint2*)(vm + (t0 + lane) * 8);
+            x = s.x ^ m.y;
+        } else {
+            x = *(const uint16_t*)(vs + (t0 + lane) * 2) ^ *(const uint16_t*)(vm + (t0 + lane) * 2);
+        }
+        const uint32_t ksv = *(const uint32_t*)(ks + (int64_t)p * 256 + lane * 4);
+        const uint32_t kmv = *(const uint32_t*)(km + (int64_t)p * 256 + lane * 4);
+#pragma unroll
+        for (int T = 0; T < 4; ++T) x ^= a[T].x ^ v[T].y;
+        acc ^= x ^ ksv ^ kmv;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_read_step(const Int4Cache& c, const Workspace& ws, unsigned* sink, hipStream_t st) {
+    const int groups = c.L * c.B * c.Hkv;
+    if (c.G == 4) hipLaunchKernelGGL(read_step_kernel<4>, dim3(groups), dim3(512), 0, st, c, ws, sink);
+    else hipLaunchKernelGGL(read_step_kernel<1>, dim3(groups), dim3(512), 0, st, c, ws, sink);
+    return hipGetLastError();
+}
+
+}  // namespace fq

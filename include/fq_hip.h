@@ -210,6 +210,17 @@ int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* que
                                  int32_t k_max, int32_t select_mode,
                                  float* scores_out, uint8_t* mask_out, fq_stream_t stream);
 
+/* Measurement only; no counterpart in the reference.  Reads exactly what
+ * fq_quest_decode_int4's single launch reads for the selection `mask`
+ * (L, B, H_q, P) -- every page's K scale / min, then the K and V codes, V
+ * scale / min and K scale / min of each KV group's union of selected pages --
+ * with the same per-workgroup order and granularity, and computes nothing:
+ * the memory system's ceiling for the step's access pattern.  `sink` is a
+ * device word written only if the folded bytes hit an unlikely constant.
+ * Workspace as fq_workspace_bytes (the union lists). */
+int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
+                         int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
 /* The two halves of fq_quest_decode_int4, for callers that time or overlap
  * them separately; call both with the same cache, query, retention, k_max,
  * num_sinks, window_pages, select_mode and workspace.  fq_quest_select_int4

@@ -262,3 +262,15 @@ def test_turbo_fused_step_at_size(mode):
             assert np.abs(o[l:l + 1, :, 0].float().cpu().numpy() - ref_o).max() <= TOL_O + 2.0 ** -8 * np.abs(ref_o).max()
             assert np.abs(lse[l:l + 1, :, 0].cpu().numpy() - ref_l).max() <= TOL_LSE
     assert (o.float() - os_.float()).abs().max().item() <= 2 * (TOL_O + 2.0 ** -8)
+
+
+def test_read_only_pass_runs_on_config1(cfg1):
+    """The bench's ceiling probe (fq_read_decode_pages) takes config 1's cache
+    and the decode's own selection mask and completes."""
+    from flashquest_amd._ops import read_decode_pages
+    planes = [cfg1[k] for k in PLANES]
+    _, _, mask = quest_decode_int4(cfg1["Q"], *planes, retention=0.25, num_sinks=4, window_pages=2,
+                                   return_selection=True)
+    for _ in range(2):
+        read_decode_pages(*planes, mask)
+    torch.cuda.synchronize()
