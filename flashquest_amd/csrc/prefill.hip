@@ -235,7 +235,6 @@ FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */
 }
 
 // ---- dense bf16 source (two-pass path) --------------------------------------
-struct DFetch { u32x4 k[4], v[4]; };   // 32 bf16 of one K row, 32 of one V^T row
 
 // The first pass: dequantise the cache and the tail once into dense bf16 K and
 // V^T (keys padded with zeros to a multiple of 64).  One 512-thread block per
@@ -452,35 +451,17 @@ __global__ __launch_bounds__(512) void prefill_dequant_turbo_kernel(PrefillParam
 }
 
 template <int SRC>
-FQ_DEV void prefill_fetch(const PrefillParams& a, KFetch& kf, VFetch& vf, DFetch& df, const uint16_t* kd_base,
-                          const uint16_t* vd_base, int key0, int b, int h, int kk, int kc, int vk, int vd) {
-    if constexpr (SRC == 16) {
-        const uint16_t* kp = kd_base + (int64_t)key0 * kPD;
-        const uint16_t* vp = vd_base + key0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            df.k[i] = *(const u32x4*)(kp + 8 * i);
-            df.v[i] = *(const u32x4*)(vp + 8 * i);
-        }
-    } else {
-        const bool whole = key0 + kPKT <= a.c.S;
-        fetch_k<SRC>(kf, a, b, h, key0 + kk, kc, whole);
-        fetch_v<SRC>(vf, a, b, h, key0 + vk, vd, whole);
-    }
+FQ_DEV void prefill_fetch(const PrefillParams& a, KFetch& kf, VFetch& vf, int key0, int b, int h, int kk, int kc, int vk,
+                          int vd) {
+    const bool whole = key0 + kPKT <= a.c.S;
+    fetch_k<SRC>(kf, a, b, h, key0 + kk, kc, whole);
+    fetch_v<SRC>(vf, a, b, h, key0 + vk, vd, whole);
 }
 
 template <int SRC>
-FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch& vf, const DFetch& df, uint16_t* sk,
-                          uint16_t* sv, int kk, int kc, int vd, int vk, int td, int tq) {
-    if constexpr (SRC == 16) {
-        uint16_t* kdst = sk + kk * kKStr + kc;
-        uint16_t* vdst = sv + td * (kDenseKT + 8) + tq;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(u32x4*)(kdst + 8 * i) = df.k[i];
-            *(u32x4*)(vdst + 8 * i) = df.v[i];
-        }
-    } else if (a.c.meta_dtype == FQ_BF16) {
+FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch& vf, uint16_t* sk, uint16_t* sv, int kk,
+                          int kc, int vd, int vk) {
+    if (a.c.meta_dtype == FQ_BF16) {
         store_k<SRC, FQ_BF16>(kf, sk + kk * kKStr + kc);
         store_v<SRC, FQ_BF16>(vf, sv + vd * kVStr + vt_pos(vk), kVStr);
     } else {
@@ -492,10 +473,8 @@ FQ_DEV void prefill_stage(const PrefillParams& a, const KFetch& kf, const VFetch
 template <int SRC, int META>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn_kernel(PrefillParams a) {
-    // One LDS stage holds ST keys: 128 for the dense source (two 64-key
-    // sub-tiles per barrier, 136 KB double-buffered), 64 for the packed source.
-    constexpr int ST = SRC == 16 ? kDenseKT : kPKT;
-    constexpr int VSTR = ST + 8;   // bf16 per V^T row (row stride = 4 banks mod 64: conflict-free reads)
+    constexpr int ST = kPKT;       // keys per LDS stage, double-buffered
+    constexpr int VSTR = kVStr;    // bf16 per V^T row (row stride = 4 banks mod 64: conflict-free reads)
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][ST * kKStr];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][kPD * VSTR];
 
@@ -506,20 +485,14 @@ void prefill_attn_kernel(PrefillParams a) {
     // different XCDs, so with H_kv * B a multiple of 8 each XCD's L2 holds the
     // K/V of its own heads.  Row blocks run last-first (the longest first).
     const int HB = c.Hkv * c.B;
-    const int KS = a.kv_splits > 1 ? a.kv_splits : 1;
-    const int nblk = gridDim.x / (HB * KS);
+    const int nblk = gridDim.x / HB;
     const int hb = blockIdx.x % HB;
-    const int rb = nblk - 1 - (int)((blockIdx.x / HB) % nblk);
-    const int split = (int)(blockIdx.x / (HB * nblk));
+    const int rb = nblk - 1 - (int)(blockIdx.x / HB);
     const int h = hb % c.Hkv, b = hb / c.Hkv;
     const int Mtot = a.Sq * a.nrep;
     const int m0 = rb * kPRows;
     const int last_wg = (min(m0 + kPRows, Mtot) - 1) / a.nrep;
-    const int nt_all = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;
-    // this workgroup's key stages [t_begin, nt) (all of them without splits)
-    const int per = (nt_all + KS - 1) / KS;
-    const int t_begin = min(nt_all, split * per);
-    const int nt = min(nt_all, t_begin + per);
+    const int nt = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;   // >= 1: key 0 is attended
 
     const int mw0 = m0 + w * kPRW;
     const bool wave_on = mw0 < Mtot;
@@ -554,43 +527,230 @@ void prefill_attn_kernel(PrefillParams a) {
         for (int db = 0; db < 8; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
-    // K loader: one key, 16 channels (packed) or 32 channels (dense, 128 keys)
-    const int kk = SRC == 16 ? tid >> 2 : tid >> 3, kc = SRC == 16 ? (tid & 3) * 32 : (tid & 7) * 16;
-    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4; // V loader (packed): 4 keys, 4 channels
-    const int td = tid >> 2, tq = (tid & 3) * 32;       // V^T loader (dense): one channel, 32 keys
-    const int64_t bh = (int64_t)b * c.Hkv + h;
-    const uint16_t* kd_base = SRC == 16 ? a.kd + (bh * a.s_pad + kk) * kPD + kc : nullptr;
-    const uint16_t* vd_base = SRC == 16 ? a.vtd + (bh * kPD + td) * a.s_pad + tq : nullptr;
+    const int kk = tid >> 3, kc = (tid & 7) * 16;         // K loader: one key, 16 channels
+    const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4;   // V loader: 4 keys, 4 channels
 
     KFetch kf;
     VFetch vf;
-    DFetch df;
-    // nt >= 1: key 0 is always attended (causal_off >= 0, S_kv >= 1)
-    // a workgroup with no stages (a split past the causal limit) stores an empty partial
-    if (t_begin < nt) {
-        prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, t_begin * ST, b, h, kk, kc, vk, vd);
-        prefill_stage<SRC>(a, kf, vf, df, s_k[0], s_v[0], kk, kc, vd, vk, td, tq);
-    }
+    prefill_fetch<SRC>(a, kf, vf, 0, b, h, kk, kc, vk, vd);
+    prefill_stage<SRC>(a, kf, vf, s_k[0], s_v[0], kk, kc, vd, vk);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): prologue loads (Q included) land before the loop
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+        const int cur = t & 1;
+        const int key0 = t * ST;
+        if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, key0 + ST, b, h, kk, kc, vk, vd);
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave_on && key0 < limit_w) {
+            v4f s[2][4];
+            qk_tile(s_k[cur], qf, s, n, g);
+            softmax_pv(s, o, m_run, l_run, s_v[cur], VSTR, qpos, key0, pmin, a.causal_off, a.Skv, a.qk_scale, n, g);
+        }
+        // the dequantising LDS writes of the next tile after this tile's math
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < nt) prefill_stage<SRC>(a, kf, vf, s_k[cur ^ 1], s_v[cur ^ 1], kk, kc, vd, vk);
+        __syncthreads();
+    }
+
+    if (!wave_on) return;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const float l = rows_sum(l_run[qb]);
+        if (!qok[qb]) continue;
+        const float inv = 1.0f / l;
+        const int m = mw0 + qb * 16 + n;
+        const int hq = h * a.nrep + m % a.nrep;
+        uint16_t* orow = (uint16_t*)a.out + b * a.o_s[0] + hq * a.o_s[1] + (int64_t)(m / a.nrep) * a.o_s[2];
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const v4f r = o[qb][db] * inv;
+            *(u32x2*)(orow + db * 16 + 4 * g) = u32x2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
+        }
+    }
+}
+
+// ---- the two-pass path's attention: LDS filled by direct-to-LDS loads -------
+// A stage is 128 keys of the dense source: K as [key][16 chunks of 8
+// channels], V^T as [channel][16 chunks of 8 keys].  Chunk c of row r sits in
+// slot c ^ (r & 15), so the 16 rows of an MFMA operand read (lanes n = 0..15,
+// one chunk each) hit 16 distinct slots, and one direct-to-LDS load of a wave
+// fills 4 whole rows (1 KB; lane L lands in slot L & 15 of row L >> 4) from
+// the matching global chunks.  No staging registers and no LDS stores: stage
+// t + 1 streams into the other buffer while stage t is computed.  Each wave
+// owns QB blocks of 16 query columns, so every K / V^T operand read from LDS
+// feeds QB matrix instructions.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int QB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_dense_kernel(PrefillParams a) {
+    constexpr int ST = kDenseKT;
+    constexpr int RW = 16 * QB, RWG = kPW * RW;
+    __shared__ __attribute__((aligned(1024))) uint16_t s_k[2][ST * kPD];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_v[2][kPD * ST];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const Int4Cache& c = a.c;
+    // KV head in the low bits of the block index (each XCD's L2 keeps its
+    // heads' K / V); row blocks run last-first (the longest first)
+    const int HB = c.Hkv * c.B;
+    const int KS = a.kv_splits > 1 ? a.kv_splits : 1;
+    const int nblk = gridDim.x / (HB * KS);
+    const int hb = blockIdx.x % HB;
+    const int rb = nblk - 1 - (int)((blockIdx.x / HB) % nblk);
+    const int split = (int)(blockIdx.x / (HB * nblk));
+    const int h = hb % c.Hkv, b = hb / c.Hkv;
+    const int Mtot = a.Sq * a.nrep;
+    const int m0 = rb * RWG;
+    const int last_wg = (min(m0 + RWG, Mtot) - 1) / a.nrep;
+    const int nt_all = (min(a.Skv, last_wg + a.causal_off + 1) + ST - 1) / ST;
+    const int per = (nt_all + KS - 1) / KS;
+    const int t_begin = min(nt_all, split * per);
+    const int nt = min(nt_all, t_begin + per);
+
+    const int mw0 = m0 + w * RW;
+    const bool wave_on = mw0 < Mtot;
+    const int pmin = min(mw0, Mtot - 1) / a.nrep;
+    const int pmax = (min(mw0 + RW, Mtot) - 1) / a.nrep;
+    const int limit_w = min(a.Skv, pmax + a.causal_off + 1);
+
+    int qpos[QB];
+    bool qok[QB];
+    v8bf qf[QB][4];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int m = mw0 + qb * 16 + n;
+        qok[qb] = m < Mtot;
+        const int mm = qok[qb] ? m : (wave_on ? mw0 : 0);
+        qpos[qb] = qok[qb] ? mm / a.nrep : pmin;
+        const int hq = h * a.nrep + mm % a.nrep;
+        const uint16_t* qrow = (const uint16_t*)a.q + b * a.q_s[0] + hq * a.q_s[1] + (int64_t)(mm / a.nrep) * a.q_s[2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[qb][ks] = *(const v8bf*)(qrow + 32 * ks + 8 * g);
+    }
+
+    v4f o[QB][8];
+    float m_run[QB], l_run[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        m_run[qb] = -INFINITY; l_run[qb] = 0.f;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // wave w fills rows 16 w .. 16 w + 15 of both tiles, 4 rows per load
+    const int64_t bh = (int64_t)b * c.Hkv + h;
+    const uint16_t* kg = a.kd + bh * a.s_pad * kPD;
+    const uint16_t* vg = a.vtd + bh * kPD * a.s_pad;
+    const int lrow = lane >> 4, slot = lane & 15;
+    auto issue_stage = [&](int buf, int key0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r0 = 16 * w + 4 * j, r = r0 + lrow;
+            const int ch = slot ^ ((4 * j + lrow) & 15);
+            __builtin_amdgcn_global_load_lds((const void*)(kg + (int64_t)(key0 + r) * kPD + ch * 8),
+                                             (lds_ptr_t)(s_k[buf] + r0 * kPD), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(vg + (int64_t)r * a.s_pad + key0 + ch * 8),
+                                             (lds_ptr_t)(s_v[buf] + r0 * ST), 16, 0, 0);
+        }
+    };
+
+    if (t_begin < nt) issue_stage(0, t_begin * ST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the first stage and Q have landed
     __syncthreads();
     for (int t = t_begin; t < nt; ++t) {
         const int cur = (t - t_begin) & 1;
         const int key0 = t * ST;
-        if (t + 1 < nt) prefill_fetch<SRC>(a, kf, vf, df, kd_base, vd_base, key0 + ST, b, h, kk, kc, vk, vd);
-        __builtin_amdgcn_sched_barrier(0);
+        // the other buffer was last read before the previous iteration's barrier
+        if (t + 1 < nt) issue_stage(cur ^ 1, key0 + ST);
 #pragma unroll
         for (int sub = 0; sub < ST / kPKT; ++sub) {
             const int k0 = key0 + sub * kPKT;
             if (wave_on && k0 < limit_w) {
-                v4f s[2][4];
-                qk_tile(s_k[cur] + sub * kPKT * kKStr, qf, s, n, g);
-                softmax_pv(s, o, m_run, l_run, s_v[cur] + sub * kPKT, VSTR, qpos, k0, pmin, a.causal_off, a.Skv,
-                           a.qk_scale, n, g);
+                // S^T = K Q^T: key rows sub * 64 + kb * 16 + n (row & 15 = n)
+                const uint16_t* sk = s_k[cur] + sub * kPKT * kPD;
+                v4f s[QB][4];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) s[qb][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
+                        const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kPD + (((4 * ks + g) ^ n) * 8));
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb)
+                            s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[qb][ks], s[qb][kb], 0, 0, 0);
+                    }
+                if (k0 + kPKT - 1 > pmin + a.causal_off || k0 + kPKT > a.Skv) {
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1) - k0 - 4 * g;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                            for (int cc = 0; cc < 4; ++cc)
+                                if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
+                    }
+                }
+                // online softmax per query column (base 2), P as bf16 P^T operands
+                float m_use[QB], alpha[QB];
+                bool moved = false;
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    float mx = fmaxf(fmaxf(s[qb][0][0], s[qb][0][1]), fmaxf(s[qb][0][2], s[qb][0][3]));
+#pragma unroll
+                    for (int kb = 1; kb < 4; ++kb)
+                        mx = fmaxf(mx, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
+                    mx = rows_max(mx);
+                    const float m_new = fmaxf(m_run[qb], mx * a.qk_scale);
+                    m_use[qb] = m_new == -INFINITY ? 0.f : m_new;
+                    alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use[qb]);
+                    moved |= m_new != m_run[qb];
+                    m_run[qb] = m_new;
+                }
+                v8bf pb[QB][2];
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    float sum = 0.f, p[4][4];
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) {
+                            p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], a.qk_scale, -m_use[qb]));
+                            sum += p[kb][cc];
+                        }
+                    l_run[qb] = fmaf(l_run[qb], alpha[qb], sum);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) {
+                            pb[qb][j][cc] = (__bf16)p[2 * j][cc];
+                            pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
+                        }
+                }
+                if (__builtin_amdgcn_ballot_w64(moved)) {   // the running max moved for some column
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+                        for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
+                }
+                // O^T += V^T P^T: channel rows db * 16 + n, key chunks 8 sub + 4 j + g (vt_pos order)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int db = 0; db < 8; ++db) {
+                        const v8bf av =
+                            *(const v8bf*)(s_v[cur] + (db * 16 + n) * ST + (((8 * sub + 4 * j + g) ^ n) * 8));
+#pragma unroll
+                        for (int qb = 0; qb < QB; ++qb)
+                            o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[qb][j], o[qb][db], 0, 0, 0);
+                    }
             }
         }
-        // the dequantising LDS writes of the next tile after this tile's math
-        __builtin_amdgcn_sched_barrier(0);
-        if (t + 1 < nt) prefill_stage<SRC>(a, kf, vf, df, s_k[cur ^ 1], s_v[cur ^ 1], kk, kc, vd, vk, td, tq);
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): stage t + 1 is in LDS
         __syncthreads();
     }
 
@@ -598,7 +758,7 @@ void prefill_attn_kernel(PrefillParams a) {
     if (KS > 1) {   // unnormalised partial + (m, l) per row for prefill_merge_kernel
         const int64_t rows = (int64_t)c.B * c.Hkv * Mtot;
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             const float l = rows_sum(l_run[qb]);
             if (!qok[qb]) continue;
             const int64_t row = ((int64_t)split * c.B * c.Hkv + hb) * Mtot + mw0 + qb * 16 + n;
@@ -614,7 +774,7 @@ void prefill_attn_kernel(PrefillParams a) {
         return;
     }
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const float l = rows_sum(l_run[qb]);
         if (!qok[qb]) continue;
         const float inv = 1.0f / l;
@@ -667,6 +827,10 @@ int64_t prefill_keys_needed(int Skv, int Sq, int causal_off) { return std::min<i
 
 int64_t prefill_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kPRows - 1) / kPRows; }
 
+constexpr int kDenseQB = 2;                       // 16-column query blocks per wave, dense path
+constexpr int kDenseRows = kPW * 16 * kDenseQB;   // query rows per dense workgroup
+int64_t dense_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kDenseRows - 1) / kDenseRows; }
+
 // The fused path (each workgroup dequantises the K/V tiles it attends) only
 // for one row block per KV head over at most 1024 keys; otherwise the
 // two-pass path (dequantise the needed keys once, in parallel, into dense
@@ -688,7 +852,7 @@ size_t prefill_dense_bytes(int Hkv, int B, int Skv, int Sq, int nrep, int causal
     const int64_t keys = prefill_keys_needed(Skv, Sq, causal_off);
     const int64_t s_pad = (keys + kDenseKT - 1) / kDenseKT * kDenseKT;
     size_t n = (size_t)(2 * s_pad * kPD * 2) * Hkv * B;
-    const int ks = prefill_kv_splits(prefill_row_blocks(Sq, nrep), (int64_t)Hkv * B, keys);
+    const int ks = prefill_kv_splits(dense_row_blocks(Sq, nrep), (int64_t)Hkv * B, keys);
     if (ks > 1) n += (size_t)ks * B * Hkv * Sq * nrep * (kPD + 2) * sizeof(float);
     return n;
 }
@@ -702,13 +866,13 @@ size_t prefill_workspace_bytes(const Int4Cache& c, int Skv, int Sq, int nrep, in
 // The attention launch of the dense path (a.kd / a.vtd / a.s_pad set), with
 // key-range splits and their merge when the row blocks are few.
 hipError_t launch_dense_attn(PrefillParams& a, int Sq, int nrep, hipStream_t st) {
-    const int64_t nblk = prefill_row_blocks(Sq, nrep);
+    const int64_t nblk = dense_row_blocks(Sq, nrep);
     const int64_t heads = (int64_t)a.c.Hkv * a.c.B;
     const int ks = prefill_kv_splits(nblk, heads, prefill_keys_needed(a.Skv, Sq, a.causal_off));
     a.kv_splits = ks;
     a.part = ks > 1 ? (float*)(a.vtd + (int64_t)a.s_pad * kPD * heads) : nullptr;
     timer_before_launch(st);
-    hipLaunchKernelGGL((prefill_attn_kernel<16, FQ_BF16>), dim3((unsigned)(nblk * heads * ks)), dim3(512), 0, st, a);
+    hipLaunchKernelGGL((prefill_dense_kernel<kDenseQB>), dim3((unsigned)(nblk * heads * ks)), dim3(512), 0, st, a);
     timer_after_launch(st);
     if (ks > 1) {
         const int64_t rows = heads * Sq * nrep;
