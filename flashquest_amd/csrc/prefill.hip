@@ -46,6 +46,7 @@ constexpr int kPRows = kPW * kPRW;     // query rows per workgroup
 constexpr int kKStr = kPD + 8;         // bf16 per K row in LDS (272 B: conflict-free 16-byte reads)
 constexpr int kVStr = kPKT + 8;        // bf16 per V^T row in LDS (144 B)
 constexpr int kDenseKT = 128;          // keys per LDS stage of the dense (two-pass) source
+constexpr float kLazyLog2 = 8.0f;      // dense pass: rescale O only when a maximum grows by > 2^8
 
 struct PrefillParams {
     Int4Cache c;
@@ -630,29 +631,53 @@ void prefill_dense_kernel(PrefillParams a) {
         for (int ks = 0; ks < 4; ++ks) qf[qb][ks] = *(const v8bf*)(qrow + 32 * ks + 8 * g);
     }
 
-    v4f o[QB][8];
-    float m_run[QB], l_run[QB];
+    // o[qb][0..7]: O^T of the 128 channels; o[qb][8]: a block of ones times P^T,
+    // i.e. sum p (the softmax denominator) of this lane's column in every row
+    v4f o[QB][9];
+    float m_run[QB];      // the reference maximum the exponents are taken against (log2 domain)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        m_run[qb] = -INFINITY; l_run[qb] = 0.f;
+        m_run[qb] = -INFINITY;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < 9; ++db) o[qb][db] = v4f{0.f, 0.f, 0.f, 0.f};
     }
+    v8bf ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
 
-    // wave w fills rows 16 w .. 16 w + 15 of both tiles, 4 rows per load
+    // wave w fills rows 16 w .. 16 w + 15 of both tiles, 4 rows per load: a
+    // stage's uniform base address plus per-lane byte offsets fixed for the kernel
     const int64_t bh = (int64_t)b * c.Hkv + h;
-    const uint16_t* kg = a.kd + bh * a.s_pad * kPD;
-    const uint16_t* vg = a.vtd + bh * kPD * a.s_pad;
+    const int64_t dense_bytes = (int64_t)a.s_pad * kPD * 2;      // one (b, h) slice of K or of V^T
+    // wave-uniform by construction; readfirstlane keeps them in scalar registers
+    auto uniform_ptr = [](const void* p) {
+        const uint64_t v = (uint64_t)p;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+        return (void*)(((uint64_t)hi << 32) | lo);
+    };
+    const int nrec = __builtin_amdgcn_readfirstlane((int)min(dense_bytes, (int64_t)INT32_MAX));
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.kd + bh * a.s_pad * kPD), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.vtd + bh * kPD * a.s_pad), (short)0, nrec, 0x00020000);
+    const int wu = __builtin_amdgcn_readfirstlane(w);
     const int lrow = lane >> 4, slot = lane & 15;
-    auto issue_stage = [&](int buf, int key0) {
+    int koff[4], voff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 16 * wu + 4 * j + lrow, ch = slot ^ ((4 * j + lrow) & 15);
+        koff[j] = (r * kPD + ch * 8) * 2;
+        voff[j] = (r * a.s_pad + ch * 8) * 2;
+    }
+    auto issue_stage = [&](int buf, int key0_) {
+        const int key0 = __builtin_amdgcn_readfirstlane(key0_);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int r0 = 16 * w + 4 * j, r = r0 + lrow;
-            const int ch = slot ^ ((4 * j + lrow) & 15);
-            __builtin_amdgcn_global_load_lds((const void*)(kg + (int64_t)(key0 + r) * kPD + ch * 8),
-                                             (lds_ptr_t)(s_k[buf] + r0 * kPD), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(vg + (int64_t)r * a.s_pad + key0 + ch * 8),
-                                             (lds_ptr_t)(s_v[buf] + r0 * ST), 16, 0, 0);
+            const int r0 = 16 * wu + 4 * j;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr_t)(s_k[buf] + r0 * kPD), 16, koff[j], key0 * kPD * 2,
+                                                     0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_ptr_t)(s_v[buf] + r0 * ST), 16, voff[j], key0 * 2, 0, 0);
         }
     };
 
@@ -695,47 +720,44 @@ void prefill_dense_kernel(PrefillParams a) {
                                 if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
                     }
                 }
-                // online softmax per query column (base 2), P as bf16 P^T operands
-                float m_use[QB], alpha[QB];
+                // online softmax per query column (base 2), P as bf16 P^T operands.
+                // The reference maximum moves only when a column's tile maximum
+                // exceeds it by more than 2^kLazyLog2: until then p <= 2^kLazyLog2
+                // (exact in fp32, relative bf16 rounding unchanged) and O and
+                // its denominator need no rescale.
+                float mx[QB];
                 bool moved = false;
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
-                    float mx = fmaxf(fmaxf(s[qb][0][0], s[qb][0][1]), fmaxf(s[qb][0][2], s[qb][0][3]));
+                    float t[4];
 #pragma unroll
-                    for (int kb = 1; kb < 4; ++kb)
-                        mx = fmaxf(mx, fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3])));
-                    mx = rows_max(mx);
-                    const float m_new = fmaxf(m_run[qb], mx * a.qk_scale);
-                    m_use[qb] = m_new == -INFINITY ? 0.f : m_new;
-                    alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use[qb]);
-                    moved |= m_new != m_run[qb];
-                    m_run[qb] = m_new;
+                    for (int kb = 0; kb < 4; ++kb)
+                        t[kb] = fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3]));
+                    mx[qb] = rows_max(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]))) * a.qk_scale;
+                    moved |= mx[qb] > m_run[qb] + kLazyLog2;
+                }
+                if (__builtin_amdgcn_ballot_w64(moved)) {   // wave-uniform: new references for every column
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) {
+                        const float m_new = fmaxf(m_run[qb], mx[qb]);
+                        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.f : m_new));
+                        m_run[qb] = m_new;
+#pragma unroll
+                        for (int db = 0; db < 9; ++db) o[qb][db] *= alpha;
+                    }
                 }
                 v8bf pb[QB][2];
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) {
-                    float sum = 0.f, p[4][4];
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int cc = 0; cc < 4; ++cc) {
-                            p[kb][cc] = __builtin_amdgcn_exp2f(fmaf(s[qb][kb][cc], a.qk_scale, -m_use[qb]));
-                            sum += p[kb][cc];
-                        }
-                    l_run[qb] = fmaf(l_run[qb], alpha[qb], sum);
+                    const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
 #pragma unroll
                         for (int cc = 0; cc < 4; ++cc) {
-                            pb[qb][j][cc] = (__bf16)p[2 * j][cc];
-                            pb[qb][j][4 + cc] = (__bf16)p[2 * j + 1][cc];
+                            pb[qb][j][cc] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j][cc], a.qk_scale, -m_use));
+                            pb[qb][j][4 + cc] =
+                                (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j + 1][cc], a.qk_scale, -m_use));
                         }
-                }
-                if (__builtin_amdgcn_ballot_w64(moved)) {   // the running max moved for some column
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-                        for (int db = 0; db < 8; ++db) o[qb][db] *= alpha[qb];
                 }
                 // O^T += V^T P^T: channel rows db * 16 + n, key chunks 8 sub + 4 j + g (vt_pos order)
 #pragma unroll
@@ -748,6 +770,11 @@ void prefill_dense_kernel(PrefillParams a) {
                         for (int qb = 0; qb < QB; ++qb)
                             o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[qb][j], o[qb][db], 0, 0, 0);
                     }
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        o[qb][8] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qb][j], o[qb][8], 0, 0, 0);
             }
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): stage t + 1 is in LDS
@@ -759,7 +786,7 @@ void prefill_dense_kernel(PrefillParams a) {
         const int64_t rows = (int64_t)c.B * c.Hkv * Mtot;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            const float l = rows_sum(l_run[qb]);
+            const float l = o[qb][8][0];
             if (!qok[qb]) continue;
             const int64_t row = ((int64_t)split * c.B * c.Hkv + hb) * Mtot + mw0 + qb * 16 + n;
             float* prow = a.part + row * kPD;
@@ -775,7 +802,7 @@ void prefill_dense_kernel(PrefillParams a) {
     }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        const float l = rows_sum(l_run[qb]);
+        const float l = o[qb][8][0];
         if (!qok[qb]) continue;
         const float inv = 1.0f / l;
         const int m = mw0 + qb * 16 + n;
