@@ -681,6 +681,95 @@ void prefill_dense_kernel(PrefillParams a) {
         }
     };
 
+    // S^T = K Q^T for one 64-key sub-tile (sk: its first key row; row & 15 = n)
+    auto qk = [&](const uint16_t* sk, v4f (&s)[QB][4]) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) s[qb][kb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kPD + (((4 * ks + g) ^ n) * 8));
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[qb][ks], s[qb][kb], 0, 0, 0);
+            }
+    };
+    // causal / length mask of a sub-tile starting at key k0 (only near the diagonal or the end)
+    auto diag_mask = [&](int k0, v4f (&s)[QB][4]) {
+        if (k0 + kPKT - 1 > pmin + a.causal_off || k0 + kPKT > a.Skv) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1) - k0 - 4 * g;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc)
+                        if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
+            }
+        }
+    };
+    // per-column maxima (log2 domain); true where one exceeds the reference by
+    // more than 2^kLazyLog2: the reference then moves (raise_ref).  Until it
+    // does, p <= 2^kLazyLog2 (exact in fp32, relative bf16 rounding unchanged)
+    // and O and its denominator need no rescale.
+    auto tile_max = [&](const v4f (&s)[QB][4], float (&mx)[QB]) {
+        bool moved = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            float t4[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                t4[kb] = fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3]));
+            mx[qb] = rows_max(fmaxf(fmaxf(t4[0], t4[1]), fmaxf(t4[2], t4[3]))) * a.qk_scale;
+            moved |= mx[qb] > m_run[qb] + kLazyLog2;
+        }
+        return moved;
+    };
+    auto raise_ref = [&](const float (&mx)[QB]) {      // wave-uniform: new references for every column
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float m_new = fmaxf(m_run[qb], mx[qb]);
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.f : m_new));
+            m_run[qb] = m_new;
+#pragma unroll
+            for (int db = 0; db < 9; ++db) o[qb][db] *= alpha;
+        }
+    };
+    // P = exp2(s * qk_scale - reference) as the bf16 P^T operands
+    auto exp_p = [&](const v4f (&s)[QB][4], v8bf (&pb)[QB][2]) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+            const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    pb[qb][j][cc] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j][cc], a.qk_scale, -m_use));
+                    pb[qb][j][4 + cc] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j + 1][cc], a.qk_scale, -m_use));
+                }
+        }
+    };
+    // O^T += V^T P^T (channel rows db * 16 + n, key chunks 8 sub + 4 j + g, vt_pos
+    // order) and the denominator block ones * P^T
+    auto pv = [&](const uint16_t* sv, int sub, const v8bf (&pb)[QB][2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const v8bf av = *(const v8bf*)(sv + (db * 16 + n) * ST + (((8 * sub + 4 * j + g) ^ n) * 8));
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[qb][j], o[qb][db], 0, 0, 0);
+            }
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                o[qb][8] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qb][j], o[qb][8], 0, 0, 0);
+        }
+    };
+
     if (t_begin < nt) issue_stage(0, t_begin * ST);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the first stage and Q have landed
     __syncthreads();
@@ -689,93 +778,33 @@ void prefill_dense_kernel(PrefillParams a) {
         const int key0 = t * ST;
         // the other buffer was last read before the previous iteration's barrier
         if (t + 1 < nt) issue_stage(cur ^ 1, key0 + ST);
-#pragma unroll
-        for (int sub = 0; sub < ST / kPKT; ++sub) {
-            const int k0 = key0 + sub * kPKT;
-            if (wave_on && k0 < limit_w) {
-                // S^T = K Q^T: key rows sub * 64 + kb * 16 + n (row & 15 = n)
-                const uint16_t* sk = s_k[cur] + sub * kPKT * kPD;
-                v4f s[QB][4];
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) s[qb][kb] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) {
-                        const v8bf ak = *(const v8bf*)(sk + (kb * 16 + n) * kPD + (((4 * ks + g) ^ n) * 8));
-#pragma unroll
-                        for (int qb = 0; qb < QB; ++qb)
-                            s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, qf[qb][ks], s[qb][kb], 0, 0, 0);
-                    }
-                if (k0 + kPKT - 1 > pmin + a.causal_off || k0 + kPKT > a.Skv) {
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) {
-                        const int lim = min(qpos[qb] + a.causal_off, a.Skv - 1) - k0 - 4 * g;
-#pragma unroll
-                        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                            for (int cc = 0; cc < 4; ++cc)
-                                if (kb * 16 + cc > lim) s[qb][kb][cc] = -INFINITY;
-                    }
-                }
-                // online softmax per query column (base 2), P as bf16 P^T operands.
-                // The reference maximum moves only when a column's tile maximum
-                // exceeds it by more than 2^kLazyLog2: until then p <= 2^kLazyLog2
-                // (exact in fp32, relative bf16 rounding unchanged) and O and
-                // its denominator need no rescale.
-                float mx[QB];
-                bool moved = false;
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    float t[4];
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-                        t[kb] = fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3]));
-                    mx[qb] = rows_max(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]))) * a.qk_scale;
-                    moved |= mx[qb] > m_run[qb] + kLazyLog2;
-                }
-                if (__builtin_amdgcn_ballot_w64(moved)) {   // wave-uniform: new references for every column
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb) {
-                        const float m_new = fmaxf(m_run[qb], mx[qb]);
-                        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - (m_new == -INFINITY ? 0.f : m_new));
-                        m_run[qb] = m_new;
-#pragma unroll
-                        for (int db = 0; db < 9; ++db) o[qb][db] *= alpha;
-                    }
-                }
-                v8bf pb[QB][2];
-#pragma unroll
-                for (int qb = 0; qb < QB; ++qb) {
-                    const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-#pragma unroll
-                        for (int cc = 0; cc < 4; ++cc) {
-                            pb[qb][j][cc] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j][cc], a.qk_scale, -m_use));
-                            pb[qb][j][4 + cc] =
-                                (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qb][2 * j + 1][cc], a.qk_scale, -m_use));
-                        }
-                }
-                // O^T += V^T P^T: channel rows db * 16 + n, key chunks 8 sub + 4 j + g (vt_pos order)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int db = 0; db < 8; ++db) {
-                        const v8bf av =
-                            *(const v8bf*)(s_v[cur] + (db * 16 + n) * ST + (((8 * sub + 4 * j + g) ^ n) * 8));
-#pragma unroll
-                        for (int qb = 0; qb < QB; ++qb)
-                            o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[qb][j], o[qb][db], 0, 0, 0);
-                    }
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int qb = 0; qb < QB; ++qb)
-                        o[qb][8] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qb][j], o[qb][8], 0, 0, 0);
-            }
+        // Both 64-key sub-tiles: q.k of sub-tile 1 is issued before sub-tile
+        // 0's softmax and the maximum of sub-tile 1 follows sub-tile 0's p.v,
+        // so the matrix instructions of one overlap the vector work of the other.
+        const bool act0 = wave_on && key0 < limit_w, act1 = wave_on && key0 + kPKT < limit_w;
+        if (act1) {
+            v4f s0[QB][4], s1[QB][4];
+            float mx0[QB], mx1[QB];
+            v8bf p0[QB][2], p1[QB][2];
+            qk(s_k[cur], s0);
+            diag_mask(key0, s0);
+            qk(s_k[cur] + kPKT * kPD, s1);
+            if (__builtin_amdgcn_ballot_w64(tile_max(s0, mx0))) raise_ref(mx0);
+            diag_mask(key0 + kPKT, s1);
+            exp_p(s0, p0);
+            pv(s_v[cur], 0, p0);
+            if (__builtin_amdgcn_ballot_w64(tile_max(s1, mx1))) raise_ref(mx1);
+            exp_p(s1, p1);
+            pv(s_v[cur], 1, p1);
+        } else if (act0) {
+            v4f s0[QB][4];
+            float mx0[QB];
+            v8bf p0[QB][2];
+            qk(s_k[cur], s0);
+            diag_mask(key0, s0);
+            if (__builtin_amdgcn_ballot_w64(tile_max(s0, mx0))) raise_ref(mx0);
+            exp_p(s0, p0);
+            pv(s_v[cur], 0, p0);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): stage t + 1 is in LDS
         __syncthreads();
