@@ -122,3 +122,35 @@ def test_fused_duo_rejects_prefill_and_bad_pattern():
     with pytest.raises(ValueError, match="head_pattern"):
         quest_duo_fused_sdpa(c.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"], d["V_uint8"], d["V_scale"],
                              d["V_mn"], head_pattern=torch.tensor([True, True, True]), page_size=64)
+
+
+def test_random_shapes_match_oracle_decode():
+    """A seeded grid of ragged shapes (tests/test_kernel_sparse_edges.py:149-183
+    draws the same ranges with hypothesis): S_kv 64..512 tokens (partial last
+    pages), 1-2 KV heads, 1/2/4 query heads each, D 64/128, retention
+    0.25/0.5/1: the whole decode step (scores, selection, attention) against
+    the oracle, selection bit-exact."""
+    from flashquest_amd.eager.decode import quest_decode_int4, quest_decode_int8
+    rng = np.random.default_rng(2024)
+    for i in range(15):
+        S = int(rng.integers(64, 513))
+        Hkv = int(rng.choice([1, 2]))
+        rep = int(rng.choice([1, 2, 4]))
+        D = int(rng.choice([64, 128]))
+        r = float(rng.choice([0.25, 0.5, 1.0]))
+        kw = dict(retention=r, num_sinks=1, window_pages=1, return_selection=True)
+        c = Int4Case(seed=900 + i, B=1, Hq=Hkv * rep, Hkv=Hkv, S=S, D=D)
+        o, lse, mask = quest_decode_int4(c.q_dev(), **c.device(), **kw)
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=r, num_sinks=1, window_pages=1)
+        c8 = Int8Case(seed=950 + i, B=1, Hq=Hkv * rep, Hkv=Hkv, S=S, D=D)
+        o8, lse8, mask8 = quest_decode_int8(c8.q_dev(), **c8.device(), **kw)
+        ref8 = O.decode_step(c8.Q, c8.ku, c8.ks, c8.km, c8.vu, c8.vs, c8.vm, retention=r, num_sinks=1,
+                             window_pages=1, bits=8)
+        torch.cuda.synchronize()
+        case = (S, Hkv, rep, D, r)
+        assert np.array_equal(mask.cpu().numpy(), ref["mask"]), case
+        assert max_err(o[:, :, 0], ref["O"]) <= _tol("bf16", ref["O"]), case
+        assert max_err(lse[:, :, 0], ref["lse"]) <= 1e-4, case
+        assert np.array_equal(mask8.cpu().numpy(), ref8["mask"]), case
+        assert max_err(o8[:, :, 0], ref8["O"]) <= _tol("bf16", ref8["O"]), case
+        assert max_err(lse8[:, :, 0], ref8["lse"]) <= 1e-4, case
