@@ -154,6 +154,8 @@ def read_decode_pages(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask: to
     if mask.dtype != torch.bool or mask.dim() != 4:
         raise ValueError(f"mask must be a 4D (L, B, H_q, P) bool tensor, got {mask.dtype} {tuple(mask.shape)}")
     H_q = mask.shape[2]
+    if (mask.shape[0], mask.shape[1], mask.shape[3]) != (c.L, c.B, c.P):
+        raise ValueError(f"mask {tuple(mask.shape)} does not match the cache's (L={c.L}, B={c.B}, H_q, P={c.P})")
     ws = L.workspace(mask.device, L.lib().fq_workspace_bytes(c, H_q))
     sink = torch.zeros(1, dtype=torch.int32, device=mask.device)
     L.check(L.lib().fq_read_decode_pages(c, mask.data_ptr(), L.strides(mask, 4), H_q, sink.data_ptr(),
