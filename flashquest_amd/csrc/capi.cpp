@@ -900,6 +900,10 @@ static int prefill_check_tail_query(const fq_tail* tail, const fq_prefill* q, in
     if (!aligned(q->q, 16) || !aligned(q->out, 8)) return fail(FQ_ERR_UNSUPPORTED, "Q/O alignment");
     const int64_t rows = (int64_t)q->S_q * (q->H_q / Hkv);
     if ((rows + 255) / 256 * Hkv * B > 0x7FFFFFFF) return fail(FQ_ERR_UNSUPPORTED, "grid too large");
+    // the dense pass addresses one head's bf16 K (or V^T) with 32-bit byte offsets
+    if (((int64_t)S + t.len + 128) * D * 2 > 0x7FFFFFFF)
+        return fail(FQ_ERR_UNSUPPORTED, "prefill over %lld keys exceeds one call's 2 GiB per-head K range",
+                    (long long)S + t.len);
     return FQ_OK;
 }
 
