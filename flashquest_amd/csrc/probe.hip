@@ -71,8 +71,10 @@ __global__ __launch_bounds__(512) void read_step_kernel(Int4Cache c, Workspace w
 
 hipError_t launch_read_step(const Int4Cache& c, const Workspace& ws, unsigned* sink, hipStream_t st) {
     const int groups = c.L * c.B * c.Hkv;
+    timer_before_launch(st);
     if (c.G == 4) hipLaunchKernelGGL(read_step_kernel<4>, dim3(groups), dim3(512), 0, st, c, ws, sink);
     else hipLaunchKernelGGL(read_step_kernel<1>, dim3(groups), dim3(512), 0, st, c, ws, sink);
+    timer_after_launch(st);
     return hipGetLastError();
 }
 
