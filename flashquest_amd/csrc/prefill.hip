@@ -24,6 +24,12 @@
 // the softmax statistics are per lane and P leaves the S^T accumulator already
 // in the layout of the P^T operand (keys 4g..4g+3 and 16+4g..16+4g+3 of a
 // 32-key step; V^T is read with the same key order).
+//
+// That single pass (prefill_attn_kernel) serves short prompts.  Longer ones
+// take two: prefill_dequant_kernel writes the attended keys once as dense
+// bf16 K and V^T, then prefill_dense_kernel runs the same products over
+// 128-key stages that direct-to-LDS buffer loads fill (no staging registers),
+// optionally split over key ranges with prefill_merge_kernel combining them.
 #include <algorithm>
 
 #include "fq_common.h"
