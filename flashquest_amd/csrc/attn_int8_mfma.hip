@@ -132,9 +132,13 @@ void attn_int8_mfma_kernel(Int8Params a) {
     __builtin_amdgcn_sched_barrier(0);
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
+    ScoreRowRegs<NREP, NT> srow;        // kSelectOnly: the group's precomputed scores
+    const bool from_scores = FUSED && a.sel.enabled == kSelectOnly;
+    const int score_rows = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
     if constexpr (FUSED) {
         ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
-        score_group_load<MT, NT>(sr, c, tid, l, b, h);
+        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        else score_group_load<MT, NT>(sr, c, tid, l, b, h);
     }
     float qv_raw;
     {
@@ -168,7 +172,9 @@ void attn_int8_mfma_kernel(Int8Params a) {
             s_qraw[qi >> 7][qi & 127] = qv_raw;
         }
         __syncthreads();
-        if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM)
+        if (from_scores)     // uniform: a scoring launch wrote the group's scores
+            scores_to_keys<NREP, NT>(srow, s_key, score_rows, c.P, tid);
+        else if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM)
             score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P, 255.0f);
         else
             score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P, 255.0f);

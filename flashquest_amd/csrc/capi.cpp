@@ -423,9 +423,9 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
 // Decode steps that split KV groups over several workgroups (too few groups
 // to fill the GPU) score each group once in a scoring launch over all CUs; the
 // attention workgroups then select from those scores (kSelectOnly) instead of
-// each re-scoring the group's pages.  INT4, unrotated.
+// each re-scoring the group's pages.  INT4 and INT8, unrotated.
 static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q) {
-    return c.L * c.B * c.Hkv < 192 && !q.rot && c.bits != 8;
+    return c.L * c.B * c.Hkv < 192 && !q.rot;
 }
 
 static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
