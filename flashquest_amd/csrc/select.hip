@@ -5,6 +5,7 @@
 //   scoring   src/flashquest/eager/criticality.py:128-163
 //   selection src/flashquest/eager/selection.py:65-126
 //   compact   src/flashquest/eager/selection.py:129-164
+#include "fused_common.h"
 #include "select_common.h"
 
 namespace fq {
@@ -321,6 +322,34 @@ __global__ __launch_bounds__(kThreads) void select_groups_wave_kernel(GroupSelec
 }
 
 // ---------------------------------------------------------------------------
+// The same selection for few groups (a single layer's decode step): one
+// 8-wave workgroup per group runs the in-LDS selection of the fused decode
+// (block_select_group), so the group's rows are searched by 8 waves instead of
+// one.  P <= 64 kSelC.  The list puts the forced pages first.
+// ---------------------------------------------------------------------------
+template <int NREP>
+__global__ __launch_bounds__(512) void select_groups_block_kernel(GroupSelectParams a) {
+    constexpr int NT = 512, NW = 8;
+    __shared__ uint32_t s_key[NREP * 64 * kSelC];
+    __shared__ BlockSelectLds s_bsel;
+    __shared__ int s_ent[64 * kSelC];
+    const int g = blockIdx.x, tid = threadIdx.x, P = a.P;
+    const int rows = a.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
+    ScoreRowRegs<NREP, NT> srow;
+    scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * P, rows, P, tid);
+    const float ret_l = group_retention(a, g)[min(lane_id(), NREP - 1)];     // lane r: head r's retention
+    scores_to_keys<NREP, NT>(srow, s_key, rows, P, tid);
+    __syncthreads();
+    const int n = block_select_group<kSelC, NW, NREP>(s_key, P, a.mode, ret_l, a.k_max, a.num_sinks, a.window, s_ent,
+                                                      s_bsel);
+    int* entries = a.ws.entries + (int64_t)g * P;
+    for (int i = tid; i < n; i += NT) entries[i] = s_ent[i];
+    if (a.mask_out)       // uniform; the keys are no longer needed: their LDS is the scratch
+        block_write_mask<NT, NREP>(s_ent, n, P, (uint8_t*)s_key, a.mask_out + (int64_t)g * NREP * P, tid);
+    if (tid == 0) a.ws.n_sel[g] = n;
+}
+
+// ---------------------------------------------------------------------------
 // Standalone selection: one workgroup per (b, h, s_q) score row.
 // ---------------------------------------------------------------------------
 struct SelectParams {
@@ -472,7 +501,14 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !ws || !select_groups) return e;
     const dim3 wgrid((G + kThreads / 64 - 1) / (kThreads / 64));
-    if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, wgrid, dim3(kThreads), 0, st, sp, G);
+    if (G < 192 && c.P <= 64 * kSelC && q.nrep <= 4) {     // few groups: a workgroup per group
+        switch (q.nrep) {
+            case 1: hipLaunchKernelGGL(select_groups_block_kernel<1>, dim3(G), dim3(512), 0, st, sp); break;
+            case 2: hipLaunchKernelGGL(select_groups_block_kernel<2>, dim3(G), dim3(512), 0, st, sp); break;
+            case 3: hipLaunchKernelGGL(select_groups_block_kernel<3>, dim3(G), dim3(512), 0, st, sp); break;
+            default: hipLaunchKernelGGL(select_groups_block_kernel<4>, dim3(G), dim3(512), 0, st, sp); break;
+        }
+    } else if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, wgrid, dim3(kThreads), 0, st, sp, G);
     else if (c.P <= 64 * 32) hipLaunchKernelGGL(select_groups_wave_kernel<32>, wgrid, dim3(kThreads), 0, st, sp, G);
     else hipLaunchKernelGGL(select_groups_kernel, dim3(G), dim3(kThreads), 0, st, sp);
     return hipGetLastError();
