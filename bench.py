@@ -251,6 +251,26 @@ def time_steps(fn_pre, fn_timed, steps, warmup, flush, kernel_timer=False):
     return sum(ms) / len(ms), wall, kernel_ms
 
 
+def per_layer_graph_ms(calls, steps, warmup, flush):
+    """The reference's per-layer call pattern: `calls` (one decode step per
+    layer, in order) captured once in a HIP graph; mean ms per replay."""
+    for f in calls:
+        f()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for f in calls:
+            f()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for f in calls:
+                f()
+    torch.cuda.synchronize()
+    ms, _, _ = time_steps(lambda: None, graph.replay, steps, warmup, flush)
+    return ms
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int4_mfma_config1_traffic.json")
 
 
@@ -464,21 +484,7 @@ def main():
         # the reference's per-layer call pattern: 28 sequential (select, attend) pairs in one HIP graph
         per_layer = [decoder(args.retention, k, args.select,
                              c={key: t[l] for key, t in cache.items()}) for l in range(L)]
-        for d in per_layer:
-            d()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            for d in per_layer:
-                d()
-            torch.cuda.synchronize()
-            with torch.cuda.graph(graph, stream=s):
-                for d in per_layer:
-                    d()
-        torch.cuda.synchronize()
-        pl_ms, _, _ = time_steps(noop, graph.replay, args.steps, args.warmup, flush)
-        extra["per_layer_graph_us"] = pl_ms * 1e3
+        extra["per_layer_graph_us"] = per_layer_graph_ms(per_layer, args.steps, args.warmup, flush) * 1e3
         # the same, with a 37-token bf16 partial page per layer (the usual decode
         # step): the tail is attended in the split-merge launch
         T_tail = 37
@@ -493,22 +499,8 @@ def main():
                                                                 "V_scale", "V_mn")], retention=args.retention,
                                     num_sinks=4, window_pages=2, k_max_static=k, select_mode=args.select,
                                     K_tail=kt[l], V_tail=vt[l]) for l in range(L)]
-        for d in per_layer_t:
-            d()
-        s2 = torch.cuda.Stream()
-        s2.wait_stream(torch.cuda.current_stream())
-        graph_t = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s2):
-            for d in per_layer_t:
-                d()
-            torch.cuda.synchronize()
-            with torch.cuda.graph(graph_t, stream=s2):
-                for d in per_layer_t:
-                    d()
-        torch.cuda.synchronize()
-        plt_ms, _, _ = time_steps(noop, graph_t.replay, args.steps, args.warmup, flush)
-        extra["per_layer_graph_with_tail_us"] = plt_ms * 1e3
-        del kt, vt, tdec, per_layer_t, graph_t
+        extra["per_layer_graph_with_tail_us"] = per_layer_graph_ms(per_layer_t, args.steps, args.warmup, flush) * 1e3
+        del kt, vt, tdec, per_layer_t
         sel_ms, _, _ = time_steps(noop, dec.select, args.steps, args.warmup, flush)
         extra["select_us"] = sel_ms * 1e3 if not dec.fused else None
         wflush = Flusher(dev, write=True)
@@ -564,6 +556,11 @@ def main():
             extra.update({f"turbo_{mode}_us": t_ms * 1e3, f"turbo_{mode}_union_pages_per_kv_head": t_union / (L * 8),
                           f"turbo_{mode}_step_GBps": t_bytes / (t_ms * 1e-3) / 1e9,
                           f"turbo_{mode}_roofline_frac": t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+            tkeys = ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo", "K_scale_raw", "K_mn_raw")
+            calls = [(lambda l=l: quest_decode_turbo(tc["Q"][l:l + 1], *[tc[x][l:l + 1] for x in tkeys],
+                                                     retention=args.retention, num_sinks=4, window_pages=2,
+                                                     k_max_static=k, select_mode=mode)) for l in range(L)]
+            extra[f"turbo_{mode}_per_layer_graph_us"] = per_layer_graph_ms(calls, args.steps, args.warmup, flush) * 1e3
 
         def turbo_ops_step():
             sc = page_scores_int4_fast(tc["Q"], tc["K_scale_raw"], tc["K_mn_raw"])
@@ -590,6 +587,11 @@ def main():
         extra.update({"int8_us": i_ms * 1e3, "int8_step_bytes": i_bytes,
                       "int8_step_GBps": i_bytes / (i_ms * 1e-3) / 1e9,
                       "int8_roofline_frac": i_bytes / (i_ms * 1e-3) / 1e9 / HBM_PEAK_GBS})
+        ikeys = ("Q", "K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")
+        calls = [(lambda l=l: quest_decode_int8(*[ic[x][l:l + 1] for x in ikeys], retention=args.retention,
+                                                num_sinks=4, window_pages=2, k_max_static=k,
+                                                select_mode=args.select)) for l in range(L)]
+        extra["int8_per_layer_graph_us"] = per_layer_graph_ms(calls, args.steps, args.warmup, flush) * 1e3
         del ic, iplanes
 
         # Prefill over the packed cache (the reference's S_q > 1 branch,
