@@ -209,7 +209,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     __shared__ uint16_t s_tk[TTOK][D], s_tv[TTOK][D];
     __shared__ float s_tp[NREP][TTOK];
     uint4 tkr[2], tvr[2];
-    const int tail_T = FUSED && a.tail.in_kernel ? a.tail.len : 0;
+    const int tail_T = FUSED && a.tail.in_kernel && split == 0 ? a.tail.len : 0;   // split 0 of a group attends it
     if constexpr (FUSED) {
         ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         const TailArgs& t = a.tail;
@@ -662,7 +662,8 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
         timer_after_launch(st);                                                                        \
         if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                     \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits, a.tail);                           \
+                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits,                                  \
+                               a.tail.in_kernel ? TailArgs{} : a.tail);                                 \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE
@@ -735,12 +736,14 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
         if (!mfma_select_in_kernel(c, q, al)) return hipErrorInvalidValue;
         a.sel = *sel;
         a.splits = fused_splits(groups, al.max_entries, al.s_max);
-        // one workgroup per group: the kernel attends a 16-bit tail itself
-        // (16-byte aligned rows, at least D apart), so no merge launch follows
+        // the kernel attends a 16-bit tail itself (16-byte aligned rows, at
+        // least D apart): with one workgroup per group no merge launch follows,
+        // with several, split 0 folds it into its partial and the merge has no
+        // tail work left
         const TailArgs& t = a.tail;
         const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
         auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
-        a.tail.in_kernel = a.splits == 1 && t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 &&
+        a.tail.in_kernel = t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 &&
                            t.vs[3] >= 128 && ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
                            2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
     }
