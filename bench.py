@@ -592,6 +592,13 @@ def main():
                                                 num_sinks=4, window_pages=2, k_max_static=k,
                                                 select_mode=args.select)) for l in range(L)]
         extra["int8_per_layer_graph_us"] = per_layer_graph_ms(calls, args.steps, args.warmup, flush) * 1e3
+        kt8 = torch.randn(L, 8, 37, 128, device=dev).bfloat16()      # a 37-token partial page per layer
+        vt8 = torch.randn(L, 8, 37, 128, device=dev).bfloat16()
+        calls = [(lambda l=l: quest_decode_int8(*[ic[x][l:l + 1] for x in ikeys], retention=args.retention,
+                                                num_sinks=4, window_pages=2, k_max_static=k, select_mode=args.select,
+                                                K_tail=kt8[l:l + 1], V_tail=vt8[l:l + 1])) for l in range(L)]
+        extra["int8_per_layer_graph_with_tail_us"] = per_layer_graph_ms(calls, args.steps, args.warmup, flush) * 1e3
+        del kt8, vt8
         del ic, iplanes
 
         # Prefill over the packed cache (the reference's S_q > 1 branch,

@@ -224,8 +224,7 @@ bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLa
 
 hipError_t launch_attn_int4(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                             const AttnLaunch& al, hipStream_t st, const SelectArgs* sel, const TailArgs* tail) {
-    if (c.bits == 8 && int8_mfma_supported(c, q, al) && !(tail && tail->len > 0))
-        return launch_attn_int8_mfma(c, q, ws, al, st, sel);
+    if (c.bits == 8 && int8_mfma_supported(c, q, al)) return launch_attn_int8_mfma(c, q, ws, al, st, sel, tail);
     if (mfma_supported(c, q, al)) return launch_attn_int4_mfma(c, q, ws, al, st, sel, tail);
     if ((sel && sel->enabled) || (tail && tail->len > 0)) return hipErrorInvalidValue;
     AttnParams a{};

@@ -46,6 +46,7 @@ struct Int8Params {
     Workspace ws;
     int splits;
     SelectArgs sel;
+    TailArgs tail;          // tail.len > 0: attended (in_kernel: by split 0 of each group, else the split merge)
 };
 
 // Per-wave LDS operands: q.k A digits of the current page [k-step][row][k-group,
@@ -101,7 +102,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int8_mfma_kernel(Int8Params a) {
     constexpr int D = 128, NW = 8, NT = 512;
     static_assert(NREP <= 4, "query heads per KV head");
-    __shared__ SplitLds<D, NREP, NW> s_split;
+    constexpr int NSLOT = FUSED ? NW + 1 : NW;      // the fused kernel's extra slot: the partial-page tail
+    constexpr int TTOK = FUSED ? kTailMax : 1;
+    __shared__ SplitLds<D, NREP, NSLOT> s_split;
     __shared__ WaveLds8 s_wave[NW];
     __shared__ int s_ent[kMaxWgPages];
     __shared__ float s_q[NREP][D];
@@ -135,8 +138,26 @@ void attn_int8_mfma_kernel(Int8Params a) {
     ScoreRowRegs<NREP, NT> srow;        // kSelectOnly: the group's precomputed scores
     const bool from_scores = FUSED && a.sel.enabled == kSelectOnly;
     const int score_rows = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
+    // Partial-page tail (tail.in_kernel, split 0 of a group): its <= 64 raw
+    // 16-bit K / V rows go to LDS with q.  The loads are unconditional: without
+    // a tail the buffer is empty and they read 0.
+    __shared__ uint16_t s_tk[TTOK][D], s_tv[TTOK][D];
+    __shared__ float s_tp[NREP][TTOK];
+    uint4 tkr[2], tvr[2];
+    const int tail_T = FUSED && a.tail.in_kernel && split == 0 ? a.tail.len : 0;
     if constexpr (FUSED) {
         ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
+        const TailArgs& t = a.tail;
+        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + h * t.ks[2]) : nullptr;
+        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + h * t.vs[2]) : nullptr;
+        const auto rk = make_rsrc(tkb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.ks[3] + 2 * D : 0);
+        const auto rv = make_rsrc(tvb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.vs[3] + 2 * D : 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + NT * u, tt = i >> 4, j = i & 15;       // token tt, bytes 16j .. 16j+15
+            tkr[u] = ld128(rk, (int)(2 * tt * t.ks[3]) + 16 * j);
+            tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
+        }
         if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
         else score_group_load<MT, NT>(sr, c, tid, l, b, h);
     }
@@ -170,6 +191,12 @@ void attn_int8_mfma_kernel(Int8Params a) {
         if (tid < NREP * D) {
             s_q[qi >> 7][qi & 127] = qv_raw * q.qk_scale;
             s_qraw[qi >> 7][qi & 127] = qv_raw;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + NT * u;
+            *(uint4*)&s_tk[i >> 4][8 * (i & 15)] = tkr[u];
+            *(uint4*)&s_tv[i >> 4][8 * (i & 15)] = tvr[u];
         }
         __syncthreads();
         if (from_scores)     // uniform: a scoring launch wrote the group's scores
@@ -413,8 +440,17 @@ void attn_int8_mfma_kernel(Int8Params a) {
             if (n16 == 0) { s_split.m[w][r] = m_run[r]; s_split.l[w][r] = ll; }
         }
     }
+    int nslots = NW;
+    if constexpr (FUSED) {
+        if (tail_T > 0) {       // uniform; the tail state is the merge's last slot
+            tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
+                                        s_split.l[NW], s_split.acc[NW]);
+            nslots = NW + 1;
+        }
+    }
     __syncthreads();
-    merge_waves_and_store<D, NREP, false, NW>(s_split, q, a.ws, g, l, b, h, split, a.splits > 1);
+    merge_waves_and_store<D, NREP, false, NSLOT, NT>(s_split, q, a.ws, g, l, b, h, split,
+                                                     a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel), nslots);
 }
 
 template <typename MT, bool FUSED>
@@ -425,9 +461,10 @@ hipError_t launch_int8_nrep(const Int8Params& a, dim3 grid, hipStream_t st) {
         timer_before_launch(st);                                                                        \
         hipLaunchKernelGGL((attn_int8_mfma_kernel<MT, N, FUSED>), grid, dim3(512), 0, st, a);           \
         timer_after_launch(st);                                                                         \
-        if (a.splits > 1)                                                                               \
+        if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                      \
             hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits, TailArgs{});                     \
+                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits,                                  \
+                               a.tail.in_kernel ? TailArgs{} : a.tail);                                 \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE
@@ -459,9 +496,10 @@ bool int8_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLau
 }
 
 hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
-                                 hipStream_t st, const SelectArgs* sel) {
+                                 hipStream_t st, const SelectArgs* sel, const TailArgs* tail) {
     Int8Params a{};
     a.c = c; a.q = q; a.ws = ws;
+    if (tail) a.tail = *tail;
     const int groups = c.L * c.B * c.Hkv;
     // one workgroup per group when the groups fill the GPU, else balanced slices
     // (at least 8 pages each) for about one workgroup per CU
@@ -474,6 +512,14 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
     if (fused) {
         if (!int8_select_in_kernel(c, q, al)) return hipErrorInvalidValue;
         a.sel = *sel;
+        // split 0 of each group attends a 16-bit tail itself (16-byte aligned
+        // rows, at least D apart); other tails are attended in the split merge
+        const TailArgs& t = a.tail;
+        const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
+        auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
+        a.tail.in_kernel = t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 && t.vs[3] >= 128 &&
+                           ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
+                           2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
     }
     if (c.meta_dtype == FQ_BF16)
         return fused ? launch_int8_nrep<bf16, true>(a, grid, st) : launch_int8_nrep<bf16, false>(a, grid, st);

@@ -486,7 +486,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     if (k_max > c.P) k_max = c.P;
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
-    if (tail && tail->len > 0 && !mfma_supported(c, q, al))
+    if (tail && tail->len > 0 && !(bits == 8 ? int8_mfma_supported(c, q, al) : mfma_supported(c, q, al)))
         return fail(FQ_ERR_UNSUPPORTED, "the fused tail needs the matrix-core attention layout");
     SelectArgs sel{};
     if (q.rot && !attn_selects_in_kernel(c, q, al))
@@ -507,25 +507,48 @@ int fq_quest_attend_int4(const fq_int4_cache* cache, const fq_query* query, cons
                         workspace_bytes_, stream);
 }
 
+// The partial-page tail of a decode step: validated here, attended by the
+// attention launch (inside the kernel or in the split merge).
+static int check_tail(const fq_tail* tail, const fq_int4_cache* cache, TailArgs& t) {
+    t = TailArgs{};
+    if (!tail || tail->len <= 0) return FQ_OK;
+    if (tail->len > kTailMax) return fail(FQ_ERR_UNSUPPORTED, "tail of %d tokens (at most %d)", tail->len, kTailMax);
+    if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
+    if (!is_float_dtype(tail->dtype)) return fail(FQ_ERR_INVALID, "tail dtype");
+    if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
+    if (cache && cache->D != tail->D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, cache->D);
+    t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
+    for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
+    return FQ_OK;
+}
+
+static int decode_with_tail(const fq_int4_cache* cache, const fq_query* query, const fq_tail* tail,
+                            const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                            int32_t select_mode, void* workspace, size_t workspace_bytes_, fq_stream_t stream,
+                            int bits) {
+    TailArgs t{};
+    int st = check_tail(tail, cache, t);
+    if (st) return st;
+    st = quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr, nullptr,
+                      workspace, workspace_bytes_, stream, bits);
+    if (st) return st;
+    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, t.len > 0 ? &t : nullptr,
+                        workspace, workspace_bytes_, stream, bits);
+}
+
 int fq_quest_decode_int4_tail(const fq_int4_cache* cache, const fq_query* query, const fq_tail* tail,
                               const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
                               int32_t select_mode, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
-    TailArgs t{};
-    if (tail && tail->len > 0) {
-        if (tail->len > kTailMax) return fail(FQ_ERR_UNSUPPORTED, "tail of %d tokens (at most %d)", tail->len, kTailMax);
-        if (!tail->k || !tail->v) return fail(FQ_ERR_INVALID, "tail K/V is NULL");
-        if (!is_float_dtype(tail->dtype)) return fail(FQ_ERR_INVALID, "tail dtype");
-        if (tail->k_strides[4] != 1 || tail->v_strides[4] != 1)
-            return fail(FQ_ERR_UNSUPPORTED, "tail channel axis must be contiguous");
-        t.k = tail->k; t.v = tail->v; t.dtype = tail->dtype; t.len = tail->len;
-        for (int i = 0; i < 4; ++i) { t.ks[i] = tail->k_strides[i]; t.vs[i] = tail->v_strides[i]; }
-        if (cache && cache->D != tail->D) return fail(FQ_ERR_INVALID, "tail head_dim %d != cache head_dim %d", tail->D, cache->D);
-    }
-    int st = fq_quest_select_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, nullptr,
-                                  nullptr, workspace, workspace_bytes_, stream);
-    if (st) return st;
-    return quest_attend(cache, query, retention, num_sinks, window_pages, k_max, select_mode, t.len > 0 ? &t : nullptr,
-                        workspace, workspace_bytes_, stream);
+    return decode_with_tail(cache, query, tail, retention, num_sinks, window_pages, k_max, select_mode, workspace,
+                            workspace_bytes_, stream, 4);
+}
+
+int fq_quest_decode_int8_tail(const fq_int8_cache* cache, const fq_query* query, const fq_tail* tail,
+                              const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                              int32_t select_mode, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+    return decode_with_tail(cache, query, tail, retention, num_sinks, window_pages, k_max, select_mode, workspace,
+                            workspace_bytes_, stream, 8);
 }
 
 int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,

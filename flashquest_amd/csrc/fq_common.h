@@ -288,7 +288,7 @@ bool attn_selects_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLa
 bool int8_mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool int8_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
-                                 hipStream_t st, const SelectArgs* sel);
+                                 hipStream_t st, const SelectArgs* sel, const TailArgs* tail = nullptr);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,

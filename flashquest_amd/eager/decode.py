@@ -130,18 +130,7 @@ def quest_decode_int4(
     if return_selection:
         mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
     ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q))
-    tail = None
-    if K_tail is not None and K_tail.shape[-2] > 0:
-        if return_selection:
-            raise ValueError("return_selection is not available together with a fused tail")
-        L.require_device(K_tail, V_tail)
-        if K_tail.shape != V_tail.shape or K_tail.dtype != V_tail.dtype or K_tail.shape[-1] != D:
-            raise AssertionError("K_tail / V_tail must share shape (..., H_kv, T, D) and dtype")
-        kt = K_tail if K_tail.stride(-1) == 1 else K_tail.contiguous()
-        vt = V_tail if V_tail.stride(-1) == 1 else V_tail.contiguous()
-        lead = 5 - kt.dim()
-        tail = L.Tail(kt.data_ptr(), L.strides(kt, 5, lead), vt.data_ptr(), L.strides(vt, 5, lead),
-                      L.dtype_code(kt.dtype), kt.shape[-2], D)
+    tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
     if tail is not None:
         L.check(L.lib().fq_quest_decode_int4_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
                                                   int(window_pages), k_max, L.SELECT_MODES[select_mode],
@@ -158,6 +147,24 @@ def quest_decode_int4(
     if return_selection:
         return O, lse_out, mask
     return O, lse_out
+
+
+def _tail(K_tail, V_tail, D, return_selection):
+    """The fused step's partial-page tail descriptor (None without a tail) and
+    the tensors it points into."""
+    if K_tail is None or K_tail.shape[-2] == 0:
+        return None, ()
+    if return_selection:
+        raise ValueError("return_selection is not available together with a fused tail")
+    L.require_device(K_tail, V_tail)
+    if K_tail.shape != V_tail.shape or K_tail.dtype != V_tail.dtype or K_tail.shape[-1] != D:
+        raise AssertionError("K_tail / V_tail must share shape (..., H_kv, T, D) and dtype")
+    kt = K_tail if K_tail.stride(-1) == 1 else K_tail.contiguous()
+    vt = V_tail if V_tail.stride(-1) == 1 else V_tail.contiguous()
+    lead = 5 - kt.dim()
+    tail = L.Tail(kt.data_ptr(), L.strides(kt, 5, lead), vt.data_ptr(), L.strides(vt, 5, lead),
+                  L.dtype_code(kt.dtype), kt.shape[-2], D)
+    return tail, (kt, vt)
 
 
 def _signs(rotation_signs, D, device):
@@ -211,13 +218,17 @@ def quest_decode_int8(
     return_lse: bool = True,
     return_selection: bool = False,
     head_pattern: torch.Tensor | None = None,
+    K_tail: torch.Tensor | None = None,
+    V_tail: torch.Tensor | None = None,
 ):
     """The INT8 decode step (llama_persistent_patch.py:143-160 with the
     selection of 196-245): page_scores_int8_fast -> select_pages_vectorized ->
     flash_attn_sparse_fwd over the completed pages, for one layer (Q
     (B,H_q,1,D), 4D cache) or L layers at once (Q (L,B,H_q,1,D), 5D cache).
-    ``select_mode`` and ``head_pattern`` as quest_decode_int4.  Returns (O like
-    Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P) bool])."""
+    ``select_mode``, ``head_pattern`` and ``K_tail`` / ``V_tail`` (the
+    partial page, attended and merged in the same step) as quest_decode_int4.
+    Returns (O like Q, lse (..., H_q, 1) fp32 or None[, mask (..., H_q, P)
+    bool])."""
     if select_mode not in L.SELECT_MODES:
         raise ValueError(f"select_mode must be one of {sorted(L.SELECT_MODES)}")
     L.require_device(Q, K_uint8, K_scale)
@@ -240,11 +251,18 @@ def quest_decode_int8(
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device) if return_selection else None
     ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q))
-    L.check(L.lib().fq_quest_decode_int8(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
-                                         L.SELECT_MODES[select_mode], None,
-                                         None if mask is None else mask.data_ptr(),
-                                         ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
-            "quest_decode_int8")
+    tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
+    if tail is not None:
+        L.check(L.lib().fq_quest_decode_int8_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
+                                                  int(window_pages), k_max, L.SELECT_MODES[select_mode],
+                                                  ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                "quest_decode_int8 (tail)")
+    else:
+        L.check(L.lib().fq_quest_decode_int8(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
+                                             L.SELECT_MODES[select_mode], None,
+                                             None if mask is None else mask.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                "quest_decode_int8")
     O = O3.unsqueeze(-2)
     lse_out = lse.unsqueeze(-1) if lse is not None else None
     if return_selection:
@@ -419,8 +437,15 @@ def sparse_decode_layer(q: torch.Tensor, views: dict, *, retention, num_sinks: i
     kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
               page_size=page_size, select_mode=select_mode, head_pattern=head_pattern)
     if "K_uint8" in views:                    # INT8 (kv_bits 8)
-        o_sparse, lse_sparse = quest_decode_int8(q, views["K_uint8"], views["K_scale"], views["K_mn"],
-                                                 views["V_uint8"], views["V_scale"], views["V_mn"], **kw)
+        args = (q, views["K_uint8"], views["K_scale"], views["K_mn"], views["V_uint8"], views["V_scale"],
+                views["V_mn"])
+        if partial > 0:
+            try:
+                o, _ = quest_decode_int8(*args, K_tail=views["K_partial"], V_tail=views["V_partial"], **kw)
+                return o
+            except NotImplementedError:
+                pass                          # layouts the fused tail does not take: three operators
+        o_sparse, lse_sparse = quest_decode_int8(*args, **kw)
     elif "K_msb" in views:                    # TurboQuant K3-V3 (kv_bits 3)
         o_sparse, lse_sparse = quest_decode_turbo(q, views["K_msb"], views["K_lsb"], views["K_scale_turbo"],
                                                   views["V_msb"], views["V_lsb"], views["V_scale_turbo"],

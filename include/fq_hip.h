@@ -298,6 +298,17 @@ int fq_quest_decode_int4_tail(const fq_int4_cache* cache, const fq_query* query,
                               int32_t k_max, int32_t select_mode,
                               void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* fq_quest_decode_int8 with the bf16 / fp16 partial-page tail attended and
+ * merged in the same step (no reference counterpart; the reference's decode
+ * branch runs the sparse INT8 attention, _bf16_dense_attn_with_lse and
+ * _merge_two_attentions, llama_persistent_patch.py:202-245).  Returns
+ * FQ_ERR_UNSUPPORTED for shapes the matrix-core INT8 kernel does not take
+ * (the caller then runs the three operators). */
+int fq_quest_decode_int8_tail(const fq_int8_cache* cache, const fq_query* query, const fq_tail* tail,
+                              const float* retention, int32_t num_sinks, int32_t window_pages,
+                              int32_t k_max, int32_t select_mode,
+                              void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
 /* Whether fq_quest_attend_int4 scores and selects the pages inside its one
  * attention kernel for these arguments (1; fq_quest_select_int4 then launches
  * nothing unless scores_out or mask_out is given) or consumes page lists left

@@ -94,3 +94,44 @@ def test_fused_tail_rejects_long_tails_and_selection_output():
     with pytest.raises(ValueError):
         quest_decode_int4(c.q_dev(), **c.device(), retention=0.5, K_tail=kt[:, :, :3], V_tail=kt[:, :, :3],
                           return_selection=True)
+
+
+@pytest.mark.parametrize("layers,T,tdt,mode", [(24, 37, "bf16", "per_kv_head_sum"),
+                                               (24, 64, "f16", "per_q_head"),
+                                               (24, 21, "f32", "per_q_head"),
+                                               (1, 1, "bf16", "per_q_head"),
+                                               (1, 50, "bf16", "per_kv_head_sum")])
+def test_int8_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode):
+    """The same for the INT8 cache (kv_bits 8): quest_decode_int8 with the
+    tail, one workgroup per group (the kernel attends the tail) or split groups
+    (split 0 of each group attends it), fp32 tails in the split merge."""
+    from flashquest_amd.eager.decode import quest_decode_int8
+    from tests.cases import Int8Case
+    rng = np.random.default_rng(70 + T)
+    Hq, Hkv, P = 24, 8, 14
+    cases = [Int8Case(seed=700 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128) for i in range(layers)]
+    tails = [(O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32)),
+              O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32))) for _ in range(layers)]
+    dev = [c.device() for c in cases]
+    if layers > 1:
+        stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+        q = torch.stack([c.q_dev() for c in cases])
+        kt = torch.stack([_dev(t[0], tdt) for t in tails])
+        vt = torch.stack([_dev(t[1], tdt) for t in tails])
+    else:
+        stacked, q = dev[0], cases[0].q_dev()
+        kt, vt = _dev(tails[0][0], tdt), _dev(tails[0][1], tdt)
+    o, lse = quest_decode_int8(q, **stacked, retention=0.3, num_sinks=2, window_pages=1, select_mode=mode,
+                               K_tail=kt, V_tail=vt)
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        ref = O.decode_step(c.Q, c.ku, c.ks, c.km, c.vu, c.vs, c.vm, retention=0.3, num_sinks=2, window_pages=1,
+                            mode=mode, bits=8)
+        ot, lt = O.dense_attn_with_lse(c.Q, tails[i][0], tails[i][1])
+        ro = O.merge_two_attentions(ref["O"], ref["lse"], ot, lt)
+        m = np.maximum(ref["lse"], lt)
+        rl = m + np.log(np.exp(ref["lse"] - m) + np.exp(lt - m))
+        oi = o[i] if layers > 1 else o
+        li = lse[i] if layers > 1 else lse
+        assert max_err(oi[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max(), i
+        assert max_err(li[:, :, 0], rl) <= 1e-4, i
