@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from flashquest_amd._lib import KernelTimer  # noqa: E402
-from flashquest_amd._ops import read_decode_pages  # noqa: E402
+from flashquest_amd._ops import read_decode_pages, read_stream  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import (quantize_k, quantize_k_int4, quantize_k_turbo, quantize_v,  # noqa: E402
                                             quantize_v_int4, quantize_v_turbo)
@@ -458,6 +458,10 @@ def main():
     planes = [cache[x] for x in ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")]
     rd_ms, _, rd_kernel_ms = time_steps(noop, lambda: read_decode_pages(*planes, mask), args.steps, args.warmup, flush,
                                         kernel_timer=True)
+    # the plainest read of the same byte count: one contiguous buffer, no pattern
+    sbuf = torch.empty((total_b + 15) // 16 * 16, dtype=torch.uint8, device=dev)
+    _, _, st_kernel_ms = time_steps(noop, lambda: read_stream(sbuf), args.steps, args.warmup, flush, kernel_timer=True)
+    del sbuf
     extra = {"self_check": check, "union_pages_per_kv_head": union / (L * B * 8), "step_bytes": total_b,
              "step_GBps": total_b / (step_ms * 1e-3) / 1e9,
              "step_roofline_frac": total_b / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -468,6 +472,9 @@ def main():
              "read_only_kernel_us": rd_kernel_ms * 1e3,
              "read_only_kernel_roofline_frac": total_b / (rd_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
              "attention_kernel_over_read_only_kernel": attn_ms / rd_kernel_ms,
+             "stream_read_kernel_us": st_kernel_ms * 1e3,
+             "stream_read_GBps": total_b / (st_kernel_ms * 1e-3) / 1e9,
+             "attention_kernel_over_stream_read": attn_ms / st_kernel_ms,
              "read_only_pass_with_union_us": rd_ms * 1e3}
     if not args.no_extra:
         extra.update(config0(args, dev, flush, noop))

@@ -161,3 +161,15 @@ def read_decode_pages(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask: to
     L.check(L.lib().fq_read_decode_pages(c, mask.data_ptr(), L.strides(mask, 4), H_q, sink.data_ptr(),
                                          ws.data_ptr(), ws.numel(), L.stream_handle(mask.device)),
             "read_decode_pages")
+
+
+def read_stream(buf: torch.Tensor) -> None:
+    """Measurement only (no counterpart in the reference): read the bytes of
+    the contiguous device tensor ``buf`` with plain streaming loads and compute
+    nothing -- the HBM read rate for that byte count with no access pattern."""
+    L.require_device(buf)
+    if not buf.is_contiguous():
+        raise ValueError("read_stream takes a contiguous tensor")
+    sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
+    nbytes = buf.numel() * buf.element_size()
+    L.check(L.lib().fq_read_stream(buf.data_ptr(), nbytes, sink.data_ptr(), L.stream_handle(buf.device)), "read_stream")

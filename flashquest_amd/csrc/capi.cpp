@@ -1065,4 +1065,11 @@ int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const 
     return hip_status(launch_read_step(c, ws, sink, s), "read decode pages");
 }
 
+int fq_read_stream(const void* buf, size_t bytes, uint32_t* sink, fq_stream_t stream) {
+    if (!buf || !sink) return fail(FQ_ERR_INVALID, "NULL buffer or sink");
+    if (((uintptr_t)buf & 15) || (bytes & 15) || bytes == 0)
+        return fail(FQ_ERR_INVALID, "the stream read takes a 16-byte aligned buffer of a nonzero multiple of 16 bytes");
+    return hip_status(launch_read_stream(buf, (int64_t)bytes, sink, (hipStream_t)stream), "read stream");
+}
+
 }  // extern "C"

@@ -249,6 +249,7 @@ hipError_t launch_select_rows(const float* scores, const int64_t* sc_s, int B, i
 hipError_t launch_compact_ids(const uint8_t* mask, const int64_t* m_s, int B, int H, int S_q, int P,
                               int bucket, int32_t* ids, hipStream_t st);
 hipError_t launch_read_step(const Int4Cache& c, const Workspace& ws, unsigned* sink, hipStream_t st);
+hipError_t launch_read_stream(const void* p, int64_t bytes, unsigned* sink, hipStream_t st);
 hipError_t launch_union_from_mask(const uint8_t* mask, const int64_t* m_s, int L, int B, int Hkv,
                                   int nrep, int P, const Workspace& ws, hipStream_t st);
 hipError_t launch_union_from_ids(const int32_t* ids, const int64_t* id_s, int bucket, int L, int B,

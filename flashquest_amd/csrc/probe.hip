@@ -8,6 +8,11 @@
 // decode, so the gap between the two is what scoring, selection and the
 // attention math add.  Every loaded word is folded into a value that is
 // stored only if it hits an unlikely constant, so no load is dead.
+//
+// read_stream_kernel is the plainest read of the same byte count: one
+// contiguous buffer, 2048 workgroups of 512 threads each streaming a
+// contiguous slice with four 16-byte loads in flight per thread -- the rate
+// HBM gives a read of this size with no access pattern at all.
 #include "fused_common.h"
 
 namespace fq {
@@ -67,7 +72,35 @@ __global__ __launch_bounds__(512) void read_step_kernel(Int4Cache c, Workspace w
     if (acc == 0x9e3779b9u) sink[0] = acc;
 }
 
+__global__ __launch_bounds__(512) void read_stream_kernel(const uint4* __restrict__ p, int64_t n16, int64_t per_wg,
+                                                         unsigned* sink) {
+    constexpr int NT = 512, U = 4;
+    const int64_t base = (int64_t)blockIdx.x * per_wg, end = min(base + per_wg, n16);
+    uint32_t acc = 0;
+    for (int64_t i = base + threadIdx.x; i < end; i += NT * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = min(i + (int64_t)u * NT, end - 1);
+            v[u] = p[j];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_read_stream(const void* p, int64_t bytes, unsigned* sink, hipStream_t st) {
+    const int64_t n16 = bytes / 16;
+    constexpr int kWgs = 2048;
+    const int64_t per = (n16 + kWgs - 1) / kWgs;
+    timer_before_launch(st);
+    hipLaunchKernelGGL(read_stream_kernel, dim3(kWgs), dim3(512), 0, st, (const uint4*)p, n16, per, sink);
+    timer_after_launch(st);
+    return hipGetLastError();
+}
 
 hipError_t launch_read_step(const Int4Cache& c, const Workspace& ws, unsigned* sink, hipStream_t st) {
     const int groups = c.L * c.B * c.Hkv;

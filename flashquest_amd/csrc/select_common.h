@@ -171,8 +171,8 @@ FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
 // (P <= 64 C pages, NW waves).  keys[r * 64 C + p] holds sortable_key of row
 // r's score of page p, and 0 (below every score) for p >= P.  Every wave loads
 // every key (C per lane per row); wave r finds row r's k-th largest key with
-// wave_kth_largest (no barrier inside), or, for one row in 8 waves, all waves
-// find it together (block_kth_largest); the thresholds meet in LDS, and every
+// wave_kth_hist (no barrier inside; for one row every wave finds it, so no
+// wave waits on another); the thresholds meet in LDS, and every
 // wave then ranks the ties and lists the pages.  Ties and forced pages follow
 // wave_topk / wave_select_group; the entry list holds the forced pages first,
 // then the other selected pages, each part ascending; wave w writes the entries
@@ -181,50 +181,106 @@ FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
 // per query head.  ret_l: lane r holds query head r's retention.  All control
 // flow is wave-uniform.  Ends with a barrier; returns the list length in
 // every thread.
-struct BlockSelectLds {
+struct alignas(16) BlockSelectLds {
     uint32_t T[4];          // k-th largest key per row
-    int cnt[2][16];         // block_kth_largest: per-round candidate counts (double-buffered)
+    uint32_t hist[8][256];  // wave_kth_hist: one 256-bin digit histogram per wave
 };
 
-// The k-th largest of the keys (k >= 1) by all 8 waves of the workgroup, each
-// holding every key (C per lane): a radix-16 search from the top digit, where
-// wave w counts the keys reaching candidate digits w + 1 and w + 9 and the
-// counts meet in LDS (one barrier per digit).  T keeps the largest prefix
-// that at least k keys reach; the search stops early once exactly k keys
-// reach T (then {key >= T} is the top-k set with no tie across its boundary,
-// which the callers' rule -- keys above T, then ties at T by page index up to
-// k -- selects unchanged).  Otherwise T ends as the k-th largest key, as with
-// wave_kth_largest.  Wave-uniform.
+// DPP moves across a whole wave (gfx9 row broadcasts) and wave reductions
+// built on them: no LDS traffic, only VALU latency.
+template <int CTRL, int ROWS = 0xF> FQ_DEV int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+// Inclusive prefix sum over lanes 0..lane.
+FQ_DEV int wave_incl_sum(int v) {
+    v += dpp_i<kDppRowShr1>(v);
+    v += dpp_i<kDppRowShr2>(v);
+    v += dpp_i<kDppRowShr4>(v);
+    v += dpp_i<kDppRowShr8>(v);             // every row of 16 lanes scanned
+    v += dpp_i<kDppRowBcast15, 0xA>(v);     // rows 1 and 3 add the row before's total
+    v += dpp_i<kDppRowBcast31, 0xC>(v);     // rows 2 and 3 add rows 0-1's total
+    return v;
+}
+// Wave-wide minimum / maximum of an unsigned value, returned wave-uniform.
+FQ_DEV uint32_t wave_min_u32(uint32_t v) {
+    int x = (int)v;
+    x = (int)min((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppXor1, 0xF, 0xF, false));
+    x = (int)min((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppXor2, 0xF, 0xF, false));
+    x = (int)min((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppHalfMirror, 0xF, 0xF, false));
+    x = (int)min((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppMirror, 0xF, 0xF, false));
+    const uint32_t a = min((uint32_t)__builtin_amdgcn_readlane(x, 0), (uint32_t)__builtin_amdgcn_readlane(x, 16));
+    const uint32_t b = min((uint32_t)__builtin_amdgcn_readlane(x, 32), (uint32_t)__builtin_amdgcn_readlane(x, 48));
+    return min(a, b);
+}
+FQ_DEV uint32_t wave_max_u32(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppXor1, 0xF, 0xF, false));
+    x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppXor2, 0xF, 0xF, false));
+    x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppHalfMirror, 0xF, 0xF, false));
+    x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_update_dpp(x, x, kDppMirror, 0xF, 0xF, false));
+    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane(x, 0), (uint32_t)__builtin_amdgcn_readlane(x, 16));
+    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane(x, 32), (uint32_t)__builtin_amdgcn_readlane(x, 48));
+    return max(a, b);
+}
+
+// The k-th largest of the wave's 64 C keys (1 <= k <= 64 C) by one wave with
+// no barrier: most-significant-digit radix selection in 8-bit digits, each
+// digit's counts gathered in the wave's own 256-bin LDS histogram (hist: 256
+// words used by this wave only) and located by a wave prefix sum.  The bits
+// every key shares (the common prefix of the smallest and largest key) are
+// skipped, and the search stops once the keys reaching the current prefix are
+// exactly k (then T has exactly k keys >= T); otherwise T ends as the k-th
+// largest key -- the contract the callers rely on: keys above T, then ties at
+// T by page index, give the top k.  Wave-uniform; hist is left zeroed.
 template <int C>
-FQ_DEV uint32_t block_kth_largest(const uint32_t (&key)[C], int k, BlockSelectLds& sl) {
-    const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
-    uint32_t T = 0;
-    for (int round = 0; round < 8; ++round) {
-        const int shift = 28 - 4 * round;
-        const int d0 = w + 1, d1 = w + 9;          // d1 = 16 (wave 7) tests nothing
-        const uint32_t c0 = T | ((uint32_t)d0 << shift), c1 = T | ((uint32_t)(d1 & 15) << shift);
-        int n0 = 0, n1 = 0;
+FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist) {
+    const int lane = lane_id();
+    uint32_t lo = key[0], hi = key[0];
 #pragma unroll
-        for (int j = 0; j < C; ++j) {
-            n0 += __popcll(__ballot(key[j] >= c0));
-            n1 += __popcll(__ballot(key[j] >= c1));
-        }
-        int* cnt = sl.cnt[round & 1];
-        if (lane == 0) {
-            cnt[d0] = n0;
-            if (d1 < 16) cnt[d1] = n1;
-        }
-        __syncthreads();
-        const bool live = lane >= 1 && lane < 16;
-        const int cl = live ? cnt[lane] : 0;
-        const uint64_t ok = __ballot(live && cl >= k);       // counts fall as the digit rises
-        if (ok) {
-            const int d = 63 - __clzll(ok);
-            T |= (uint32_t)d << shift;
-            if (__builtin_amdgcn_readlane(cl, d) == k) break;
-        }
+    for (int j = 1; j < C; ++j) { lo = min(lo, key[j]); hi = max(hi, key[j]); }
+    lo = wave_min_u32(lo);
+    hi = wave_max_u32(hi);
+    if (lo == hi) return hi;
+    int b = 31 - __clz(lo ^ hi);                    // bits above b are the same in every key
+    uint32_t prefix = hi & ~((2u << b) - 1u);
+    int need = k;                                   // keys still to take from those matching prefix above b
+    uint32_t* const mine = hist + 252 - 4 * lane;   // lane l: digits 255 - 4l - m at mine[3 - m]
+    *(uint4*)mine = make_uint4(0u, 0u, 0u, 0u);
+    for (;;) {
+        const int shift = b >= 7 ? b - 7 : 0;       // this round's digit: bits [shift, b]
+        const uint32_t dmask = (2u << (b - shift)) - 1u;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+            if ((((key[j] ^ prefix) >> b) >> 1) == 0u)
+                __hip_atomic_fetch_add(&hist[(key[j] >> shift) & dmask], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WAVEFRONT);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const uint4 h = *(const uint4*)mine;
+        *(uint4*)mine = make_uint4(0u, 0u, 0u, 0u);
+        const int c0 = (int)h.w, c1 = (int)h.z, c2 = (int)h.y, c3 = (int)h.x;   // digits 255-4l, -1, -2, -3
+        const int tot = c0 + c1 + c2 + c3;
+        const int incl = wave_incl_sum(tot);       // keys with digit >= 252 - 4l (lanes 0..l)
+        const int above = incl - tot;
+        const uint64_t hit = __ballot(incl >= need);
+        const int ls = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));   // the total is >= need
+        // in lane ls (above < need <= incl): the first digit, from the top, that
+        // brings the count to need; ab = keys above it, cd = keys on it
+        int m = 3, ab = above + c0 + c1 + c2, cd = c3;
+        if (above + c0 + c1 + c2 >= need) { m = 2; ab = above + c0 + c1; cd = c2; }
+        if (above + c0 + c1 >= need) { m = 1; ab = above + c0; cd = c1; }
+        if (above + c0 >= need) { m = 0; ab = above; cd = c0; }
+        const int m_s = __builtin_amdgcn_readlane(m, ls);
+        const int ab_s = __builtin_amdgcn_readlane(ab, ls);
+        const int cd_s = __builtin_amdgcn_readlane(cd, ls);
+        prefix |= (uint32_t)(255 - 4 * ls - m_s) << shift;
+        need -= ab_s;
+        if (cd_s == need || shift == 0) return prefix;
+        b = shift - 1;
     }
-    return T;
 }
 
 template <int C, int NW, int NROWS, int NREP>
@@ -244,23 +300,22 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
 #pragma unroll
     for (int r = 0; r < NREP; ++r) rmax = fmaxf(rmax, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)));
 #pragma unroll
-    for (int r = 0; r < NROWS; ++r) {
+    for (int r = 0; r < NROWS; ++r)
         k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
-        if constexpr (NROWS == 1 && NW == 8) {      // one row: every wave takes part
-            if (k[r] > 0) {
-                const uint32_t t = block_kth_largest<C>(key[r], k[r], sl);
-                if (w == 0 && lane == 0) sl.T[r] = t;
-            } else if (w == 0 && lane == 0) {
-                sl.T[r] = 0u;
-            }
-        } else if (w == r) {
-            const uint32_t t = k[r] > 0 ? wave_kth_largest<C>(key[r], k[r]) : 0u;
-            if (lane == 0) sl.T[r] = t;
-        }
-    }
-    __syncthreads();
+    if constexpr (NROWS == 1) {      // one row: every wave finds the threshold itself
+        T[0] = k[0] > 0 ? wave_kth_hist<C>(key[0], k[0], sl.hist[w]) : 0u;
+    } else {                         // wave r finds row r's, shared through LDS
 #pragma unroll
-    for (int r = 0; r < NROWS; ++r) T[r] = sl.T[r];
+        for (int r = 0; r < NROWS; ++r) {
+            if (w == r) {
+                const uint32_t t = k[r] > 0 ? wave_kth_hist<C>(key[r], k[r], sl.hist[w]) : 0u;
+                if (lane == 0) sl.T[r] = t;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < NROWS; ++r) T[r] = sl.T[r];
+    }
     // ties at T: the lowest page indices (wave_topk's rule); identical in every wave
     uint8_t qm[C];
 #pragma unroll

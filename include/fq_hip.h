@@ -221,6 +221,13 @@ int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* que
 int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
                          int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* Measurement only; no counterpart in the reference.  Reads `bytes` (a
+ * nonzero multiple of 16) of one contiguous, 16-byte aligned device buffer
+ * with plain streaming loads and computes nothing: the rate HBM gives a read
+ * of that size with no access pattern, the reference point for
+ * fq_read_decode_pages.  `sink` as there. */
+int fq_read_stream(const void* buf, size_t bytes, uint32_t* sink, fq_stream_t stream);
+
 /* The two halves of fq_quest_decode_int4, for callers that time or overlap
  * them separately; call both with the same cache, query, retention, k_max,
  * num_sinks, window_pages, select_mode and workspace.  fq_quest_select_int4

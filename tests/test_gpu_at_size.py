@@ -274,3 +274,15 @@ def test_read_only_pass_runs_on_config1(cfg1):
     for _ in range(2):
         read_decode_pages(*planes, mask)
     torch.cuda.synchronize()
+
+
+def test_stream_read_probe_runs_and_checks_its_buffer():
+    """The bench's plain-read reference (fq_read_stream) reads a config-1-sized
+    buffer, and refuses sizes that are not whole 16-byte chunks."""
+    from flashquest_amd._ops import read_stream
+    buf = torch.zeros(332717696, dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        read_stream(buf)
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError):
+        read_stream(buf[:100])
