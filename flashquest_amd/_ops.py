@@ -132,6 +132,12 @@ def retention_rows(retention, head_pattern, H_q: int, H_kv: int, layers: int, de
     return rows, (H_q if rows.dim() == 2 else 0)
 
 
+# Device (H,) vectors of scalar retentions, made once per (value, H, device):
+# a decode step per layer would otherwise launch a fill kernel every call.
+# The kernels only read them.
+_scalar_retention: dict = {}
+
+
 def retention_tensor(retention, H: int, device) -> torch.Tensor:
     """selection.py:92-101: scalar in [0, 1] or a (H,) tensor -> device fp32 (H,)."""
     if isinstance(retention, torch.Tensor):
@@ -140,7 +146,17 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
         return retention.to(device=device, dtype=torch.float32)
     if not (0.0 <= float(retention) <= 1.0):
         raise ValueError(f"scalar retention must be in [0, 1]; got {retention}")
-    return torch.full((H,), float(retention), dtype=torch.float32, device=device)
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    key = (float(retention), H, device.type, device.index)
+    r = _scalar_retention.get(key)
+    if r is None:
+        r = torch.full((H,), float(retention), dtype=torch.float32, device=device)
+        # a tensor made during HIP graph capture lives in the graph's pool: not kept
+        if not (device.type == "cuda" and torch.cuda.is_current_stream_capturing()):
+            _scalar_retention[key] = r
+    return r
 
 
 def read_decode_pages(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask: torch.Tensor,

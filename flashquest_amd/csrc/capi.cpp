@@ -882,6 +882,18 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     }
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};
+    if (fusable && c.P <= 64 * 8 && attention_splits_request() <= 0) {   // the in-kernel selection holds 512 pages
+        // few groups (a single layer's step): the scoring launch writes the
+        // scores, the attention workgroups of each group select from them
+        st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
+                                     k_max, nullptr, s, false),
+                        "page scores");
+        if (st) return st;
+        SelectArgs sel{};
+        sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
+        sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kSelectOnly; sel.mask_out = mask_out;
+        return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, &sel, s), "quest turbo decode");
+    }
     st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                  k_max, mask_out, s),
                     "score+select");

@@ -148,9 +148,13 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     __builtin_amdgcn_sched_barrier(0);
     float ret_l = 0.f;
     ScoreRegs<NT> sr;
+    ScoreRowRegs<NREP, NT> srow;        // kSelectOnly: the group's scores from the scoring launch
+    const bool from_scores = FUSED && a.sel.enabled == kSelectOnly;
+    const int score_rows = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
     if constexpr (FUSED) {
         ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
-        score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
+        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        else score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
     }
     float qv_raw;
     {
@@ -233,24 +237,30 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     TurboPage b0, b1;
     bool first_issued = false;
 
-    int e0, e1;
+    int e0, e1, ent_base = 0;          // this split's entries are s_ent[ent_base ..]
     if constexpr (FUSED) {
+        // scores (this workgroup's own, or the scoring launch's), then the
+        // selection; every split of a group selects the same list and takes
+        // the balanced slice [e0, e1) of it
         __shared__ uint32_t s_key[NREP * 64 * kSelC];
         __shared__ BlockSelectLds s_bsel;
-        if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<bf16, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+        if (from_scores) scores_to_keys<NREP, NT>(srow, s_key, score_rows, c.P, tid);
+        else if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<bf16, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
         else score_group_regs<bf16, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
         const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
-        if (S > 0 && w < fp.count) {
+        if (S > 0 && split == 0 && w < fp.count) {   // split 0's first entries are the forced pages
             issue_page(b0, fp.page(w));
             first_issued = true;
         }
         __syncthreads();
-        e0 = 0;
-        e1 = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max, a.sel.num_sinks,
-                                                 a.sel.window, s_ent, s_bsel);
-        if (a.sel.mask_out)                          // uniform: the caller asked for the selection
-            block_write_mask<NT, NREP>(s_ent, e1, c.P, (uint8_t*)s_key, a.sel.mask_out + (int64_t)g * NREP * c.P,
+        const int total = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max,
+                                                              a.sel.num_sinks, a.sel.window, s_ent, s_bsel);
+        if (a.sel.mask_out && split == 0)            // uniform: the caller asked for the selection
+            block_write_mask<NT, NREP>(s_ent, total, c.P, (uint8_t*)s_key, a.sel.mask_out + (int64_t)g * NREP * c.P,
                                        tid);
+        e0 = (int)((int64_t)total * split / a.splits);
+        e1 = (int)((int64_t)total * (split + 1) / a.splits);
+        ent_base = e0;
     } else {
         const int n_sel = a.ws.n_sel[g];
         e0 = (int)((int64_t)n_sel * split / a.splits);
@@ -288,7 +298,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         else { tl1 |= (bits & 0xFFu) << (8 * (v - 4)); th1 |= (bits >> 8) << (8 * (v - 4)); }
     }
 
-    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[w + NW * k]); };
+    auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[ent_base + w + NW * k]); };
 
     float m_run[NREP];
 #pragma unroll
@@ -504,18 +514,28 @@ bool turbo_fused_supported(const fq_turbo_cache& c, const QueryArgs& q) {
 }
 
 // Pages from the workspace lists (splits per group chosen like the INT4
-// matrix-core kernel), or, with raw != null and sel, scored and selected in the
-// kernel (one workgroup per group).
+// matrix-core kernel); with sel = kScoreSelect and raw, scored and selected in
+// the kernel (one workgroup per group); with sel = kSelectOnly, selected in the
+// kernel from the scores a scoring launch left in the workspace, each group
+// split over workgroups like the INT4 kernel's split steps.
 hipError_t launch_attn_turbo_fused(const fq_turbo_cache& c, const Int4Cache* raw, const QueryArgs& q,
                                    const Workspace& ws, int max_entries, const SelectArgs* sel, hipStream_t st) {
     TurboFusedParams a{};
     a.c = c; a.q = q; a.ws = ws;
     const int groups = c.L * c.B * c.H_kv;
-    if (raw && sel && sel->enabled) {
+    if (sel && sel->enabled == kScoreSelect && raw) {
         a.raw = *raw;
         a.sel = *sel;
         a.splits = 1;
         return launch_turbo_fused_nrep<true>(a, dim3(1, groups), st);
+    }
+    if (sel && sel->enabled == kSelectOnly) {
+        if (c.P > 64 * kSelC) return hipErrorInvalidValue;
+        a.sel = *sel;
+        int s = (256 + groups - 1) / std::max(groups, 1);
+        s = std::min(s, (max_entries + 7) / 8);
+        a.splits = std::max(1, std::min(s, ws.s_max));
+        return launch_turbo_fused_nrep<true>(a, dim3(a.splits, groups), st);
     }
     int s = groups >= 192 ? 1 : (512 + groups - 1) / groups;
     s = std::min(s, (max_entries + 7) / 8);
