@@ -236,13 +236,14 @@ FQ_DEV uint32_t wave_max_u32(uint32_t v) {
 // largest key -- the contract the callers rely on: keys above T, then ties at
 // T by page index, give the top k.  Wave-uniform; hist is left zeroed.
 template <int C>
-FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist) {
+FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, bool* exact = nullptr) {
     const int lane = lane_id();
     uint32_t lo = key[0], hi = key[0];
 #pragma unroll
     for (int j = 1; j < C; ++j) { lo = min(lo, key[j]); hi = max(hi, key[j]); }
     lo = wave_min_u32(lo);
     hi = wave_max_u32(hi);
+    if (exact) *exact = false;
     if (lo == hi) return hi;
     int b = 31 - __clz(lo ^ hi);                    // bits above b are the same in every key
     uint32_t prefix = hi & ~((2u << b) - 1u);
@@ -278,7 +279,11 @@ FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist) {
         const int cd_s = __builtin_amdgcn_readlane(cd, ls);
         prefix |= (uint32_t)(255 - 4 * ls - m_s) << shift;
         need -= ab_s;
-        if (cd_s == need || shift == 0) return prefix;
+        if (cd_s == need) {          // exactly k keys are >= prefix
+            if (exact) *exact = true;
+            return prefix;
+        }
+        if (shift == 0) return prefix;
         b = shift - 1;
     }
 }
@@ -302,8 +307,9 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
 #pragma unroll
     for (int r = 0; r < NROWS; ++r)
         k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
+    bool exact = false;              // one row: exactly k keys >= T, no ties to rank
     if constexpr (NROWS == 1) {      // one row: every wave finds the threshold itself
-        T[0] = k[0] > 0 ? wave_kth_hist<C>(key[0], k[0], sl.hist[w]) : 0u;
+        T[0] = k[0] > 0 ? wave_kth_hist<C>(key[0], k[0], sl.hist[w], &exact) : 0u;
     } else {                         // wave r finds row r's, shared through LDS
 #pragma unroll
         for (int r = 0; r < NROWS; ++r) {
@@ -320,6 +326,10 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
     uint8_t qm[C];
 #pragma unroll
     for (int j = 0; j < C; ++j) qm[j] = 0;
+    if (exact) {         // uniform
+#pragma unroll
+        for (int j = 0; j < C; ++j) qm[j] = key[0][j] >= T[0] ? kAll : (uint8_t)0;
+    } else
 #pragma unroll
     for (int r = 0; r < NROWS; ++r) {
         if (k[r] <= 0) continue;
