@@ -326,13 +326,17 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         const int ent = entry_of(k);
         const int p = ent & 0xFFFF, qm = ent >> 16;
         const int tok0 = p * 64;
-        // ---- q.k
+        // ---- q.k: the four 16-token tiles' accumulation chains interleaved
+        // (k-step outer), so four independent matrix instructions are in flight;
+        // each tile still accumulates its k-steps in order
         float lg4[4], mp = -INFINITY;
+        v4f acc[4];
 #pragma unroll
-        for (int T = 0; T < 4; ++T) {
-            v4f acc = {0.f, 0.f, 0.f, 0.f};
+        for (int T = 0; T < 4; ++T) acc[T] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
+        for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+            for (int T = 0; T < 4; ++T) {
                 // table entry of channels 32 lg + 4 kk .. + 3: their LSB byte, MSB nibble
                 const uint32_t lw = (kk >> 2) ? pb.kl[T].y : pb.kl[T].x;
                 const int lsh = 8 * (kk & 3) - 4, msh = 4 * kk - 12;      // entry * 16, in bytes
@@ -340,9 +344,12 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
                 const uint32_t a_m = (msh >= 0 ? pb.km[T] >> msh : pb.km[T] << -msh) & 0xF000u;
                 const uint4 e = *(const uint4*)((const char*)s_lut + (a_l | a_m));
                 const v8h B = __builtin_bit_cast(v8h, (v4i){(int)e.x, (int)e.y, (int)e.z, (int)e.w});
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[kk], B, acc, 0, 0, 0);
+                acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[kk], B, acc[T], 0, 0, 0);
             }
-            const float lgt = (acc[0] + acc[1]) * bf16_bits_to_f(pb.ks[T] & 0xFFFFu);
+        }
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            const float lgt = (acc[T][0] + acc[T][1]) * bf16_bits_to_f(pb.ks[T] & 0xFFFFu);
             const bool ok = lg < NREP && ((qm >> lg) & 1) && tok0 + 16 * T + n16 < S;
             lg4[T] = ok ? lgt : -INFINITY;
             mp = fmaxf(mp, lg4[T]);
