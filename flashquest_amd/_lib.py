@@ -25,6 +25,9 @@ SELECT_MODES = {"per_q_head": FQ_SELECT_PER_Q_HEAD, "per_kv_head_sum": FQ_SELECT
 _I64x3 = ctypes.c_int64 * 3
 _I64x4 = ctypes.c_int64 * 4
 _I64x5 = ctypes.c_int64 * 5
+I64x5 = _I64x5
+I64x4 = _I64x4
+I64x3 = _I64x3
 
 
 class Int4Cache(ctypes.Structure):
@@ -221,10 +224,17 @@ def i64(values, n: int):
     return (ctypes.c_int64 * n)(*vals)
 
 
+_I64_ARRAYS = {n: ctypes.c_int64 * n for n in range(1, 9)}
+
+
 def strides(t: torch.Tensor, n: int | None = None, lead: int = 0):
     """Element strides of t, left-padded with `lead` zeros (broadcast axes)."""
-    s = [0] * lead + list(t.stride())
-    return i64(s, n if n is not None else len(s))
+    st = t.stride()
+    if n is None:
+        n = lead + len(st)
+    elif lead + len(st) != n:
+        raise ValueError(f"expected {n} strides, got {lead + len(st)}")
+    return _I64_ARRAYS[n](*((0,) * lead + st))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
@@ -232,7 +242,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_handle(device: torch.device | None = None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw HIP stream torch currently launches on for `device`."""
+    idx = device.index if isinstance(device, torch.device) else device
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def require_device(*tensors: torch.Tensor) -> None:
@@ -245,7 +259,7 @@ def require_device(*tensors: torch.Tensor) -> None:
 _ws: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Per-(device, stream) scratch buffer, zero-initialised when (re)allocated.
 
     Every region a call reads (selection lists, counts, split partials) is
@@ -253,7 +267,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     without clearing.  Calls that overlap on one stream are serialised by the
     stream; distinct streams get distinct buffers.
     """
-    key = (device.index, stream_handle(device))
+    key = (device.index, stream_handle(device) if stream is None else stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():

@@ -10,8 +10,15 @@ from . import _lib as L
 
 def _ensure_inner_contiguous(t: torch.Tensor, align_elems: int = 1) -> torch.Tensor:
     """Kernels need a unit-stride innermost axis and aligned rows; copy otherwise."""
-    if t.stride(-1) != 1 or any(s % align_elems for s in t.stride()[:-1]) or \
-            t.data_ptr() % (align_elems * t.element_size()):
+    st = t.stride()
+    ok = st[-1] == 1
+    if ok and align_elems > 1:
+        for s in st[:-1]:
+            if s % align_elems:
+                ok = False
+                break
+        ok = ok and t.data_ptr() % (align_elems * t.element_size()) == 0
+    if not ok:
         # a fresh copy: contiguous() would return a contiguous but misaligned view unchanged
         return t.clone(memory_format=torch.contiguous_format)
     return t
@@ -39,20 +46,17 @@ def int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size: int)
     if ks.dtype not in (torch.bfloat16, torch.float16):
         raise AssertionError(f"metadata dtype must be bf16 or fp16, got {ks.dtype}")
     lead = _lead(kp, 5)
-    c = L.Int4Cache()
-    c.k_packed, c.k_strides = kp.data_ptr(), L.strides(kp, 5, lead)
-    c.v_packed, c.v_strides = vp.data_ptr(), L.strides(vp, 5, lead)
-    c.k_scale, c.ks_strides = ks.data_ptr(), L.strides(ks, 5, lead)
-    c.k_mn, c.km_strides = km.data_ptr(), L.strides(km, 5, lead)
-    c.v_scale, c.vs_strides = vs.data_ptr(), L.strides(vs, 5, lead)
-    c.v_mn, c.vm_strides = vm.data_ptr(), L.strides(vm, 5, lead)
-    c.meta_dtype = L.dtype_code(ks.dtype)
+    nd = kp.dim()
+    if vp.dim() != nd or ks.dim() != nd or km.dim() != nd or vs.dim() != nd or vm.dim() != nd:
+        raise ValueError("the six cache tensors must have the same number of dimensions")
+    pad = (0,) * lead
+    a5 = L.I64x5
     shape = (1,) * lead + tuple(kp.shape)
-    c.L, c.B, c.H_kv, c.S = shape[0], shape[1], shape[2], shape[3]
-    c.D = kp.shape[-1] * 2
-    c.P = ks.shape[-2]
-    c.page_size = int(page_size)
-    c.v_groups = vs.shape[-1]
+    c = L.Int4Cache(kp.data_ptr(), a5(*(pad + kp.stride())), vp.data_ptr(), a5(*(pad + vp.stride())),
+                    ks.data_ptr(), a5(*(pad + ks.stride())), km.data_ptr(), a5(*(pad + km.stride())),
+                    vs.data_ptr(), a5(*(pad + vs.stride())), vm.data_ptr(), a5(*(pad + vm.stride())),
+                    L.dtype_code(ks.dtype), shape[0], shape[1], shape[2], shape[3], ks.shape[-2],
+                    shape[4] * 2, int(page_size), vs.shape[-1])
     return c, (kp, vp, ks, km, vs, vm)
 
 
@@ -96,16 +100,15 @@ def turbo_cache(K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale, num_pages: int, pa
 def query(Q3: torch.Tensor, O3: torch.Tensor, lse: torch.Tensor | None, sm_scale: float | None):
     """Q3/O3: (B, H_q, D) or (L, B, H_q, D); lse: (B, H_q) / (L, B, H_q) or None."""
     lead = 4 - Q3.dim()
-    q = L.Query()
-    q.q, q.q_dtype, q.q_strides = Q3.data_ptr(), L.dtype_code(Q3.dtype), L.strides(Q3, 4, lead)
-    q.out, q.out_dtype, q.o_strides = O3.data_ptr(), L.dtype_code(O3.dtype), L.strides(O3, 4, lead)
-    if lse is not None:
-        q.lse, q.lse_strides = lse.data_ptr(), L.strides(lse, 3, lead)
-    else:
-        q.lse, q.lse_strides = None, L.i64([0, 0, 0], 3)
-    q.H_q = Q3.shape[-2]
-    q.sm_scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(Q3.shape[-1])
-    return q
+    pad = (0,) * lead
+    if O3.dim() != Q3.dim() or (lse is not None and lse.dim() != Q3.dim() - 1):
+        raise ValueError("query, output and lse ranks disagree")
+    D = Q3.shape[-1]
+    return L.Query(Q3.data_ptr(), L.dtype_code(Q3.dtype), L.I64x4(*(pad + Q3.stride())),
+                   O3.data_ptr(), L.dtype_code(O3.dtype), L.I64x4(*(pad + O3.stride())),
+                   None if lse is None else lse.data_ptr(),
+                   L.I64x3(*(pad + lse.stride())) if lse is not None else L.I64x3(0, 0, 0),
+                   Q3.shape[-2], float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(D), 0, None)
 
 
 def retention_rows(retention, head_pattern, H_q: int, H_kv: int, layers: int, device):

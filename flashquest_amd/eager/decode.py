@@ -129,18 +129,19 @@ def quest_decode_int4(
     mask = None
     if return_selection:
         mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
-    ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q))
+    stream = L.stream_handle(Q.device)
+    ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q), stream)
     tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
     if tail is not None:
         L.check(L.lib().fq_quest_decode_int4_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
                                                   int(window_pages), k_max, L.SELECT_MODES[select_mode],
-                                                  ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                                                  ws.data_ptr(), ws.numel(), stream),
                 "quest_decode_int4 (tail)")
     else:
         L.check(L.lib().fq_quest_decode_int4(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
                                              L.SELECT_MODES[select_mode], None,
                                              None if mask is None else mask.data_ptr(),
-                                             ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                                             ws.data_ptr(), ws.numel(), stream),
                 "quest_decode_int4")
     O = O3.unsqueeze(-2)
     lse_out = lse.unsqueeze(-1) if lse is not None else None
@@ -250,18 +251,19 @@ def quest_decode_int8(
                                                           Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device) if return_selection else None
-    ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q))
+    stream = L.stream_handle(Q.device)
+    ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q), stream)
     tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
     if tail is not None:
         L.check(L.lib().fq_quest_decode_int8_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
                                                   int(window_pages), k_max, L.SELECT_MODES[select_mode],
-                                                  ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                                                  ws.data_ptr(), ws.numel(), stream),
                 "quest_decode_int8 (tail)")
     else:
         L.check(L.lib().fq_quest_decode_int8(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
                                              L.SELECT_MODES[select_mode], None,
                                              None if mask is None else mask.data_ptr(),
-                                             ws.data_ptr(), ws.numel(), L.stream_handle(Q.device)),
+                                             ws.data_ptr(), ws.numel(), stream),
                 "quest_decode_int8")
     O = O3.unsqueeze(-2)
     lse_out = lse.unsqueeze(-1) if lse is not None else None
@@ -329,12 +331,13 @@ def quest_decode_turbo(
     mask = None
     if return_selection:
         mask = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.bool, device=Q.device)
-    ws = L.workspace(Q.device, L.lib().fq_turbo_workspace_bytes(cache, H_q))
+    stream = L.stream_handle(Q.device)
+    ws = L.workspace(Q.device, L.lib().fq_turbo_workspace_bytes(cache, H_q), stream)
     L.check(L.lib().fq_quest_decode_turbo(cache, ksr.data_ptr(), L.strides(ksr, 5, lead), kmr.data_ptr(),
                                           L.strides(kmr, 5, lead), query, r.data_ptr(), int(num_sinks),
                                           int(window_pages), k_max, L.SELECT_MODES[select_mode],
                                           None if mask is None else mask.data_ptr(), ws.data_ptr(), ws.numel(),
-                                          L.stream_handle(Q.device)), "quest_decode_turbo")
+                                          stream), "quest_decode_turbo")
     O = O3.unsqueeze(-2)
     lse_out = lse.unsqueeze(-1) if lse is not None else None
     if return_selection:
