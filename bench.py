@@ -492,6 +492,20 @@ def main():
         per_layer = [decoder(args.retention, k, args.select,
                              c={key: t[l] for key, t in cache.items()}) for l in range(L)]
         extra["per_layer_graph_us"] = per_layer_graph_ms(per_layer, args.steps, args.warmup, flush) * 1e3
+        # the same pattern issued eagerly through the functional operator (the
+        # reference patch's call, new output tensors every layer): host-side
+        # cost included
+        from flashquest_amd.eager.decode import quest_decode_int4 as _qd4
+        lviews = [[cache[x][l] for x in ("Q", "K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")]
+                  for l in range(L)]
+
+        def eager_layers():
+            for v in lviews:
+                _qd4(v[0], *v[1:], retention=args.retention, num_sinks=4, window_pages=2, k_max_static=k,
+                     select_mode=args.select)
+        eager_ms, _, _ = time_steps(noop, eager_layers, args.steps, args.warmup, flush)
+        extra["per_layer_eager_us"] = eager_ms * 1e3
+        del lviews
         # the same, with a 37-token bf16 partial page per layer (the usual decode
         # step): the tail is attended in the split-merge launch
         T_tail = 37
