@@ -370,7 +370,8 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // k: this wave's k-th page (entry w + NW * k); callers clamp k to the last
     // page, so every step issues the same loads and the waits match on every path
     auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[ent_base + w + NW * k]); };
-    auto issue = [&](PageBuf& bf, int k) { issue_page(bf, entry_of(k) & 0xFFFF); };
+    // past the wave's last page: kNoPage (loads out of range, no memory traffic)
+    auto issue = [&](PageBuf& bf, int k) { issue_page(bf, k < n_mine ? entry_of(k) & 0xFFFF : kNoPage); };
 
     // running references (wave-uniform) and accumulators.  With fp16 metadata
     // p * V_scale <= 65504 needs no bound; bf16 metadata is divided by s_run.
@@ -601,15 +602,14 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 
     // One page in flight ahead of the one being computed.
     {
-        // issued unconditionally: an idle wave reads some page of the slice (or
-        // zeros past its end) and discards it, but every path into the loop
-        // then has the same loads in flight
+        // issued unconditionally (past the wave's last page they read nothing),
+        // so every path into the loop has the same loads in flight
         if constexpr (NW == 8) s_left[w] = n_mine;
         if (!first_issued) issue(b0, 0);
         for (int k = 0; k < n_mine; k += 2) {
-            issue(b1, min(k + 1, n_mine - 1));
+            issue(b1, k + 1);
             compute(b0, k);
-            issue(b0, min(k + 2, n_mine - 1));
+            issue(b0, k + 2);
             if (k + 1 < n_mine) compute(b1, k + 1);
         }
         __builtin_amdgcn_s_setprio(0);

@@ -12,6 +12,10 @@ namespace fq {
 
 constexpr int kThreads = 256;      // 4 wave64 per workgroup
 constexpr int kMaxPages = 8192;    // 512k tokens at 64 tokens / page
+// A page index past every cache slice (kMaxPages pages): page loads issued
+// past a wave's last page use it, so their buffer loads fall outside the
+// slice's range and return zeros without a memory access.
+constexpr int kNoPage = 0x7FFF;
 constexpr int kMaxRows = 16;       // query rows per KV group in scoring (n_rep * S_q)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
