@@ -19,6 +19,14 @@ namespace fq {
 
 FQ_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A workgroup barrier for data exchanged through LDS only: it waits for this
+// wave's LDS operations, not for its global loads, which stay in flight.
+FQ_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 FQ_DEV void merge_weights(float m_self, float m_other, float& M, float& w_self, float& w_other) {
     M = fmaxf(m_self, m_other);
     w_self = m_self == -INFINITY ? 0.f : exp2_fast(m_self - M);
@@ -308,7 +316,7 @@ FQ_DEV void tail_state_lds(const uint16_t (*tk)[D], const uint16_t (*tv)[D], boo
             if (j == 0 && t < T) sp[r][t] = v;
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int r = w; r < NREP; r += NT / 64) {
         const float v = lane < T ? sp[r][lane] : -INFINITY;
         float m = v;
@@ -321,7 +329,7 @@ FQ_DEV void tail_state_lds(const uint16_t (*tk)[D], const uint16_t (*tv)[D], boo
         if (lane < T) sp[r][lane] = pe;
         if (lane == 0) { m_out[r] = m; l_out[r] = ls; }
     }
-    __syncthreads();
+    lds_barrier();
     // p.v: thread (channel d, token group hf) over tokens hf, hf + NH, ...; the
     // groups meet in acc_out
     const int d = tid % D, hf = tid / D;
@@ -338,13 +346,13 @@ FQ_DEV void tail_state_lds(const uint16_t (*tk)[D], const uint16_t (*tv)[D], boo
         for (int r = 0; r < NREP; ++r) acc_out[r][d] = a[r];
     }
     for (int g2 = 1; g2 < NH; ++g2) {
-        __syncthreads();
+        lds_barrier();
         if (hf == g2) {
 #pragma unroll
             for (int r = 0; r < NREP; ++r) acc_out[r][d] += a[r];
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Split merge (the rule of _merge_two_attentions, llama_persistent_patch.py:50-61,

@@ -417,6 +417,13 @@ void attn_int8_mfma_kernel(Int8Params a) {
         auto page_of = [&](int u) { return entry_of(min(u, max(nsteps - 1, 0)) >> 1) & 0xFFFF; };
         auto half_of = [&](int u) { return min(u, max(nsteps - 1, 0)) & 1; };
         if (!first_issued) issue_half(b0, page_of(0), 0);
+        if constexpr (FUSED) {
+            // the partial-page tail's state (the merge's last slot) while the
+            // first half page is in flight: its barriers wait on LDS only
+            if (tail_T > 0)      // uniform
+                tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
+                                            s_split.l[NW], s_split.acc[NW]);
+        }
         for (int u = 0; u < nsteps; u += 2) {
             issue_half(b1, page_of(u + 1), half_of(u + 1));
             compute(b0, u >> 1, 0);
@@ -442,11 +449,7 @@ void attn_int8_mfma_kernel(Int8Params a) {
     }
     int nslots = NW;
     if constexpr (FUSED) {
-        if (tail_T > 0) {       // uniform; the tail state is the merge's last slot
-            tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
-                                        s_split.l[NW], s_split.acc[NW]);
-            nslots = NW + 1;
-        }
+        if (tail_T > 0) nslots = NW + 1;       // the tail state (computed before the page loop) joins the merge
     }
     __syncthreads();
     merge_waves_and_store<D, NREP, false, NSLOT, NT>(s_split, q, a.ws, g, l, b, h, split,

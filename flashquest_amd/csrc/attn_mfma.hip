@@ -606,6 +606,14 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         // so every path into the loop has the same loads in flight
         if constexpr (NW == 8) s_left[w] = n_mine;
         if (!first_issued) issue(b0, 0);
+        if constexpr (FUSED) {
+            // The partial-page tail's attention state (the merge's last slot),
+            // while each wave's first page is in flight: its barriers wait on
+            // LDS only
+            if (tail_T > 0)      // uniform
+                tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
+                                            s_split.l[NW], s_split.acc[NW]);
+        }
         for (int k = 0; k < n_mine; k += 2) {
             issue(b1, k + 1);
             compute(b0, k);
@@ -641,11 +649,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     }
     int nslots = NW;
     if constexpr (FUSED) {
-        if (tail_T > 0) {       // uniform; the tail state is the merge's last slot
-            tail_state_lds<D, NREP, NT>(s_tk, s_tv, a.tail.dtype == FQ_BF16, tail_T, s_q, s_tp, s_split.m[NW],
-                                        s_split.l[NW], s_split.acc[NW]);
-            nslots = NW + 1;
-        }
+        if (tail_T > 0) nslots = NW + 1;       // the tail state (computed before the page loop) joins the merge
     }
     __syncthreads();
     merge_waves_and_store<D, NREP, false, NSLOT, NT>(s_split, q, a.ws, g, l, b, h, split,
