@@ -19,13 +19,6 @@ namespace fq {
 
 FQ_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// A workgroup barrier for data exchanged through LDS only: it waits for this
-// wave's LDS operations, not for its global loads, which stay in flight.
-FQ_DEV void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 FQ_DEV void merge_weights(float m_self, float m_other, float& M, float& w_self, float& w_other) {
     M = fmaxf(m_self, m_other);

@@ -331,7 +331,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 issue_page(b0, fp.page(w));
                 first_issued = true;
             }
-            __syncthreads();
+            lds_barrier();      // the keys; the forced pages stay in flight through the selection
             // every split of the group selects the same list; split s takes
             // the balanced slice [e0, e1) of it
             const int total = block_select_group<kSelC, NW, NREP>(s_key, c.P, a.sel.mode, ret_l, a.sel.k_max,

@@ -95,6 +95,15 @@ template <int NL> FQ_DEV float row_sum(float v) {
 }
 
 // ------------------------------------------------------- block helpers ----
+// A workgroup barrier for data exchanged through LDS only: it waits for this
+// wave's LDS operations, not for its global loads, which stay in flight
+// (__syncthreads also waits for those).
+FQ_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Ordered compaction over [0, n): calls write(i, rank) for every i with
 // flag(i), rank = number of flagged j < i.  Returns the flagged count.
 // Must be called by all kThreads threads; s_tmp needs 5 ints of LDS.

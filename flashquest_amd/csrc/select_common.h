@@ -318,7 +318,7 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
                 if (lane == 0) sl.T[r] = t;
             }
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int r = 0; r < NROWS; ++r) T[r] = sl.T[r];
     }
@@ -362,7 +362,7 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
         }
         n += __popcll(bal);
     }
-    __syncthreads();
+    lds_barrier();
     return n;
 }
 
@@ -373,9 +373,9 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
 template <int NT, int NREP>
 FQ_DEV void block_write_mask(const int* entries, int n, int P, uint8_t* scratch, uint8_t* mask, int tid) {
     for (int i = tid; i < P; i += NT) scratch[i] = 0;
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < n; e += NT) scratch[entries[e] & 0xFFFF] = (uint8_t)(entries[e] >> 16);
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < NREP * P; i += NT) {
         const int r = i / P, p = i - r * P;
         mask[i] = (scratch[p] >> r) & 1;
