@@ -506,7 +506,7 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
     const int groups = c.L * c.B * c.Hkv;
     // one workgroup per group when the groups fill the GPU, else balanced slices
     // (at least 8 pages each) for about one workgroup per CU
-    int s = groups >= 192 ? 1 : (256 + groups - 1) / std::max(groups, 1);
+    int s = groups >= 192 || al.max_entries <= kFusedSmallPages ? 1 : (256 + groups - 1) / std::max(groups, 1);
     s = std::min(s, (al.max_entries + 7) / 8);
     s = std::max(s, (al.max_entries + kMaxWgPages - 1) / kMaxWgPages);
     a.splits = std::max(1, std::min(s, al.s_max));

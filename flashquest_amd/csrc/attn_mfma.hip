@@ -697,7 +697,7 @@ MfmaSplit mfma_splits(int groups, int max_entries, int s_max, int request) {
 // per CU, each scoring and selecting the group's pages itself (the same list
 // in every split) and attending a balanced slice of it, at least 8 pages.
 int fused_splits(int groups, int max_entries, int s_max) {
-    if (groups >= 192) return 1;
+    if (groups >= 192 || max_entries <= kFusedSmallPages) return 1;
     int s = (256 + groups - 1) / std::max(groups, 1);
     s = std::min(s, (max_entries + 7) / 8);
     return std::max(1, std::min(s, s_max));

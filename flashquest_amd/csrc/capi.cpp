@@ -424,8 +424,8 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
 // to fill the GPU) score each group once in a scoring launch over all CUs; the
 // attention workgroups then select from those scores (kSelectOnly) instead of
 // each re-scoring the group's pages.  INT4 and INT8, unrotated.
-static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q) {
-    return c.L * c.B * c.Hkv < 192 && !q.rot;
+static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q, int bound) {
+    return c.L * c.B * c.Hkv < 192 && !q.rot && bound > kFusedSmallPages;
 }
 
 static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
@@ -450,7 +450,8 @@ static int quest_select(const fq_int4_cache* cache, const fq_query* query, const
     // is one call, writes the mask too)
     if ((!mask_out || mask_from_attention) && !sc_user &&
         decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws)) {
-        if (!attend_from_scores(c, q)) return FQ_OK;      // the attention kernel scores too
+        if (!attend_from_scores(c, q, quest_bound(c, q, num_sinks, window_pages, k_max, select_mode)))
+            return FQ_OK;      // the attention kernel scores too
         return hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks,
                                        window_pages, k_max, nullptr, (hipStream_t)stream, false),
                           "page scores");
@@ -494,7 +495,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     if (attn_selects_in_kernel(c, q, al)) {
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.mask_out = mask_out;
-        sel.enabled = attend_from_scores(c, q) ? kSelectOnly : kScoreSelect;
+        sel.enabled = attend_from_scores(c, q, al.max_entries) ? kSelectOnly : kScoreSelect;
     }
     return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail),
                       bits == 8 ? "sparse int8 attention" : "sparse int4 attention");

@@ -16,6 +16,11 @@ constexpr int kMaxPages = 8192;    // 512k tokens at 64 tokens / page
 // past a wave's last page use it, so their buffer loads fall outside the
 // slice's range and return zeros without a memory access.
 constexpr int kNoPage = 0x7FFF;
+// A decode step whose lists hold at most this many pages per KV group runs as
+// one launch with one workgroup per group (it scores, selects and attends
+// itself: a few pages per wave) even when the groups do not fill the GPU;
+// longer lists split each group over workgroups behind a scoring launch.
+constexpr int kFusedSmallPages = 40;
 constexpr int kMaxRows = 16;       // query rows per KV group in scoring (n_rep * S_q)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
