@@ -158,6 +158,11 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
         r = torch.full((H,), float(retention), dtype=torch.float32, device=device)
         # a tensor made during HIP graph capture lives in the graph's pool: not kept
         if not (device.type == "cuda" and torch.cuda.is_current_stream_capturing()):
+            if len(_scalar_retention) >= 256:       # callers that vary the retention every step
+                _scalar_retention.clear()
+            if device.type == "cuda":
+                # shared by calls on every stream: the fill must be done before any reads it
+                torch.cuda.current_stream(device).synchronize()
             _scalar_retention[key] = r
     return r
 
