@@ -1,0 +1,73 @@
+"""Host-side plumbing of the per-call operators (no GPU): descriptors built
+from tensors carry exactly the tensors' addresses, strides and shapes, and
+scalar retentions become one shared, read-only device vector per (value,
+heads, device)."""
+import pytest
+import torch
+
+from flashquest_amd import _lib as L
+from flashquest_amd import _ops
+
+
+def _planes(lead=(), S=256, P=4, D=128, G=4, meta=torch.float16):
+    kp = torch.zeros(*lead, 2, 8, S, D // 2, dtype=torch.uint8)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(*lead, 2, 8, P, D, dtype=meta)
+    km = torch.zeros_like(ks)
+    vs = torch.zeros(*lead, 2, 8, S, G, dtype=meta)
+    vm = torch.zeros_like(vs)
+    return kp, ks, km, vp, vs, vm
+
+
+@pytest.mark.parametrize("lead", [(), (3,)])
+def test_int4_descriptor_fields(lead):
+    kp, ks, km, vp, vs, vm = _planes(lead)
+    c, keep = _ops.int4_cache(kp, ks, km, vp, vs, vm, 64)
+    pad = [0] * (1 - len(lead))
+    assert c.k_packed == kp.data_ptr() and c.v_mn == vm.data_ptr()
+    assert list(c.k_strides) == pad + list(kp.stride()) and list(c.vs_strides) == pad + list(vs.stride())
+    assert (c.L, c.B, c.H_kv, c.S, c.P, c.D, c.page_size, c.v_groups) == \
+        ((lead[0] if lead else 1), 2, 8, 256, 4, 128, 64, 4)
+    assert c.meta_dtype == L.FQ_F16
+    assert all(a is b for a, b in zip(keep, (kp, vp, ks, km, vs, vm)))
+
+
+def test_int4_descriptor_rejects_mixed_ranks_and_copies_misaligned_views():
+    kp, ks, km, vp, vs, vm = _planes()
+    with pytest.raises(ValueError):
+        _ops.int4_cache(kp, ks[0], km, vp, vs, vm, 64)
+    # a K-metadata view whose rows are not 8-element aligned is copied, not passed on
+    wide = torch.zeros(2, 8, 4, 136, dtype=torch.float16)[..., 3:131]
+    c, keep = _ops.int4_cache(kp, wide, km, vp, vs, vm, 64)
+    assert keep[2] is not wide and keep[2].is_contiguous() and c.k_scale == keep[2].data_ptr()
+
+
+def test_query_descriptor_fields():
+    q = torch.zeros(2, 24, 128, dtype=torch.bfloat16)
+    o = torch.zeros(2, 24, 128, dtype=torch.float32)
+    lse = torch.zeros(2, 24, dtype=torch.float32)
+    d = _ops.query(q, o, lse, None)
+    assert d.q == q.data_ptr() and d.out == o.data_ptr() and d.lse == lse.data_ptr()
+    assert list(d.q_strides) == [0] + list(q.stride()) and list(d.lse_strides) == [0] + list(lse.stride())
+    assert (d.q_dtype, d.out_dtype, d.H_q) == (L.FQ_BF16, L.FQ_F32, 24)
+    assert abs(d.sm_scale - 128 ** -0.5) < 1e-7 and d.retention_layer_stride == 0 and not d.rotation_signs
+    nolse = _ops.query(q, o, None, 0.5)
+    assert not nolse.lse and list(nolse.lse_strides) == [0, 0, 0] and nolse.sm_scale == 0.5
+    with pytest.raises(ValueError):
+        _ops.query(q, o[0], None, None)
+
+
+def test_scalar_retention_vectors_are_shared_and_bounded():
+    a = _ops.retention_tensor(0.25, 24, "cpu")
+    assert a.shape == (24,) and a.dtype == torch.float32 and bool((a == 0.25).all())
+    assert _ops.retention_tensor(0.25, 24, torch.device("cpu")) is a
+    b = _ops.retention_tensor(0.5, 24, "cpu")
+    assert b is not a and bool((b == 0.5).all())
+    assert _ops.retention_tensor(0.25, 12, "cpu") is not a
+    for i in range(300):
+        _ops.retention_tensor(i / 1000.0, 4, "cpu")
+    assert len(_ops._scalar_retention) <= 256
+    with pytest.raises(ValueError):
+        _ops.retention_tensor(1.5, 24, "cpu")
+    per_head = torch.linspace(0, 1, 24)
+    assert torch.equal(_ops.retention_tensor(per_head, 24, "cpu"), per_head)
