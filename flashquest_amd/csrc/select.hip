@@ -307,18 +307,59 @@ __global__ __launch_bounds__(kThreads) void select_groups_kernel(GroupSelectPara
 
 // ---------------------------------------------------------------------------
 // The same per-group selection with one wave per group and no workgroup
-// barriers (wave_select_group, select_common.h).  Used for P <= 64 C.
+// barriers (wave_select_group, select_common.h).  Used for P <= 64 C; launched
+// with one wave per workgroup, so that the groups spread over the CUs.
 // ---------------------------------------------------------------------------
 template <int C>
 __global__ __launch_bounds__(kThreads) void select_groups_wave_kernel(GroupSelectParams a, int G) {
-    const int g = blockIdx.x * (kThreads / 64) + wave_id();
+    __shared__ uint32_t s_hist[kThreads / 64][256];        // each wave's own radix-search counts
+    const int g = blockIdx.x * (blockDim.x / 64) + wave_id();
     if (g >= G) return;                      // whole wave
     const int P = a.P;
     int* entries = a.ws.entries + (int64_t)g * P;
     uint8_t* mo = a.mask_out ? a.mask_out + ((int64_t)g * a.nrep) * P : nullptr;
     const int n = wave_select_group<C>(a.ws.scores + (int64_t)g * a.nrep * P, P, a.nrep, a.mode,
-                                       group_retention(a, g), a.k_max, a.num_sinks, a.window, entries, mo);
+                                       group_retention(a, g), a.k_max, a.num_sinks, a.window, entries, mo,
+                                       s_hist[wave_id()]);
     if (lane_id() == 0) a.ws.n_sel[g] = n;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k per query head with the rows spread over the waves of a workgroup:
+// one group per 4-wave workgroup, wave w searches rows w, w + 4, ... (each a
+// wave_topk of its own), the selection bits meet in LDS, and wave 0 lists the
+// group as wave_select_group does (same entries, same mask).  P <= 64 C.
+// ---------------------------------------------------------------------------
+template <int C>
+__global__ __launch_bounds__(kThreads) void select_groups_rows_kernel(GroupSelectParams a) {
+    constexpr int NW = kThreads / 64;
+    __shared__ uint32_t s_hist[NW][256];
+    __shared__ uint8_t s_qm[NW][C][64];
+    const int g = blockIdx.x, w = wave_id(), lane = lane_id(), P = a.P;
+    const float* sc = a.ws.scores + (int64_t)g * a.nrep * P;
+    const float* ret = group_retention(a, g);
+    uint8_t qm[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) qm[j] = 0;
+    for (int r = w; r < a.nrep; r += NW) {
+        uint32_t key[C];
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int i = 64 * j + lane;
+            key[j] = i < P ? sortable_key(sc[r * P + i]) : 0u;      // 0: below every score
+        }
+        wave_topk<C>(key, qm, k_for(ret[r], P, a.k_max), (uint8_t)(1u << r), s_hist[w]);
+    }
+#pragma unroll
+    for (int j = 0; j < C; ++j) s_qm[w][j][lane] = qm[j];
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int j = 0; j < C; ++j)
+        for (int v = 1; v < NW; ++v) qm[j] |= s_qm[v][j][lane];
+    uint8_t* mo = a.mask_out ? a.mask_out + ((int64_t)g * a.nrep) * P : nullptr;
+    const int n = wave_list_group<C>(qm, P, a.nrep, a.num_sinks, a.window, a.ws.entries + (int64_t)g * P, mo);
+    if (lane == 0) a.ws.n_sel[g] = n;
 }
 
 // ---------------------------------------------------------------------------
@@ -500,7 +541,6 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
 #undef FQ_SCORE
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !ws || !select_groups) return e;
-    const dim3 wgrid((G + kThreads / 64 - 1) / (kThreads / 64));
     if (G < 192 && c.P <= 64 * kSelC && q.nrep <= 4) {     // few groups: a workgroup per group
         switch (q.nrep) {
             case 1: hipLaunchKernelGGL(select_groups_block_kernel<1>, dim3(G), dim3(512), 0, st, sp); break;
@@ -508,8 +548,13 @@ hipError_t launch_score(const Int4Cache& c, const QueryArgs& q, int S_q, const i
             case 3: hipLaunchKernelGGL(select_groups_block_kernel<3>, dim3(G), dim3(512), 0, st, sp); break;
             default: hipLaunchKernelGGL(select_groups_block_kernel<4>, dim3(G), dim3(512), 0, st, sp); break;
         }
-    } else if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, wgrid, dim3(kThreads), 0, st, sp, G);
-    else if (c.P <= 64 * 32) hipLaunchKernelGGL(select_groups_wave_kernel<32>, wgrid, dim3(kThreads), 0, st, sp, G);
+    } else if (c.P > 64 * 8 && c.P <= 64 * 32 && q.nrep > 1 && select_mode == FQ_SELECT_PER_Q_HEAD) {
+        if (c.P <= 64 * 16) hipLaunchKernelGGL(select_groups_rows_kernel<16>, dim3(G), dim3(kThreads), 0, st, sp);
+        else hipLaunchKernelGGL(select_groups_rows_kernel<32>, dim3(G), dim3(kThreads), 0, st, sp);
+    } else if (c.P <= 64 * 8) hipLaunchKernelGGL(select_groups_wave_kernel<8>, dim3(G), dim3(64), 0, st, sp, G);
+    // one wave per workgroup: the groups spread over as many CUs as there are
+    else if (c.P <= 64 * 16) hipLaunchKernelGGL(select_groups_wave_kernel<16>, dim3(G), dim3(64), 0, st, sp, G);
+    else if (c.P <= 64 * 32) hipLaunchKernelGGL(select_groups_wave_kernel<32>, dim3(G), dim3(64), 0, st, sp, G);
     else hipLaunchKernelGGL(select_groups_kernel, dim3(G), dim3(kThreads), 0, st, sp);
     return hipGetLastError();
 }

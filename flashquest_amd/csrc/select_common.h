@@ -33,9 +33,20 @@ FQ_DEV uint32_t wave_kth_largest(const uint32_t (&key)[C], int k) {
 }
 
 template <int C>
-FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit) {
+FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, bool* exact = nullptr);
+
+// hist: 256 words of LDS used by this wave only (wave_kth_hist's digit counts).
+template <int C>
+FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t bit, uint32_t* hist) {
     if (k <= 0) return;
-    const uint32_t T = wave_kth_largest<C>(key, k);
+    bool exact;
+    const uint32_t T = wave_kth_hist<C>(key, k, hist, &exact);
+    if (exact) {         // exactly k keys >= T: no ties to rank
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+            if (key[j] >= T) qm[j] |= bit;
+        return;
+    }
     // T is the k-th largest key; keys above it are in, ties fill the rest by index
     int gt = 0;
 #pragma unroll
@@ -51,6 +62,10 @@ FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t
     }
 }
 
+template <int C>
+FQ_DEV int wave_list_group(uint8_t (&qm)[C], int P, int nrep, int num_sinks, int window, int* entries,
+                           uint8_t* mask_out);
+
 // One KV group's selection by one wave (P <= 64 C): scores of row r at
 // sc[r * P + p] (nrep rows per query head, or one summed row), top-k per
 // query head or once per KV head with the group's largest retention, forced
@@ -59,7 +74,7 @@ FQ_DEV void wave_topk(const uint32_t (&key)[C], uint8_t (&qm)[C], int k, uint8_t
 // the per-head boolean rows mask_out[r * P + p].  Returns the list length.
 template <int C>
 FQ_DEV int wave_select_group(const float* sc, int P, int nrep, int mode, const float* retention, int k_max,
-                             int num_sinks, int window, int* entries, uint8_t* mask_out) {
+                             int num_sinks, int window, int* entries, uint8_t* mask_out, uint32_t* hist) {
     const int lane = lane_id();
     uint32_t key[C];
     uint8_t qm[C];
@@ -83,14 +98,26 @@ FQ_DEV int wave_select_group(const float* sc, int P, int nrep, int mode, const f
         for (int r = 0; r < nrep; ++r) {
             if (r + 1 < nrep) fetch((r + 1) & 1, r + 1);
             make_keys(r & 1);
-            wave_topk<C>(key, qm, k_for(__shfl(ret_l, r, 64), P, k_max), (uint8_t)(1u << r));
+            wave_topk<C>(key, qm, k_for(__shfl(ret_l, r, 64), P, k_max), (uint8_t)(1u << r), hist);
         }
     } else {
         float rmax = 0.f;
         for (int r = 0; r < nrep; ++r) rmax = fmaxf(rmax, __shfl(ret_l, r, 64));
         make_keys(0);
-        wave_topk<C>(key, qm, k_for(rmax, P, k_max), all_bits);
+        wave_topk<C>(key, qm, k_for(rmax, P, k_max), all_bits, hist);
     }
+    return wave_list_group<C>(qm, P, nrep, num_sinks, window, entries, mask_out);
+}
+
+// The end of wave_select_group: qm[j] holds the selection bits (bit r: query
+// row r) of page 64 j + lane; forces the sink and window pages into every row,
+// writes the ascending entry list (page | bits << 16) and, if mask_out, the
+// per-row mask; returns the list length.
+template <int C>
+FQ_DEV int wave_list_group(uint8_t (&qm)[C], int P, int nrep, int num_sinks, int window, int* entries,
+                           uint8_t* mask_out) {
+    const int lane = lane_id();
+    const uint8_t all_bits = (uint8_t)((1u << nrep) - 1u);
     const int ns = num_sinks < P ? num_sinks : P;
     const int wnd = window < P ? window : P;
     int n = 0;
@@ -236,7 +263,7 @@ FQ_DEV uint32_t wave_max_u32(uint32_t v) {
 // largest key -- the contract the callers rely on: keys above T, then ties at
 // T by page index, give the top k.  Wave-uniform; hist is left zeroed.
 template <int C>
-FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, bool* exact = nullptr) {
+FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, bool* exact) {
     const int lane = lane_id();
     uint32_t lo = key[0], hi = key[0];
 #pragma unroll

@@ -81,3 +81,26 @@ def test_selection_on_adversarial_scores(pattern, B, retention, mode):
     tol = 2e-3 + 2.0 ** -8 * float(np.abs(ref["O"]).max())
     assert max_err(o[:, :, 0], ref["O"]) <= tol
     assert max_err(lse[:, :, 0], ref["lse"]) <= 1e-4 * max(1.0, float(np.abs(ref["lse"][np.isfinite(ref["lse"])]).max()))
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+@pytest.mark.parametrize("P,mode", [(1000, "per_q_head"), (2048, "per_q_head"), (1000, "per_kv_head_sum")])
+def test_selection_on_adversarial_scores_long(pattern, P, mode):
+    """Long steps (more than 512 pages) take the standalone group selection of
+    up to 2048 pages: per query head, one wave per row of the group."""
+    from flashquest_amd.eager.decode import quest_decode_int4
+    rng = np.random.default_rng(zlib.crc32(f"long/{pattern}/{P}/{mode}".encode()))
+    case = Int4Case(seed=int(rng.integers(1 << 30)), B=1, Hq=6, Hkv=2, S=64 * P, D=128)
+    _shape_scores(case, pattern, rng)
+    for return_selection in (True, False):
+        res = quest_decode_int4(case.q_dev(), **case.device(), retention=0.3, num_sinks=2, window_pages=1,
+                                select_mode=mode, return_selection=return_selection)
+        ref = O.decode_step(case.Q, case.kp, case.ks, case.km, case.vp, case.vs, case.vm, retention=0.3,
+                            num_sinks=2, window_pages=1, mode=mode)
+        torch.cuda.synchronize()
+        if return_selection:
+            assert np.array_equal(res[2].cpu().numpy(), ref["mask"]), (pattern, P, mode)
+        o, lse = res[0], res[1]
+        tol = 2e-3 + 2.0 ** -8 * float(np.abs(ref["O"]).max())
+        assert max_err(o[:, :, 0], ref["O"]) <= tol
+        assert max_err(lse[:, :, 0], ref["lse"]) <= 1e-4 * max(1.0, float(np.abs(ref["lse"][np.isfinite(ref["lse"])]).max()))
