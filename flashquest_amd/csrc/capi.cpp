@@ -792,6 +792,24 @@ int fq_quantize_turbo(const void* x, int32_t in_dtype, const int64_t x_strides[4
                       "quantize turbo");
 }
 
+// The TurboQuant cache descriptor as the decode entries read it: head_dim,
+// page count, contiguous plane rows, tensors present once the cache holds
+// tokens, and per-token fp16/bf16 scales on 2-byte boundaries.
+static int check_turbo_cache(const fq_turbo_cache* c) {
+    if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
+    if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
+    if (c->L < 1 || c->B < 1 || c->H_kv < 1) return fail(FQ_ERR_INVALID, "empty L/B/H_kv");
+    if (c->P < 1 || c->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", c->P);
+    if (c->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
+    if (!c->k_msb || !c->k_lsb || !c->k_scale || !c->v_msb || !c->v_lsb || !c->v_scale)
+        return fail(FQ_ERR_INVALID, "NULL cache tensor");
+    if (c->kmsb_strides[4] != 1 || c->klsb_strides[4] != 1 || c->vmsb_strides[4] != 1 || c->vlsb_strides[4] != 1)
+        return fail(FQ_ERR_UNSUPPORTED, "innermost turbo plane axis must be contiguous");
+    if (((uintptr_t)c->k_scale | (uintptr_t)c->v_scale) & 1)
+        return fail(FQ_ERR_UNSUPPORTED, "scales must be 2-byte aligned");
+    return FQ_OK;
+}
+
 size_t fq_turbo_workspace_bytes(const fq_turbo_cache* cache, int32_t H_q) {
     if (!cache || cache->H_kv < 1 || H_q % cache->H_kv) return 0;
     const int G = cache->L * cache->B * cache->H_kv;
@@ -802,16 +820,10 @@ size_t fq_turbo_workspace_bytes(const fq_turbo_cache* cache, int32_t H_q) {
 int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query, const uint8_t* mask,
                              const int64_t mask_strides[4], void* workspace, size_t workspace_bytes_,
                              fq_stream_t stream) {
-    if (!cache) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
-    if (cache->D != 64 && cache->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", cache->D);
-    if (cache->P < 1 || cache->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", cache->P);
-    if (cache->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
-    for (int i = 0; i < 5; ++i)
-        if ((i == 4) != 0 && (cache->kmsb_strides[4] != 1 || cache->klsb_strides[4] != 1 ||
-                              cache->vmsb_strides[4] != 1 || cache->vlsb_strides[4] != 1))
-            return fail(FQ_ERR_UNSUPPORTED, "innermost turbo plane axis must be contiguous");
+    int st = check_turbo_cache(cache);
+    if (st) return st;
     QueryArgs q{};
-    int st = check_query(query, cache->D, cache->H_kv, &q);
+    st = check_query(query, cache->D, cache->H_kv, &q);
     if (st) return st;
     if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode is INT4 only");
     const int G = cache->L * cache->B * cache->H_kv;
@@ -835,18 +847,13 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
                           const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
                           int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
                           fq_stream_t stream) {
-    if (!cache) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
-    if (cache->D != 64 && cache->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", cache->D);
-    if (cache->P < 1 || cache->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", cache->P);
-    if (cache->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
-    if (cache->kmsb_strides[4] != 1 || cache->klsb_strides[4] != 1 || cache->vmsb_strides[4] != 1 ||
-        cache->vlsb_strides[4] != 1)
-        return fail(FQ_ERR_UNSUPPORTED, "innermost turbo plane axis must be contiguous");
+    int st = check_turbo_cache(cache);
+    if (st) return st;
     if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
     if (select_mode != FQ_SELECT_PER_Q_HEAD && select_mode != FQ_SELECT_PER_KV_HEAD_SUM)
         return fail(FQ_ERR_INVALID, "select_mode=%d", select_mode);
     QueryArgs q{};
-    int st = check_query(query, cache->D, cache->H_kv, &q);
+    st = check_query(query, cache->D, cache->H_kv, &q);
     if (st) return st;
     if (q.rot) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode is INT4 only");
     if (((uintptr_t)q.q) & 1) return fail(FQ_ERR_UNSUPPORTED, "query must be 2-byte aligned");
@@ -999,6 +1006,8 @@ static int prefill_turbo_check(const fq_turbo_cache* c, const fq_tail* tail, con
             return fail(FQ_ERR_INVALID, "NULL cache tensor");
         if (c->kmsb_strides[4] != 1 || c->klsb_strides[4] != 1 || c->vmsb_strides[4] != 1 || c->vlsb_strides[4] != 1)
             return fail(FQ_ERR_UNSUPPORTED, "innermost plane axis must be contiguous");
+        if (((uintptr_t)c->k_scale | (uintptr_t)c->v_scale) & 1)
+            return fail(FQ_ERR_UNSUPPORTED, "scales must be 2-byte aligned");
     }
     int st = prefill_check_tail_query(tail, q, c->D, c->H_kv, c->B, c->S, t);
     if (st) return st;

@@ -71,3 +71,37 @@ def test_scalar_retention_vectors_are_shared_and_bounded():
         _ops.retention_tensor(1.5, 24, "cpu")
     per_head = torch.linspace(0, 1, 24)
     assert torch.equal(_ops.retention_tensor(per_head, 24, "cpu"), per_head)
+
+
+def _turbo_desc(S=256, P=4, D=128, Hkv=2):
+    c = L.TurboCache()
+    c.k_msb = c.v_msb = c.k_lsb = c.v_lsb = c.k_scale = c.v_scale = 4096
+    c.kmsb_strides = c.vmsb_strides = L.i64([0, Hkv * S * D // 8, S * D // 8, D // 8, 1], 5)
+    c.klsb_strides = c.vlsb_strides = L.i64([0, Hkv * S * D // 4, S * D // 4, D // 4, 1], 5)
+    c.kst_strides = c.vst_strides = L.i64([0, Hkv * S, S, 1, 1], 5)
+    c.L, c.B, c.H_kv, c.S, c.P, c.D, c.page_size = 1, 1, Hkv, S, P, D, 64
+    return c
+
+
+@pytest.mark.parametrize("field,value,code,msg", [("v_scale", 4097, "FQ_ERR_UNSUPPORTED", "aligned"),
+                                                  ("k_scale", 4097, "FQ_ERR_UNSUPPORTED", "aligned"),
+                                                  ("v_lsb", None, "FQ_ERR_INVALID", "NULL cache tensor"),
+                                                  ("D", 96, "FQ_ERR_UNSUPPORTED", "head_dim"),
+                                                  ("P", 0, "FQ_ERR_UNSUPPORTED", "pages")])
+def test_turbo_descriptor_checks_before_any_launch(field, value, code, msg):
+    """Every TurboQuant decode entry rejects a misaligned per-token scale, a
+    missing plane, an unsupported head_dim or page count (no GPU needed: the
+    checks run before anything reaches the device)."""
+    lib = L.lib()
+    c = _turbo_desc()
+    setattr(c, field, value)
+    want = getattr(L, code)
+    z5 = L.i64([0, 0, 0, 0, 1], 5)
+    assert lib.fq_quest_decode_turbo(c, 4096, z5, 4096, z5, None, None, 0, 0, -1, 0, None, None, 0, None) == want
+    assert msg in lib.fq_last_error().decode()
+    assert lib.fq_sparse_turbo_fwd_mask(c, None, None, L.i64([0, 0, 0, 1], 4), None, 0, None) == want
+    assert msg in lib.fq_last_error().decode()
+    # the unmodified descriptor passes the cache checks and stops at the missing query
+    assert lib.fq_quest_decode_turbo(_turbo_desc(), 4096, z5, 4096, z5, None, None, 0, 0, -1, 0, None, None, 0,
+                                     None) == L.FQ_ERR_INVALID
+    assert msg not in lib.fq_last_error().decode()
