@@ -84,13 +84,15 @@ def test_selection_on_adversarial_scores(pattern, B, retention, mode):
 
 
 @pytest.mark.parametrize("pattern", PATTERNS)
-@pytest.mark.parametrize("P,mode", [(1000, "per_q_head"), (2048, "per_q_head"), (1000, "per_kv_head_sum")])
-def test_selection_on_adversarial_scores_long(pattern, P, mode):
+@pytest.mark.parametrize("P,mode,Hq", [(1000, "per_q_head", 6), (2048, "per_q_head", 6), (1000, "per_kv_head_sum", 6),
+                                       (700, "per_q_head", 16)])
+def test_selection_on_adversarial_scores_long(pattern, P, mode, Hq):
     """Long steps (more than 512 pages) take the standalone group selection of
-    up to 2048 pages: per query head, one wave per row of the group."""
+    up to 2048 pages: per query head, one wave per row of the group (two rows
+    per wave at 8 query heads per KV head)."""
     from flashquest_amd.eager.decode import quest_decode_int4
-    rng = np.random.default_rng(zlib.crc32(f"long/{pattern}/{P}/{mode}".encode()))
-    case = Int4Case(seed=int(rng.integers(1 << 30)), B=1, Hq=6, Hkv=2, S=64 * P, D=128)
+    rng = np.random.default_rng(zlib.crc32(f"long/{pattern}/{P}/{mode}/{Hq}".encode()))
+    case = Int4Case(seed=int(rng.integers(1 << 30)), B=1, Hq=Hq, Hkv=2, S=64 * P, D=128)
     _shape_scores(case, pattern, rng)
     for return_selection in (True, False):
         res = quest_decode_int4(case.q_dev(), **case.device(), retention=0.3, num_sinks=2, window_pages=1,
