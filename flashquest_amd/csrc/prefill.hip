@@ -855,31 +855,51 @@ void prefill_dense_kernel(PrefillParams a) {
 
 // Combines the key-range partials of the split path: per row (b, h, m)
 // M = max m_i, L = sum 2^(m_i - M) l_i, O = sum 2^(m_i - M) O_i / L, in split
-// order; one wave per row, lane = two channels.
+// order; one wave per row, lane = two channels.  The splits go in batches of
+// 8 whose loads are all issued before any is used; the running maximum moves
+// once per batch (earlier sums are rescaled by 2^(M_old - M_new)).
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams a) {
+    constexpr int kBatch = 8;
     const int64_t rows = (int64_t)a.c.B * a.c.Hkv * a.Sq * a.nrep;
     const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
     if (row >= rows) return;
     const int lane = threadIdx.x & 63;
     const int KS = a.kv_splits;
     const float* ml = a.part + (int64_t)KS * rows * kPD;
-    float M = -INFINITY;
-    for (int sp = 0; sp < KS; ++sp) M = fmaxf(M, ml[(sp * rows + row) * 2]);
-    float L = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int sp = 0; sp < KS; ++sp) {
-        const float m = ml[(sp * rows + row) * 2];
-        const float wt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-        L = fmaf(wt, ml[(sp * rows + row) * 2 + 1], L);
-        const float* po = a.part + (sp * rows + row) * kPD;
-        o0 = fmaf(wt, po[2 * lane], o0);
-        o1 = fmaf(wt, po[2 * lane + 1], o1);
+    float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int sp0 = 0; sp0 < KS; sp0 += kBatch) {
+        float m[kBatch], l[kBatch];
+        float2 po[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t sp = min(sp0 + u, KS - 1);
+            m[u] = ml[(sp * rows + row) * 2];
+            l[u] = ml[(sp * rows + row) * 2 + 1];
+            po[u] = *(const float2*)(a.part + (sp * rows + row) * kPD + 2 * lane);
+        }
+        float Mb = M;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (sp0 + u < KS) Mb = fmaxf(Mb, m[u]);
+        if (Mb == -INFINITY) continue;          // nothing attended yet
+        const float r = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mb);
+        L *= r; o0 *= r; o1 *= r;
+        M = Mb;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (sp0 + u >= KS) break;
+            const float wt = m[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[u] - M);
+            L = fmaf(wt, l[u], L);
+            o0 = fmaf(wt, po[u].x, o0);
+            o1 = fmaf(wt, po[u].y, o1);
+        }
     }
     const int Mtot = a.Sq * a.nrep;
-    const int m = (int)(row % Mtot);
+    const int mi = (int)(row % Mtot);
     const int hb = (int)(row / Mtot);
     const int h = hb % a.c.Hkv, b = hb / a.c.Hkv;
-    const int hq = h * a.nrep + m % a.nrep;
-    uint16_t* orow = (uint16_t*)a.out + b * a.o_s[0] + hq * a.o_s[1] + (int64_t)(m / a.nrep) * a.o_s[2];
+    const int hq = h * a.nrep + mi % a.nrep;
+    uint16_t* orow = (uint16_t*)a.out + b * a.o_s[0] + hq * a.o_s[1] + (int64_t)(mi / a.nrep) * a.o_s[2];
     const float inv = 1.0f / L;
     *(uint32_t*)(orow + 2 * lane) = pack_bf16(o0 * inv, o1 * inv);
 }
