@@ -198,6 +198,19 @@ FQ_DEV void fetch_v(VFetch& f, const PrefillParams& a, int b, int h, int key0, i
     const uint8_t* rows = c.vp + b * c.vp_s[1] + h * c.vp_s[2] + (int64_t)key0 * c.vp_s[3] + (BITS == 4 ? vd / 2 : vd);
     const uint16_t* vs = (const uint16_t*)c.vsc + b * c.vsc_s[1] + h * c.vsc_s[2] + (int64_t)key0 * c.vsc_s[3] + grp;
     const uint16_t* vm = (const uint16_t*)c.vmn + b * c.vmn_s[1] + h * c.vmn_s[2] + (int64_t)key0 * c.vmn_s[3] + grp;
+    // per-token metadata (one group) of 4 whole keys: one 8-byte load each for
+    // scale and min (the 4 keys' values are adjacent)
+    if (whole && c.G == 1 && c.vsc_s[3] == 1 && c.vmn_s[3] == 1 && (((uintptr_t)vs | (uintptr_t)vm) & 7) == 0) {
+        const u32x2 s4 = *(const u32x2*)vs, m4 = *(const u32x2*)vm;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f.raw[j].x = BITS == 4 ? (uint32_t)*(const uint16_t*)(rows + j * c.vp_s[3])
+                                   : *(const uint32_t*)(rows + j * c.vp_s[3]);
+            f.sc[j] = ((j < 2 ? s4.x : s4.y) >> (16 * (j & 1))) & 0xFFFFu;
+            f.mn[j] = ((j < 2 ? m4.x : m4.y) >> (16 * (j & 1))) & 0xFFFFu;
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = key0 + j;
