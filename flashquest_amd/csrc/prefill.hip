@@ -262,16 +262,45 @@ FQ_DEV void store_v(const VFetch& f, uint16_t* dst /* V^T row vd, column key0 */
 template <int BITS, int META>
 __global__ __launch_bounds__(512) void prefill_dequant_kernel(PrefillParams a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_v[kPD * kVStr];
+    __shared__ u32x4 s_kmeta[2][16];        // the tile's K page scale / min (one page per tile)
     const int tid = threadIdx.x;
     const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int key0 = tile * kPKT;
     const bool whole = key0 + kPKT <= a.c.S;
     const int kk = tid >> 3, kc = (tid & 7) * 16;
     const int vk = (tid & 15) * 4, vd = (tid >> 4) * 4;
+    // A tile inside the completed pages with one page per tile: its 64 keys
+    // share one row of K scale / min, loaded once into LDS instead of by every
+    // thread (uniform per block)
+    const bool one_page = whole && a.c.page % kPKT == 0;
     KFetch kf;
     VFetch vf;
-    fetch_k<BITS>(kf, a, b, h, key0 + kk, kc, whole);
+    if (one_page) {
+        const Int4Cache& c = a.c;
+        const uint8_t* row = c.kp + b * c.kp_s[1] + h * c.kp_s[2] + (int64_t)(key0 + kk) * c.kp_s[3];
+        if (BITS == 4) {
+            const u32x2 v = *(const u32x2*)(row + kc / 2);
+            kf.c0 = u32x4{v.x, v.y, 0u, 0u};
+        } else {
+            kf.c0 = *(const u32x4*)(row + kc);
+        }
+        kf.kind = 0;
+        if (tid < 32) {
+            const bool sc = tid < 16;
+            const int64_t page = key0 / c.page;
+            const uint16_t* src = sc ? (const uint16_t*)c.ksc + b * c.ksc_s[1] + h * c.ksc_s[2] + page * c.ksc_s[3]
+                                     : (const uint16_t*)c.kmn + b * c.kmn_s[1] + h * c.kmn_s[2] + page * c.kmn_s[3];
+            s_kmeta[tid >> 4][tid & 15] = *(const u32x4*)(src + 8 * (tid & 15));
+        }
+    } else {
+        fetch_k<BITS>(kf, a, b, h, key0 + kk, kc, whole);
+    }
     fetch_v<BITS>(vf, a, b, h, key0 + vk, vd, whole);
+    if (one_page) {
+        __syncthreads();
+        kf.s0 = s_kmeta[0][kc / 8]; kf.s1 = s_kmeta[0][kc / 8 + 1];
+        kf.m0 = s_kmeta[1][kc / 8]; kf.m1 = s_kmeta[1][kc / 8 + 1];
+    }
     const int64_t bh = (int64_t)b * a.c.Hkv + h;
     store_k<BITS, META>(kf, a.kd + (bh * a.s_pad + key0 + kk) * kPD + kc);
     store_v<BITS, META>(vf, &s_v[vd * kVStr + vt_pos(vk)], kVStr);
