@@ -963,12 +963,23 @@ int64_t dense_row_blocks(int Sq, int nrep) { return ((int64_t)Sq * nrep + kDense
 // (few query rows over many keys, e.g. a chunk with causal_off = S_kv - S_q),
 // workgroups take slices of at least 4 key stages and a merge launch combines
 // their partials.
+// Between 128 and 256 workgroups (one round on 256 CUs with some idle), the
+// split count k <= 8 with the fewest rounds per unit of work,
+// ceil(wgs k / 256) / k, evens the rounds out (192 workgroups: 4 splits, 3
+// full rounds of a quarter of the work each).
 int prefill_kv_splits(int64_t nblk, int64_t heads, int64_t keys) {
     const int64_t wgs = nblk * heads;
     const int64_t stages = (keys + kDenseKT - 1) / kDenseKT;
-    if (wgs >= 128 || stages < 8) return 1;
-    const int64_t ks = std::min<int64_t>((256 + wgs - 1) / wgs, stages / 4);
-    return (int)std::max<int64_t>(1, ks);
+    if (stages < 8) return 1;
+    if (wgs < 128) return (int)std::max<int64_t>(1, std::min<int64_t>((256 + wgs - 1) / wgs, stages / 4));
+    if (wgs >= 256) return 1;
+    int best = 1;
+    double best_cost = 1.0;                  // rounds per unit of work with k = 1: one round
+    for (int k = 2; k <= 8 && stages / k >= 4; ++k) {
+        const double cost = (double)((wgs * k + 255) / 256) / k;
+        if (cost < best_cost - 1e-9) { best = k; best_cost = cost; }
+    }
+    return best;
 }
 
 // Dense K / V^T of the attended keys, then (with key-range splits) the partials.

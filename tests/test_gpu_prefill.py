@@ -218,6 +218,12 @@ def test_prefill_key_range_splits(kw):
     _check(PrefillCase(13, **kw))
 
 
+def test_prefill_key_range_splits_between_128_and_256_workgroups():
+    # 10 row blocks x 16 (sequence, KV head) pairs = 160 workgroups: split in 3
+    # key ranges so the 480 workgroups fill two rounds of the CUs
+    _check(PrefillCase(21, B=2, Hq=24, Hkv=8, S=2048, T=30, Sq=800, causal_offset=2078 - 800))
+
+
 def test_prefill_turbo_key_range_splits():
     from flashquest_amd.kernel import flash_attn_prefill_turbo
     S, T, Sq = 4096, 20, 48
