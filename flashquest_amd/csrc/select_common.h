@@ -278,7 +278,7 @@ FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, b
     uint32_t* const mine = hist + 252 - 4 * lane;   // lane l: digits 255 - 4l - m at mine[3 - m]
     *(uint4*)mine = make_uint4(0u, 0u, 0u, 0u);
     for (;;) {
-        const int shift = b >= 7 ? b - 7 : 0;       // this round's digit: bits [shift, b]
+        const int shift = b >= 7 ? b - 7 : 0;       // this pass's digit: bits [shift, b]
         const uint32_t dmask = (2u << (b - shift)) - 1u;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
