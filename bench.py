@@ -1,6 +1,6 @@
 """Benchmark of the sparse INT4 decode-attention step on one MI355X.
 
-Workload: 28 independent layers' KV caches, batch 1,
+Workload (benchmark config 1): 28 independent layers' KV caches, batch 1,
 24 query / 8 KV heads, head_dim 128, 32k context = 512 pages of 64 tokens,
 retention 0.25 (top-128 pages per KV head, per-KV-head selection from the
 summed group scores) plus 4 sink and 2 window pages.  K/V are seeded synthetic
@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip control / per-layer / per-q-head lines")
     ap.add_argument("--cpu-layers", type=int, default=10, help="layers in the CPU baseline sample")
     ap.add_argument("--no-batch16", dest="batch16", action="store_false",
-                    help="skip the batch-16 line (BASELINE config 4) among the extras")
+                    help="skip the batch-16 line (benchmark config 4) among the extras")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="for rocprofv3 --pmc runs: a 256 MiB device copy (calibration), then 3 flushed steps")
     ap.add_argument("--profile-int8", action="store_true",
@@ -69,7 +69,7 @@ ROT_SEED = 4242
 
 
 def rotation_signs(D=128, dev="cuda"):
-    """The seeded +-1 vector of the randomised WHT."""
+    """The seeded +-1 vector of the randomised WHT (benchmark config 3)."""
     g = torch.Generator()
     g.manual_seed(ROT_SEED)
     return (torch.randint(0, 2, (D,), generator=g) * 2 - 1).float().to(dev)
@@ -311,8 +311,8 @@ def self_check(cache, dec, mask, k, args):
 
 
 def config0(args, dev, flush, noop):
-    """one layer, 8k context (128 pages), r = 0.20, the
-    BASELINE layout (fp16 metadata, V in 32-channel groups), batch 1: the
+    """Benchmark config 0: one layer, 8k context (128 pages), r = 0.20, the
+    benchmark layout (fp16 metadata, V in 32-channel groups), batch 1: the
     whole decode step of one layer (8 KV groups: split over workgroups, the
     split merge), and the CPU baseline on the same layer."""
     from oracle import torch_eager as TE
@@ -529,7 +529,7 @@ def main():
         extra["step_us_after_write_flush"] = wf_ms * 1e3
         del wflush
 
-        # rotated INT4 (K, V rotated by x -> WHT(s x) / sqrt(128)
+        # benchmark config 3: rotated INT4 (K, V rotated by x -> WHT(s x) / sqrt(128)
         # before quantisation).  The single launch rotates Q in its prologue and
         # O back in its store.
         signs = rotation_signs(dev=dev)
@@ -652,7 +652,7 @@ def main():
                       "prefill_reference_sequence_ms": pr_ms, "prefill_speedup_vs_reference_sequence": pr_ms / pf_ms})
         del qp, pk
 
-        # batch 16 independent sequences, 28 layers, 32k each
+        # benchmark config 4: batch 16 independent sequences, 28 layers, 32k each
         if B == 1 and args.batch16:
             bc = make_cache(L, 16, P=P, dev=dev)
             bmask = torch.zeros(L, 16, Hq, P, dtype=torch.bool, device=dev)

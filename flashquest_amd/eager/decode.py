@@ -90,7 +90,7 @@ def quest_decode_int4(
     ``head_pattern`` (H_kv,) or (L, H_kv) bool: DuoAttention's per-KV-head
     retrieval (True) / streaming (False) pattern; streaming heads keep only
     the sink and window pages (llama_persistent_patch.py:214-220).
-    ``rotation_signs`` (D,) +-1 (no reference function): the
+    ``rotation_signs`` (D,) +-1 (benchmark config 3, no reference function): the
     cache holds K and V rotated by x -> WHT(s x) / sqrt(D); Q is rotated the
     same way (fp32) before scoring and attention and O rotated back,
     O = s WHT(O_rot) / sqrt(D), lse unchanged (the rotation is orthogonal).

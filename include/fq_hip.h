@@ -89,7 +89,7 @@ typedef struct fq_query {
      * every layer (0), or (L, H_q) with this layer stride (H_q or more), e.g.
      * a DuoAttention head pattern per layer (llama_persistent_patch.py:214-220). */
     int64_t retention_layer_stride;
-    /* Rotated decode (a cache quantised in the basis
+    /* Rotated decode (benchmark config 3: a cache quantised in the basis
      * x -> WHT(s x) / sqrt(128)): with a device fp32 (128,) sign vector s, the
      * single-launch INT4 decode rotates q the same way (fp32 butterflies, then
      * times fp32(1/sqrt(128))) before scoring and attention, and writes

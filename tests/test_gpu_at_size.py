@@ -1,4 +1,4 @@
-"""The benchmarked decode at the BASELINE geometries, against the CPU oracle.
+"""The benchmarked decode at the benchmark configurations' geometries, against the CPU oracle.
 
 The whole-step decode over all layers is one kernel launch when the KV groups
 fill the GPU (L*B*H_kv >= 192): every workgroup scores its group's 512 pages,
