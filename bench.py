@@ -59,6 +59,9 @@ def parse():
                     help="for rocprofv3 runs: 10 flushed fused INT8 decode steps (--select mode) only")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for rocprofv3 runs: 5 prefills of a 32k-token prompt over one INT4 layer only")
+    ap.add_argument("--profile-per-layer", action="store_true",
+                    help="for rocprofv3 runs: the reference's per-layer call pattern (28 single-layer steps "
+                         "in one HIP graph), 5 flushed replays only")
     ap.add_argument("--profile-turbo", action="store_true",
                     help="for rocprofv3 runs: 10 flushed fused TurboQuant decode steps (--select mode) only")
     return ap.parse_args()
@@ -430,6 +433,14 @@ def main():
         return QuestDecoder(c["Q"], c["K_packed"], c["K_scale"], c["K_mn"], c["V_packed"], c["V_scale"], c["V_mn"],
                             retention=retention, num_sinks=4, window_pages=2, k_max_static=kmax,
                             select_mode=mode, mask_out=mask)
+
+    if args.profile_per_layer:
+        per_layer = [decoder(args.retention, k, args.select,
+                             c={key: t[l] for key, t in cache.items()}) for l in range(L)]
+        per_layer_graph_ms(per_layer, 5, 1, flush)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_per_layer": "done", "select": args.select}))
+        return
 
     if args.profile_kernels:
         src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
