@@ -64,6 +64,37 @@ def test_layer_patterns_in_one_multilayer_call(mode, splits):
         assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
 
 
+@pytest.mark.parametrize("mode", ["per_q_head", "per_kv_head_sum"])
+def test_layer_patterns_past_512_pages(mode):
+    # more than 512 pages: the standalone group selection (per query head one
+    # wave per row); streaming heads have retention 0, so only their forced pages
+    from flashquest_amd.eager.decode import quest_decode_int4
+    Lyr, Hq, Hkv, P = 2, 6, 2, 700
+    rng = np.random.default_rng(321)
+    cases = [Int4Case(seed=900 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P - 20, D=128) for i in range(Lyr)]
+    pattern = np.array([[True, False], [False, True]])
+    dev = [c.device() for c in cases]
+    stacked = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+    q = torch.stack([c.q_dev() for c in cases])
+    o, lse, mask = quest_decode_int4(q, **stacked, retention=0.25, num_sinks=3, window_pages=2, select_mode=mode,
+                                     return_selection=True, head_pattern=torch.from_numpy(pattern))
+    torch.cuda.synchronize()
+    forced = _forced(P, 3, 2)
+    rep = Hq // Hkv
+    for i, c in enumerate(cases):
+        rrow = _retention_rows(pattern[i], 0.25, rep)
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=rrow, num_sinks=3, window_pages=2,
+                            mode=mode)
+        m = mask[i].cpu().numpy()
+        assert np.array_equal(m, ref["mask"]), i
+        for h in range(Hkv):
+            if not pattern[i, h]:
+                assert np.array_equal(m[0, h * rep:(h + 1) * rep], np.broadcast_to(forced, (rep, P))), (i, h)
+        tol = 2e-3 + 2.0 ** -8 * float(np.abs(ref["O"]).max())
+        assert max_err(o[i][:, :, 0], ref["O"]) <= tol, i
+        assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
+
+
 def test_quest_duo_fused_sdpa_signature_and_semantics():
     from flashquest_amd.duo import quest_duo_fused_sdpa
     Hq, Hkv, P = 8, 4, 24
