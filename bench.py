@@ -341,43 +341,62 @@ def config0(args, dev, flush, noop):
         try:
             for rep in range(12):
                 t0 = time.perf_counter()
-                TE.decode_layer(host["Q"][:, 0].float(), host["K_packed"], host["K_scale"], host["K_mn"],
-                                host["V_packed"], host["V_scale"], host["V_mn"], retention=0.2, select=args.select)
+                o_cpu, sel_cpu = TE.decode_layer(host["Q"][:, 0].float(), host["K_packed"], host["K_scale"],
+                                                 host["K_mn"], host["V_packed"], host["V_scale"], host["V_mn"],
+                                                 retention=0.2, select=args.select, return_selection=True)
                 if rep >= 2:
                     times.append(time.perf_counter() - t0)
         finally:
             torch.set_num_threads(prev)
         out["config0_cpu_baseline_us"] = sorted(times)[len(times) // 2] * 1e6
         out["config0_cpu_threads"] = threads
+        out["config0_cpu_check"] = cpu_check(o_cpu[None], sel_cpu[None], d0.O3[0].cpu(), m0[0].cpu())
     return out
 
 
-def cpu_baseline(cache, args, n_layers):
+def cpu_check(o_cpu, sel_cpu, o_gpu, sel_gpu):
+    """The CPU path as the checker of the GPU step on the same layers: how many
+    (layer, query head) selections agree (the CPU path scores with torch
+    matmuls, the reference's own order), and max |O_gpu - O_cpu| over the
+    heads whose selections agree."""
+    same = (sel_cpu == sel_gpu).all(-1)                       # (layers, H_q)
+    err = (o_gpu.float() - o_cpu).abs().amax(-1)              # (layers, H_q)
+    return {"rows": int(same.numel()), "selection_rows_equal": int(same.sum()),
+            "max_abs_O_vs_cpu_path": float(err[same].max()) if bool(same.any()) else None}
+
+
+def cpu_baseline(cache, args, n_layers, o_gpu, sel_gpu):
     """The reference's eager CPU path restated in PyTorch (oracle/torch_eager.py:
     two fp32 matmuls for the scores, topk + forced pages, fp32 dequant of the
-    selected pages, fp32 softmax attention), timed on the host with all of the
-    box's CPU share; median layer time x layers."""
+    selected pages, fp32 softmax attention), timed on the host with the box's
+    CPU share; median layer time x layers.  Its outputs check the GPU step's
+    (o_gpu (L, H_q, D), sel_gpu (L, H_q, P)) on the sampled layers."""
     from oracle import torch_eager as TE
-    threads = max(1, min(16, os.cpu_count() or 1))        # a one-GPU box's CPU share is 16
+    # a one-GPU box's CPU share is 16 threads (os.cpu_count() there reports the whole host)
+    threads = max(1, min(16, os.cpu_count() or 1))
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     host = {k: v[:n_layers, 0].cpu() for k, v in cache.items()}
-    times = []
+    times, outs, sels = [], [], []
     try:
         for rep in range(2):                               # first pass warms up
             for l in range(n_layers):
                 t0 = time.perf_counter()
-                TE.decode_layer(host["Q"][l, :, 0].float(), host["K_packed"][l], host["K_scale"][l],
-                                host["K_mn"][l], host["V_packed"][l], host["V_scale"][l], host["V_mn"][l],
-                                retention=args.retention, select=args.select)
+                o, sel = TE.decode_layer(host["Q"][l, :, 0].float(), host["K_packed"][l], host["K_scale"][l],
+                                         host["K_mn"][l], host["V_packed"][l], host["V_scale"][l], host["V_mn"][l],
+                                         retention=args.retention, select=args.select, return_selection=True)
                 if rep:
                     times.append(time.perf_counter() - t0)
+                    outs.append(o)
+                    sels.append(sel)
     finally:
         torch.set_num_threads(prev)
     per_layer = sorted(times)[len(times) // 2]
+    check = cpu_check(torch.stack(outs), torch.stack(sels), o_gpu[:n_layers].cpu(), sel_gpu[:n_layers].cpu())
     return {"value": per_layer * args.layers * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n_layers} layers of the same workload (batch 1), median layer time x {args.layers}; "
-                      f"eager PyTorch restatement of the reference CPU path, {threads} threads"}
+                      f"eager PyTorch restatement of the reference CPU path, {threads} threads",
+            "check": check}
 
 
 def main():
@@ -694,13 +713,16 @@ def main():
             "kernel": kname, "kernel_us": attn_ms * 1e3, "algorithmic_bytes_per_launch": kernel_b}
     cpu = None
     if not args.no_cpu_baseline and B == 1:
-        cpu = cpu_baseline(cache, args, min(args.cpu_layers, L))
+        dec()                       # the timed step's output (deterministic) for the check
+        torch.cuda.synchronize()
+        cpu = cpu_baseline(cache, args, min(args.cpu_layers, L), dec.O3[:, 0], mask[:, 0])
     line = {
         "metric": METRIC, "value": step_ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4 KV; q.k on int8 MFMA (exact 3-digit split of q*K_scale, int32 accumulate); p.v on fp16 MFMA "
-                 "(p*V_scale rounded to fp16, fp32 accumulate); fp32 softmax",
+                 "with p*V_scale as fp16 hi + lo parts (fp32-level operand, 2^-22 relative) times the exact INT4 "
+                 "codes, fp32 accumulate; fp32 softmax; fp16 output",
         "data": "synthetic",
         "config": {"workload": f"BASELINE config 1: {L} independent layers x batch {B}, {Hq}/8 heads, D=128, "
                                f"{P} pages x 64 tokens, retention {args.retention} ({args.select} top-{k} + 4 sink "

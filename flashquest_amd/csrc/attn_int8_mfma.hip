@@ -16,8 +16,12 @@
 //         q.k = sum A (code - 128) + 128 sum A + q.K_mn, the last two per head
 //         and page on the VALU.  int32 accumulation is exact.
 //   p.v : v_mfma_f32_16x16x32_f16.  A = p_t * V_scale[t] (/ a running bound
-//         with bf16 metadata) in fp16, B = the codes as fp16 subnormals
-//         (bits = code, value = code * 2^-24, exact), plus sum_t p_t V_mn[t].
+//         with bf16 metadata) split into fp16 parts hi = fp16(A) in rows r
+//         and lo = fp16(A - hi) in rows 4 + r (the V metadata is per token,
+//         so rows 4..7 are free), B = the codes as fp16 subnormals (bits =
+//         code, value = code * 2^-24, exact); the two row sets are added at
+//         the end, so each product carries A to 2^-22 relative (fp32-level,
+//         like the reference's fp32 p * v); plus sum_t p_t V_mn[t].
 // With 8-bit codes a page is twice the INT4 bytes, so the loads run half a
 // page (32 tokens) ahead of the half being computed to keep both buffers in
 // registers.
@@ -383,11 +387,14 @@ void attn_int8_mfma_kernel(Int8Params a) {
             bias = fmaf(pr[t], vm_t[t], bias);
         }
         if (lg < NREP) {
-            const int row = lg, kq = (n16 & 3) ^ ((row >> 2) & 3);
             float x0 = pr[0] * vs_t[0], x1 = pr[1] * vs_t[1];
             if constexpr (kBound) { x0 *= inv_s; x1 *= inv_s; }
-            const h2v hv = __builtin_convertvector((f2v){x0, x1}, h2v);
-            *(uint32_t*)&W.apv[row][kq][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+            const f2v xv = {x0, x1};
+            const h2v hv = __builtin_convertvector(xv, h2v);
+            const h2v lv = __builtin_convertvector(xv - __builtin_convertvector(hv, f2v), h2v);
+            const int kq = n16 & 3, kql = kq ^ 1;      // rows lg (hi) and 4 + lg (lo), swizzled
+            *(uint32_t*)&W.apv[lg][kq][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+            *(uint32_t*)&W.apv[4 + lg][kql][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, lv);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         const v8h ap = *(const v8h*)&W.apv[n16][lg ^ ((n16 >> 2) & 3)][0];
@@ -434,6 +441,11 @@ void attn_int8_mfma_kernel(Int8Params a) {
     }
 
     // ---- wave state -> LDS (head r in lane group 0 component r; channel 8 n16 + j)
+    // the lo rows 4 + r (lane group 1) join the hi rows
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) pacc[j][r] += __shfl_xor(pacc[j][r], 16, 64);
     l_acc = row_sum<16>(l_acc);
     bias = row_sum<16>(bias);
     const float pv_unscale = s_run * kSubnormal8;

@@ -11,10 +11,14 @@
 //         fixed-point number per page (3 balanced int8 digits in rows
 //         4r+digit, r = query head), B = the codes; plus sum_d q_d * K_mn[p,d].
 //         int32 accumulation is exact, so the only rounding is 2^-23 of max|A|.
-//   p.v : v_mfma_f32_16x16x32_f16.  A = p_t * V_scale[t,g] in fp16 (rows 4g+r,
-//         g = V channel group), B = the codes as fp16 subnormals (bits = code,
-//         value = code * 2^-24, exact), fp32 accumulation; plus
-//         sum_t p_t * V_mn[t,g].  Rounding is relative to each term (2^-12).
+//   p.v : v_mfma_f32_16x16x32_f16.  A = p_t * V_scale[t,g] (rows 4g+r, g = V
+//         channel group) split into fp16 parts hi = fp16(A), lo = fp16(A - hi)
+//         (per-token V metadata: lo in the free rows 4 + r of the same operand,
+//         added at the end; grouped: a second operand), both multiplied by the same B = the codes as fp16 subnormals (bits =
+//         code, value = code * 2^-24, exact) into one fp32 accumulator; plus
+//         sum_t p_t * V_mn[t,g] on the VALU.  hi + lo equals the fp32 A to
+//         2^-22 relative (the lo part's own fp16 rounding), so the products
+//         carry fp32-level precision like the reference's fp32 p * v.
 //
 // Single pass per page: each wave owns every 4th page of its workgroup's
 // split, loads a page (K, V, metadata) one page ahead of the one it computes,
@@ -54,7 +58,8 @@ struct MfmaParams {
 // the 16-byte operand reads (row = lane & 15, k-group = lane >> 4) conflict-free.
 struct WaveLds {
     uint8_t aqk[2][16][4][16];      // q.k: int8 digits, rows 4r + digit
-    uint8_t apv[2][16][4][16];      // p.v: fp16, rows 4g + r (8 halves per k-group)
+    uint8_t apv[2][16][4][16];      // p.v: fp16 hi parts, rows 4g + r (8 halves per k-group)
+    uint8_t apl[2][16][4][16];      // p.v: fp16 lo parts, same layout
 };
 FQ_DEV int swz(int row, int kg) { return kg ^ ((row >> 2) & 3); }
 
@@ -538,7 +543,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             }
         }
 
-        // ---- p.v: A = p * V_scale (/ s_run) in fp16, 2 steps of 32 tokens x 8 tiles
+        // ---- p.v: A = p * V_scale (/ s_run) as fp16 hi + lo, 2 steps of 32 tokens x 8 tiles
         float pr[4];
 #pragma unroll
         for (int T = 0; T < 4; ++T) {
@@ -562,14 +567,26 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 const int q = swz(row, n16 & 3);
 #pragma unroll
                 for (int st = 0; st < 2; ++st) {
-                    const h2v hv = __builtin_convertvector((f2v){a4[2 * st], a4[2 * st + 1]}, h2v);
+                    const f2v av = {a4[2 * st], a4[2 * st + 1]};
+                    const h2v hv = __builtin_convertvector(av, h2v);
+                    const h2v lv = __builtin_convertvector(av - __builtin_convertvector(hv, f2v), h2v);
                     *(uint32_t*)&W.apv[st][row][q][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+                    if constexpr (G == 1)        // rows 4..7 are free: lo in row 4 + r, same operand
+                        *(uint32_t*)&W.apv[st][row + 4][swz(row + 4, n16 & 3)][4 * (n16 >> 2)] =
+                            __builtin_bit_cast(uint32_t, lv);
+                    else
+                        *(uint32_t*)&W.apl[st][row][q][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, lv);
                 }
             }
         }
         wave_lds_fence();
         const v8h ap0 = *(const v8h*)&W.apv[0][n16][swz(n16, lg)][0];
         const v8h ap1 = *(const v8h*)&W.apv[1][n16][swz(n16, lg)][0];
+        v8h al0, al1;
+        if constexpr (G != 1) {
+            al0 = *(const v8h*)&W.apl[0][n16][swz(n16, lg)][0];
+            al1 = *(const v8h*)&W.apl[1][n16][swz(n16, lg)][0];
+        }
         // B: nibbles of the V dwords, two tokens per dword as fp16 subnormal bit patterns
         uint32_t nl[16], nh[16];
 #pragma unroll
@@ -592,9 +609,13 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 }
                 const v8h blo = __builtin_bit_cast(v8h, (v4i){(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]});
                 const v8h bhi = __builtin_bit_cast(v8h, (v4i){(int)bh[0], (int)bh[1], (int)bh[2], (int)bh[3]});
-                const v8h a = st ? ap1 : ap0;
+                const v8h a = st ? ap1 : ap0, al = st ? al1 : al0;
                 pacc[2 * cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo, pacc[2 * cc], 0, 0, 0);
                 pacc[2 * cc + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi, pacc[2 * cc + 1], 0, 0, 0);
+                if constexpr (G != 1) {
+                    pacc[2 * cc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, blo, pacc[2 * cc], 0, 0, 0);
+                    pacc[2 * cc + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bhi, pacc[2 * cc + 1], 0, 0, 0);
+                }
             }
         }
         wave_lds_fence();
@@ -624,6 +645,12 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     }
 
     // ------------------------------------------------ wave state -> LDS
+    if constexpr (G == 1) {     // the lo rows 4 + r (lane group 1) join the hi rows
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) pacc[t][r] += __shfl_xor(pacc[t][r], 16, 64);
+    }
     l_acc = row_sum<16>(l_acc);
 #pragma unroll
     for (int gv = 0; gv < G; ++gv) bias[gv] = row_sum<16>(bias[gv]);

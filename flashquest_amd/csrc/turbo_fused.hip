@@ -103,11 +103,15 @@ FQ_DEV void split_f16(float x, _Float16& hi, _Float16& lo) {
 // after the rotation).
 //
 // p.v (v_mfma_f32_16x16x32_f16, 32 tokens x 16 channels per step): A = p *
-// V_scale / s_run in fp16 (rows = query heads, s_run a running bound of the
-// V scales), B = fp16 codebook values built in registers: byte permutes
-// assemble each token's 3-bit code and look it up in the 8-entry fp16 table
-// (low bytes, high bytes) with v_perm.  Column n16 of channel tile j is
-// channel 8 n16 + j.
+// V_scale / s_run (s_run a running bound of the V scales) as fp16 hi parts in
+// rows r (query heads) and lo parts in rows 4 + r; B = the codebook values
+// built in registers, byte permutes assembling each token's 3-bit code and
+// looking it up in 8-entry tables with v_perm: once their fp16 hi parts, once
+// their fp16 lo parts (two matrix instructions per tile and step into one
+// accumulator).  Rows r then hold A_hi (c_hi + c_lo), rows 4 + r A_lo (c_hi +
+// c_lo), added at the end: each product p * V_scale * codebook to 2^-22
+// relative, fp32-level like the reference's fp32 p * v.  Column n16 of
+// channel tile j is channel 8 n16 + j.
 template <int NREP, bool FUSED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_turbo_fused_kernel(TurboFusedParams a) {
@@ -289,13 +293,18 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             }
         }
     }
-    // fp16 codebook as byte tables for v_perm: low bytes of codes 0-3 / 4-7, high bytes
-    uint32_t tl0 = 0, tl1 = 0, th0 = 0, th1 = 0;
+    // the codebook's fp16 hi / lo parts as byte tables for v_perm:
+    // [part][low / high byte][codes 0-3 / 4-7]
+    uint32_t tbv[2][2][2] = {};
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-        const uint32_t bits = __builtin_bit_cast(uint16_t, (_Float16)kTurboCodebookF[v]);
-        if (v < 4) { tl0 |= (bits & 0xFFu) << (8 * v); th0 |= (bits >> 8) << (8 * v); }
-        else { tl1 |= (bits & 0xFFu) << (8 * (v - 4)); th1 |= (bits >> 8) << (8 * (v - 4)); }
+        _Float16 hi, lo;
+        split_f16(kTurboCodebookF[v], hi, lo);
+        const uint32_t bh = __builtin_bit_cast(uint16_t, hi), bl = __builtin_bit_cast(uint16_t, lo);
+        tbv[0][0][v >> 2] |= (bh & 0xFFu) << (8 * (v & 3));
+        tbv[0][1][v >> 2] |= (bh >> 8) << (8 * (v & 3));
+        tbv[1][0][v >> 2] |= (bl & 0xFFu) << (8 * (v & 3));
+        tbv[1][1][v >> 2] |= (bl >> 8) << (8 * (v & 3));
     }
 
     auto entry_of = [&](int k) { return __builtin_amdgcn_readfirstlane(s_ent[ent_base + w + NW * k]); };
@@ -405,13 +414,15 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             pr[T] = exp2_fast(lg4[T] - m_lane);
             l_acc += pr[T];
         }
-        if (lg < NREP) {
-            const int row = lg, kq = (n16 & 3) ^ ((row >> 2) & 3);
+        if (lg < NREP) {       // rows lg (hi parts) and 4 + lg (lo parts), k-groups swizzled by row
+            const int kq = n16 & 3;
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
-                const float x0 = pr[2 * st] * vs_t[2 * st] * inv_s, x1 = pr[2 * st + 1] * vs_t[2 * st + 1] * inv_s;
-                const h2v hv = __builtin_convertvector((f2v){x0, x1}, h2v);
-                *(uint32_t*)&W[st][row][kq][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+                const f2v xv = {pr[2 * st] * vs_t[2 * st] * inv_s, pr[2 * st + 1] * vs_t[2 * st + 1] * inv_s};
+                const h2v hv = __builtin_convertvector(xv, h2v);
+                const h2v lv = __builtin_convertvector(xv - __builtin_convertvector(hv, f2v), h2v);
+                *(uint32_t*)&W[st][lg][kq][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, hv);
+                *(uint32_t*)&W[st][4 + lg][kq ^ 1][4 * (n16 >> 2)] = __builtin_bit_cast(uint32_t, lv);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -421,7 +432,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         // ---- p.v B: codes of channel 8 n16 + j for the step's 8 tokens, 4 at a time
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            uint32_t bw[8][4];       // [channel tile j][dword]
+            uint32_t bw[8][4], bwl[8][4];       // [channel tile j][dword]: codebook hi / lo parts
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 // operand k = 4 hh + kk: token index i = 4 (2 st + (kk & 1)) + 2 hh + (kk >> 1)
@@ -437,17 +448,23 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
                     // byte k: msb bit j of token k at bit 2, its lsb field j below
                     const uint32_t mj = j >= 2 ? m4 >> (j - 2) : m4 << (2 - j);
                     const uint32_t sel = (mj & 0x04040404u) | ((lx >> (2 * (j & 3))) & 0x03030303u);
-                    const uint32_t lo = __builtin_amdgcn_perm(tl1, tl0, sel);
-                    const uint32_t hi = __builtin_amdgcn_perm(th1, th0, sel);
+                    const uint32_t lo = __builtin_amdgcn_perm(tbv[0][0][1], tbv[0][0][0], sel);
+                    const uint32_t hi = __builtin_amdgcn_perm(tbv[0][1][1], tbv[0][1][0], sel);
                     bw[j][2 * hh] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
                     bw[j][2 * hh + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+                    const uint32_t llo = __builtin_amdgcn_perm(tbv[1][0][1], tbv[1][0][0], sel);
+                    const uint32_t lhi = __builtin_amdgcn_perm(tbv[1][1][1], tbv[1][1][0], sel);
+                    bwl[j][2 * hh] = __builtin_amdgcn_perm(lhi, llo, 0x05010400u);
+                    bwl[j][2 * hh + 1] = __builtin_amdgcn_perm(lhi, llo, 0x07030602u);
                 }
             }
             const v8h a = st ? ap1 : ap0;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const v8h bv = __builtin_bit_cast(v8h, (v4i){(int)bw[j][0], (int)bw[j][1], (int)bw[j][2], (int)bw[j][3]});
+                const v8h bl = __builtin_bit_cast(v8h, (v4i){(int)bwl[j][0], (int)bwl[j][1], (int)bwl[j][2], (int)bwl[j][3]});
                 pacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, pacc[j], 0, 0, 0);
+                pacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, pacc[j], 0, 0, 0);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -466,7 +483,12 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     }
 
     // ---- wave state -> LDS: head r's sums in lane group r (over the 16 token
-    // columns); outputs of channel 8 n16 + j in lane group 0, component r
+    // columns); outputs of channel 8 n16 + j in lane group 0, component r, plus
+    // the lo rows 4 + r in lane group 1
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) pacc[j][r] += __shfl_xor(pacc[j][r], 16, 64);
     l_acc = row_sum<16>(l_acc);
 #pragma unroll
     for (int r = 0; r < NREP; ++r) {

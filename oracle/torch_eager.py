@@ -28,9 +28,10 @@ def _unpack(packed: torch.Tensor) -> torch.Tensor:
 
 
 def decode_layer(q, kp, ks, km, vp, vs, vm, *, retention: float, num_sinks: int = 4, window_pages: int = 2,
-                 page: int = 64, select: str = "per_kv_head_sum"):
+                 page: int = 64, select: str = "per_kv_head_sum", return_selection: bool = False):
     """One layer, batch 1.  q (H_q, D) fp32; kp/vp (H_kv, S, D/2) uint8;
-    ks/km (H_kv, P, D); vs/vm (H_kv, S, G).  Returns O (H_q, D) fp32."""
+    ks/km (H_kv, P, D); vs/vm (H_kv, S, G).  Returns O (H_q, D) fp32, and with
+    return_selection also the page selection (H_q, P) bool."""
     Hq, D = q.shape
     Hkv, P = ks.shape[0], ks.shape[1]
     rep = Hq // Hkv
@@ -65,4 +66,6 @@ def decode_layer(q, kp, ks, km, vp, vs, vm, *, retention: float, num_sinks: int 
         tok_mask = sel[h][:, pages].repeat_interleave(page, 1)
         logits = logits.masked_fill(~tok_mask, float("-inf"))
         out[h] = torch.softmax(logits, dim=-1) @ vd
+    if return_selection:
+        return out.view(Hq, D), sel.reshape(Hq, P)
     return out.view(Hq, D)

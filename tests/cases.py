@@ -88,3 +88,82 @@ class Int8Case:
 
     def q_dev(self):
         return to_dev_half(self.Q, self.dtype)[:, :, None, :]
+
+
+def fp64_selection_check(q, K_scale, K_mn, got_rows, retention, mode, num_sinks=4, window_pages=2, levels=15.0):
+    """Selection against the exact (fp64) page scores, order-independently.
+
+    The reference scores with torch matmuls (criticality.py:128-163) and picks
+    with torch.topk (selection.py:103-117); neither fixes an fp32 summation
+    order.  Any fp32 evaluation of a score differs from the exact value by at
+    most tau = (D + 16) * 2^-24 * sum |terms| (every order of the D products,
+    the head sum and the x15 scaling).  A row is *ambiguous* when some page
+    inside the exact top-k and some page outside it lie within their taus of
+    each other (the margin idea of scripts/profile_contribution.py:194-199,
+    249): there the reference itself could pick either.  On every other row
+    the selection is fixed by the mathematics, and the GPU must equal it.
+
+    q (1, H_q, D); K_scale / K_mn (1, H_kv, P, D); got_rows: the GPU mask of
+    the step, (1, H_q, P) (per-KV-head modes repeat the group's row).
+    Returns the counts (rows, ambiguous, mismatched, ambiguous_differing): the
+    last is how many ambiguous rows the GPU resolved differently from the
+    fp64 top-k (informative only: either choice is within fp32 error).
+    """
+    q = np.asarray(q, np.float64)[0]
+    sc = np.asarray(K_scale, np.float64)[0]
+    mn = np.asarray(K_mn, np.float64)[0]
+    Hq, D = q.shape
+    Hkv, P = sc.shape[0], sc.shape[1]
+    rep = Hq // Hkv
+    qg = q.reshape(Hkv, rep, D)
+    qp = np.maximum(qg, 0.0)
+    s = qg @ np.swapaxes(mn, 1, 2) + levels * (qp @ np.swapaxes(sc, 1, 2))          # (Hkv, rep, P)
+    a = np.abs(qg) @ np.swapaxes(np.abs(mn), 1, 2) + levels * (qp @ np.swapaxes(sc, 1, 2))
+    got = np.asarray(got_rows)[0].reshape(Hkv, rep, P)
+    if mode == "per_kv_head_sum":
+        s, a, got = s.sum(1, keepdims=True), a.sum(1, keepdims=True), got[:, :1]
+    s, a, got = s.reshape(-1, P), a.reshape(-1, P), got.reshape(-1, P)
+    tau = (D + 16) * 2.0 ** -24 * a
+    nrow = s.shape[0]
+    k = O.k_per_head(retention, nrow, P) if not np.isscalar(retention) else O.k_per_head(retention, 1, P).repeat(nrow)
+    forced = np.zeros(P, bool)
+    forced[:min(num_sinks, P)] = True
+    if window_pages > 0:
+        forced[max(P - window_pages, 0):] = True
+    amb = mis = amb_diff = 0
+    for i in range(nrow):
+        kk = int(k[i])
+        order = np.argsort(-s[i], kind="stable")
+        top = order[:kk]
+        want = forced.copy()
+        want[top] = True
+        differs = not np.array_equal(want, got[i])
+        if 0 < kk < P:
+            rest = order[kk:]
+            if np.min(s[i, top] - tau[i, top]) <= np.max(s[i, rest] + tau[i, rest]):
+                amb += 1
+                amb_diff += int(differs)
+                continue
+        mis += int(differs)
+    return nrow, amb, mis, amb_diff
+
+
+TOL_O = 2e-3      # north-star bar: decode output vs the fp32 oracle, max-abs
+
+
+def decode_tol(ref_o, out_dtype="f16"):
+    """Tolerance for a decode output of type out_dtype against the oracle.
+
+    fp16 / fp32 output: the flat 2e-3 wherever the output type can hold it,
+    i.e. max|O| <= 2 (fp16 rounds |O| < 2 by at most 2^-11 * 2 ~ 1e-3, which
+    leaves 1e-3 for the kernel).  Larger outputs (the rescale stress cases
+    reach |O| ~ 20) add the part of the fp16 rounding, 2^-11 |O|, beyond
+    that 1e-3.  bf16 output (the reference's own output type) adds its
+    rounding, 2^-8 |O|, which alone exceeds 2e-3 once |O| > 0.5.
+    """
+    m = float(np.abs(np.asarray(ref_o)).max()) if np.size(ref_o) else 0.0
+    if out_dtype == "bf16":
+        return TOL_O + 2.0 ** -8 * m
+    if out_dtype == "f32":
+        return TOL_O
+    return TOL_O + max(0.0, 2.0 ** -11 * m - 1e-3)

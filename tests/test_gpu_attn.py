@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import fq_oracle as O
-from tests.cases import Int4Case, max_err, to_dev
+from tests.cases import decode_tol, Int4Case, max_err, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -12,9 +12,7 @@ TOL_O = 2e-3      # fp16/bf16 output vs the fp32 oracle (plus ou
 
 
 def _tol(case, ref_o):
-    # output rounding to the query dtype adds half an ulp of |O|
-    ulp = 2.0 ** (-8 if case.dtype == "bf16" else -11)
-    return TOL_O + ulp * float(np.abs(ref_o).max())
+    return decode_tol(ref_o, case.dtype)
 
 
 def _rand_mask(case, frac, rng):

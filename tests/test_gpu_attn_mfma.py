@@ -13,7 +13,7 @@ import torch
 
 from flashquest_amd import _lib as L
 from oracle import fq_oracle as O
-from tests.cases import Int4Case, max_err, to_dev
+from tests.cases import decode_tol, Int4Case, max_err, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -21,8 +21,7 @@ TOL_O = 2e-3
 
 
 def _tol(case, ref_o):
-    ulp = 2.0 ** (-8 if case.dtype == "bf16" else -11)
-    return TOL_O + ulp * float(np.abs(ref_o).max())
+    return decode_tol(ref_o, case.dtype)
 
 
 def _requantise(case):

@@ -17,13 +17,13 @@ import pytest
 import torch
 
 from oracle import fq_oracle as O
-from tests.cases import Int4Case, Int8Case, max_err, to_dev
+from tests.cases import decode_tol, Int4Case, Int8Case, max_err, to_dev
 
 pytestmark = pytest.mark.gpu
 
 
 def _tol(dtype, ref_o):
-    return 2e-3 + 2.0 ** (-8 if dtype == "bf16" else -11) * float(np.abs(ref_o).max())
+    return decode_tol(ref_o, dtype)
 
 
 @pytest.mark.parametrize("retention", [0.25, 0.5])
