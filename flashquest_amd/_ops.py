@@ -146,7 +146,8 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
     if isinstance(retention, torch.Tensor):
         if retention.shape != (H,):
             raise ValueError(f"per-head retention must be shape ({H},); got {tuple(retention.shape)}")
-        return retention.to(device=device, dtype=torch.float32)
+        # the kernels read H contiguous floats: a strided view is copied
+        return retention.to(device=device, dtype=torch.float32).contiguous()
     if not (0.0 <= float(retention) <= 1.0):
         raise ValueError(f"scalar retention must be in [0, 1]; got {retention}")
     device = torch.device(device)
@@ -159,6 +160,11 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
         # a tensor made during HIP graph capture lives in the graph's pool: not kept
         if not (device.type == "cuda" and torch.cuda.is_current_stream_capturing()):
             if len(_scalar_retention) >= 256:       # callers that vary the retention every step
+                # kernels queued on any stream may still read the cached
+                # vectors: let every one of them finish before the memory can
+                # be reused
+                for d in {k[3] for k in _scalar_retention if k[2] == "cuda"}:
+                    torch.cuda.synchronize(d)
                 _scalar_retention.clear()
             if device.type == "cuda":
                 # shared by calls on every stream: the fill must be done before any reads it

@@ -185,7 +185,9 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
     for (int i = 0; i < 4; ++i) { o.q_s[i] = q->q_strides[i]; o.o_s[i] = q->o_strides[i]; }
     for (int i = 0; i < 3; ++i) o.lse_s[i] = q->lse_strides[i];
     o.Hq = q->H_q; o.nrep = nrep;
-    if (q->retention_layer_stride < 0) return fail(FQ_ERR_INVALID, "negative retention layer stride");
+    if (q->retention_layer_stride < 0 || (q->retention_layer_stride > 0 && q->retention_layer_stride < q->H_q))
+        return fail(FQ_ERR_INVALID, "retention layer stride %lld must be 0 or at least H_q=%d",
+                    (long long)q->retention_layer_stride, q->H_q);
     o.ret_ls = q->retention_layer_stride;
     o.rot = q->rotation_signs;
     if (o.rot && D != 128) return fail(FQ_ERR_UNSUPPORTED, "the rotated decode takes head_dim 128");

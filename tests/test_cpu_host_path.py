@@ -105,3 +105,27 @@ def test_turbo_descriptor_checks_before_any_launch(field, value, code, msg):
     assert lib.fq_quest_decode_turbo(_turbo_desc(), 4096, z5, 4096, z5, None, None, 0, 0, -1, 0, None, None, 0,
                                      None) == L.FQ_ERR_INVALID
     assert msg not in lib.fq_last_error().decode()
+
+
+@pytest.mark.parametrize("stride,ok", [(0, True), (24, True), (48, True), (1, False), (23, False), (-24, False)])
+def test_retention_layer_stride_is_zero_or_a_whole_row(stride, ok):
+    """fq_query.retention_layer_stride is 0 (one row for every layer) or at
+    least H_q (one row per layer); a stride that would make layers read
+    overlapping rows is refused before anything reaches the device."""
+    kp, ks, km, vp, vs, vm = _planes()
+    c, keep = _ops.int4_cache(kp, ks, km, vp, vs, vm, 64)
+    q = torch.zeros(2, 24, 128, dtype=torch.float16)
+    d = _ops.query(q, torch.zeros_like(q), None, None)
+    d.retention_layer_stride = stride
+    rc = L.lib().fq_quest_decode_int4(c, d, None, 4, 2, -1, 0, None, None, None, 0, None)
+    msg = L.lib().fq_last_error().decode()
+    if ok:
+        assert "retention layer stride" not in msg
+    else:
+        assert rc == L.FQ_ERR_INVALID and "retention layer stride" in msg
+
+
+def test_strided_per_head_retention_is_made_contiguous():
+    r = torch.linspace(0, 1, 48)[::2]
+    t = _ops.retention_tensor(r, 24, "cpu")
+    assert t.is_contiguous() and torch.equal(t, r)
