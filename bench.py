@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from flashquest_amd._lib import KernelTimer  # noqa: E402
-from flashquest_amd._ops import read_decode_pages, read_stream  # noqa: E402
+from flashquest_amd._probe import read_decode_pages, read_stream  # noqa: E402
 from flashquest_amd.eager.decode import QuestDecoder  # noqa: E402
 from flashquest_amd.kernel.kv_quant import (quantize_k, quantize_k_int4, quantize_k_turbo, quantize_v,  # noqa: E402
                                             quantize_v_int4, quantize_v_turbo)

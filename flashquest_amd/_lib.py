@@ -112,8 +112,6 @@ SIGNATURES = {
                                             _P, _P, _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int4_noalloc": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I,
                                                     _I, _I, _P, _P, _P]),
-    "fq_read_decode_pages": (ctypes.c_int, [ctypes.POINTER(Int4Cache), _P, _I64P, _I, _P, _P, ctypes.c_size_t, _P]),
-    "fq_read_stream": (ctypes.c_int, [_P, ctypes.c_size_t, _P, _P]),
     "fq_quest_select_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, _P, _P, ctypes.c_size_t, _P]),
     "fq_int4_cache_append": (ctypes.c_int, [ctypes.POINTER(Int4Cache), _I, _P, _I64P, _P, _I64P, _I, _P, _I64P,
@@ -147,6 +145,8 @@ SIGNATURES = {
     "fq_int8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Int4Cache), _I]),
     "fq_page_scores_int8": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
                                            _I, _I, _I, _I, _I, _I, _P]),
+    "fq_page_scores_int8_summary": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _P, _P,
+                                                   _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "fq_sparse_int8_fwd_mask": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I64P,
                                                _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,

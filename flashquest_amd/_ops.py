@@ -171,35 +171,3 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
                 torch.cuda.current_stream(device).synchronize()
             _scalar_retention[key] = r
     return r
-
-
-def read_decode_pages(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, mask: torch.Tensor,
-                      page_size: int = 64) -> None:
-    """Measurement only (no counterpart in the reference): read exactly the
-    bytes a single-launch INT4 decode step reads for the selection ``mask``
-    (L, B, H_q, P), in the same order, and compute nothing.  Its time is the
-    memory system's ceiling for the step's access pattern."""
-    c, keep = int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size)
-    L.require_device(mask, *keep)
-    if mask.dtype != torch.bool or mask.dim() != 4:
-        raise ValueError(f"mask must be a 4D (L, B, H_q, P) bool tensor, got {mask.dtype} {tuple(mask.shape)}")
-    H_q = mask.shape[2]
-    if (mask.shape[0], mask.shape[1], mask.shape[3]) != (c.L, c.B, c.P):
-        raise ValueError(f"mask {tuple(mask.shape)} does not match the cache's (L={c.L}, B={c.B}, H_q, P={c.P})")
-    ws = L.workspace(mask.device, L.lib().fq_workspace_bytes(c, H_q))
-    sink = torch.zeros(1, dtype=torch.int32, device=mask.device)
-    L.check(L.lib().fq_read_decode_pages(c, mask.data_ptr(), L.strides(mask, 4), H_q, sink.data_ptr(),
-                                         ws.data_ptr(), ws.numel(), L.stream_handle(mask.device)),
-            "read_decode_pages")
-
-
-def read_stream(buf: torch.Tensor) -> None:
-    """Measurement only (no counterpart in the reference): read the bytes of
-    the contiguous device tensor ``buf`` with plain streaming loads and compute
-    nothing -- the HBM read rate for that byte count with no access pattern."""
-    L.require_device(buf)
-    if not buf.is_contiguous():
-        raise ValueError("read_stream takes a contiguous tensor")
-    sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
-    nbytes = buf.numel() * buf.element_size()
-    L.check(L.lib().fq_read_stream(buf.data_ptr(), nbytes, sink.data_ptr(), L.stream_handle(buf.device)), "read_stream")

@@ -50,7 +50,7 @@ struct KernelTimer {
 };
 static thread_local KernelTimer g_timer;
 
-static int fail(int code, const char* fmt, ...) {
+int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -60,7 +60,7 @@ static int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-static int hip_status(hipError_t e, const char* what) {
+int hip_status(hipError_t e, const char* what) {
     if (e == hipSuccess) return FQ_OK;
     return fail(FQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
@@ -126,7 +126,7 @@ static bool rows_aligned16(const void* p, const int64_t* strides, int n_outer, i
 
 // bits = 4: packed INT4 (two codes per byte); bits = 8: one code byte per
 // channel (the INT8 cache of flash_attn_sparse_fwd), V metadata per token.
-static int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits = 4, bool allow_empty = false) {
+int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits, bool allow_empty) {
     if (!c) return fail(FQ_ERR_INVALID, "cache descriptor is NULL");
     if (c->D != 64 && c->D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", c->D);
     if (!is_half(c->meta_dtype)) return fail(FQ_ERR_UNSUPPORTED, "metadata dtype must be bf16 or fp16");
@@ -607,6 +607,35 @@ int fq_page_scores_int8(const void* q, int32_t q_dtype, const int64_t q_strides[
     return st;
 }
 
+int fq_page_scores_int8_summary(const void* q, int32_t q_dtype, const int64_t q_strides[4], const uint8_t* k_codes,
+                                const int64_t kc_strides[4], const void* k_scale, const int64_t ks_strides[4],
+                                const void* k_mn, const int64_t km_strides[4], int32_t meta_dtype,
+                                uint16_t* page_min, uint16_t* page_max, const int64_t pm_strides[4], float* scores,
+                                const int64_t sc_strides[4], int32_t B, int32_t H_q, int32_t H_kv, int32_t S,
+                                int32_t P, int32_t D, int32_t page_size, fq_stream_t stream) {
+    if (H_kv < 1 || H_q % H_kv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, H_kv);
+    if (D != 64 && D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", D);
+    if (!is_half(meta_dtype) || !is_float_dtype(q_dtype)) return fail(FQ_ERR_UNSUPPORTED, "dtype");
+    if (!q || !k_codes || !k_scale || !k_mn || !scores) return fail(FQ_ERR_INVALID, "NULL tensor");
+    if ((page_min == nullptr) != (page_max == nullptr)) return fail(FQ_ERR_INVALID, "page_min / page_max: both or neither");
+    if (page_size < 1) return fail(FQ_ERR_INVALID, "page_size must be >= 1");
+    if (S < 0 || P != (S + page_size - 1) / page_size)
+        return fail(FQ_ERR_INVALID, "pages=%d != ceil(S=%d / page_size=%d)", P, S, page_size);
+    if (kc_strides[3] != 1 || kc_strides[2] % 4 || kc_strides[1] % 4 || kc_strides[0] % 4 || ((uintptr_t)k_codes & 3))
+        return fail(FQ_ERR_UNSUPPORTED, "K codes need a contiguous channel axis and 4-byte aligned token rows");
+    if (B == 0 || P == 0) return FQ_OK;
+    if ((int64_t)B * H_kv > 65535) return fail(FQ_ERR_UNSUPPORTED, "batch x KV heads > 65535");
+    SummaryArgs a{};
+    a.codes = k_codes; a.ks = k_scale; a.km = k_mn; a.meta_dtype = meta_dtype;
+    a.q = q; a.q_dtype = q_dtype; a.scores = scores; a.pmin = page_min; a.pmax = page_max;
+    for (int i = 0; i < 4; ++i) {
+        a.c_s[i] = kc_strides[i]; a.ks_s[i] = ks_strides[i]; a.km_s[i] = km_strides[i];
+        a.q_s[i] = q_strides[i]; a.sc_s[i] = sc_strides[i]; a.pm_s[i] = page_min ? pm_strides[i] : 0;
+    }
+    a.B = B; a.Hq = H_q; a.Hkv = H_kv; a.S = S; a.P = P; a.D = D; a.page = page_size;
+    return hip_status(launch_page_summary_scores(a, (hipStream_t)stream), "page summary scores");
+}
+
 int fq_quantize_k_int8(const void* k, int32_t in_dtype, const int64_t k_strides[4], int32_t B, int32_t H,
                        int32_t S, int32_t D, int32_t page_size, uint8_t* codes, const int64_t c_strides[4],
                        void* scale, const int64_t s_strides[4], void* mn, const int64_t m_strides[4],
@@ -1064,36 +1093,6 @@ int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* que
     if (st) return st;
     return fq_quest_decode_int4(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out,
                                 mask_out, ws, (size_t)FQ_NOALLOC_SCRATCH_BYTES, stream);
-}
-
-int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
-                         int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
-    Int4Cache c{};
-    int st = check_cache(cache, &c);
-    if (st) return st;
-    if (H_q < 1 || H_q % c.Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, c.Hkv);
-    if (c.D != 128 || c.page != 64 || (c.G != 1 && c.G != 4))
-        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes the matrix-core decode's layout");
-    if (c.kp_s[3] != 64 || c.vp_s[3] != 64 || c.ksc_s[3] != 128 || c.kmn_s[3] != 128 || c.vsc_s[3] != c.G ||
-        c.vmn_s[3] != c.G)
-        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes packed token / page rows");
-    if (!mask || !sink) return fail(FQ_ERR_INVALID, "NULL mask or sink");
-    const int G = c.L * c.B * c.Hkv, nrep = H_q / c.Hkv;
-    const size_t need = workspace_bytes(G, c.P, nrep, nrep, c.D);
-    if (!workspace || workspace_bytes_ < need)
-        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
-    Workspace ws = carve_workspace(workspace, G, c.P, nrep, nrep, c.D);
-    hipStream_t s = (hipStream_t)stream;
-    st = hip_status(launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, nrep, c.P, ws, s), "page union");
-    if (st) return st;
-    return hip_status(launch_read_step(c, ws, sink, s), "read decode pages");
-}
-
-int fq_read_stream(const void* buf, size_t bytes, uint32_t* sink, fq_stream_t stream) {
-    if (!buf || !sink) return fail(FQ_ERR_INVALID, "NULL buffer or sink");
-    if (((uintptr_t)buf & 15) || (bytes & 15) || bytes == 0)
-        return fail(FQ_ERR_INVALID, "the stream read takes a 16-byte aligned buffer of a nonzero multiple of 16 bytes");
-    return hip_status(launch_read_stream(buf, (int64_t)bytes, sink, (hipStream_t)stream), "read stream");
 }
 
 }  // extern "C"

@@ -250,6 +250,11 @@ void timer_before_launch(hipStream_t st);
 void timer_after_launch(hipStream_t st);
 // fq_set_attention_splits value (0 = automatic).
 int attention_splits_request();
+// Host helpers of the C ABI (capi.cpp), shared with the measurement library:
+// error reporting (fq_last_error), HIP status mapping and cache descriptor checks.
+int fail(int code, const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);
+int check_cache(const fq_int4_cache* c, Int4Cache* out, int bits = 4, bool allow_empty = false);
 size_t workspace_bytes(int G, int P, int rows, int nrep, int D);
 Workspace carve_workspace(void* base, int G, int P, int rows, int nrep, int D);
 AttnLaunch choose_split(int G, int max_entries, int s_max);
@@ -310,6 +315,19 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
                                  hipStream_t st, const SelectArgs* sel, const TailArgs* tail = nullptr);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+// Page summary scores over the INT8 cache (summary.hip).
+struct SummaryArgs {
+    const uint8_t* codes; int64_t c_s[4];          // (B, H_kv, S, D) bytes
+    const void* ks; int64_t ks_s[4];               // (B, H_kv, P, D) elements
+    const void* km; int64_t km_s[4];
+    int meta_dtype;
+    const void* q; int q_dtype; int64_t q_s[4];    // (B, H_q, 1, D)
+    float* scores; int64_t sc_s[4];                // (B, H_q, 1, P)
+    uint16_t* pmin; uint16_t* pmax; int64_t pm_s[4];   // optional bf16 summaries (B, H_kv, P, D)
+    int B, Hq, Hkv, S, P, D, page;
+};
+
+hipError_t launch_page_summary_scores(const SummaryArgs& a, hipStream_t st);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                                  const AttnLaunch& al, hipStream_t st, const SelectArgs* sel,
                                  const TailArgs* tail = nullptr);

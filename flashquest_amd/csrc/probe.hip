@@ -9,10 +9,14 @@
 // attention math add.  Every loaded word is folded into a value that is
 // stored only if it hits an unlikely constant, so no load is dead.
 //
+// Built into its own library, libfq_probe.so (entries in fq_probe.h), which
+// bench.py loads; the product library libfq_hip.so does not contain it.
+//
 // read_stream_kernel is the plainest read of the same byte count: one
 // contiguous buffer, 2048 workgroups of 512 threads each streaming a
 // contiguous slice with four 16-byte loads in flight per thread -- the rate
 // HBM gives a read of this size with no access pattern at all.
+#include "fq_probe.h"
 #include "fused_common.h"
 
 namespace fq {
@@ -112,3 +116,39 @@ hipError_t launch_read_step(const Int4Cache& c, const Workspace& ws, unsigned* s
 }
 
 }  // namespace fq
+
+using namespace fq;
+
+extern "C" {
+
+int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
+                         int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes_, fq_stream_t stream) {
+    Int4Cache c{};
+    int st = check_cache(cache, &c);
+    if (st) return st;
+    if (H_q < 1 || H_q % c.Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, c.Hkv);
+    if (c.D != 128 || c.page != 64 || (c.G != 1 && c.G != 4))
+        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes the matrix-core decode's layout");
+    if (c.kp_s[3] != 64 || c.vp_s[3] != 64 || c.ksc_s[3] != 128 || c.kmn_s[3] != 128 || c.vsc_s[3] != c.G ||
+        c.vmn_s[3] != c.G)
+        return fail(FQ_ERR_UNSUPPORTED, "the read-only pass takes packed token / page rows");
+    if (!mask || !sink) return fail(FQ_ERR_INVALID, "NULL mask or sink");
+    const int G = c.L * c.B * c.Hkv, nrep = H_q / c.Hkv;
+    const size_t need = workspace_bytes(G, c.P, nrep, nrep, c.D);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(FQ_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes_);
+    Workspace ws = carve_workspace(workspace, G, c.P, nrep, nrep, c.D);
+    hipStream_t s = (hipStream_t)stream;
+    st = hip_status(fq::launch_union_from_mask(mask, mask_strides, c.L, c.B, c.Hkv, nrep, c.P, ws, s), "page union");
+    if (st) return st;
+    return hip_status(launch_read_step(c, ws, sink, s), "read decode pages");
+}
+
+int fq_read_stream(const void* buf, size_t bytes, uint32_t* sink, fq_stream_t stream) {
+    if (!buf || !sink) return fail(FQ_ERR_INVALID, "NULL buffer or sink");
+    if (((uintptr_t)buf & 15) || (bytes & 15) || bytes == 0)
+        return fail(FQ_ERR_INVALID, "the stream read takes a 16-byte aligned buffer of a nonzero multiple of 16 bytes");
+    return hip_status(launch_read_stream(buf, (int64_t)bytes, sink, (hipStream_t)stream), "read stream");
+}
+
+}  // extern "C"

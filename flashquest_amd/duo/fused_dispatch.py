@@ -1,26 +1,27 @@
-"""DuoAttention decode in one fused call (src/flashquest/duo/fused_dispatch.py:19-78).
+"""DuoAttention decode in one call (src/flashquest/duo/fused_dispatch.py:19-78).
 
-quest_duo_fused_sdpa keeps the reference's signature over the INT8 cache:
-streaming KV heads get retention 0, so their query heads keep exactly the
-sink and window pages, retrieval heads the top ``retention`` share of their
-pages; scoring, selection and attention then run as one HIP decode step
-(quest_decode_int8, per-query-head selection).
+quest_duo_fused_sdpa keeps the reference's signature and its three steps over
+the INT8 cache, each a HIP launch:
 
-Scoring: the reference's helper scores from the dequantised keys' exact page
-minimum / maximum (page_summary + page_scores); its attention patch, which
-this build follows, scores from the page metadata (min = K_mn, max = K_mn +
-255 K_scale; _criticality_scores, llama_persistent_patch.py:152-153 with
-criticality.py:98-125).  The two bounds agree where a page channel's codes
-reach 0 and 255; the quantiser maps the channel minimum to code 0 and the
-maximum to 255 up to the rounding of the half-precision scale, so the
-selections can differ only on pages whose scores fall within that rounding of
-the k-th score.
+1. Quest scores from the exact page summary of the bf16-dequantised keys
+   (dequantize_k -> compute_page_summary -> page_scores, fused_dispatch.py:
+   64-67): ``page_scores_int8_summary``, one launch.
+2. ``select_pages`` with the per-query-head retention vector: retrieval heads
+   keep ``retention``, streaming heads 0, so they select exactly the sink and
+   window pages (fused_dispatch.py:56-62, 69-72).
+3. ``flash_attn_sparse_fwd`` over that mask (fused_dispatch.py:74-77).
+
+(The decode step ``quest_decode_int8(..., head_pattern=...)`` is the faster
+single-launch form of the same pattern; it scores from the page metadata, as
+the reference's attention patch does.)
 """
 from __future__ import annotations
 
 import torch
 
-from ..eager.decode import quest_decode_int8
+from ..eager.criticality import page_scores_int8_summary
+from ..eager.selection import select_pages
+from ..kernel import flash_attn_sparse_fwd
 
 
 def quest_duo_fused_sdpa(Q: torch.Tensor, K_uint8: torch.Tensor, K_scale: torch.Tensor, K_mn: torch.Tensor,
@@ -30,13 +31,18 @@ def quest_duo_fused_sdpa(Q: torch.Tensor, K_uint8: torch.Tensor, K_scale: torch.
     """Q (B, H_q, 1, D); INT8 cache (B, H_kv, S, D) codes, (B, H_kv, P, D) K
     scale/min, (B, H_kv, S, 1) V scale/min; head_pattern (H_kv,) bool, True =
     retrieval.  Returns O (B, H_q, 1, D) in Q's dtype."""
-    if Q.shape[2] != 1:
-        raise NotImplementedError(f"quest_duo_fused_sdpa decodes one token per call (S_q={Q.shape[2]})")
+    B, H_q, S_q, D = Q.shape
+    if S_q != 1:
+        raise NotImplementedError(f"quest_duo_fused_sdpa decodes one token per call (S_q={S_q})")
     H_kv = K_uint8.shape[1]
     if tuple(head_pattern.shape) != (H_kv,):
         raise ValueError(f"head_pattern needs one entry per KV head, shape ({H_kv},); "
                          f"got {tuple(head_pattern.shape)}")
-    O, _ = quest_decode_int8(Q, K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, retention=float(retention),
-                             num_sinks=num_sinks, window_pages=window_pages, page_size=page_size,
-                             select_mode="per_q_head", return_lse=False, head_pattern=head_pattern.bool())
+    n_rep = H_q // H_kv
+    per_q = head_pattern.bool().cpu().repeat_interleave(n_rep)
+    r = torch.where(per_q, torch.full((H_q,), float(retention)), torch.zeros(H_q))
+    scores = page_scores_int8_summary(Q, K_uint8, K_scale, K_mn, page_size)
+    sel = select_pages(scores, r, num_sinks, window_pages)
+    O, _ = flash_attn_sparse_fwd(Q, K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, selection_mask=sel,
+                                 page_size=page_size, return_lse=False)
     return O

@@ -5,6 +5,8 @@ radix select over the fp32 scores; equal scores go to the lower page index.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .. import _lib as L
@@ -36,8 +38,35 @@ def select_pages_vectorized(
 
 
 def select_pages(scores, retention, num_sinks: int, window_pages: int) -> torch.Tensor:
-    """selection.py:9-62 (the per-head loop form); same result as the vectorized form."""
-    return select_pages_vectorized(scores, retention, num_sinks, window_pages)
+    """selection.py:9-62, the per-head loop form.  Its k differs from the
+    vectorized form's: each head's fp32 retention is read back to the host
+    (``.item()``, a double) and k = ceil(r * P) is taken in double precision
+    (r >= 1: every page, r <= 0: none), where select_pages_vectorized rounds
+    r * P to fp32 first (selection.py:103).  The two differ when fp32(r * P)
+    rounds onto an integer that the double product exceeds.  Like the
+    reference, this reads the retention on the host; each head's k is then
+    passed to the selection kernel as the retention fp32((k - 1/2) / P), whose
+    fp32 ceil(r * P) is exactly k."""
+    B, H, S_q, P = scores.shape
+    if isinstance(retention, torch.Tensor):
+        if retention.shape != (H,):
+            raise ValueError(f"per-head retention must be shape ({H},); got {tuple(retention.shape)}")
+        r_host = retention.detach().float().cpu().tolist()
+    else:
+        if not (0.0 <= float(retention) <= 1.0):
+            raise ValueError(f"scalar retention must be in [0, 1]; got {retention}")
+        r_host = [float(torch.tensor(float(retention), dtype=torch.float32))] * H
+    adj = []
+    for r in r_host:
+        if r >= 1.0:
+            adj.append(1.0)
+        elif r <= 0.0:
+            adj.append(0.0)
+        else:
+            k = min(math.ceil(r * P), P)
+            adj.append(1.0 if k >= P else (k - 0.5) / P)
+    r_dev = torch.tensor(adj, dtype=torch.float32).to(scores.device)
+    return select_pages_vectorized(scores, r_dev, num_sinks, window_pages)
 
 
 def build_compact_selection(mask: torch.Tensor, BUCKET_MAX: int) -> torch.Tensor:

@@ -210,24 +210,6 @@ int fq_quest_decode_int4_noalloc(const fq_int4_cache* cache, const fq_query* que
                                  int32_t k_max, int32_t select_mode,
                                  float* scores_out, uint8_t* mask_out, fq_stream_t stream);
 
-/* Measurement only; no counterpart in the reference.  Reads exactly what
- * fq_quest_decode_int4's single launch reads for the selection `mask`
- * (L, B, H_q, P) -- every page's K scale / min, then the K and V codes, V
- * scale / min and K scale / min of each KV group's union of selected pages --
- * with the same per-workgroup order and granularity, and computes nothing:
- * the memory system's ceiling for the step's access pattern.  `sink` is a
- * device word written only if the folded bytes hit an unlikely constant.
- * Workspace as fq_workspace_bytes (the union lists). */
-int fq_read_decode_pages(const fq_int4_cache* cache, const uint8_t* mask, const int64_t mask_strides[4],
-                         int32_t H_q, uint32_t* sink, void* workspace, size_t workspace_bytes, fq_stream_t stream);
-
-/* Measurement only; no counterpart in the reference.  Reads `bytes` (a
- * nonzero multiple of 16) of one contiguous, 16-byte aligned device buffer
- * with plain streaming loads and computes nothing: the rate HBM gives a read
- * of that size with no access pattern, the reference point for
- * fq_read_decode_pages.  `sink` as there. */
-int fq_read_stream(const void* buf, size_t bytes, uint32_t* sink, fq_stream_t stream);
-
 /* The two halves of fq_quest_decode_int4, for callers that time or overlap
  * them separately; call both with the same cache, query, retention, k_max,
  * num_sinks, window_pages, select_mode and workspace.  fq_quest_select_int4
@@ -418,6 +400,26 @@ int fq_page_scores_int8(const void* q, int32_t q_dtype, const int64_t q_strides[
                         float* scores, const int64_t sc_strides[4],
                         int32_t B, int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D,
                         fq_stream_t stream);
+
+/* Replaces the scoring of quest_duo_fused_sdpa (duo/fused_dispatch.py:64-67):
+ * dequantize_k (kernel/kv_quant.py:64-75, bf16 keys) -> compute_page_summary
+ * (eager/page_summary.py:7-39, per page and channel the min / max key over
+ * the page's valid tokens) -> page_scores (eager/criticality.py:7-31,
+ * sum_d max(q_d * max_d, q_d * min_d) in fp32, GQA broadcast).  Decode
+ * queries (B, H_q, 1, D); INT8 codes (B, H_kv, S, D) with a contiguous channel
+ * axis and 4-byte aligned token rows; K scale / min (B, H_kv, P, D) in
+ * meta_dtype, P = ceil(S / page_size); scores (B, H_q, 1, P).  page_min /
+ * page_max (bf16, strides pm_strides, (B, H_kv, P, D)): the summaries, or
+ * both NULL.  fp32 order: per 4 channels left to right, then a butterfly over
+ * the D/4 partial sums. */
+int fq_page_scores_int8_summary(const void* q, int32_t q_dtype, const int64_t q_strides[4],
+                                const uint8_t* k_codes, const int64_t kc_strides[4],
+                                const void* k_scale, const int64_t ks_strides[4],
+                                const void* k_mn, const int64_t km_strides[4], int32_t meta_dtype,
+                                uint16_t* page_min, uint16_t* page_max, const int64_t pm_strides[4],
+                                float* scores, const int64_t sc_strides[4],
+                                int32_t B, int32_t H_q, int32_t H_kv, int32_t S, int32_t P, int32_t D,
+                                int32_t page_size, fq_stream_t stream);
 
 /* Replaces flash_attn_sparse_fwd (kernel/sparse_fwd.py:160-228, kernel
  * 23-157): sparse GQA decode attention over the INT8 cache for a boolean page

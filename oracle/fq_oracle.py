@@ -298,6 +298,50 @@ def sparse_int8_attention(Q, K_u8, K_scale, K_mn, V_u8, V_scale, V_mn, page_mask
 # Page scoring (eager/criticality.py:7-31, 128-163)
 # ----------------------------------------------------------------------------
 
+def page_summary_int8(K_u8, K_scale, K_mn, page_size: int):
+    """dequantize_k (kv_quant.py:64-75: codes * fp32(scale) + fp32(mn), then
+    bf16) followed by compute_page_summary (page_summary.py:7-39: per page and
+    channel the min / max over the page's tokens, a partial last page padded
+    with +-inf).  Returns (page_min, page_max) (B, H, P, D) as fp32 values of
+    the bf16 keys."""
+    kd = round_bf16(dequant_k_int8(K_u8, K_scale, K_mn, page_size))
+    B, H, S, D = kd.shape
+    P = (S + page_size - 1) // page_size
+    pad = P * page_size - S
+    lo = np.concatenate([kd, np.full((B, H, pad, D), np.inf, F32)], axis=2)
+    hi = np.concatenate([kd, np.full((B, H, pad, D), -np.inf, F32)], axis=2)
+    lo = lo.reshape(B, H, P, page_size, D).min(axis=3)
+    hi = hi.reshape(B, H, P, page_size, D).max(axis=3)
+    return lo.astype(F32), hi.astype(F32)
+
+
+def page_scores_quest_fixed(Q, page_min, page_max):
+    """page_scores (criticality.py:7-31) with this build's fixed fp32 order:
+    term_d = max(q_d * max_d, q_d * min_d) (each product rounded to fp32);
+    lane j sums terms 4j .. 4j+3 left to right, then the D/4 lane sums combine
+    by the butterfly v_j += v_(j ^ o) for o = D/8, D/16, ..., 1.
+    Q (B, H_q, D); summaries (B, H_kv, P, D).  Returns (B, H_q, P) fp32."""
+    Q = np.asarray(Q, F32)
+    B, Hq, D = Q.shape
+    Hkv, P = page_min.shape[1], page_min.shape[2]
+    rep = Hq // Hkv
+    mn = np.repeat(np.asarray(page_min, F32), rep, axis=1)
+    mx = np.repeat(np.asarray(page_max, F32), rep, axis=1)
+    q = Q[:, :, None, :]
+    term = np.maximum((q * mx).astype(F32), (q * mn).astype(F32)).astype(F32)   # (B, Hq, P, D)
+    t4 = term.reshape(B, Hq, P, D // 4, 4)
+    v = t4[..., 0].copy()
+    for i in range(1, 4):
+        v = (v + t4[..., i]).astype(F32)
+    nl = D // 4
+    idx = np.arange(nl)
+    o = nl // 2
+    while o >= 1:
+        v = (v + v[..., idx ^ o]).astype(F32)
+        o //= 2
+    return v[..., 0]
+
+
 def page_scores_quest(Q, page_min, page_max):
     """criticality.py:7-31: sum_d max(q_d*min_d, q_d*max_d), fp64, GQA-broadcast.
 
@@ -475,6 +519,39 @@ def select_pages_vectorized(scores, retention, num_sinks: int, window_pages: int
     for h in range(H):
         mask[h] = topk_mask_rows(rows[h], np.full((B * Sq,), k_eff[h]))
     mask = mask.reshape(H, B, Sq, P).transpose(1, 0, 2, 3).copy()
+    if num_sinks > 0:
+        mask[..., :min(num_sinks, P)] = True
+    if window_pages > 0:
+        mask[..., P - min(window_pages, P):] = True
+    return mask
+
+
+def select_pages(scores, retention, num_sinks: int, window_pages: int):
+    """selection.py:9-62 (the per-head loop form): per head, r = the fp32
+    retention read back as a double; r >= 1 selects every page, r <= 0 none,
+    otherwise the top ceil(r * P) (double product), then the sink and window
+    pages.  scores (B, H, S_q, P) -> bool mask."""
+    scores = np.asarray(scores, F32)
+    B, H, Sq, P = scores.shape
+    if np.isscalar(retention):
+        if not 0.0 <= float(retention) <= 1.0:
+            raise ValueError("scalar retention must be in [0, 1]")
+        r = np.full((H,), retention, dtype=F32)
+    else:
+        r = np.asarray(retention, dtype=F32)
+        if r.shape != (H,):
+            raise ValueError("per-head retention must be shape (H,)")
+    mask = np.zeros((B, H, Sq, P), dtype=bool)
+    for h in range(H):
+        rh = float(r[h])
+        if rh >= 1.0:
+            mask[:, h] = True
+            continue
+        if rh <= 0.0:
+            continue
+        k = math.ceil(rh * P)
+        rows = scores[:, h].reshape(B * Sq, P)
+        mask[:, h] = topk_mask_rows(rows, np.full((B * Sq,), k)).reshape(B, Sq, P)
     if num_sinks > 0:
         mask[..., :min(num_sinks, P)] = True
     if window_pages > 0:

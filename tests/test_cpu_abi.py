@@ -31,3 +31,20 @@ def test_workspace_size_is_pure_host_arithmetic():
     n = lib.fq_workspace_bytes(c, 24)
     assert n > 28 * 8 * 512 * 4
     assert lib.fq_workspace_bytes(c, 25) == 0
+
+
+def test_probe_library_is_separate_and_exports_its_entries():
+    """The benchmark's measurement probes live in libfq_probe.so with their own
+    header (csrc/fq_probe.h), not in the product library or its public header."""
+    from flashquest_amd import _probe
+    text = open(os.path.join(ROOT, "flashquest_amd", "csrc", "fq_probe.h")).read()
+    names = sorted(set(re.findall(r"^\s*int\s+(fq_\w+)\(", text, re.M)))
+    assert names == sorted(_probe.SIGNATURES) == ["fq_read_decode_pages", "fq_read_stream"]
+    lib = _probe.probe_lib()
+    for n in names:
+        assert hasattr(lib, n)
+        assert not hasattr(_lib.load_library(), n), n
+        assert n not in _declared()
+    # a refused call reports through the product library's fq_last_error
+    assert lib.fq_read_stream(None, 16, None, None) == _lib.FQ_ERR_INVALID
+    assert "NULL buffer" in _lib.lib().fq_last_error().decode()

@@ -386,7 +386,7 @@ def test_turbo_fused_step_at_size(turbo_cfg1, mode, qdtype):
 def test_read_only_pass_runs_on_config1(cfg1):
     """The bench's ceiling probe (fq_read_decode_pages) takes config 1's cache
     and the decode's own selection mask and completes."""
-    from flashquest_amd._ops import read_decode_pages
+    from flashquest_amd._probe import read_decode_pages
     planes = [cfg1[k] for k in PLANES]
     _, _, mask = quest_decode_int4(cfg1["Q"], *planes, retention=0.25, num_sinks=4, window_pages=2,
                                    return_selection=True)
@@ -398,7 +398,7 @@ def test_read_only_pass_runs_on_config1(cfg1):
 def test_stream_read_probe_runs_and_checks_its_buffer():
     """The bench's plain-read reference (fq_read_stream) reads a config-1-sized
     buffer, and refuses sizes that are not whole 16-byte chunks."""
-    from flashquest_amd._ops import read_stream
+    from flashquest_amd._probe import read_stream
     buf = torch.zeros(332717696, dtype=torch.uint8, device="cuda")
     for _ in range(2):
         read_stream(buf)

@@ -4,6 +4,8 @@ exactly the sink and window pages, retrieval heads the top-k of their scores,
 and attention follows the selection.  A (layers, KV heads) pattern in one
 multi-layer call gives each layer its own retention row (the single-launch
 kernel and the split path agree bit for bit on the selection)."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -95,27 +97,99 @@ def test_layer_patterns_past_512_pages(mode):
         assert max_err(lse[i][:, :, 0], ref["lse"]) <= 1e-4, i
 
 
-def test_quest_duo_fused_sdpa_signature_and_semantics():
-    from flashquest_amd.duo import quest_duo_fused_sdpa
-    Hq, Hkv, P = 8, 4, 24
-    case = Int8Case(seed=77, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128)
+@pytest.mark.parametrize("D,Hq,Hkv,S,meta,qdt", [(128, 8, 4, 64 * 24, "bf16", "bf16"),
+                                                  (128, 24, 8, 64 * 40 + 17, "bf16", "f16"),
+                                                  (64, 8, 1, 64 * 9 + 63, "f16", "bf16"),
+                                                  (128, 4, 4, 37, "bf16", "f32")])
+def test_page_summary_scores_bit_exact(D, Hq, Hkv, S, meta, qdt):
+    """The Duo dispatch's scoring (dequantize_k -> compute_page_summary ->
+    page_scores, duo/fused_dispatch.py:64-67) in one launch: the bf16 page
+    summaries and the fixed-order fp32 scores equal the oracle's bit for bit,
+    partial last pages included."""
+    from flashquest_amd.eager.criticality import page_scores_int8_summary
+    case = Int8Case(seed=D + S, B=2, Hq=Hq, Hkv=Hkv, S=S, D=D, meta=meta, dtype="bf16")
     d = case.device()
-    pattern = torch.tensor([True, False, True, False])
+    q = case.q_dev() if qdt == "bf16" else case.q_dev().to({"f16": torch.float16, "f32": torch.float32}[qdt])
+    sc, pmin, pmax = page_scores_int8_summary(q, d["K_uint8"], d["K_scale"], d["K_mn"], 64, return_summary=True)
+    torch.cuda.synchronize()
+    lo, hi = O.page_summary_int8(case.ku, case.ks, case.km, 64)
+    assert np.array_equal(pmin.float().cpu().numpy(), lo) and np.array_equal(pmax.float().cpu().numpy(), hi)
+    ref = O.page_scores_quest_fixed(q[:, :, 0].float().cpu().numpy(), lo, hi)
+    assert np.array_equal(sc[:, :, 0].cpu().numpy(), ref)
+    # strided codes (a view of a longer cache) give the same scores
+    big = torch.zeros(2, Hkv, S + 64, D, dtype=torch.uint8, device=q.device)
+    big[:, :, :S] = d["K_uint8"]
+    sc2 = page_scores_int8_summary(q, big[:, :, :S], d["K_scale"], d["K_mn"], 64)
+    torch.cuda.synchronize()
+    assert torch.equal(sc, sc2)
+
+
+def test_select_pages_loop_form_double_precision_k():
+    """select_pages (selection.py:9-62) takes k = ceil(r * P) in double
+    precision: 0.07 of 100 pages keeps 8 (the vectorized form keeps 7)."""
+    from flashquest_amd.eager.selection import select_pages, select_pages_vectorized
+    sc = torch.arange(100, dtype=torch.float32, device="cuda").view(1, 1, 1, 100).repeat(1, 3, 1, 1)
+    r = torch.tensor([0.07, 0.0, 1.0])
+    m = select_pages(sc, r, 1, 1)
+    mv = select_pages_vectorized(sc, r, 1, 1)
+    torch.cuda.synchronize()
+    ref = O.select_pages(sc.cpu().numpy(), r.numpy(), 1, 1)
+    assert np.array_equal(m.cpu().numpy(), ref)
+    assert int(m[0, 0].sum()) == 9 and int(mv[0, 0].sum()) == 8        # + sink 0 (the top-k holds window 99)
+    assert int(m[0, 1].sum()) == 2 and bool(m[0, 2].all())
+
+
+@pytest.mark.parametrize("Hq,Hkv,P,pattern", [(8, 4, 24, [True, False, True, False]),
+                                               (24, 8, 64, [True] * 8),
+                                               (24, 8, 40, [False, True] * 4)])
+def test_quest_duo_fused_sdpa_reference_semantics(Hq, Hkv, P, pattern):
+    """quest_duo_fused_sdpa against the oracle's restatement of the
+    reference's three steps: page summary scores of the bf16-dequantised keys,
+    select_pages with retention 0.25 on retrieval heads and 0 on streaming
+    heads, INT8 sparse attention over that mask.  The selection is checked
+    bit for bit (same fixed score order) and against the fp64 Quest bound
+    wherever its top-k boundary is not an fp32 near-tie."""
+    from flashquest_amd.duo import quest_duo_fused_sdpa
+    from flashquest_amd.eager.criticality import page_scores_int8_summary
+    from flashquest_amd.eager.selection import select_pages
+    case = Int8Case(seed=77 + P, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128)
+    d = case.device()
+    pat = torch.tensor(pattern)
     o = quest_duo_fused_sdpa(case.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"], d["V_uint8"], d["V_scale"],
-                             d["V_mn"], head_pattern=pattern, retention=0.25, num_sinks=4, window_pages=2)
+                             d["V_mn"], head_pattern=pat, retention=0.25, num_sinks=4, window_pages=2)
     torch.cuda.synchronize()
-    rrow = _retention_rows(pattern.numpy(), 0.25, Hq // Hkv)
-    ref = O.decode_step(case.Q, case.ku, case.ks, case.km, case.vu, case.vs, case.vm, retention=rrow, num_sinks=4,
-                        window_pages=2, bits=8)
+    lo, hi = O.page_summary_int8(case.ku, case.ks, case.km, 64)
+    scores = O.page_scores_quest_fixed(case.Q, lo, hi)
+    rrow = _retention_rows(pat.numpy(), 0.25, Hq // Hkv)
+    mask = O.select_pages(scores[:, :, None, :], rrow, 4, 2)[:, :, 0, :]
+    ref_o, _ = O.sparse_int8_attention(case.Q, case.ku, case.ks, case.km, case.vu, case.vs, case.vm, mask, 64)
     assert o.shape == (1, Hq, 1, 128) and o.dtype == torch.bfloat16
-    assert max_err(o[:, :, 0], ref["O"]) <= 2e-3 + 2.0 ** -8 * float(np.abs(ref["O"]).max())
-    # all-streaming: attention over sinks and window only (duo's EP2)
-    o_s = quest_duo_fused_sdpa(case.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"], d["V_uint8"], d["V_scale"],
-                               d["V_mn"], head_pattern=torch.zeros(Hkv, dtype=torch.bool))
+    assert max_err(o[:, :, 0], ref_o) <= decode_tol(ref_o, "bf16")
+    # the mask itself, through the operators the dispatch calls
+    sel = select_pages(page_scores_int8_summary(case.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"]),
+                       torch.from_numpy(rrow), 4, 2)
     torch.cuda.synchronize()
-    forced = np.broadcast_to(_forced(P, 4, 2), (1, Hq, P))
-    ro, _ = O.sparse_int8_attention(case.Q, case.ku, case.ks, case.km, case.vu, case.vs, case.vm, forced, 64)
-    assert max_err(o_s[:, :, 0], ro) <= 2e-3 + 2.0 ** -8 * float(np.abs(ro).max())
+    assert np.array_equal(sel[:, :, 0].cpu().numpy(), mask)
+    exact = O.page_scores_quest(case.Q, lo, hi)
+    k = math.ceil(float(np.float32(0.25)) * P)
+    forced = _forced(P, 4, 2)
+    rep = Hq // Hkv
+    amb = 0
+    for h in range(Hq):
+        if rrow[h] == 0:
+            assert np.array_equal(mask[0, h], forced)
+            continue
+        order = np.argsort(-exact[0, h], kind="stable")
+        mag = np.maximum(np.abs(lo[0, h // rep]), np.abs(hi[0, h // rep])).astype(np.float64)
+        tau = 140 * 2.0 ** -24 * (mag @ np.abs(case.Q[0, h]).astype(np.float64))
+        top, rest = order[:k], order[k:]
+        if np.min(exact[0, h, top] - tau[top]) <= np.max(exact[0, h, rest] + tau[rest]):
+            amb += 1
+            continue
+        want = forced.copy()
+        want[top] = True
+        assert np.array_equal(mask[0, h], want), h
+    print(f"[duo] Hq={Hq} P={P}: ambiguous rows {amb}", flush=True)
     with pytest.raises(ValueError, match="head_pattern"):
         quest_duo_fused_sdpa(case.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"], d["V_uint8"], d["V_scale"],
-                             d["V_mn"], head_pattern=torch.tensor([True, False, True]))
+                             d["V_mn"], head_pattern=torch.tensor([True] * (Hkv + 1)))
