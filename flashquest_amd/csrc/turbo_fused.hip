@@ -432,40 +432,45 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         // ---- p.v B: codes of channel 8 n16 + j for the step's 8 tokens, 4 at a time
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            uint32_t bw[8][4], bwl[8][4];       // [channel tile j][dword]: codebook hi / lo parts
+            // per half hh: operand k = 4 hh + kk is token i = 4 (2 st + (kk & 1)) + 2 hh + (kk >> 1);
+            // m4: the 4 tokens' MSB bytes, ll / lh: their LSB fields of channels 0-3 / 4-7
+            uint32_t m4[2], ll[2], lh[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                // operand k = 4 hh + kk: token index i = 4 (2 st + (kk & 1)) + 2 hh + (kk >> 1)
                 const int i0 = 8 * st + 2 * hh, i1 = i0 + 4, i2 = i0 + 1, i3 = i0 + 5;
-                const uint32_t m4 = pb.vm[i0] | (pb.vm[i1] << 8) | (pb.vm[i2] << 16) | (pb.vm[i3] << 24);
+                m4[hh] = pb.vm[i0] | (pb.vm[i1] << 8) | (pb.vm[i2] << 16) | (pb.vm[i3] << 24);
                 const uint32_t x01 = __builtin_amdgcn_perm(pb.vl[i1], pb.vl[i0], 0x05010400u);
                 const uint32_t x23 = __builtin_amdgcn_perm(pb.vl[i3], pb.vl[i2], 0x05010400u);
-                const uint32_t ll = __builtin_amdgcn_perm(x23, x01, 0x05040100u);   // low bytes: channels 0-3
-                const uint32_t lh = __builtin_amdgcn_perm(x23, x01, 0x07060302u);   // high bytes: channels 4-7
+                ll[hh] = __builtin_amdgcn_perm(x23, x01, 0x05040100u);
+                lh[hh] = __builtin_amdgcn_perm(x23, x01, 0x07060302u);
+            }
+            const v8h a = st ? ap1 : ap0;
+            v8h bl_prev;        // tile j - 1's lo-part operand: its matrix instruction follows tile j's
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t lx = j < 4 ? ll : lh;
+            for (int j = 0; j < 8; ++j) {
+                uint32_t bw[4], bwl[4];       // channel tile j: codebook hi / lo parts
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint32_t lx = j < 4 ? ll[hh] : lh[hh];
                     // byte k: msb bit j of token k at bit 2, its lsb field j below
-                    const uint32_t mj = j >= 2 ? m4 >> (j - 2) : m4 << (2 - j);
+                    const uint32_t mj = j >= 2 ? m4[hh] >> (j - 2) : m4[hh] << (2 - j);
                     const uint32_t sel = (mj & 0x04040404u) | ((lx >> (2 * (j & 3))) & 0x03030303u);
                     const uint32_t lo = __builtin_amdgcn_perm(tbv[0][0][1], tbv[0][0][0], sel);
                     const uint32_t hi = __builtin_amdgcn_perm(tbv[0][1][1], tbv[0][1][0], sel);
-                    bw[j][2 * hh] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-                    bw[j][2 * hh + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+                    bw[2 * hh] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                    bw[2 * hh + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
                     const uint32_t llo = __builtin_amdgcn_perm(tbv[1][0][1], tbv[1][0][0], sel);
                     const uint32_t lhi = __builtin_amdgcn_perm(tbv[1][1][1], tbv[1][1][0], sel);
-                    bwl[j][2 * hh] = __builtin_amdgcn_perm(lhi, llo, 0x05010400u);
-                    bwl[j][2 * hh + 1] = __builtin_amdgcn_perm(lhi, llo, 0x07030602u);
+                    bwl[2 * hh] = __builtin_amdgcn_perm(lhi, llo, 0x05010400u);
+                    bwl[2 * hh + 1] = __builtin_amdgcn_perm(lhi, llo, 0x07030602u);
                 }
-            }
-            const v8h a = st ? ap1 : ap0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const v8h bv = __builtin_bit_cast(v8h, (v4i){(int)bw[j][0], (int)bw[j][1], (int)bw[j][2], (int)bw[j][3]});
-                const v8h bl = __builtin_bit_cast(v8h, (v4i){(int)bwl[j][0], (int)bwl[j][1], (int)bwl[j][2], (int)bwl[j][3]});
+                const v8h bv = __builtin_bit_cast(v8h, (v4i){(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]});
+                const v8h bl = __builtin_bit_cast(v8h, (v4i){(int)bwl[0], (int)bwl[1], (int)bwl[2], (int)bwl[3]});
                 pacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv, pacc[j], 0, 0, 0);
-                pacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, pacc[j], 0, 0, 0);
+                if (j > 0) pacc[j - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl_prev, pacc[j - 1], 0, 0, 0);
+                bl_prev = bl;
             }
+            pacc[7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl_prev, pacc[7], 0, 0, 0);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     };
