@@ -265,10 +265,14 @@ FQ_DEV uint32_t wave_max_u32(uint32_t v) {
 template <int C>
 FQ_DEV uint32_t wave_kth_hist(const uint32_t (&key)[C], int k, uint32_t* hist, bool* exact) {
     const int lane = lane_id();
-    uint32_t lo = key[0], hi = key[0];
+    // lo: the smallest key above 0.  Key 0 marks a slot past the last page
+    // (below every score, never among the top k <= P), so leaving it out of
+    // the common prefix only skips more leading bits when P < 64 C.
+    uint32_t lo = key[0] ? key[0] : ~0u, hi = key[0];
 #pragma unroll
-    for (int j = 1; j < C; ++j) { lo = min(lo, key[j]); hi = max(hi, key[j]); }
+    for (int j = 1; j < C; ++j) { lo = min(lo, key[j] ? key[j] : ~0u); hi = max(hi, key[j]); }
     lo = wave_min_u32(lo);
+    if (lo > hi) lo = hi;            // no key above 0
     hi = wave_max_u32(hi);
     if (exact) *exact = false;
     if (lo == hi) return hi;
