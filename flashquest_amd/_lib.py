@@ -147,6 +147,11 @@ SIGNATURES = {
                                            _I, _I, _I, _I, _I, _I, _P]),
     "fq_page_scores_int8_summary": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _P, _P,
                                                    _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "fq_page_summary": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _I, _P, _P, _I64P, _P]),
+    "fq_page_scores_quest": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
+                                            _I, _I, _I, _I, _I, _I, _P]),
+    "fq_page_scores_int8_bound": (ctypes.c_int, [_P, _I, _I64P, _P, _I64P, _P, _I64P, _I, _P, _I64P,
+                                                 _I, _I, _I, _I, _I, _I, _P]),
     "fq_sparse_int8_fwd_mask": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I64P,
                                                _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,

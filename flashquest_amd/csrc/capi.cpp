@@ -636,6 +636,62 @@ int fq_page_scores_int8_summary(const void* q, int32_t q_dtype, const int64_t q_
     return hip_status(launch_page_summary_scores(a, (hipStream_t)stream), "page summary scores");
 }
 
+int fq_page_summary(const void* k, int32_t k_dtype, const int64_t k_strides[4], int32_t B, int32_t H, int32_t S,
+                    int32_t D, int32_t page_size, void* page_min, void* page_max, const int64_t pm_strides[4],
+                    fq_stream_t stream) {
+    if (!is_float_dtype(k_dtype)) return fail(FQ_ERR_INVALID, "K dtype must be bf16, fp16 or fp32");
+    if (page_size < 1) return fail(FQ_ERR_INVALID, "page_size must be >= 1");
+    if (D < 1 || D > 1024) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in [1, 1024]", D);
+    if (B < 0 || H < 0 || S < 0) return fail(FQ_ERR_INVALID, "negative size");
+    const int P = (S + page_size - 1) / page_size;
+    if ((int64_t)B * H * P == 0) return FQ_OK;
+    if (!k || !page_min || !page_max) return fail(FQ_ERR_INVALID, "NULL tensor");
+    if ((int64_t)B * H > 65535) return fail(FQ_ERR_UNSUPPORTED, "batch x heads > 65535");
+    PageMinMaxArgs a{};
+    a.k = k; a.k_dtype = k_dtype; a.pmin = page_min; a.pmax = page_max;
+    for (int i = 0; i < 4; ++i) { a.k_s[i] = k_strides[i]; a.pm_s[i] = pm_strides[i]; }
+    a.B = B; a.H = H; a.S = S; a.P = P; a.D = D; a.page = page_size;
+    return hip_status(launch_page_minmax(a, (hipStream_t)stream), "page summary");
+}
+
+static int quest_scores(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* lo,
+                        const int64_t lo_strides[4], const void* hi, const int64_t hi_strides[4], int32_t b_dtype,
+                        bool from_meta, float levels, float* scores, const int64_t sc_strides[4], int32_t B,
+                        int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D, fq_stream_t stream) {
+    if (H_kv < 1 || H_q % H_kv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", H_q, H_kv);
+    if (D != 64 && D != 128) return fail(FQ_ERR_UNSUPPORTED, "head_dim=%d not in (64, 128)", D);
+    if (!is_float_dtype(q_dtype) || !is_float_dtype(b_dtype)) return fail(FQ_ERR_INVALID, "dtype");
+    if (B < 0 || S_q < 0 || P < 0) return fail(FQ_ERR_INVALID, "negative size");
+    if ((int64_t)B * P * S_q == 0) return FQ_OK;
+    if (!q || !lo || !hi || !scores) return fail(FQ_ERR_INVALID, "NULL tensor");
+    if ((int64_t)B * H_kv > 65535) return fail(FQ_ERR_UNSUPPORTED, "batch x KV heads > 65535");
+    QuestScoreArgs a{};
+    a.q = q; a.q_dtype = q_dtype; a.lo = lo; a.hi = hi; a.b_dtype = b_dtype; a.from_meta = from_meta;
+    a.levels = levels; a.scores = scores;
+    for (int i = 0; i < 4; ++i) {
+        a.q_s[i] = q_strides[i]; a.lo_s[i] = lo_strides[i]; a.hi_s[i] = hi_strides[i]; a.sc_s[i] = sc_strides[i];
+    }
+    a.B = B; a.Hq = H_q; a.Sq = S_q; a.Hkv = H_kv; a.P = P; a.D = D;
+    return hip_status(launch_quest_scores(a, (hipStream_t)stream), "quest page scores");
+}
+
+int fq_page_scores_quest(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* page_min,
+                         const int64_t pmin_strides[4], const void* page_max, const int64_t pmax_strides[4],
+                         int32_t bound_dtype, float* scores, const int64_t sc_strides[4], int32_t B, int32_t H_q,
+                         int32_t S_q, int32_t H_kv, int32_t P, int32_t D, fq_stream_t stream) {
+    return quest_scores(q, q_dtype, q_strides, page_min, pmin_strides, page_max, pmax_strides, bound_dtype, false, 0.f,
+                        scores, sc_strides, B, H_q, S_q, H_kv, P, D, stream);
+}
+
+int fq_page_scores_int8_bound(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* k_scale,
+                              const int64_t ks_strides[4], const void* k_mn, const int64_t km_strides[4],
+                              int32_t meta_dtype, float* scores, const int64_t sc_strides[4], int32_t B, int32_t H_q,
+                              int32_t S_q, int32_t H_kv, int32_t P, int32_t D, fq_stream_t stream) {
+    if (!is_half(meta_dtype)) return fail(FQ_ERR_INVALID, "metadata dtype must be bf16 or fp16");
+    return quest_scores(q, q_dtype, q_strides, k_mn, km_strides, k_scale, ks_strides, meta_dtype, true, 255.0f,
+                        scores, sc_strides, B, H_q, S_q, H_kv, P, D, stream);
+}
+
 int fq_quantize_k_int8(const void* k, int32_t in_dtype, const int64_t k_strides[4], int32_t B, int32_t H,
                        int32_t S, int32_t D, int32_t page_size, uint8_t* codes, const int64_t c_strides[4],
                        void* scale, const int64_t s_strides[4], void* mn, const int64_t m_strides[4],

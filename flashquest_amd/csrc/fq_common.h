@@ -328,6 +328,23 @@ struct SummaryArgs {
 };
 
 hipError_t launch_page_summary_scores(const SummaryArgs& a, hipStream_t st);
+// compute_page_summary over any float K, and Quest scores from page bounds
+// (summary.hip).
+struct PageMinMaxArgs {
+    const void* k; int k_dtype; int64_t k_s[4];        // (B, H, S, D)
+    void* pmin; void* pmax; int64_t pm_s[4];           // (B, H, P, D), K's dtype
+    int B, H, S, P, D, page;
+};
+hipError_t launch_page_minmax(const PageMinMaxArgs& a, hipStream_t st);
+struct QuestScoreArgs {
+    const void* q; int q_dtype; int64_t q_s[4];        // (B, H_q, S_q, D)
+    const void* lo; const void* hi; int b_dtype; int64_t lo_s[4], hi_s[4];   // (B, H_kv, P, D)
+    bool from_meta;                                    // lo = K_mn, hi = K_mn + levels * K_scale (hi = K_scale)
+    float levels;
+    float* scores; int64_t sc_s[4];                    // (B, H_q, S_q, P)
+    int B, Hq, Sq, Hkv, P, D;
+};
+hipError_t launch_quest_scores(const QuestScoreArgs& a, hipStream_t st);
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws,
                                  const AttnLaunch& al, hipStream_t st, const SelectArgs* sel,
                                  const TailArgs* tail = nullptr);

@@ -98,6 +98,68 @@ __global__ __launch_bounds__(kThreads) void page_summary_scores_kernel(SummaryAr
     }
 }
 
+// compute_page_summary (eager/page_summary.py:7-39) over any float K: thread
+// d of workgroup (page, b x h) takes channel d's minimum and maximum over the
+// page's valid tokens, NaN propagating as in torch's min / max; the results
+// are elements of K, stored in K's dtype.
+__global__ __launch_bounds__(1024) void page_minmax_kernel(PageMinMaxArgs a) {
+    const int p = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+    if (d >= a.D) return;
+    const int b = bh / a.H, h = bh % a.H;
+    const int64_t base = b * a.k_s[0] + h * a.k_s[1] + d * a.k_s[3];
+    const int t0 = p * a.page, t1 = min(t0 + a.page, a.S);
+    float lo = INFINITY, hi = -INFINITY;
+    for (int t = t0; t < t1; ++t) {
+        const float x = load_any(a.k, a.k_dtype, base + (int64_t)t * a.k_s[2]);
+        lo = (x < lo || x != x) ? (lo != lo ? lo : x) : lo;
+        hi = (x > hi || x != x) ? (hi != hi ? hi : x) : hi;
+    }
+    const int64_t o = b * a.pm_s[0] + h * a.pm_s[1] + p * a.pm_s[2] + d * a.pm_s[3];
+    store_any(a.pmin, a.k_dtype, o, lo);
+    store_any(a.pmax, a.k_dtype, o, hi);
+}
+
+// Quest scores from page bounds, one wave per (page, b x KV head), for every
+// query row of the group (n_rep heads x S_q positions): the bounds go to
+// LDS as fp32 (lo / hi, or from the INT8 metadata lo = K_mn, hi = K_mn +
+// levels * K_scale in fp32 -- criticality.py:66-67), then each row's
+// sum_d max(q_d * hi_d, q_d * lo_d) in the fixed order of the summary kernel
+// above (4 channels per lane left to right, then the butterfly).
+template <int D>
+__global__ __launch_bounds__(64) void quest_scores_kernel(QuestScoreArgs a) {
+    constexpr int NJ = D / 4;
+    __shared__ float s_lo[D], s_hi[D];
+    const int p = blockIdx.x, bh = blockIdx.y, L = threadIdx.x;
+    const int b = bh / a.Hkv, h = bh % a.Hkv;
+    for (int d = L; d < D; d += 64) {
+        const int64_t ol = b * a.lo_s[0] + h * a.lo_s[1] + p * a.lo_s[2] + d * a.lo_s[3];
+        const int64_t oh = b * a.hi_s[0] + h * a.hi_s[1] + p * a.hi_s[2] + d * a.hi_s[3];
+        const float lo = load_any(a.lo, a.b_dtype, ol);
+        const float x = load_any(a.hi, a.b_dtype, oh);
+        s_lo[d] = lo;
+        s_hi[d] = a.from_meta ? __fadd_rn(lo, __fmul_rn(a.levels, x)) : x;
+    }
+    __syncthreads();
+    const int nrep = a.Hq / a.Hkv;
+    for (int r = 0; r < nrep * a.Sq; ++r) {
+        const int hq = h * nrep + r / a.Sq, sq = r % a.Sq;
+        float acc = 0.f;
+        if (L < NJ) {
+            const int64_t qo = b * a.q_s[0] + hq * a.q_s[1] + sq * a.q_s[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 4 * L + i;
+                const float qd = load_any(a.q, a.q_dtype, qo + d * a.q_s[3]);
+                const float term = fmaxf(__fmul_rn(qd, s_hi[d]), __fmul_rn(qd, s_lo[d]));
+                acc = i == 0 ? term : acc + term;
+            }
+        }
+#pragma unroll
+        for (int o = NJ / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (L == 0) a.scores[b * a.sc_s[0] + hq * a.sc_s[1] + sq * a.sc_s[2] + p * a.sc_s[3]] = acc;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_page_summary_scores(const SummaryArgs& a, hipStream_t st) {
@@ -109,6 +171,19 @@ hipError_t launch_page_summary_scores(const SummaryArgs& a, hipStream_t st) {
         if (a.D == 128) FQ_L(f16, 128); else FQ_L(f16, 64);
     }
 #undef FQ_L
+    return hipGetLastError();
+}
+
+hipError_t launch_page_minmax(const PageMinMaxArgs& a, hipStream_t st) {
+    const int threads = (a.D + 63) / 64 * 64;
+    hipLaunchKernelGGL(page_minmax_kernel, dim3(a.P, a.B * a.H), dim3(threads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_quest_scores(const QuestScoreArgs& a, hipStream_t st) {
+    dim3 grid(a.P, a.B * a.Hkv);
+    if (a.D == 128) hipLaunchKernelGGL((quest_scores_kernel<128>), grid, dim3(64), 0, st, a);
+    else hipLaunchKernelGGL((quest_scores_kernel<64>), grid, dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

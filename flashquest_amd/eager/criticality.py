@@ -61,11 +61,56 @@ def page_scores_int8_fast(Q: torch.Tensor, K_scale: torch.Tensor, K_mn: torch.Te
     return out
 
 
+def page_scores(Q: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor) -> torch.Tensor:
+    """criticality.py:7-31: scores[b, h, s, p] = sum_d max(Q_d * max_d, Q_d * min_d)
+    in fp32 (a fixed order: 4 channels per lane left to right, then a
+    butterfly over the D/4 partial sums).
+
+    Args:
+        Q: (B, H, S_q, D) bf16/fp16/fp32.  page_min, page_max: (B, H_b, P, D)
+        with H_b = H (the reference's one summary row per head) or any H_b
+        dividing H (query head h reads row h // (H / H_b)).
+    Returns:
+        (B, H, S_q, P) fp32.
+    """
+    B, H, S_q, D = Q.shape
+    H_b, P = page_min.shape[1], page_min.shape[2]
+    if page_max.shape != page_min.shape:
+        raise ValueError(f"page_min {tuple(page_min.shape)} and page_max {tuple(page_max.shape)} differ")
+    if H % H_b != 0:
+        raise ValueError(f"H={H} must be divisible by the summaries' {H_b} heads")
+    L.require_device(Q, page_min, page_max)
+    lo, hi = page_min, page_max
+    if hi.dtype != lo.dtype:
+        hi = hi.to(lo.dtype)
+    out = torch.empty(B, H, S_q, P, dtype=torch.float32, device=Q.device)
+    L.check(L.lib().fq_page_scores_quest(
+        Q.data_ptr(), L.dtype_code(Q.dtype), L.strides(Q, 4), lo.data_ptr(), L.strides(lo, 4), hi.data_ptr(),
+        L.strides(hi, 4), L.dtype_code(lo.dtype), out.data_ptr(), L.strides(out, 4), B, H, S_q, H_b, P, D,
+        L.stream_handle(Q.device)), "page_scores")
+    return out
+
+
 def page_scores_int8(Q: torch.Tensor, K_scale: torch.Tensor, K_mn: torch.Tensor) -> torch.Tensor:
     """criticality.py:34-74: the Quest bound from the INT8 page range,
-    sum_d max(Q_d * K_mn, Q_d * (K_mn + 255 * K_scale)) in fp32; equal to
-    page_scores_int8_fast in exact arithmetic."""
-    return page_scores_int8_fast(Q, K_scale, K_mn)
+    sum_d max(Q_d * K_mn, Q_d * (K_mn + 255 * K_scale)) in fp32 with the
+    reference's bounds (fp32(K_mn) and fp32(K_mn) + 255 * fp32(K_scale));
+    equal to page_scores_int8_fast in exact arithmetic, and (unlike it) to
+    the reference's per-term rounding.  Q (B, H_q, S_q, D); K_scale, K_mn
+    (B, H_kv, P, D) bf16/fp16.  Returns (B, H_q, S_q, P) fp32."""
+    B, H_q, S_q, D = Q.shape
+    H_kv, P = K_scale.shape[1], K_scale.shape[2]
+    if H_q % H_kv != 0:
+        raise ValueError(f"H_q={H_q} must be divisible by H_kv={H_kv}")
+    L.require_device(Q, K_scale, K_mn)
+    if K_scale.dtype != K_mn.dtype:
+        raise AssertionError("K_scale and K_mn must share a dtype")
+    out = torch.empty(B, H_q, S_q, P, dtype=torch.float32, device=Q.device)
+    L.check(L.lib().fq_page_scores_int8_bound(
+        Q.data_ptr(), L.dtype_code(Q.dtype), L.strides(Q, 4), K_scale.data_ptr(), L.strides(K_scale, 4),
+        K_mn.data_ptr(), L.strides(K_mn, 4), L.dtype_code(K_scale.dtype), out.data_ptr(), L.strides(out, 4),
+        B, H_q, S_q, H_kv, P, D, L.stream_handle(Q.device)), "page_scores_int8")
+    return out
 
 
 def page_scores_int8_summary(Q: torch.Tensor, K_uint8: torch.Tensor, K_scale: torch.Tensor, K_mn: torch.Tensor,

@@ -421,6 +421,38 @@ int fq_page_scores_int8_summary(const void* q, int32_t q_dtype, const int64_t q_
                                 int32_t B, int32_t H_q, int32_t H_kv, int32_t S, int32_t P, int32_t D,
                                 int32_t page_size, fq_stream_t stream);
 
+/* Replaces compute_page_summary (eager/page_summary.py:7-39): per page and
+ * channel the minimum and maximum of K (B, H, S, D; bf16, fp16 or fp32, any
+ * strides) over the page's valid tokens (a partial last page: its tokens),
+ * NaN propagating; page_min / page_max (B, H, ceil(S / page_size), D) in K's
+ * dtype. */
+int fq_page_summary(const void* k, int32_t k_dtype, const int64_t k_strides[4], int32_t B, int32_t H,
+                    int32_t S, int32_t D, int32_t page_size, void* page_min, void* page_max,
+                    const int64_t pm_strides[4], fq_stream_t stream);
+
+/* Replaces page_scores (eager/criticality.py:7-31): scores (B, H_q, S_q, P)
+ * fp32 = sum_d max(q_d * max_d, q_d * min_d) for queries (B, H_q, S_q, D) and
+ * page bounds (B, H_kv, P, D) in bound_dtype, query head h reading bound row
+ * h / (H_q / H_kv) (H_kv = H_q: the reference's one row per head).  fp32
+ * order as fq_page_scores_int8_summary.  D in (64, 128). */
+int fq_page_scores_quest(const void* q, int32_t q_dtype, const int64_t q_strides[4],
+                         const void* page_min, const int64_t pmin_strides[4],
+                         const void* page_max, const int64_t pmax_strides[4], int32_t bound_dtype,
+                         float* scores, const int64_t sc_strides[4],
+                         int32_t B, int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D,
+                         fq_stream_t stream);
+
+/* Replaces page_scores_int8 (eager/criticality.py:34-74): the same scores
+ * with the bounds taken from the INT8 page metadata as the reference forms
+ * them, min = fp32(K_mn), max = fp32(K_mn) + 255 * fp32(K_scale) (fp32
+ * multiply, then add).  Arguments as fq_page_scores_int8. */
+int fq_page_scores_int8_bound(const void* q, int32_t q_dtype, const int64_t q_strides[4],
+                              const void* k_scale, const int64_t ks_strides[4],
+                              const void* k_mn, const int64_t km_strides[4], int32_t meta_dtype,
+                              float* scores, const int64_t sc_strides[4],
+                              int32_t B, int32_t H_q, int32_t S_q, int32_t H_kv, int32_t P, int32_t D,
+                              fq_stream_t stream);
+
 /* Replaces flash_attn_sparse_fwd (kernel/sparse_fwd.py:160-228, kernel
  * 23-157): sparse GQA decode attention over the INT8 cache for a boolean page
  * mask (L*B, H_q, P) (strides as fq_sparse_int4_fwd_mask). */

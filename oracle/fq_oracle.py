@@ -315,6 +315,29 @@ def page_summary_int8(K_u8, K_scale, K_mn, page_size: int):
     return lo.astype(F32), hi.astype(F32)
 
 
+def compute_page_summary(K, page_size: int):
+    """page_summary.py:7-39: per page and channel the min / max of K (B, H, S,
+    D) over the page's tokens (a partial last page padded with +-inf, so only
+    its valid tokens count).  Returns (page_min, page_max) (B, H, P, D)."""
+    K = np.asarray(K)
+    B, H, S, D = K.shape
+    P = (S + page_size - 1) // page_size
+    pad = P * page_size - S
+    lo = np.concatenate([K, np.full((B, H, pad, D), np.inf, K.dtype)], axis=2)
+    hi = np.concatenate([K, np.full((B, H, pad, D), -np.inf, K.dtype)], axis=2)
+    return lo.reshape(B, H, P, page_size, D).min(axis=3), hi.reshape(B, H, P, page_size, D).max(axis=3)
+
+
+def page_scores_int8_bound_fixed(Q, K_scale, K_mn):
+    """page_scores_int8 (criticality.py:34-74) in this build's fixed order:
+    the bounds as the reference forms them, min = fp32(K_mn), max = fp32(K_mn)
+    + 255 * fp32(K_scale) (fp32 multiply, then fp32 add), then
+    page_scores_quest_fixed.  Q (B, H_q, D).  Returns (B, H_q, P) fp32."""
+    mn = np.asarray(K_mn, F32)
+    mx = (mn + (F32(255.0) * np.asarray(K_scale, F32)).astype(F32)).astype(F32)
+    return page_scores_quest_fixed(Q, mn, mx)
+
+
 def page_scores_quest_fixed(Q, page_min, page_max):
     """page_scores (criticality.py:7-31) with this build's fixed fp32 order:
     term_d = max(q_d * max_d, q_d * min_d) (each product rounded to fp32);

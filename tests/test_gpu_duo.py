@@ -193,3 +193,52 @@ def test_quest_duo_fused_sdpa_reference_semantics(Hq, Hkv, P, pattern):
     with pytest.raises(ValueError, match="head_pattern"):
         quest_duo_fused_sdpa(case.q_dev(), d["K_uint8"], d["K_scale"], d["K_mn"], d["V_uint8"], d["V_scale"],
                              d["V_mn"], head_pattern=torch.tensor([True] * (Hkv + 1)))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_compute_page_summary(dtype):
+    """compute_page_summary (page_summary.py:7-39) on the GPU: bit for bit
+    against the oracle for each K dtype, a partial last page, a strided K view
+    and a NaN (propagated by torch's min / max)."""
+    from flashquest_amd.eager import compute_page_summary
+    rng = np.random.default_rng(11)
+    K = rng.standard_normal((2, 3, 64 * 5 + 9, 128)).astype(np.float32)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    Kd = torch.from_numpy(K).to(tdt).cuda()
+    Kh = Kd.float().cpu().numpy()
+    lo, hi = compute_page_summary(Kd, 64)
+    ref_lo, ref_hi = O.compute_page_summary(Kh, 64)
+    assert lo.dtype == tdt and lo.shape == (2, 3, 6, 128)
+    assert np.array_equal(lo.float().cpu().numpy(), ref_lo) and np.array_equal(hi.float().cpu().numpy(), ref_hi)
+    big = torch.zeros(2, 3, Kd.shape[2], 256, dtype=tdt, device="cuda")
+    big[..., 64:192] = Kd
+    lo2, hi2 = compute_page_summary(big[..., 64:192], 64)
+    assert torch.equal(lo2, lo) and torch.equal(hi2, hi)
+    Kd[1, 2, 70, 5] = float("nan")
+    lo3, hi3 = compute_page_summary(Kd, 64)
+    torch.cuda.synchronize()
+    assert torch.isnan(lo3[1, 2, 1, 5]) and torch.isnan(hi3[1, 2, 1, 5])
+    assert int(torch.isnan(lo3).sum()) == 1 and int(torch.isnan(hi3).sum()) == 1
+
+
+@pytest.mark.parametrize("H,Hb,Sq,D,qdt", [(4, 4, 1, 128, "bf16"), (8, 2, 3, 128, "f16"), (6, 3, 2, 64, "f32")])
+def test_page_scores_bit_exact(H, Hb, Sq, D, qdt):
+    """page_scores (criticality.py:7-31) from summaries: bit for bit against
+    the oracle's fixed order, one summary row per head (the reference's) or
+    shared by a GQA group, several query positions; and the Quest bound."""
+    from flashquest_amd.eager import compute_page_summary, page_scores
+    rng = np.random.default_rng(H + D)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[qdt]
+    K = torch.from_numpy(rng.standard_normal((2, Hb, 64 * 6, D)).astype(np.float32)).to(torch.bfloat16).cuda()
+    Q = torch.from_numpy(rng.standard_normal((2, H, Sq, D)).astype(np.float32)).to(tdt).cuda()
+    lo, hi = compute_page_summary(K, 64)
+    sc = page_scores(Q, lo, hi)
+    torch.cuda.synchronize()
+    qh = Q.float().cpu().numpy()
+    for s in range(Sq):
+        ref = O.page_scores_quest_fixed(qh[:, :, s], lo.float().cpu().numpy(), hi.float().cpu().numpy())
+        assert np.array_equal(sc[:, :, s].cpu().numpy(), ref), s
+        exact = O.page_scores_quest(qh[:, :, s], lo.float().cpu().numpy(), hi.float().cpu().numpy())
+        kd = K.float().cpu().numpy().astype(np.float64)
+        qk = np.einsum("bhd,bhsd->bhs", qh[:, :, s].astype(np.float64), np.repeat(kd, H // Hb, axis=1))
+        assert np.all(exact >= qk.reshape(2, H, 6, 64).max(-1) - 1e-9)

@@ -109,3 +109,39 @@ def test_select_pages_loop_form_known_answers():
     r = np.array([0.07, 0.0], np.float32)
     m = O.select_pages(np.repeat(hundred, 2, 1), r, 1, 0)
     assert m[0, 0].sum() == 9 and m[0, 1].sum() == 1      # + sink page 0
+
+
+def test_compute_page_summary_reference_known_answers():
+    """test_eager_page_summary.py:6-37: increasing keys give each page's first /
+    last key; a partial tail page summarises its valid keys; page size 1 gives
+    the keys themselves."""
+    K = np.arange(1 * 2 * 12 * 8, dtype=np.float32).reshape(1, 2, 12, 8)
+    lo, hi = O.compute_page_summary(K, 4)
+    assert lo.shape == (1, 2, 3, 8) and np.array_equal(lo[0, 0, 0], K[0, 0, 0]) and np.array_equal(hi[0, 0, 0], K[0, 0, 3])
+    K2 = np.random.default_rng(0).standard_normal((1, 1, 10, 4)).astype(np.float32)
+    lo2, hi2 = O.compute_page_summary(K2, 4)
+    assert lo2.shape == (1, 1, 3, 4) and np.array_equal(hi2[0, 0, 2], K2[0, 0, 8:10].max(0))
+    K3 = np.random.default_rng(1).standard_normal((1, 1, 5, 3)).astype(np.float32)
+    lo3, hi3 = O.compute_page_summary(K3, 1)
+    assert np.array_equal(lo3[:, :, :, :], K3) and np.array_equal(hi3, K3)
+
+
+def test_page_scores_int8_bound_follows_the_reference_expression():
+    """page_scores_int8 (criticality.py:59-74) evaluated by torch on the CPU:
+    the fixed-order sum differs only by fp32 summation order, and the bounds
+    are the reference's exactly (fp32(K_mn) + 255 * fp32(K_scale))."""
+    codes, scale, mn = _int8_cache(5, H=2, S=256, D=128)
+    rng = np.random.default_rng(6)
+    q = O.round_bf16(rng.standard_normal((1, 4, 128)).astype(np.float32))
+    got = O.page_scores_int8_bound_fixed(q, scale, mn)
+    kmn = torch.from_numpy(mn).to(torch.bfloat16).float().repeat_interleave(2, dim=1)
+    kmx = (torch.from_numpy(mn).to(torch.bfloat16).float() + 255.0 * torch.from_numpy(scale).to(torch.bfloat16).float()
+           ).repeat_interleave(2, dim=1)
+    qt = torch.from_numpy(q).unsqueeze(2)
+    ref = torch.maximum(qt * kmx, qt * kmn).sum(-1).numpy()
+    mag = np.einsum("bhd,bhpd->bhp", np.abs(q).astype(np.float64),
+                    np.maximum(np.abs(kmn.numpy()), np.abs(kmx.numpy())).astype(np.float64))
+    assert np.all(np.abs(got - ref) <= 2 * 140 * 2.0 ** -24 * mag)
+    # the bounds themselves are bit-equal to torch's
+    hi = (np.asarray(mn, np.float32) + (np.float32(255.0) * np.asarray(scale, np.float32))).astype(np.float32)
+    assert np.array_equal(np.repeat(hi, 2, axis=1), kmx.numpy())
