@@ -431,4 +431,74 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(QueryArgs q, Wor
     store_outputs<D, NREP, ROT>(q, l, b, h, s_out, s_L, s_M);
 }
 
+// The same merge for few splits (<= SM) and no tail to fold in, as a latency
+// path: one wave per (group, query head), lane d holding channels d and
+// d + 64, every split's (m, l) and partial acc loaded in one round, then
+// M = max_s m_s, w_s = exp2(m_s - M) (0 for an empty split), L = sum_s w_s l_s,
+// O = (sum_s w_s acc_s) / L, splits summed in ascending order.  ROT (or
+// q.rot): O rotated back by the wave butterflies, as store_outputs does.
+template <bool ROT, int SM>
+__global__ __launch_bounds__(64) void merge_splits_wave_kernel(QueryArgs q, Workspace ws, int Hkv, int B,
+                                                                int splits) {
+    constexpr int D = 128;
+    const int g = blockIdx.x, r = blockIdx.y, nrep = q.nrep;
+    const int h = g % Hkv, b = (g / Hkv) % B, l = g / (Hkv * B);
+    const int lane = threadIdx.x;
+    const int64_t base = (int64_t)g * ws.s_max * nrep + r;
+    float m[SM], lv[SM], a0[SM], a1[SM];
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+        const int64_t pr = base + (int64_t)min(s, splits - 1) * nrep;
+        m[s] = ws.part_ml[pr * 2];
+        lv[s] = ws.part_ml[pr * 2 + 1];
+        a0[s] = ws.part_acc[pr * D + lane];
+        a1[s] = ws.part_acc[pr * D + lane + 64];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < SM; ++s)
+        if (s < splits) M = fmaxf(M, m[s]);
+    float L = 0.f, A0 = 0.f, A1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+        if (s < splits) {
+            const float w = m[s] == -INFINITY ? 0.f : exp2_fast(m[s] - M);
+            L = fmaf(w, lv[s], L);
+            A0 = fmaf(w, a0[s], A0);
+            A1 = fmaf(w, a1[s], A1);
+        }
+    }
+    float v0 = L > 0.f ? A0 / L : 0.f, v1 = L > 0.f ? A1 / L : 0.f;
+    if (ROT || q.rot) {
+        const float inv = 1.0f / sqrtf((float)D);
+        const float s0 = q.rot ? q.rot[lane] : 1.f, s1 = q.rot ? q.rot[lane + 64] : 1.f;
+        wave_hadamard128(v0, v1);
+        v0 *= inv * s0;
+        v1 *= inv * s1;
+    }
+    const int hq = h * nrep + r;
+    const int64_t ob = l * q.o_s[0] + b * q.o_s[1] + hq * q.o_s[2];
+    store_any(q.out, q.out_dtype, ob + lane * q.o_s[3], v0);
+    store_any(q.out, q.out_dtype, ob + (lane + 64) * q.o_s[3], v1);
+    if (q.lse && lane == 0)
+        q.lse[l * q.lse_s[0] + b * q.lse_s[1] + hq * q.lse_s[2]] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
+// The split merge launch of the D = 128 matrix-core paths: the one-round wave
+// merge for up to 32 splits without a tail, merge_splits_kernel otherwise.
+template <int NREP, bool ROT>
+inline void launch_split_merge(const QueryArgs& q, const Workspace& ws, int Hkv, int B, int groups, int splits,
+                               const TailArgs& tail, hipStream_t st) {
+    if (tail.len == 0 && splits <= 32) {
+        const dim3 grid(groups, NREP);
+        if (splits <= 8) hipLaunchKernelGGL((merge_splits_wave_kernel<ROT, 8>), grid, dim3(64), 0, st, q, ws, Hkv, B, splits);
+        else if (splits <= 16) hipLaunchKernelGGL((merge_splits_wave_kernel<ROT, 16>), grid, dim3(64), 0, st, q, ws, Hkv, B, splits);
+        else if (splits <= 24) hipLaunchKernelGGL((merge_splits_wave_kernel<ROT, 24>), grid, dim3(64), 0, st, q, ws, Hkv, B, splits);
+        else hipLaunchKernelGGL((merge_splits_wave_kernel<ROT, 32>), grid, dim3(64), 0, st, q, ws, Hkv, B, splits);
+        return;
+    }
+    hipLaunchKernelGGL((merge_splits_kernel<128, NREP, ROT>), dim3(groups), dim3(kThreads), 0, st, q, ws, Hkv, B, 0,
+                       splits, tail);
+}
+
 }  // namespace fq

@@ -692,9 +692,8 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
         timer_after_launch(st);                                                                        \
         if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                     \
-            hipLaunchKernelGGL((merge_splits_kernel<128, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
-                               a.q, a.ws, a.c.Hkv, a.c.B, 0, a.splits,                                  \
-                               a.tail.in_kernel ? TailArgs{} : a.tail);                                 \
+            launch_split_merge<N, false>(a.q, a.ws, a.c.Hkv, a.c.B, grid.y, a.splits,                  \
+                                         a.tail.in_kernel ? TailArgs{} : a.tail, st);                   \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE

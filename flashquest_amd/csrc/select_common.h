@@ -198,8 +198,10 @@ FQ_DEV ForcedPages forced_pages(int P, int num_sinks, int window) {
 // (P <= 64 C pages, NW waves).  keys[r * 64 C + p] holds sortable_key of row
 // r's score of page p, and 0 (below every score) for p >= P.  Every wave loads
 // every key (C per lane per row); wave r finds row r's k-th largest key with
-// wave_kth_hist (no barrier inside; for one row every wave finds it, so no
-// wave waits on another); the thresholds meet in LDS, and every
+// wave_kth_hist (no barrier inside; for one row only the last wave searches,
+// so its SIMD is not shared with a partner wave doing the same search, and
+// the last wave issues no forced-page loads before it); the thresholds meet
+// in LDS, and every
 // wave then ranks the ties and lists the pages.  Ties and forced pages follow
 // wave_topk / wave_select_group; the entry list holds the forced pages first,
 // then the other selected pages, each part ascending; wave w writes the entries
@@ -339,8 +341,15 @@ FQ_DEV int block_select_rows(const uint32_t* keys, int P, float ret_l, int k_max
     for (int r = 0; r < NROWS; ++r)
         k[r] = k_for(NROWS == 1 ? rmax : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ret_l), r)), P, k_max);
     bool exact = false;              // one row: exactly k keys >= T, no ties to rank
-    if constexpr (NROWS == 1) {      // one row: every wave finds the threshold itself
-        T[0] = k[0] > 0 ? wave_kth_hist<C>(key[0], k[0], sl.hist[w], &exact) : 0u;
+    if constexpr (NROWS == 1) {      // one row: the last wave finds the threshold, shared through LDS
+        if (w == NW - 1) {
+            bool ex = false;
+            const uint32_t t = k[0] > 0 ? wave_kth_hist<C>(key[0], k[0], sl.hist[w], &ex) : 0u;
+            if (lane == 0) { sl.T[0] = t; sl.T[1] = ex ? 1u : 0u; }
+        }
+        lds_barrier();
+        T[0] = sl.T[0];
+        exact = sl.T[1] != 0u;
     } else {                         // wave r finds row r's, shared through LDS
 #pragma unroll
         for (int r = 0; r < NROWS; ++r) {

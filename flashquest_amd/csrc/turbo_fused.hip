@@ -517,8 +517,7 @@ hipError_t launch_turbo_fused_nrep(const TurboFusedParams& a, dim3 grid, hipStre
         hipLaunchKernelGGL((attn_turbo_fused_kernel<N, FUSED>), grid, dim3(512), 0, st, a);                 \
         timer_after_launch(st);                                                                             \
         if (a.splits > 1)                                                                                   \
-            hipLaunchKernelGGL((merge_splits_kernel<128, N, true>), dim3(grid.y), dim3(kThreads), 0, st, a.q, \
-                               a.ws, a.c.H_kv, a.c.B, 0, a.splits, TailArgs{});                                         \
+            launch_split_merge<N, true>(a.q, a.ws, a.c.H_kv, a.c.B, grid.y, a.splits, TailArgs{}, st);         \
         break;
         FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4)
 #undef FQ_CASE
