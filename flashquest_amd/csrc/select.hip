@@ -178,8 +178,9 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
     float* ws_scores = a.ws_scores ? a.ws_scores + (int64_t)g * a.rows * c.P : nullptr;
 
     // The workgroup streams its chunk pass by pass (PPP pages per pass) with
-    // kPasses passes of metadata in flight ahead of the one being scored; past
-    // the end the loads repeat the last page, so every step issues the same loads.
+    // kPasses passes of metadata in flight ahead of the one being scored (a
+    // partial last pass re-reads the chunk's last page); no loads are issued
+    // past the chunk's last pass, so the workgroup ends with nothing in flight.
     const int p_begin = blockIdx.x * a.ppc;
     const int p_end = min(c.P, p_begin + a.ppc);
     const int npass = (p_end - p_begin + PPP - 1) / PPP;
@@ -190,7 +191,8 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
         mv[u] = *(const uint4*)(kmn + p * c.kmn_s[3] + lane_in_page * 8);
     };
 #pragma unroll
-    for (int u = 0; u < kPasses; ++u) fetch(u, u);
+    for (int u = 0; u < kPasses; ++u)
+        if (u < npass) fetch(u, u);          // uniform: no loads past the chunk's passes
     load_q_rows<D>(a, l, b, h, s_q, s_qp);
     __syncthreads();
     const float levels = c.bits == 8 ? 255.0f : 15.0f;     // INT8 / INT4 code range
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreParams a) {
                 if (ws_scores && a.mode == FQ_SELECT_PER_KV_HEAD_SUM && lane_in_page == 0)
                     ws_scores[p] = acc_kv;
             }
-            fetch(u, pass0 + u + kPasses);
+            if (pass0 + u + kPasses < npass) fetch(u, pass0 + u + kPasses);     // uniform
         }
     }
 }
