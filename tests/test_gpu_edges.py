@@ -154,3 +154,38 @@ def test_random_shapes_match_oracle_decode():
         assert np.array_equal(mask8.cpu().numpy(), ref8["mask"]), case
         assert max_err(o8[:, :, 0], ref8["O"]) <= _tol("bf16", ref8["O"]), case
         assert max_err(lse8[:, :, 0], ref8["lse"]) <= 1e-4, case
+
+
+def test_strided_per_head_retention_matches_oracle():
+    """A per-head retention that is a strided view of a longer device vector
+    (every second entry) selects with those heads' values: each head's k
+    follows its own retention, the mask equals the oracle's for the same
+    values, INT4 and INT8."""
+    from flashquest_amd.eager.decode import quest_decode_int4, quest_decode_int8
+    Hkv, rep, S, D = 2, 3, 1024, 128
+    Hq = Hkv * rep
+    vals = np.array([0.1, 0.9, 0.25, 0.6, 0.4, 0.05], dtype=np.float32)
+    wide = torch.zeros(2 * Hq, dtype=torch.float32, device="cuda")
+    wide[::2] = torch.from_numpy(vals).cuda()
+    wide[1::2] = 1.0                                   # the entries the view skips select everything
+    r = wide[::2]
+    assert not r.is_contiguous()
+    kw = dict(retention=r, num_sinks=1, window_pages=1, return_selection=True)
+    c = Int4Case(seed=77, B=1, Hq=Hq, Hkv=Hkv, S=S, D=D)
+    o, lse, mask = quest_decode_int4(c.q_dev(), **c.device(), **kw)
+    ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=vals, num_sinks=1, window_pages=1)
+    c8 = Int8Case(seed=78, B=1, Hq=Hq, Hkv=Hkv, S=S, D=D)
+    o8, lse8, mask8 = quest_decode_int8(c8.q_dev(), **c8.device(), **kw)
+    ref8 = O.decode_step(c8.Q, c8.ku, c8.ks, c8.km, c8.vu, c8.vs, c8.vm, retention=vals, num_sinks=1,
+                         window_pages=1, bits=8)
+    torch.cuda.synchronize()
+    P = S // 64
+    m = mask.cpu().numpy()
+    # per head: k = ceil(fp32(r) * P) selected pages plus the forced ones outside them
+    for h in range(Hq):
+        k = math.ceil(float(np.float32(vals[h]) * np.float32(P)))
+        assert k <= m[0, h].sum() <= k + 2, (h, k, int(m[0, h].sum()))
+    assert np.array_equal(m, ref["mask"])
+    assert max_err(o[:, :, 0], ref["O"]) <= _tol("bf16", ref["O"])
+    assert np.array_equal(mask8.cpu().numpy(), ref8["mask"])
+    assert max_err(o8[:, :, 0], ref8["O"]) <= _tol("bf16", ref8["O"])
