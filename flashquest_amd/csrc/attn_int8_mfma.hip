@@ -255,11 +255,13 @@ void attn_int8_mfma_kernel(Int8Params a) {
     float l_acc = 0.f, bias = 0.f;
     float Cr = 0.f, unscale = 0.f;           // the current page's q.K_mn + 128 sum A (head lg), digit scale
 
+    // the INT4 kernel's priority rule for the two waves of a SIMD: the one
+    // with more pages left, on a tie the younger, runs at the higher priority
     __shared__ int s_left[NW];
     auto balance = [&](int k) {
         s_left[w] = n_mine - k;
         const int other = __builtin_amdgcn_readfirstlane(s_left[w ^ 4]);
-        if (n_mine - k > other) __builtin_amdgcn_s_setprio(1);
+        if (n_mine - k > other || (n_mine - k == other && w >= 4)) __builtin_amdgcn_s_setprio(1);
         else __builtin_amdgcn_s_setprio(0);
     };
 

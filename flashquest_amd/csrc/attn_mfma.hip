@@ -397,14 +397,16 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // With 8 waves two share a SIMD (waves w and w ^ 4) and the issue arbiter
     // favours the older one, which would leave the younger wave's pages to
     // run alone at the end.  Each wave publishes its remaining page count and
-    // takes the higher priority while it has more left than its partner.  The
+    // takes the higher priority while it has more left than its partner, or as
+    // many and it is the younger of the two (with the older one winning ties,
+    // the pair ended one page apart: ~0.9 us of a config-1 step).  The
     // priority changes only timing, never which wave computes which page.
     __shared__ int s_left[NW];
     auto balance = [&](int k) {
         if constexpr (NW == 8) {
             s_left[w] = n_mine - k;
             const int other = __builtin_amdgcn_readfirstlane(s_left[w ^ 4]);
-            if (n_mine - k > other) __builtin_amdgcn_s_setprio(1);
+            if (n_mine - k > other || (n_mine - k == other && w >= 4)) __builtin_amdgcn_s_setprio(1);
             else __builtin_amdgcn_s_setprio(0);
         }
     };

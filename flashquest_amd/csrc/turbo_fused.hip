@@ -321,12 +321,13 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     auto& W = s_apv[w];
 
     // the idle partner-wave priority rule of the INT4 fused decode: two waves
-    // share a SIMD; the one with more pages left takes the higher priority
+    // share a SIMD; the one with more pages left (on a tie the younger) takes
+    // the higher priority
     __shared__ int s_left[NW];
     auto balance = [&](int k) {
         s_left[w] = n_mine - k;
         const int other = __builtin_amdgcn_readfirstlane(s_left[w ^ 4]);
-        if (n_mine - k > other) __builtin_amdgcn_s_setprio(1);
+        if (n_mine - k > other || (n_mine - k == other && w >= 4)) __builtin_amdgcn_s_setprio(1);
         else __builtin_amdgcn_s_setprio(0);
     };
 
