@@ -81,3 +81,34 @@ def test_fused_turbo_decode_matches_oracle(mode, Hq, sinks, window, P):
         for oo, ll in ((o, lse), (o2, lse2)):
             assert max_err(oo[i][:, :, 0], ref_o) <= _tol(ref_o), i
             assert max_err(ll[i][:, :, 0], ref_l) <= 1e-4, i
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_single_layer_turbo_decode_splits_match_oracle(mode):
+    """One layer of 8 KV groups over 200 pages (the reference's per-layer call
+    shape): a scoring launch, the attention workgroups select from its scores
+    with each group split over several workgroups, and the one-round split
+    merge rotates O back.  Selection bit-exact, O and lse against the oracle."""
+    from flashquest_amd.eager import quest_decode_turbo
+    rng = np.random.default_rng(4242)
+    Hq, Hkv, P = 24, 8, 200
+    S = 64 * (P - 1) + 40
+    Q, planes, raw = _turbo_case(rng, 1, Hq, Hkv, S)
+    r = np.linspace(0.1, 0.4, Hq).astype(np.float32)
+    Qd = to_dev_half(Q, "bf16")[:, :, None]
+    pl = [to_dev(planes[i]) if i in (0, 1, 3, 4) else to_dev_half(planes[i], "bf16") for i in range(6)]
+    ksr, kmr = to_dev_half(raw[0], "bf16"), to_dev_half(raw[1], "bf16")
+    kw = dict(retention=torch.from_numpy(r), num_sinks=4, window_pages=2, select_mode=mode)
+    o, lse, mask = quest_decode_turbo(Qd, *pl, ksr, kmr, return_selection=True, **kw)
+    torch.cuda.synchronize()
+    scores = O.page_scores_fixed(Q, raw[0], raw[1], mode)
+    rep = Hq // Hkv
+    if mode == "per_q_head":
+        ref_mask = O.select_pages_vectorized(scores[:, :, None, :], r, 4, 2)[:, :, 0, :]
+    else:
+        m = O.select_pages_vectorized(scores[:, :, None, :], r.reshape(Hkv, rep).max(-1), 4, 2)[:, :, 0, :]
+        ref_mask = np.repeat(m, rep, axis=1)
+    assert np.array_equal(mask.cpu().numpy(), ref_mask)
+    ref_o, ref_l = O.sparse_turbo_attention(Q, *planes, ref_mask, 64)
+    assert max_err(o[:, :, 0], ref_o) <= _tol(ref_o)
+    assert max_err(lse[:, :, 0], ref_l) <= 1e-4
