@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import fq_oracle as O
-from tests.cases import Int4Case, max_err, to_dev_half
+from tests.cases import Int4Case, Int8Case, max_err, to_dev_half
 
 pytestmark = pytest.mark.gpu
 
@@ -135,3 +135,44 @@ def test_int8_fused_tail_matches_sparse_plus_tail_merge(layers, T, tdt, mode):
         li = lse[i] if layers > 1 else lse
         assert max_err(oi[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max(), i
         assert max_err(li[:, :, 0], rl) <= 1e-4, i
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+@pytest.mark.parametrize("T", [0, 37])
+def test_single_layer_split_step_matches_oracle(bits, mode, T):
+    """One layer of 8 KV groups over 200 pages (the reference's per-layer call
+    at a realistic context): a scoring launch, then each group split over
+    several attention workgroups that select from its scores, the tail (if
+    any) attended by split 0, and the one-round split merge.  Selection
+    bit-exact, O and lse against the oracle (with the tail: the oracle's
+    sparse attention merged with dense attention over the tail)."""
+    from flashquest_amd.eager import quest_decode_int4, quest_decode_int8
+    rng = np.random.default_rng(300 + T + bits)
+    Hq, Hkv, P = 24, 8, 200
+    if bits == 4:
+        c = Int4Case(seed=77, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, page=64, dtype="bf16", meta="f16", vgroup=32)
+        fn = quest_decode_int4
+    else:
+        c = Int8Case(seed=78, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128)
+        fn = quest_decode_int8
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, select_mode=mode)
+    if T:
+        kt = O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32))
+        vt = O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32))
+        o, lse = fn(c.q_dev(), **c.device(), K_tail=_dev(kt, "bf16"), V_tail=_dev(vt, "bf16"), **kw)
+    else:
+        o, lse, mask = fn(c.q_dev(), **c.device(), return_selection=True, **kw)
+    torch.cuda.synchronize()
+    planes = (c.kp, c.ks, c.km, c.vp, c.vs, c.vm) if bits == 4 else (c.ku, c.ks, c.km, c.vu, c.vs, c.vm)
+    ref = O.decode_step(c.Q, *planes, retention=0.25, num_sinks=4, window_pages=2, mode=mode, bits=bits)
+    ro, rl = ref["O"], ref["lse"]
+    if T:
+        ot, lt = O.dense_attn_with_lse(c.Q, kt, vt)
+        ro = O.merge_two_attentions(ref["O"], ref["lse"], ot, lt)
+        m = np.maximum(ref["lse"], lt)
+        rl = m + np.log(np.exp(ref["lse"] - m) + np.exp(lt - m))
+    else:
+        assert np.array_equal(mask.cpu().numpy(), ref["mask"])
+    assert max_err(o[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max()
+    assert max_err(lse[:, :, 0], rl) <= 1e-4
