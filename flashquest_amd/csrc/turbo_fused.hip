@@ -345,6 +345,9 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         for (int T = 0; T < 4; ++T) acc[T] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
+            // the k-step's four table reads go out together, then its four
+            // matrix instructions (one read in flight at a time otherwise)
+            uint4 e[4];
 #pragma unroll
             for (int T = 0; T < 4; ++T) {
                 // table entry of channels 32 lg + 4 kk .. + 3: their LSB byte, MSB nibble
@@ -352,8 +355,13 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
                 const int lsh = 8 * (kk & 3) - 4, msh = 4 * kk - 12;      // entry * 16, in bytes
                 const uint32_t a_l = (lsh >= 0 ? lw >> lsh : lw << -lsh) & 0xFF0u;
                 const uint32_t a_m = (msh >= 0 ? pb.km[T] >> msh : pb.km[T] << -msh) & 0xF000u;
-                const uint4 e = *(const uint4*)((const char*)s_lut + (a_l | a_m));
-                const v8h B = __builtin_bit_cast(v8h, (v4i){(int)e.x, (int)e.y, (int)e.z, (int)e.w});
+                e[T] = *(const uint4*)((const char*)s_lut + (a_l | a_m));
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);     // 4 LDS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);     // then 4 matrix instructions
+#pragma unroll
+            for (int T = 0; T < 4; ++T) {
+                const v8h B = __builtin_bit_cast(v8h, (v4i){(int)e[T].x, (int)e[T].y, (int)e[T].z, (int)e[T].w});
                 acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[kk], B, acc[T], 0, 0, 0);
             }
         }
