@@ -365,6 +365,44 @@ def cpu_check(o_cpu, sel_cpu, o_gpu, sel_gpu):
             "max_abs_O_vs_cpu_path": float(err[same].max()) if bool(same.any()) else None}
 
 
+def sampled_cpu_check(cache, pairs, o_gpu, sel_gpu, retention, select, signs=None):
+    """The CPU path (oracle/torch_eager.py) as the checker of a GPU step on a
+    sample of (layer, sequence) pairs: o_gpu (L, B, H_q, D), sel_gpu (L, B,
+    H_q, P) or None (every page).  With signs (config 3's rotated cache) the
+    CPU path rotates q into the cache's basis, x -> WHT(s x) / sqrt(D)
+    (Sylvester Hadamard matrix), and O back, y -> s WHT(y) / sqrt(D)."""
+    from oracle import torch_eager as TE
+    threads = max(1, min(16, os.cpu_count() or 1))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    H = None
+    if signs is not None:
+        H = torch.ones(1, 1)
+        while H.shape[0] < 128:
+            H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
+        s = signs.float().cpu()
+    outs, sels, og, sg = [], [], [], []
+    try:
+        for l, b in pairs:
+            v = {k: cache[k][l, b].cpu() for k in ("Q", "K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")}
+            q = v["Q"][:, 0].float()
+            if H is not None:
+                q = (q * s) @ H / math.sqrt(128)
+            o, sel = TE.decode_layer(q, v["K_packed"], v["K_scale"], v["K_mn"], v["V_packed"], v["V_scale"],
+                                     v["V_mn"], retention=retention, select=select, return_selection=True)
+            if H is not None:
+                o = (o @ H / math.sqrt(128)) * s
+            outs.append(o)
+            sels.append(sel)
+            og.append(o_gpu[l, b].float().cpu())
+            sg.append(sel if sel_gpu is None else sel_gpu[l, b].cpu())
+    finally:
+        torch.set_num_threads(prev)
+    out = cpu_check(torch.stack(outs), torch.stack(sels), torch.stack(og), torch.stack(sg))
+    out["pairs"] = [list(x) for x in pairs]
+    return out
+
+
 def cpu_baseline(cache, args, n_layers, o_gpu, sel_gpu):
     """The reference's eager CPU path restated in PyTorch (oracle/torch_eager.py:
     two fp32 matmuls for the scores, topk + forced pages, fp32 dequant of the
@@ -514,6 +552,11 @@ def main():
         sb, ab, _, _ = step_bytes(cache, full_mask)
         extra.update({"all_pages_control_us": ctl_ms * 1e3, "sparse_speedup_vs_all_pages": ctl_ms / step_ms,
                       "all_pages_GBps": (sb + ab) / (ctl_ms * 1e-3) / 1e9})
+        if not args.no_cpu_baseline:
+            ctl()
+            torch.cuda.synchronize()
+            extra["config2_cpu_check"] = sampled_cpu_check(cache, [(0, 0), (13, 0), (27, 0)][:L], ctl.O3, None, 1.0,
+                                                           args.select)
         other = "per_q_head" if args.select == "per_kv_head_sum" else "per_kv_head_sum"
         alt = decoder(args.retention, k, other)
         alt_ms, _, _ = time_steps(noop, alt, args.steps, args.warmup, flush)
@@ -574,6 +617,11 @@ def main():
         torch.cuda.synchronize()
         rs_b, ra_b, _, _ = step_bytes(rc, rmask)
         r_ms, _, _ = time_steps(noop, rdec, args.steps, args.warmup, flush)
+        if not args.no_cpu_baseline:
+            rdec()
+            torch.cuda.synchronize()
+            extra["config3_cpu_check"] = sampled_cpu_check(rc, [(0, 0), (13, 0), (27, 0)][:L], rdec.O3, rmask,
+                                                           args.retention, args.select, signs=signs)
         extra.update({"config3_rotated_us": r_ms * 1e3, "config3_fused": rdec.fused,
                       "config3_step_GBps": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9,
                       "config3_roofline_frac": (rs_b + ra_b) / (r_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -692,6 +740,11 @@ def main():
             bs_b, ba_b, _, _ = step_bytes(bc, bmask)
             bdec.mask_out = None
             b_ms, _, _ = time_steps(noop, bdec, args.steps, args.warmup, flush)
+            if not args.no_cpu_baseline:
+                bdec()
+                torch.cuda.synchronize()
+                extra["config4_cpu_check"] = sampled_cpu_check(bc, [(0, 0), (5, 7), (13, 15), (27, 3)], bdec.O3,
+                                                               bmask, args.retention, args.select)
             extra.update({"config4_batch16_us": b_ms * 1e3, "config4_step_bytes": bs_b + ba_b,
                           "config4_step_GBps": (bs_b + ba_b) / (b_ms * 1e-3) / 1e9,
                           "config4_roofline_frac": (bs_b + ba_b) / (b_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
