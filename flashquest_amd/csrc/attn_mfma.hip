@@ -150,7 +150,12 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 
     const Int4Cache& c = a.c;
     const QueryArgs& q = a.q;
-    const int g = blockIdx.y, split = blockIdx.x;
+    // the group of this workgroup: workgroups go to the XCDs round-robin by
+    // index, so index i takes group (i % 8) * (G / 8) + i / 8, giving every
+    // XCD a mix of KV heads and layers instead of one KV head of every layer
+    const int gy = blockIdx.y, GY = gridDim.y;
+    const int g = (gridDim.x == 1 && GY % 8 == 0) ? (gy % 8) * (GY / 8) + gy / 8 : gy;
+    const int split = blockIdx.x;
     const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
     const int L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
     const int n16 = L & 15, lg = L >> 4;
