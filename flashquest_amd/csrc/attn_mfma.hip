@@ -589,7 +589,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         wave_lds_fence();
         const v8h ap0 = *(const v8h*)&W.apv[0][n16][swz(n16, lg)][0];
         const v8h ap1 = *(const v8h*)&W.apv[1][n16][swz(n16, lg)][0];
-        v8h al0, al1;
+        v8h al0 = {}, al1 = {};          // used with G != 1 only
         if constexpr (G != 1) {
             al0 = *(const v8h*)&W.apl[0][n16][swz(n16, lg)][0];
             al1 = *(const v8h*)&W.apl[1][n16][swz(n16, lg)][0];

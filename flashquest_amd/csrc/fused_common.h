@@ -46,8 +46,8 @@ FQ_DEV uint32_t ld16(__amdgpu_buffer_rsrc_t r, int off) { return __builtin_amdgc
 
 // Page scores of one KV group (P <= 64 * kSelC pages) by a whole workgroup of
 // NT threads: 16 lanes per page, NT / 16 pages per pass.  score_group_load
-// issues every pass's metadata loads (pages past P re-read page P-1, so there
-// is no branch between loads and use); score_group_regs scores them --
+// issues the metadata loads of the passes that hold pages (a partial last
+// pass re-reads page P-1); score_group_regs scores them --
 // score_kernel's arithmetic and order exactly -- and stores the sortable keys
 // s_key[r * 64 kSelC + p] per query head, or (SUM, per_kv_head_sum) s_key[p]
 // for the group's summed query, with 0 (below every score) for p >= P.
@@ -65,9 +65,11 @@ FQ_DEV void score_group_load(ScoreRegs<NT>& sr, const Int4Cache& c, int tid, int
     const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2] + lip * 8;
 #pragma unroll
     for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
-        const int p = min(u * PPP + pip, c.P - 1);
-        sr.sv[u] = *(const uint4*)(ksc + p * 128);
-        sr.mv[u] = *(const uint4*)(kmn + p * 128);
+        if (u * PPP < c.P) {          // uniform: no loads for passes past the group's pages
+            const int p = min(u * PPP + pip, c.P - 1);
+            sr.sv[u] = *(const uint4*)(ksc + p * 128);
+            sr.mv[u] = *(const uint4*)(kmn + p * 128);
+        }
     }
 }
 
@@ -131,9 +133,14 @@ FQ_DEV void score_group_regs_q(const ScoreRegs<NT>& sr, const float (&qin)[NREP]
 #pragma unroll
     for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
         const int p = u * PPP + pip;
-        score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
-            if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
-        }, levels);
+        if (u * PPP < P) {            // uniform
+            score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
+                if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
+            }, levels);
+        } else if (lip == 0) {        // a pass past the group's pages: their keys are 0
+#pragma unroll
+            for (int r = 0; r < NR; ++r) s_key[r * 64 * kSelC + p] = 0u;
+        }
     }
 }
 
