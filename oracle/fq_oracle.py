@@ -15,8 +15,9 @@ Rounding conventions (the reference runs its cache writes on CUDA torch):
     ``tensor / tensor`` is IEEE fp32 division;
   * ``round`` is round-half-to-even; ``clamp_min(eps)`` on a half tensor is
     ``half(max(float(x), eps))``;
-  * ``argmin`` / ``topk`` ties go to the lower index (documented for argmin;
-    this build's rule for topk).
+  * ``argmin`` / ``topk`` ties go to the lower index (documented for argmin).
+  These rules are checked against torch executing the same operations on the
+  GPU (tests/test_gpu_torch_arith_pins.py).
 
 Pinning status (what checks each function; see tests/test_oracle_*.py):
   quantize_k_int4 / quantize_v_int4   closed form + reference KATs + invariants
