@@ -629,6 +629,23 @@ void prefill_attn_kernel(PrefillParams a) {
 // owns QB blocks of 16 query columns, so every K / V^T operand read from LDS
 // feeds QB matrix instructions.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor words (base, stride 0, num_records, the flags word of a raw
+// buffer) for dma16_to_lds; p is wave-uniform.
+FQ_DEV i32x4 dma_rsrc(const void* p, int num_records) {
+    const uint64_t v = (uint64_t)p;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)v),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(v >> 32) & 0xFFFFu)), num_records, 0x00020000};
+}
+// Lane L loads 16 bytes at (voff + soff) of the buffer into LDS at dst + 16 L
+// (buffer_load_dwordx4 ... lds, the LDS address in m0).  dst and soff are
+// wave-uniform.  The load counts in vmcnt like any buffer load.
+FQ_DEV void dma16_to_lds(i32x4 rsrc, const uint16_t* dst, int voff, int soff) {
+    const int lds = __builtin_amdgcn_readfirstlane((int)(size_t)(lds_ptr_t)dst);
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+}
 
 template <int QB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -661,8 +678,6 @@ void prefill_dense_kernel(PrefillParams a) {
     const int mw0 = m0 + w * RW;
     const bool wave_on = mw0 < Mtot;
     const int pmin = min(mw0, Mtot - 1) / a.nrep;
-    const int pmax = (min(mw0 + RW, Mtot) - 1) / a.nrep;
-    const int limit_w = min(a.Skv, pmax + a.causal_off + 1);
 
     int qpos[QB];
     bool qok[QB];
@@ -697,18 +712,7 @@ void prefill_dense_kernel(PrefillParams a) {
     // stage's uniform base address plus per-lane byte offsets fixed for the kernel
     const int64_t bh = (int64_t)b * c.Hkv + h;
     const int64_t dense_bytes = (int64_t)a.s_pad * kPD * 2;      // one (b, h) slice of K or of V^T
-    // wave-uniform by construction; readfirstlane keeps them in scalar registers
-    auto uniform_ptr = [](const void* p) {
-        const uint64_t v = (uint64_t)p;
-        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-        return (void*)(((uint64_t)hi << 32) | lo);
-    };
     const int nrec = __builtin_amdgcn_readfirstlane((int)min(dense_bytes, (int64_t)INT32_MAX));
-    const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.kd + bh * a.s_pad * kPD), (short)0, nrec, 0x00020000);
-    const __amdgpu_buffer_rsrc_t vrs =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.vtd + bh * kPD * a.s_pad), (short)0, nrec, 0x00020000);
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const int lrow = lane >> 4, slot = lane & 15;
     int koff[4], voff[4];
@@ -718,15 +722,21 @@ void prefill_dense_kernel(PrefillParams a) {
         koff[j] = (r * kPD + ch * 8) * 2;
         voff[j] = (r * a.s_pad + ch * 8) * 2;
     }
-    auto issue_stage = [&](int buf, int key0_) {
+    // The stage loads are issued as inline assembly: the compiler does not see
+    // their LDS writes, so it adds no waits of its own before the LDS reads of
+    // the other buffers while they are in flight (it cannot tell a load issued
+    // in the previous iteration from the buffer read in this one).  The loop
+    // orders them itself with the vmcnt waits and barriers below.
+    const i32x4 krw = dma_rsrc(a.kd + bh * a.s_pad * kPD, nrec), vrw = dma_rsrc(a.vtd + bh * kPD * a.s_pad, nrec);
+    auto issue_k = [&](int buf, int key0_) {
         const int key0 = __builtin_amdgcn_readfirstlane(key0_);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r0 = 16 * wu + 4 * j;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr_t)(s_k[buf] + r0 * kPD), 16, koff[j], key0 * kPD * 2,
-                                                     0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_ptr_t)(s_v[buf] + r0 * ST), 16, voff[j], key0 * 2, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j) dma16_to_lds(krw, s_k[buf] + (16 * wu + 4 * j) * kPD, koff[j], key0 * kPD * 2);
+    };
+    auto issue_v = [&](int buf, int key0_) {
+        const int key0 = __builtin_amdgcn_readfirstlane(key0_);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16_to_lds(vrw, s_v[buf] + (16 * wu + 4 * j) * ST, voff[j], key0 * 2);
     };
 
     // S^T = K Q^T for one 64-key sub-tile (sk: its first key row; row & 15 = n)
@@ -764,7 +774,6 @@ void prefill_dense_kernel(PrefillParams a) {
     // does, p <= 2^kLazyLog2 (exact in fp32, relative bf16 rounding unchanged)
     // and O and its denominator need no rescale.
     auto tile_max = [&](const v4f (&s)[QB][4], float (&mx)[QB]) {
-        bool moved = false;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             float t4[4];
@@ -772,9 +781,13 @@ void prefill_dense_kernel(PrefillParams a) {
             for (int kb = 0; kb < 4; ++kb)
                 t4[kb] = fmaxf(fmaxf(s[qb][kb][0], s[qb][kb][1]), fmaxf(s[qb][kb][2], s[qb][kb][3]));
             mx[qb] = rows_max(fmaxf(fmaxf(t4[0], t4[1]), fmaxf(t4[2], t4[3]))) * a.qk_scale;
-            moved |= mx[qb] > m_run[qb] + kLazyLog2;
         }
-        return moved;
+    };
+    auto moved = [&](const float (&mx)[QB]) {
+        bool mv = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) mv |= mx[qb] > m_run[qb] + kLazyLog2;
+        return mv;
     };
     auto raise_ref = [&](const float (&mx)[QB]) {      // wave-uniform: new references for every column
 #pragma unroll
@@ -818,44 +831,69 @@ void prefill_dense_kernel(PrefillParams a) {
         }
     };
 
-    if (t_begin < nt) issue_stage(0, t_begin * ST);
+    // Stage t sits in buffer (t - t_begin) & 1.  The loop is pipelined across
+    // stages so that every phase pairs matrix work with vector work:
+    //   q.k of sub-tile 0 (stage t)        | exp of sub-tile 1 (stage t - 1)
+    //   p.v of sub-tile 1 (stage t - 1)    | maximum of sub-tile 0
+    //   -- barrier: V(t - 1) is free, V(t) has landed; V(t + 1) is issued --
+    //   q.k of sub-tile 1                  | exp of sub-tile 0
+    //   p.v of sub-tile 0                  | maximum of sub-tile 1
+    // O accumulates the sub-tiles in key order.  Every wave computes
+    // every sub-tile of the workgroup's stages (a wave with no rows computes
+    // none): the causal / length mask zeroes the keys past a wave's rows (exact
+    // zeros added to O and its denominator).
+    // K(t + 1) is issued at the top of iteration t, V(t + 1) after the middle
+    // barrier; the waits count the 4 loads per wave issued after the ones needed.
+    if (t_begin < nt) {
+        issue_k(0, t_begin * ST);
+        issue_v(0, t_begin * ST);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the first stage and Q have landed
     __syncthreads();
+    v4f s1p[QB][4];       // sub-tile 1 scores of the previous stage
     for (int t = t_begin; t < nt; ++t) {
         const int cur = (t - t_begin) & 1;
         const int key0 = t * ST;
-        // the other buffer was last read before the previous iteration's barrier
-        if (t + 1 < nt) issue_stage(cur ^ 1, key0 + ST);
-        // Both 64-key sub-tiles: q.k of sub-tile 1 is issued before sub-tile
-        // 0's softmax and the maximum of sub-tile 1 follows sub-tile 0's p.v,
-        // so the matrix instructions of one overlap the vector work of the other.
-        const bool act0 = wave_on && key0 < limit_w, act1 = wave_on && key0 + kPKT < limit_w;
-        if (act1) {
-            v4f s0[QB][4], s1[QB][4];
-            float mx0[QB], mx1[QB];
-            v8bf p0[QB][2], p1[QB][2];
+        const bool more = t + 1 < nt;
+        // the other K buffer was last read before the previous iteration's end barrier
+        if (more) issue_k(cur ^ 1, key0 + ST);
+        v4f s0[QB][4];
+        float mx0[QB];
+        if (wave_on && t > t_begin) {
+            v8bf pp[QB][2];
+            exp_p(s1p, pp);
             qk(s_k[cur], s0);
             diag_mask(key0, s0);
-            qk(s_k[cur] + kPKT * kPD, s1);
-            if (__builtin_amdgcn_ballot_w64(tile_max(s0, mx0))) raise_ref(mx0);
-            diag_mask(key0 + kPKT, s1);
-            exp_p(s0, p0);
-            pv(s_v[cur], 0, p0);
-            if (__builtin_amdgcn_ballot_w64(tile_max(s1, mx1))) raise_ref(mx1);
-            exp_p(s1, p1);
-            pv(s_v[cur], 1, p1);
-        } else if (act0) {
-            v4f s0[QB][4];
-            float mx0[QB];
-            v8bf p0[QB][2];
+            tile_max(s0, mx0);
+            pv(s_v[cur ^ 1], 1, pp);
+        } else if (wave_on) {
             qk(s_k[cur], s0);
             diag_mask(key0, s0);
-            if (__builtin_amdgcn_ballot_w64(tile_max(s0, mx0))) raise_ref(mx0);
-            exp_p(s0, p0);
-            pv(s_v[cur], 0, p0);
+            tile_max(s0, mx0);
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): stage t + 1 is in LDS
+        if (more) __builtin_amdgcn_s_waitcnt(0x0F74);   // vmcnt(4): V(t) is in LDS (K(t + 1) may be in flight)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
+        if (more) issue_v(cur ^ 1, key0 + ST);
+        if (wave_on) {
+            if (__builtin_amdgcn_ballot_w64(moved(mx0))) raise_ref(mx0);
+            v8bf p0[QB][2];
+            float mx1[QB];
+            exp_p(s0, p0);
+            qk(s_k[cur] + kPKT * kPD, s1p);
+            diag_mask(key0 + kPKT, s1p);
+            tile_max(s1p, mx1);
+            pv(s_v[cur], 0, p0);
+            if (__builtin_amdgcn_ballot_w64(moved(mx1))) raise_ref(mx1);
+        }
+        if (more) __builtin_amdgcn_s_waitcnt(0x0F74);   // vmcnt(4): K(t + 1) is in LDS (V(t + 1) may be in flight)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    }
+    if (wave_on && t_begin < nt) {   // the last stage's sub-tile 1 (its V buffer is not reloaded)
+        v8bf pp[QB][2];
+        exp_p(s1p, pp);
+        pv(s_v[(nt - 1 - t_begin) & 1], 1, pp);
     }
 
     if (!wave_on) return;
