@@ -58,7 +58,8 @@ def parse():
     ap.add_argument("--profile-int8", action="store_true",
                     help="for rocprofv3 runs: 10 flushed fused INT8 decode steps (--select mode) only")
     ap.add_argument("--profile-prefill", action="store_true",
-                    help="for rocprofv3 runs: 5 prefills of a 32k-token prompt over one INT4 layer only")
+                    help="for rocprofv3 runs: 8 prefills of a 32k-token prompt over one INT4 layer only "
+                         "(3 to bring the clock up, then the 5 that are reported)")
     ap.add_argument("--profile-per-layer", action="store_true",
                     help="for rocprofv3 runs: the reference's per-layer call pattern (28 single-layer steps "
                          "in one HIP graph), 5 flushed replays only")
@@ -462,7 +463,7 @@ def main():
     if args.profile_prefill:
         from flashquest_amd.kernel import flash_attn_prefill_int4
         qp, pk, kt, vt = prefill_inputs(P * 64, 24, dev)   # config 1 shape: 24 query / 8 KV heads
-        for _ in range(5):
+        for _ in range(8):       # the first 3 bring the GPU clock up; the last 5 are the ones reported
             flash_attn_prefill_int4(qp, *pk, kt, vt, page_size=64)
         torch.cuda.synchronize()
         print(json.dumps({"profile_prefill": "done", "tokens": P * 64}))
