@@ -201,7 +201,7 @@ hipError_t launch_nrep(const AttnParams& a, dim3 grid, hipStream_t st) {
             hipLaunchKernelGGL((merge_splits_kernel<D, N, false>), dim3(grid.y), dim3(kThreads), 0, st, \
                                a.q, a.ws, a.c.Hkv, a.c.B, a.pps, a.splits, TailArgs{});                                       \
         break;
-        FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4) FQ_CASE(8)
+        FQ_CASE(1) FQ_CASE(2) FQ_CASE(3) FQ_CASE(4) FQ_CASE(5) FQ_CASE(6) FQ_CASE(7) FQ_CASE(8)
 #undef FQ_CASE
         default: return hipErrorInvalidValue;
     }

@@ -178,8 +178,8 @@ static int check_query(const fq_query* q, int D, int Hkv, QueryArgs* out) {
         return fail(FQ_ERR_INVALID, "query/output dtype must be bf16, fp16 or fp32");
     if (q->H_q < 1 || q->H_q % Hkv) return fail(FQ_ERR_INVALID, "H_q=%d must be divisible by H_kv=%d", q->H_q, Hkv);
     const int nrep = q->H_q / Hkv;
-    if (nrep != 1 && nrep != 2 && nrep != 3 && nrep != 4 && nrep != 8)
-        return fail(FQ_ERR_UNSUPPORTED, "GQA ratio %d not in (1, 2, 3, 4, 8)", nrep);
+    if (nrep > 8)    // the selection keeps one bit per query head of a group
+        return fail(FQ_ERR_UNSUPPORTED, "GQA ratio %d above 8", nrep);
     QueryArgs& o = *out;
     o.q = q->q; o.q_dtype = q->q_dtype; o.out = q->out; o.out_dtype = q->out_dtype; o.lse = q->lse;
     for (int i = 0; i < 4; ++i) { o.q_s[i] = q->q_strides[i]; o.o_s[i] = q->o_strides[i]; }

@@ -61,7 +61,7 @@ def _check(case):
     return err
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (2, 2), (8, 4), (8, 1), (24, 8)])
+@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (2, 2), (8, 4), (8, 1), (24, 8), (10, 2), (6, 1), (14, 2)])
 def test_prefill_int4_whole_prompt(Hq, Hkv):
     # the first prefill: the cache holds the prompt (completed pages + tail), S_q == S_kv
     _check(PrefillCase(Hq + Hkv, Hq=Hq, Hkv=Hkv, S=320, T=23))

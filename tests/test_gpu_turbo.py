@@ -26,7 +26,8 @@ def _tol(ref):
     return 2e-3 + 2 ** -8 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("B,Hq,Hkv", [(2, 6, 2), (1, 3, 3), (3, 4, 2), (1, 2, 1), (2, 8, 2), (1, 8, 1)])
+@pytest.mark.parametrize("B,Hq,Hkv", [(2, 6, 2), (1, 3, 3), (3, 4, 2), (1, 2, 1), (2, 8, 2), (1, 8, 1), (1, 10, 2),
+                                     (2, 6, 1), (1, 7, 1)])
 def test_turbo_mask_attention_matches_oracle(B, Hq, Hkv):
     from flashquest_amd.kernel import flash_attn_sparse_turbo_fwd
     rng = np.random.default_rng(100 + Hq * 7 + Hkv)
@@ -46,7 +47,8 @@ def test_turbo_mask_attention_matches_oracle(B, Hq, Hkv):
 
 
 @pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
-@pytest.mark.parametrize("Hq,sinks,window,P", [(24, 3, 2, 20), (24, 0, 0, 20), (16, 9, 1, 12), (8, 4, 2, 6)])
+@pytest.mark.parametrize("Hq,sinks,window,P", [(24, 3, 2, 20), (24, 0, 0, 20), (16, 9, 1, 12), (8, 4, 2, 6),
+                                              (40, 3, 2, 20), (56, 1, 1, 12)])
 def test_fused_turbo_decode_matches_oracle(mode, Hq, sinks, window, P):
     # 24 layers x 8 KV heads = 192 KV groups: one workgroup per group, which
     # scores and selects its pages; a second call also writes the kernel's
