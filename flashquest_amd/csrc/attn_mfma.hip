@@ -206,6 +206,15 @@ void attn_int4_mfma_kernel(MfmaParams a) {
 #pragma unroll
         for (int r = 0; r < NREP; ++r) qsr[r] = ld128(rq, (int)(2 * (r * q.q_s[2] + 8 * (tid & 15))));
     }
+    // Rotation signs (rotated decode), loaded with q: loads complete in
+    // order, so one issued after the metadata loads would wait for all of them
+    // and the scoring could not overlap the metadata's arrival.
+    uint32_t rsg0 = 0u, rsg1 = 0u;
+    if constexpr (FUSED) {
+        const auto rr = make_rsrc(q.rot, q.rot && D == 128 ? 4 * D : 0);
+        rsg0 = ld32(rr, 4 * L);
+        rsg1 = ld32(rr, 4 * (L + 64));
+    }
     __builtin_amdgcn_sched_barrier(0);      // q's loads go out before the metadata loads
     // retention of query head L of the group (lanes past NREP repeat the last)
     float ret_l = 0.f;
@@ -321,7 +330,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                 __syncthreads();
                 if (q.rot) {       // uniform: wave r rotates head r, q -> WHT(s q) / sqrt(D), in fp32
                     if (w < NREP) {
-                        float x0 = s_qraw[w][L] * q.rot[L], x1 = s_qraw[w][L + 64] * q.rot[L + 64];
+                        float x0 = s_qraw[w][L] * __uint_as_float(rsg0), x1 = s_qraw[w][L + 64] * __uint_as_float(rsg1);
                         wave_hadamard128(x0, x1);
                         const float inv = 1.0f / sqrtf((float)D);
                         x0 *= inv;
