@@ -51,6 +51,43 @@ def merge_two_attentions(O_a, lse_a, O_b, lse_b) -> torch.Tensor:
     return out.view(O_a.shape)
 
 
+_FUSED_TAIL_REFUSED = "the fused tail needs the matrix-core attention layout"
+
+
+def _tail_by_merge(run_sparse, Q3, O3, lse, K_tail, V_tail, sm_scale):
+    """The reference's own partial-page sequence (llama_persistent_patch.py:
+    232-245) for the shapes whose fused tail the library refuses (GQA ratios
+    above 4, head_dim 64, other page sizes): sparse attention over the
+    completed pages into fp32 O and lse (run_sparse(O, lse)), then
+    _bf16_dense_attn_with_lse over the tail (fp32 arithmetic, bf16 O, as
+    there), then _merge_two_attentions (fp32, cast to O3's dtype)."""
+    D = Q3.shape[-1]
+    if sm_scale is not None and float(sm_scale) != 1.0 / math.sqrt(D):
+        raise NotImplementedError("the partial-page merge takes the default sm_scale (1/sqrt(head_dim))")
+    O_sp = torch.empty(Q3.shape, dtype=torch.float32, device=Q3.device)
+    lse_sp = torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q3.device)
+    run_sparse(O_sp, lse_sp)
+    H_q, H_kv, T = Q3.shape[-2], K_tail.shape[-3], K_tail.shape[-2]
+    n = O_sp.numel() // (H_q * D)
+    q = Q3.reshape(n, H_q, 1, D).float()
+    kt = K_tail.reshape(n, H_kv, T, D).float()
+    vt = V_tail.reshape(n, H_kv, T, D).float()
+    O_t, lse_t = bf16_dense_attn_with_lse(q, kt, vt)
+    oa = O_sp.reshape(-1, D)
+    ob = O_t.float().reshape(-1, D)
+    la = lse_sp.reshape(-1).contiguous()
+    lb = lse_t.reshape(-1).contiguous()
+    merged = torch.empty_like(oa)
+    lse_m = torch.empty_like(la)
+    L.check(L.lib().fq_merge_attn(oa.data_ptr(), la.data_ptr(), ob.data_ptr(), lb.data_ptr(),
+                                  L.dtype_code(oa.dtype), oa.stride(0), ob.stride(0), merged.data_ptr(),
+                                  merged.stride(0), lse_m.data_ptr(), oa.shape[0], D, L.stream_handle(Q3.device)),
+            "merge_two_attentions")
+    O3.copy_(merged.view(O3.shape))
+    if lse is not None:
+        lse.copy_(lse_m.view(lse.shape))
+
+
 def quest_decode_int4(
     Q: torch.Tensor,
     K_packed: torch.Tensor,
@@ -133,10 +170,22 @@ def quest_decode_int4(
     ws = L.workspace(Q.device, L.lib().fq_workspace_bytes(cache, H_q), stream)
     tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
     if tail is not None:
-        L.check(L.lib().fq_quest_decode_int4_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
-                                                  int(window_pages), k_max, L.SELECT_MODES[select_mode],
-                                                  ws.data_ptr(), ws.numel(), stream),
-                "quest_decode_int4 (tail)")
+        try:
+            L.check(L.lib().fq_quest_decode_int4_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
+                                                      int(window_pages), k_max, L.SELECT_MODES[select_mode],
+                                                      ws.data_ptr(), ws.numel(), stream),
+                    "quest_decode_int4 (tail)")
+        except NotImplementedError as e:
+            if _FUSED_TAIL_REFUSED not in str(e) or _rotation is not None:
+                raise
+
+            def run_sparse(O_sp, lse_sp):
+                q2 = _ops.query(Q3, O_sp, lse_sp, sm_scale)
+                q2.retention_layer_stride = query.retention_layer_stride
+                L.check(L.lib().fq_quest_decode_int4(cache, q2, r.data_ptr(), int(num_sinks), int(window_pages),
+                                                     k_max, L.SELECT_MODES[select_mode], None, None,
+                                                     ws.data_ptr(), ws.numel(), stream), "quest_decode_int4")
+            _tail_by_merge(run_sparse, Q3, O3, lse, tail_keep[0], tail_keep[1], sm_scale)
     else:
         L.check(L.lib().fq_quest_decode_int4(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
                                              L.SELECT_MODES[select_mode], None,
@@ -255,10 +304,22 @@ def quest_decode_int8(
     ws = L.workspace(Q.device, L.lib().fq_int8_workspace_bytes(cache, H_q), stream)
     tail, tail_keep = _tail(K_tail, V_tail, D, return_selection)
     if tail is not None:
-        L.check(L.lib().fq_quest_decode_int8_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
-                                                  int(window_pages), k_max, L.SELECT_MODES[select_mode],
-                                                  ws.data_ptr(), ws.numel(), stream),
-                "quest_decode_int8 (tail)")
+        try:
+            L.check(L.lib().fq_quest_decode_int8_tail(cache, query, tail, r.data_ptr(), int(num_sinks),
+                                                      int(window_pages), k_max, L.SELECT_MODES[select_mode],
+                                                      ws.data_ptr(), ws.numel(), stream),
+                    "quest_decode_int8 (tail)")
+        except NotImplementedError as e:
+            if _FUSED_TAIL_REFUSED not in str(e):
+                raise
+
+            def run_sparse(O_sp, lse_sp):
+                q2 = _ops.query(Q3, O_sp, lse_sp, sm_scale)
+                q2.retention_layer_stride = query.retention_layer_stride
+                L.check(L.lib().fq_quest_decode_int8(cache, q2, r.data_ptr(), int(num_sinks), int(window_pages),
+                                                     k_max, L.SELECT_MODES[select_mode], None, None,
+                                                     ws.data_ptr(), ws.numel(), stream), "quest_decode_int8")
+            _tail_by_merge(run_sparse, Q3, O3, lse, tail_keep[0], tail_keep[1], sm_scale)
     else:
         L.check(L.lib().fq_quest_decode_int8(cache, query, r.data_ptr(), int(num_sinks), int(window_pages), k_max,
                                              L.SELECT_MODES[select_mode], None,

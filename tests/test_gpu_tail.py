@@ -176,3 +176,47 @@ def test_single_layer_split_step_matches_oracle(bits, mode, T):
         assert np.array_equal(mask.cpu().numpy(), ref["mask"])
     assert max_err(o[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max()
     assert max_err(lse[:, :, 0], rl) <= 1e-4
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rep,layers,T,mode", [(5, 1, 37, "per_q_head"), (6, 4, 64, "per_kv_head_sum"),
+                                               (7, 1, 1, "per_kv_head_sum"), (7, 4, 20, "per_q_head")])
+def test_tail_with_gqa_ratios_above_four(bits, rep, layers, T, mode):
+    """GQA ratios 5-7 take the general attention kernels; with a bf16 tail
+    the tail is attended in their split merge.  Against the oracle's sparse
+    attention merged with the dense tail attention, INT4 and INT8."""
+    from flashquest_amd.eager.decode import quest_decode_int4, quest_decode_int8
+    rng = np.random.default_rng(90 + rep + T + bits)
+    Hkv, P = 2, 9
+    Hq = Hkv * rep
+    mk = Int4Case if bits == 4 else Int8Case
+    cases = [mk(seed=700 + 10 * bits + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, page=64, dtype="bf16", meta="bf16")
+             for i in range(layers)]
+    tails = [(O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32)),
+              O.round_bf16(rng.standard_normal((1, Hkv, T, 128)).astype(np.float32))) for _ in range(layers)]
+    dev = [c.device() for c in cases]
+    if layers > 1:
+        planes = {k: torch.stack([d[k] for d in dev]) for k in dev[0]}
+        q = torch.stack([c.q_dev() for c in cases])
+        kt = torch.stack([to_dev_half(t[0], "bf16") for t in tails])
+        vt = torch.stack([to_dev_half(t[1], "bf16") for t in tails])
+    else:
+        planes, q = dev[0], cases[0].q_dev()
+        kt, vt = to_dev_half(tails[0][0], "bf16"), to_dev_half(tails[0][1], "bf16")
+    fn = quest_decode_int4 if bits == 4 else quest_decode_int8
+    o, lse = fn(q, **planes, retention=0.3, num_sinks=2, window_pages=1, select_mode=mode, K_tail=kt, V_tail=vt)
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        if bits == 4:
+            ro, rl = _merged_ref(c, tails[i][0], tails[i][1], 0.3, 2, 1, mode)
+        else:
+            ref = O.decode_step(c.Q, c.ku, c.ks, c.km, c.vu, c.vs, c.vm, retention=0.3, num_sinks=2,
+                                window_pages=1, mode=mode, bits=8)
+            ot, lt = O.dense_attn_with_lse(c.Q, tails[i][0], tails[i][1])
+            ro = O.merge_two_attentions(ref["O"], ref["lse"], ot, lt)
+            m = np.maximum(ref["lse"], lt)
+            rl = m + np.log(np.exp(ref["lse"] - m) + np.exp(lt - m))
+        oi = o[i] if layers > 1 else o
+        li = lse[i] if layers > 1 else lse
+        assert max_err(oi[:, :, 0], ro) <= 2e-3 + 2 ** -8 * np.abs(ro).max(), (rep, i)
+        assert max_err(li[:, :, 0], rl) <= 1e-4, (rep, i)
