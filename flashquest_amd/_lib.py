@@ -156,6 +156,8 @@ SIGNATURES = {
                                                _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quest_select_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
+                                            _P, _P, _P, ctypes.c_size_t, _P]),
     "fq_quantize_k_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,
                                           _I, _P]),
     "fq_quantize_v_int8": (ctypes.c_int, [_P, _I, _I64P, _I, _I, _I, _I, _P, _I64P, _P, _I64P, _P, _I64P,

@@ -594,6 +594,14 @@ int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, cons
                         workspace_bytes_, stream, 8, mask_out);
 }
 
+int fq_quest_select_int8(const fq_int8_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                         fq_stream_t stream) {
+    return quest_select(cache, query, retention, num_sinks, window_pages, k_max, select_mode, scores_out, mask_out,
+                        workspace, workspace_bytes_, stream, 8);
+}
+
 size_t fq_int8_workspace_bytes(const fq_int8_cache* cache, int32_t H_q) { return fq_workspace_bytes(cache, H_q); }
 
 int fq_page_scores_int8(const void* q, int32_t q_dtype, const int64_t q_strides[4], const void* k_scale,

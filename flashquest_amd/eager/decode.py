@@ -149,6 +149,15 @@ def quest_decode_int4(
     D = Q.shape[-1]
     if D not in (64, 128):
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
+    H_kv = K_scale.shape[-3]
+    nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
+    if nrep > 4 and D == 128 and page_size == 64 and _rotation is None:
+        return _chunked_decode(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), H_kv, nrep, out,
+                                    dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
+                                         k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
+                                         sm_scale=sm_scale, return_lse=return_lse,
+                                         return_selection=return_selection, K_tail=K_tail, V_tail=V_tail,
+                                         head_pattern=head_pattern))
     layered = Q.dim() == 5
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
@@ -197,6 +206,115 @@ def quest_decode_int4(
     if return_selection:
         return O, lse_out, mask
     return O, lse_out
+
+
+def _head_chunks(nrep: int):
+    """(offset, size) chunks of a KV group's query heads, each of at most 4
+    heads (what the matrix-core kernels take), sizes as equal as possible."""
+    n = -(-nrep // 4)
+    base, extra = divmod(nrep, n)
+    chunks, off = [], 0
+    for i in range(n):
+        size = base + (1 if i < extra else 0)
+        chunks.append((off, size))
+        off += size
+    return chunks
+
+
+def _heads(x, axis, H_kv, nrep, off, size):
+    """The (H_kv, size) query heads [off, off + size) of every KV group of the
+    H_kv * nrep head axis `axis` of x, as a contiguous tensor."""
+    return x.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).flatten(axis, axis + 1).contiguous()
+
+
+def _put_heads(dst, src, axis, H_kv, nrep, off, size):
+    dst.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).copy_(src.unflatten(axis, (H_kv, size)))
+
+
+def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
+    """quest_decode_int4 / quest_decode_int8 (bits 4 / 8) for 5 to 8 query
+    heads per KV head (the reference's kernels take any ratio,
+    sparse_int4_fwd.py:54-55, sparse_fwd.py): the group's query heads
+    in chunks of at most 4, each on the matrix-core kernels.  per_q_head
+    selects every head on its own, so each chunk is an ordinary step over its
+    heads.  per_kv_head_sum selects once per KV group from all of its heads
+    (one selection pass over the whole query, its mask kept), then each chunk
+    attends the group's pages through the mask entry.  A partial-page tail is
+    merged as the reference does (llama_persistent_patch.py:232-245)."""
+    head_axis = Q.dim() - 3
+    H_q, D, P = Q.shape[-3], Q.shape[-1], planes[1].shape[-2]
+    O = torch.empty_like(Q) if out is None else out
+    lse = torch.empty(Q.shape[:-2], dtype=torch.float32, device=Q.device) if kw["return_lse"] else None
+    mask = torch.empty(Q.shape[:-2] + (P,), dtype=torch.bool, device=Q.device) if kw["return_selection"] else None
+    retention = kw["retention"]
+
+    def ret_chunk(off, size):
+        if not torch.is_tensor(retention):
+            return retention
+        r = retention.to(device=Q.device, dtype=torch.float32)
+        return _heads(r, r.dim() - 1, H_kv, nrep, off, size)
+
+    if kw["select_mode"] == "per_q_head":
+        for off, size in _head_chunks(nrep):
+            sub = dict(kw, retention=ret_chunk(off, size))
+            step = quest_decode_int4 if bits == 4 else quest_decode_int8
+            res = step(_heads(Q, head_axis, H_kv, nrep, off, size), *planes, **sub)
+            _put_heads(O, res[0], head_axis, H_kv, nrep, off, size)
+            if lse is not None:
+                _put_heads(lse, res[1][..., 0], head_axis, H_kv, nrep, off, size)
+            if mask is not None:
+                _put_heads(mask, res[2], head_axis, H_kv, nrep, off, size)
+        O_out = O
+    else:
+        if kw["K_tail"] is not None and kw["K_tail"].shape[-2] > 0 and kw["return_selection"]:
+            raise ValueError("return_selection is not available together with a fused tail")
+        Q3 = Q[..., 0, :]
+        lib = L.lib()
+        if bits == 4:
+            cache, keep = _ops.int4_cache(*planes, kw["page_size"])
+            ws_bytes, select, attend = lib.fq_workspace_bytes, lib.fq_quest_select_int4, lib.fq_sparse_int4_fwd_mask
+        else:
+            cache, keep = _ops.int8_cache(*planes, kw["page_size"])
+            ws_bytes, select, attend = (lib.fq_int8_workspace_bytes, lib.fq_quest_select_int8,
+                                        lib.fq_sparse_int8_fwd_mask)
+        name = f"quest_decode_int{bits}"
+        stream = L.stream_handle(Q.device)
+        sel = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.uint8, device=Q.device)
+        query = _ops.query(Q3, torch.empty_like(Q3), None, kw["sm_scale"])     # the selection writes no O
+        r, query.retention_layer_stride = _ops.retention_rows(retention, kw["head_pattern"], H_q, H_kv,
+                                                              Q3.shape[0] if Q3.dim() == 4 else 1, Q.device)
+        k_max = -1 if kw["k_max_static"] is None else min(int(kw["k_max_static"]), P)
+        ws = L.workspace(Q.device, ws_bytes(cache, H_q), stream)
+        L.check(select(cache, query, r.data_ptr(), int(kw["num_sinks"]), int(kw["window_pages"]), k_max,
+                       L.SELECT_MODES["per_kv_head_sum"], None, sel.data_ptr(), ws.data_ptr(), ws.numel(), stream),
+                f"{name} (selection)")
+
+        def run_sparse(O3, lse3):
+            for off, size in _head_chunks(nrep):
+                qc = _heads(Q3, Q3.dim() - 2, H_kv, nrep, off, size)
+                mc = _heads(sel, sel.dim() - 2, H_kv, nrep, off, size)
+                oc = torch.empty(qc.shape, dtype=O3.dtype, device=Q.device)
+                lc = torch.empty(qc.shape[:-1], dtype=torch.float32, device=Q.device)
+                qd = _ops.query(qc, oc, lc, kw["sm_scale"])
+                wsc = L.workspace(Q.device, ws_bytes(cache, qc.shape[-2]), stream)
+                L.check(attend(cache, qd, mc.data_ptr(), L.strides(mc, 4, 4 - mc.dim()), wsc.data_ptr(), wsc.numel(),
+                               stream), f"{name} (attention)")
+                _put_heads(O3, oc, O3.dim() - 2, H_kv, nrep, off, size)
+                _put_heads(lse3, lc, lse3.dim() - 1, H_kv, nrep, off, size)
+
+        O3 = O[..., 0, :]
+        lse3 = lse if lse is not None else torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device)
+        if kw["K_tail"] is not None and kw["K_tail"].shape[-2] > 0:
+            _tail_by_merge(run_sparse, Q3, O3, lse3, kw["K_tail"], kw["V_tail"], kw["sm_scale"])
+        else:
+            run_sparse(O3, lse3)
+        if mask is not None:
+            mask.copy_(sel.bool())
+        O_out = O
+    lse_out = lse.unsqueeze(-1) if lse is not None else None
+    if kw["return_selection"]:
+        return O_out, lse_out, mask
+    return O_out, lse_out
 
 
 def _tail(K_tail, V_tail, D, return_selection):
@@ -287,6 +405,14 @@ def quest_decode_int8(
     D = Q.shape[-1]
     if D not in (64, 128):
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
+    H_kv = K_scale.shape[-3]
+    nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
+    if nrep > 4 and D == 128 and page_size == 64:
+        return _chunked_decode(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), H_kv, nrep, None,
+                               dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
+                                    k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
+                                    sm_scale=sm_scale, return_lse=return_lse, return_selection=return_selection,
+                                    K_tail=K_tail, V_tail=V_tail, head_pattern=head_pattern))
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
     P = K_scale.shape[-2]

@@ -469,6 +469,16 @@ int fq_quest_decode_int8(const fq_int8_cache* cache, const fq_query* query, cons
                          float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes,
                          fq_stream_t stream);
 
+/* The selection half of fq_quest_decode_int8 (page_scores_int8_fast and
+ * select_pages_vectorized of llama_persistent_patch.py:143-160, 196-245),
+ * as fq_quest_select_int4 for the INT8 cache: with mask_out it always writes
+ * the (L*B, H_q, P) selection.  Callers that attend a KV group's query heads
+ * in several calls use it to select once from all of the group's heads. */
+int fq_quest_select_int8(const fq_int8_cache* cache, const fq_query* query, const float* retention,
+                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                         float* scores_out, uint8_t* mask_out, void* workspace, size_t workspace_bytes,
+                         fq_stream_t stream);
+
 /* Replace quantize_k / quantize_v (kernel/kv_quant.py:43-61, 78-89): uint8
  * codes, K scale/min per (page, channel) with the arithmetic in the input
  * dtype ("/ 255.0"), V per token in fp32; metadata written as meta_dtype. */
