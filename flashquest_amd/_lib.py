@@ -122,6 +122,8 @@ SIGNATURES = {
                                              _I64P, _I, _P, _I64P, _P, _I64P, _I, _I, _P]),
     "fq_quest_decode_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, ctypes.POINTER(Query),
                                              _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
+    "fq_quest_select_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), _P, _I64P, _P, _I64P, ctypes.POINTER(Query),
+                                             _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int4_tail": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), ctypes.POINTER(Tail),
                                                  _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "fq_quest_decode_int8_tail": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), ctypes.POINTER(Tail),

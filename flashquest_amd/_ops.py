@@ -91,6 +91,9 @@ def turbo_cache(K_msb, K_lsb, K_scale, V_msb, V_lsb, V_scale, num_pages: int, pa
     c.v_scale, c.vst_strides = ts[5].data_ptr(), L.strides(ts[5], 5, lead)
     shape = (1,) * lead + tuple(ts[0].shape)
     c.L, c.B, c.H_kv, c.S = shape[0], shape[1], shape[2], shape[3]
+    if num_pages > -(-c.S // page_size):
+        raise ValueError(f"TurboQuant cache: {num_pages} pages but the planes hold {c.S} tokens "
+                         f"({-(-c.S // page_size)} pages of {page_size})")
     c.D = ts[0].shape[-1] * 8
     c.P = int(num_pages)
     c.page_size = int(page_size)

@@ -896,6 +896,11 @@ static int check_turbo_cache(const fq_turbo_cache* c) {
     if (c->L < 1 || c->B < 1 || c->H_kv < 1) return fail(FQ_ERR_INVALID, "empty L/B/H_kv");
     if (c->P < 1 || c->P > kMaxPages) return fail(FQ_ERR_UNSUPPORTED, "pages=%d", c->P);
     if (c->page_size < 1) return fail(FQ_ERR_INVALID, "page_size");
+    // the raw K metadata beside the descriptor is read for every page: a page
+    // count past the planes' tokens names rows the caller never wrote
+    if ((int64_t)c->P > ((int64_t)c->S + c->page_size - 1) / c->page_size)
+        return fail(FQ_ERR_INVALID, "pages=%d but the planes hold %lld tokens of page_size %d", c->P,
+                    (long long)c->S, c->page_size);
     if (!c->k_msb || !c->k_lsb || !c->k_scale || !c->v_msb || !c->v_lsb || !c->v_scale)
         return fail(FQ_ERR_INVALID, "NULL cache tensor");
     if (c->kmsb_strides[4] != 1 || c->klsb_strides[4] != 1 || c->vmsb_strides[4] != 1 || c->vlsb_strides[4] != 1)
@@ -937,11 +942,13 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
     return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "sparse turbo attention");
 }
 
-int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
-                          const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
-                          const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
-                          int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
-                          fq_stream_t stream) {
+// The TurboQuant step (select_only false) or its selection half alone (true:
+// scores and the selection, mask_out written when given, no attention).
+static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
+                       const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
+                       const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                       int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                       fq_stream_t stream, bool select_only) {
     int st = check_turbo_cache(cache);
     if (st) return st;
     if (!retention) return fail(FQ_ERR_INVALID, "retention is NULL");
@@ -977,7 +984,7 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     hipStream_t s = (hipStream_t)stream;
     const int bound = quest_bound(c, q, num_sinks, window_pages, k_max, select_mode);
     const bool fusable = turbo_fused_supported(*cache, q);
-    if (fusable && G >= 192 && c.P <= 64 * 8 && attention_splits_request() <= 0) {
+    if (!select_only && fusable && G >= 192 && c.P <= 64 * 8 && attention_splits_request() <= 0) {
         SelectArgs sel{};
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
@@ -985,7 +992,7 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     }
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};
-    if (fusable && c.P <= 64 * 8 && attention_splits_request() <= 0) {   // the in-kernel selection holds 512 pages
+    if (!select_only && fusable && c.P <= 64 * 8 && attention_splits_request() <= 0) {   // in-kernel selection: 512 pages
         // few groups (a single layer's step): the scoring launch writes the
         // scores, the attention workgroups of each group select from them
         st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
@@ -1000,10 +1007,28 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, 
     st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                  k_max, mask_out, s),
                     "score+select");
-    if (st) return st;
+    if (st || select_only) return st;
     if (fusable) return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, nullptr, s), "quest turbo decode");
     const AttnLaunch al = choose_split(G, bound, ws.s_max);
     return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "quest turbo decode");
+}
+
+int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
+                          const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
+                          const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                          int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                          fq_stream_t stream) {
+    return quest_turbo(cache, k_scale_raw, ksr_strides, k_mn_raw, kmr_strides, query, retention, num_sinks,
+                       window_pages, k_max, select_mode, mask_out, workspace, workspace_bytes_, stream, false);
+}
+
+int fq_quest_select_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
+                          const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
+                          const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
+                          int32_t select_mode, uint8_t* mask_out, void* workspace, size_t workspace_bytes_,
+                          fq_stream_t stream) {
+    return quest_turbo(cache, k_scale_raw, ksr_strides, k_mn_raw, kmr_strides, query, retention, num_sinks,
+                       window_pages, k_max, select_mode, mask_out, workspace, workspace_bytes_, stream, true);
 }
 
 static bool aligned(const void* p, int bytes) { return ((uintptr_t)p & (uintptr_t)(bytes - 1)) == 0; }

@@ -231,10 +231,11 @@ def _put_heads(dst, src, axis, H_kv, nrep, off, size):
     dst.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).copy_(src.unflatten(axis, (H_kv, size)))
 
 
-def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
-    """quest_decode_int4 / quest_decode_int8 (bits 4 / 8) for 5 to 8 query
-    heads per KV head (the reference's kernels take any ratio,
-    sparse_int4_fwd.py:54-55, sparse_fwd.py): the group's query heads
+def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
+    """quest_decode_int4 / quest_decode_int8 / quest_decode_turbo (bits 4 / 8
+    / 3; raw: TurboQuant's (K_scale_raw, K_mn_raw)) for 5 to 8 query heads per
+    KV head (the reference's kernels take any ratio, sparse_int4_fwd.py:54-55,
+    sparse_turbo_fwd.py): the group's query heads
     in chunks of at most 4, each on the matrix-core kernels.  per_q_head
     selects every head on its own, so each chunk is an ordinary step over its
     heads.  per_kv_head_sum selects once per KV group from all of its heads
@@ -242,7 +243,10 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
     attends the group's pages through the mask entry.  A partial-page tail is
     merged as the reference does (llama_persistent_patch.py:232-245)."""
     head_axis = Q.dim() - 3
-    H_q, D, P = Q.shape[-3], Q.shape[-1], planes[1].shape[-2]
+    # pages: K_scale (..., P, D) for INT4 / INT8; TurboQuant's planes are per
+    # token, its page count is the raw K metadata's (..., P, D)
+    H_q, D = Q.shape[-3], Q.shape[-1]
+    P = raw[0].shape[-2] if bits == 3 else planes[1].shape[-2]
     O = torch.empty_like(Q) if out is None else out
     lse = torch.empty(Q.shape[:-2], dtype=torch.float32, device=Q.device) if kw["return_lse"] else None
     mask = torch.empty(Q.shape[:-2] + (P,), dtype=torch.bool, device=Q.device) if kw["return_selection"] else None
@@ -257,8 +261,11 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
     if kw["select_mode"] == "per_q_head":
         for off, size in _head_chunks(nrep):
             sub = dict(kw, retention=ret_chunk(off, size))
-            step = quest_decode_int4 if bits == 4 else quest_decode_int8
-            res = step(_heads(Q, head_axis, H_kv, nrep, off, size), *planes, **sub)
+            qc = _heads(Q, head_axis, H_kv, nrep, off, size)
+            if bits == 3:
+                res = quest_decode_turbo(qc, *planes, *raw, **sub)
+            else:
+                res = (quest_decode_int4 if bits == 4 else quest_decode_int8)(qc, *planes, **sub)
             _put_heads(O, res[0], head_axis, H_kv, nrep, off, size)
             if lse is not None:
                 _put_heads(lse, res[1][..., 0], head_axis, H_kv, nrep, off, size)
@@ -266,18 +273,27 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
                 _put_heads(mask, res[2], head_axis, H_kv, nrep, off, size)
         O_out = O
     else:
-        if kw["K_tail"] is not None and kw["K_tail"].shape[-2] > 0 and kw["return_selection"]:
+        if kw.get("K_tail") is not None and kw["K_tail"].shape[-2] > 0 and kw["return_selection"]:
             raise ValueError("return_selection is not available together with a fused tail")
         Q3 = Q[..., 0, :]
         lib = L.lib()
         if bits == 4:
             cache, keep = _ops.int4_cache(*planes, kw["page_size"])
             ws_bytes, select, attend = lib.fq_workspace_bytes, lib.fq_quest_select_int4, lib.fq_sparse_int4_fwd_mask
-        else:
+        elif bits == 8:
             cache, keep = _ops.int8_cache(*planes, kw["page_size"])
             ws_bytes, select, attend = (lib.fq_int8_workspace_bytes, lib.fq_quest_select_int8,
                                         lib.fq_sparse_int8_fwd_mask)
-        name = f"quest_decode_int{bits}"
+        else:
+            cache, keep = _ops.turbo_cache(*planes, P, kw["page_size"])
+            ksr, kmr = (x if x.stride(-1) == 1 else x.contiguous() for x in raw)
+            lead = 5 - ksr.dim()
+
+            def select(c, qd, *args):        # the raw K metadata goes before the query
+                return lib.fq_quest_select_turbo(c, ksr.data_ptr(), L.strides(ksr, 5, lead), kmr.data_ptr(),
+                                                 L.strides(kmr, 5, lead), qd, *args[:5], *args[6:])
+            ws_bytes, attend = lib.fq_turbo_workspace_bytes, lib.fq_sparse_turbo_fwd_mask
+        name = "quest_decode_turbo" if bits == 3 else f"quest_decode_int{bits}"
         stream = L.stream_handle(Q.device)
         sel = torch.empty(Q3.shape[:-1] + (P,), dtype=torch.uint8, device=Q.device)
         query = _ops.query(Q3, torch.empty_like(Q3), None, kw["sm_scale"])     # the selection writes no O
@@ -304,7 +320,7 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw):
 
         O3 = O[..., 0, :]
         lse3 = lse if lse is not None else torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device)
-        if kw["K_tail"] is not None and kw["K_tail"].shape[-2] > 0:
+        if kw.get("K_tail") is not None and kw["K_tail"].shape[-2] > 0:
             _tail_by_merge(run_sparse, Q3, O3, lse3, kw["K_tail"], kw["V_tail"], kw["sm_scale"])
         else:
             run_sparse(O3, lse3)
@@ -500,6 +516,14 @@ def quest_decode_turbo(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     if K_scale_raw.dtype != torch.bfloat16 or K_mn_raw.dtype != torch.bfloat16:
         raise AssertionError("K_scale_raw / K_mn_raw must be bf16")
+    H_kv = K_msb.shape[-3]
+    nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
+    if nrep > 4 and D == 128 and page_size == 64:
+        return _chunked_decode(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), H_kv, nrep, None,
+                               dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
+                                    k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
+                                    sm_scale=sm_scale, return_lse=return_lse, return_selection=return_selection,
+                                    head_pattern=head_pattern), raw=(K_scale_raw, K_mn_raw))
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
     P = K_scale_raw.shape[-2]

@@ -386,6 +386,18 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache,
                           int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                           uint8_t* mask_out, void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
+/* The selection half of fq_quest_decode_turbo (the page scores and
+ * select_pages_vectorized of llama_persistent_patch.py:196-245 on the raw K
+ * metadata), same arguments; with mask_out it writes the (L*B, H_q, P)
+ * selection and runs no attention.  Callers that attend a KV group's query
+ * heads in several calls use it to select once from all of the group's heads. */
+int fq_quest_select_turbo(const fq_turbo_cache* cache,
+                          const void* k_scale_raw, const int64_t ksr_strides[5],
+                          const void* k_mn_raw, const int64_t kmr_strides[5],
+                          const fq_query* query, const float* retention,
+                          int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
+                          uint8_t* mask_out, void* workspace, size_t workspace_bytes, fq_stream_t stream);
+
 /* ---- INT8 family (kv_bits = 8, the reference dispatcher's default) ---- */
 
 /* Workspace for the INT8 entry points (same sizing as fq_workspace_bytes). */

@@ -87,11 +87,15 @@ def _turbo_desc(S=256, P=4, D=128, Hkv=2):
                                                   ("k_scale", 4097, "FQ_ERR_UNSUPPORTED", "aligned"),
                                                   ("v_lsb", None, "FQ_ERR_INVALID", "NULL cache tensor"),
                                                   ("D", 96, "FQ_ERR_UNSUPPORTED", "head_dim"),
-                                                  ("P", 0, "FQ_ERR_UNSUPPORTED", "pages")])
+                                                  ("P", 0, "FQ_ERR_UNSUPPORTED", "pages"),
+                                                  ("P", 5, "FQ_ERR_INVALID", "tokens of page_size"),
+                                                  ("P", 9, "FQ_ERR_INVALID", "tokens of page_size")])
 def test_turbo_descriptor_checks_before_any_launch(field, value, code, msg):
     """Every TurboQuant decode entry rejects a misaligned per-token scale, a
-    missing plane, an unsupported head_dim or page count (no GPU needed: the
-    checks run before anything reaches the device)."""
+    missing plane, an unsupported head_dim or page count, including more pages
+    than the planes' tokens fill (the raw K metadata would be read past what
+    the caller wrote; no GPU needed: the checks run before anything reaches
+    the device)."""
     lib = L.lib()
     c = _turbo_desc()
     setattr(c, field, value)
@@ -101,10 +105,25 @@ def test_turbo_descriptor_checks_before_any_launch(field, value, code, msg):
     assert msg in lib.fq_last_error().decode()
     assert lib.fq_sparse_turbo_fwd_mask(c, None, None, L.i64([0, 0, 0, 1], 4), None, 0, None) == want
     assert msg in lib.fq_last_error().decode()
+    assert lib.fq_quest_select_turbo(c, 4096, z5, 4096, z5, None, None, 0, 0, -1, 0, None, None, 0, None) == want
+    assert msg in lib.fq_last_error().decode()
     # the unmodified descriptor passes the cache checks and stops at the missing query
     assert lib.fq_quest_decode_turbo(_turbo_desc(), 4096, z5, 4096, z5, None, None, 0, 0, -1, 0, None, None, 0,
                                      None) == L.FQ_ERR_INVALID
     assert msg not in lib.fq_last_error().decode()
+
+
+def test_turbo_cache_rejects_more_pages_than_its_tokens():
+    """The Python descriptor builder refuses a page count past the planes'
+    tokens (a per-token plane's length is not a page count) before any call."""
+    S, D = 64 * 3 + 10, 128
+    planes = [torch.zeros(1, 2, S, D // 8, dtype=torch.uint8), torch.zeros(1, 2, S, D // 4, dtype=torch.uint8),
+              torch.zeros(1, 2, S, 1, dtype=torch.bfloat16)] * 2
+    _ops.turbo_cache(*planes, 4, 64)
+    with pytest.raises(ValueError, match="pages"):
+        _ops.turbo_cache(*planes, 5, 64)
+    with pytest.raises(ValueError, match="pages"):
+        _ops.turbo_cache(*planes, S, 64)
 
 
 @pytest.mark.parametrize("stride,ok", [(0, True), (24, True), (48, True), (1, False), (23, False), (-24, False)])

@@ -48,7 +48,7 @@ def test_turbo_mask_attention_matches_oracle(B, Hq, Hkv):
 
 @pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
 @pytest.mark.parametrize("Hq,sinks,window,P", [(24, 3, 2, 20), (24, 0, 0, 20), (16, 9, 1, 12), (8, 4, 2, 6),
-                                              (40, 3, 2, 20), (56, 1, 1, 12)])
+                                              (40, 3, 2, 20), (56, 1, 1, 12), (64, 2, 1, 10)])
 def test_fused_turbo_decode_matches_oracle(mode, Hq, sinks, window, P):
     # 24 layers x 8 KV heads = 192 KV groups: one workgroup per group, which
     # scores and selects its pages; a second call also writes the kernel's
