@@ -174,3 +174,54 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
                 torch.cuda.current_stream(device).synchronize()
             _scalar_retention[key] = r
     return r
+
+
+# ---- GQA ratios above 4 on the matrix-core kernels ---------------------------
+# Those kernels take at most 4 query heads per KV head; a group of 5 to 8 is
+# attended in chunks of its query heads, each chunk reading the group's pages.
+
+def head_chunks(nrep: int):
+    """(offset, size) chunks of a KV group's query heads, each of at most 4
+    heads, sizes as equal as possible (8 -> 4 + 4, 7 -> 4 + 3, 5 -> 3 + 2)."""
+    n = -(-nrep // 4)
+    base, extra = divmod(nrep, n)
+    chunks, off = [], 0
+    for i in range(n):
+        size = base + (1 if i < extra else 0)
+        chunks.append((off, size))
+        off += size
+    return chunks
+
+
+def heads(x, axis: int, H_kv: int, nrep: int, off: int, size: int):
+    """The query heads [off, off + size) of every KV group of x's head axis
+    `axis` (H_kv * nrep heads, group-major), as a contiguous tensor."""
+    return x.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).flatten(axis, axis + 1).contiguous()
+
+
+def put_heads(dst, src, axis: int, H_kv: int, nrep: int, off: int, size: int):
+    """Writes src (H_kv * size heads on `axis`) back into those heads of dst."""
+    dst.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).copy_(src.unflatten(axis, (H_kv, size)))
+
+
+def wants_head_chunks(H_q: int, H_kv: int, D: int, page_size: int) -> bool:
+    """5 to 8 query heads per KV head on the matrix-core layout (head_dim 128,
+    64-token pages): chunked; other shapes take the general kernels whole."""
+    return H_q % H_kv == 0 and 4 < H_q // H_kv <= 8 and D == 128 and page_size == 64
+
+
+def attend_in_head_chunks(Q, H_kv: int, per_head, call, return_lse: bool):
+    """Q (B, H_q, 1, D); per_head (B, H_q, ...) the per-query-head selection
+    (mask or id lists); call(Q_chunk, per_head_chunk) -> (O, lse).  Returns
+    (O like Q, lse (B, H_q, 1) fp32 or None)."""
+    H_q = Q.shape[1]
+    nrep = H_q // H_kv
+    O = torch.empty_like(Q)
+    lse = torch.empty(Q.shape[0], H_q, 1, dtype=torch.float32, device=Q.device) if return_lse else None
+    for off, size in head_chunks(nrep):
+        oc, lc = call(heads(Q, 1, H_kv, nrep, off, size), heads(per_head, 1, H_kv, nrep, off, size))
+        put_heads(O, oc, 1, H_kv, nrep, off, size)
+        if lse is not None:
+            put_heads(lse, lc, 1, H_kv, nrep, off, size)
+    return O, lse
+

@@ -208,29 +208,6 @@ def quest_decode_int4(
     return O, lse_out
 
 
-def _head_chunks(nrep: int):
-    """(offset, size) chunks of a KV group's query heads, each of at most 4
-    heads (what the matrix-core kernels take), sizes as equal as possible."""
-    n = -(-nrep // 4)
-    base, extra = divmod(nrep, n)
-    chunks, off = [], 0
-    for i in range(n):
-        size = base + (1 if i < extra else 0)
-        chunks.append((off, size))
-        off += size
-    return chunks
-
-
-def _heads(x, axis, H_kv, nrep, off, size):
-    """The (H_kv, size) query heads [off, off + size) of every KV group of the
-    H_kv * nrep head axis `axis` of x, as a contiguous tensor."""
-    return x.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).flatten(axis, axis + 1).contiguous()
-
-
-def _put_heads(dst, src, axis, H_kv, nrep, off, size):
-    dst.unflatten(axis, (H_kv, nrep)).narrow(axis + 1, off, size).copy_(src.unflatten(axis, (H_kv, size)))
-
-
 def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
     """quest_decode_int4 / quest_decode_int8 / quest_decode_turbo (bits 4 / 8
     / 3; raw: TurboQuant's (K_scale_raw, K_mn_raw)) for 5 to 8 query heads per
@@ -256,21 +233,21 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
         if not torch.is_tensor(retention):
             return retention
         r = retention.to(device=Q.device, dtype=torch.float32)
-        return _heads(r, r.dim() - 1, H_kv, nrep, off, size)
+        return _ops.heads(r, r.dim() - 1, H_kv, nrep, off, size)
 
     if kw["select_mode"] == "per_q_head":
-        for off, size in _head_chunks(nrep):
+        for off, size in _ops.head_chunks(nrep):
             sub = dict(kw, retention=ret_chunk(off, size))
-            qc = _heads(Q, head_axis, H_kv, nrep, off, size)
+            qc = _ops.heads(Q, head_axis, H_kv, nrep, off, size)
             if bits == 3:
                 res = quest_decode_turbo(qc, *planes, *raw, **sub)
             else:
                 res = (quest_decode_int4 if bits == 4 else quest_decode_int8)(qc, *planes, **sub)
-            _put_heads(O, res[0], head_axis, H_kv, nrep, off, size)
+            _ops.put_heads(O, res[0], head_axis, H_kv, nrep, off, size)
             if lse is not None:
-                _put_heads(lse, res[1][..., 0], head_axis, H_kv, nrep, off, size)
+                _ops.put_heads(lse, res[1][..., 0], head_axis, H_kv, nrep, off, size)
             if mask is not None:
-                _put_heads(mask, res[2], head_axis, H_kv, nrep, off, size)
+                _ops.put_heads(mask, res[2], head_axis, H_kv, nrep, off, size)
         O_out = O
     else:
         if kw.get("K_tail") is not None and kw["K_tail"].shape[-2] > 0 and kw["return_selection"]:
@@ -306,17 +283,17 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
                 f"{name} (selection)")
 
         def run_sparse(O3, lse3):
-            for off, size in _head_chunks(nrep):
-                qc = _heads(Q3, Q3.dim() - 2, H_kv, nrep, off, size)
-                mc = _heads(sel, sel.dim() - 2, H_kv, nrep, off, size)
+            for off, size in _ops.head_chunks(nrep):
+                qc = _ops.heads(Q3, Q3.dim() - 2, H_kv, nrep, off, size)
+                mc = _ops.heads(sel, sel.dim() - 2, H_kv, nrep, off, size)
                 oc = torch.empty(qc.shape, dtype=O3.dtype, device=Q.device)
                 lc = torch.empty(qc.shape[:-1], dtype=torch.float32, device=Q.device)
                 qd = _ops.query(qc, oc, lc, kw["sm_scale"])
                 wsc = L.workspace(Q.device, ws_bytes(cache, qc.shape[-2]), stream)
                 L.check(attend(cache, qd, mc.data_ptr(), L.strides(mc, 4, 4 - mc.dim()), wsc.data_ptr(), wsc.numel(),
                                stream), f"{name} (attention)")
-                _put_heads(O3, oc, O3.dim() - 2, H_kv, nrep, off, size)
-                _put_heads(lse3, lc, lse3.dim() - 1, H_kv, nrep, off, size)
+                _ops.put_heads(O3, oc, O3.dim() - 2, H_kv, nrep, off, size)
+                _ops.put_heads(lse3, lc, lse3.dim() - 1, H_kv, nrep, off, size)
 
         O3 = O[..., 0, :]
         lse3 = lse if lse is not None else torch.empty(Q3.shape[:-1], dtype=torch.float32, device=Q.device)

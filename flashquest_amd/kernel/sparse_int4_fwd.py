@@ -72,6 +72,12 @@ def flash_attn_sparse_int4_fwd(
     num_pages = K_scale.shape[2]
     assert selection_mask.shape == (B, H_q, 1, num_pages)
     assert selection_mask.dtype == torch.bool
+    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # 5-8 query heads per KV head
+        return _ops.attend_in_head_chunks(
+            Q, H_kv, selection_mask,
+            lambda q, m: flash_attn_sparse_int4_fwd(q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
+                                                    selection_mask=m, page_size=page_size, sm_scale=sm_scale,
+                                                    return_lse=return_lse), return_lse)
     mask3 = selection_mask[:, :, 0, :]
     return _run(L.lib().fq_sparse_int4_fwd_mask, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
                 page_size, sm_scale, return_lse, mask3.data_ptr(), L.strides(mask3, 4, 1))

@@ -10,6 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib as L
+from .. import _ops
 from .sparse_int4_fwd import _check_common, _run
 
 
@@ -39,5 +40,11 @@ def flash_attn_sparse_int4_fwd_compact(
     Bs, H_qs, bucket = sel.shape
     assert Bs == B and H_qs == H_q
     L.require_device(sel)
+    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # 5-8 query heads per KV head
+        return _ops.attend_in_head_chunks(
+            Q, H_kv, sel,
+            lambda q, ids: flash_attn_sparse_int4_fwd_compact(q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
+                                                              selected_page_ids=ids, page_size=page_size,
+                                                              sm_scale=sm_scale, return_lse=return_lse), return_lse)
     return _run(L.lib().fq_sparse_int4_fwd_ids, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,
                 page_size, sm_scale, return_lse, sel.data_ptr(), L.strides(sel, 4, 1), bucket)

@@ -26,6 +26,8 @@ def _rand_mask(case, frac, rng):
     (8, 1, 128, 16, "bf16", "bf16", None),
     (4, 4, 128, 64, "f16", "bf16", None),
     (8, 2, 64, 64, "bf16", "f16", 32),
+    (16, 2, 128, 64, "f16", "f16", 32),    # 8 query heads per KV head: chunks of 4 on the matrix cores
+    (10, 2, 128, 64, "bf16", "bf16", None),  # 5: chunks of 3 + 2
 ])
 def test_mask_kernel_matches_oracle(Hq, Hkv, D, page, dtype, meta, vgroup):
     from flashquest_amd.kernel import flash_attn_sparse_int4_fwd
@@ -69,8 +71,9 @@ def test_compact_ids_match_mask_kernel_and_padding_invariance():
     # tests/test_sparse_int4_fwd_compact_parity.py:10-48, _padding.py:30-68
     from flashquest_amd.eager import build_compact_selection
     from flashquest_amd.kernel import flash_attn_sparse_int4_fwd, flash_attn_sparse_int4_fwd_compact
-    for seed in range(3):
-        case = Int4Case(seed=40 + seed, B=1, Hq=24, Hkv=8, S=64 * 32, D=128)
+    for seed in range(4):
+        Hq = 64 if seed == 3 else 24     # the last case: 8 query heads per KV head, attended in chunks
+        case = Int4Case(seed=40 + seed, B=1, Hq=Hq, Hkv=8, S=64 * 32, D=128)
         mask = to_dev(_rand_mask(case, 0.25, case.rng))[:, :, None, :]
         t = case.device()
         o_m, l_m = flash_attn_sparse_int4_fwd(case.q_dev(), **t, selection_mask=mask)
@@ -78,7 +81,7 @@ def test_compact_ids_match_mask_kernel_and_padding_invariance():
             ids = build_compact_selection(mask, bucket)
             o_c, l_c = flash_attn_sparse_int4_fwd_compact(case.q_dev(), **t, selected_page_ids=ids)
             assert torch.equal(o_c, o_m) and torch.equal(l_c, l_m)
-    sent = torch.full((1, 24, 1, 8), -1, dtype=torch.int32, device="cuda")
+    sent = torch.full((1, Hq, 1, 8), -1, dtype=torch.int32, device="cuda")
     o, lse = flash_attn_sparse_int4_fwd_compact(case.q_dev(), **t, selected_page_ids=sent)
     assert torch.all(o == 0) and torch.isneginf(lse).all()
 
