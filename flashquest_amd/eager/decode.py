@@ -541,7 +541,8 @@ class QuestDecoder:
     ``attend()`` are the two halves of fq_quest_decode_int4, ``__call__`` runs
     both.
     Every launch goes to torch's current stream, so the calls can be captured
-    in a HIP graph after one eager call has sized the workspace.
+    in a HIP graph after one eager call has sized the workspace.  With 5 to 8
+    query heads per KV head the step is quest_decode_int4's chunked one.
     """
 
     def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
@@ -553,6 +554,20 @@ class QuestDecoder:
         self.Q3 = Q[..., 0, :]
         self.O3 = torch.empty_like(self.Q3) if out is None else out[..., 0, :]
         self.lse = lse
+        self.device = Q.device
+        # 5-8 query heads per KV head: the step is quest_decode_int4's chunked
+        # one (its tensors come from the graph's pool when captured; the
+        # retention is moved to the device here, not during a capture)
+        self._chunked = None
+        if (_ops.wants_head_chunks(Q.shape[-3], K_scale.shape[-3], Q.shape[-1], page_size)
+                and rotation_signs is None and mask_out is None):
+            ret = retention.to(device=Q.device, dtype=torch.float32) if torch.is_tensor(retention) else retention
+            self._chunked = (Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn),
+                             dict(retention=ret, num_sinks=num_sinks, window_pages=window_pages,
+                                  k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
+                                  sm_scale=sm_scale, return_lse=lse is not None, K_tail=K_tail, V_tail=V_tail,
+                                  head_pattern=head_pattern))
+            return
         self.cache, self._keep = _ops.int4_cache(K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, page_size)
         self.query = _ops.query(self.Q3, self.O3, lse, sm_scale)
         H_q = self.Q3.shape[-2]
@@ -579,17 +594,27 @@ class QuestDecoder:
     def fused(self) -> bool:
         """True when attend() is the whole step: one attention kernel that scores
         and selects its own pages (select() then launches nothing)."""
+        if self._chunked is not None:
+            return False
         r = L.lib().fq_quest_fused_int4(self.cache, self.query, self.sinks, self.window, self.k_max, self.mode)
         if r < 0:
             L.check(-r, "quest fused query")
         return r == 1
 
     def select(self):
+        if self._chunked is not None:      # the chunked step selects inside attend()
+            return
         L.check(L.lib().fq_quest_select_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
                                              self.k_max, self.mode, None, L.ptr(self.mask_out), self.ws.data_ptr(),
                                              self.ws.numel(), L.stream_handle(self.device)), "quest select")
 
     def attend(self):
+        if self._chunked is not None:
+            Q, planes, kw = self._chunked
+            _, lse = quest_decode_int4(Q, *planes, out=self.O3.unsqueeze(-2), **kw)
+            if self.lse is not None:
+                self.lse.copy_(lse[..., 0])
+            return
         if self.tail is not None:      # selection (when a kernel does it), attention, tail and merge
             L.check(L.lib().fq_quest_decode_int4_tail(self.cache, self.query, self.tail, self.r.data_ptr(),
                                                       self.sinks, self.window, self.k_max, self.mode,
@@ -601,7 +626,7 @@ class QuestDecoder:
                                              L.stream_handle(self.device)), "quest attend")
 
     def __call__(self):
-        if self.tail is None:
+        if self._chunked is None and self.tail is None:
             self.select()
         self.attend()
         return self.O3.unsqueeze(-2)

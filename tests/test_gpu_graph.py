@@ -33,11 +33,14 @@ def _capture(calls):
     return graph
 
 
-@pytest.mark.parametrize("per_layer,mode,tail", [(True, "per_kv_head_sum", 0), (True, "per_q_head", 37),
-                                                 (False, "per_kv_head_sum", 0), (False, "per_q_head", 21)])
-def test_graph_replays_equal_the_eager_step(per_layer, mode, tail):
+@pytest.mark.parametrize("per_layer,mode,tail,Hq", [(True, "per_kv_head_sum", 0, 24), (True, "per_q_head", 37, 24),
+                                                    (False, "per_kv_head_sum", 0, 24), (False, "per_q_head", 21, 24),
+                                                    (True, "per_q_head", 0, 64), (False, "per_kv_head_sum", 0, 64),
+                                                    (True, "per_kv_head_sum", 30, 64)])
+def test_graph_replays_equal_the_eager_step(per_layer, mode, tail, Hq):
+    """Hq = 64 (8 query heads per KV head): the chunked step, captured."""
     from flashquest_amd.eager.decode import QuestDecoder, quest_decode_int4
-    layers, Hq, Hkv, P = 6, 24, 8, 40
+    layers, Hkv, P = 6, 8, 40
     cases = [Int4Case(seed=300 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, dtype="f16", meta="f16", vgroup=32)
              for i in range(layers)]
     dev = [c.device() for c in cases]
