@@ -562,6 +562,15 @@ def main():
         alt = decoder(args.retention, k, other)
         alt_ms, _, _ = time_steps(noop, alt, args.steps, args.warmup, flush)
         extra[f"{other}_us"] = alt_ms * 1e3
+        # 8 query heads per KV head (64 query / 8 KV heads, the Llama-3-70B
+        # layout) on otherwise the same synthetic layers: the query heads of a
+        # group in two chunks of 4 on the matrix-core kernels
+        c8 = make_cache(L, B, Hq=64, P=P, dev=dev)
+        for mode in ("per_kv_head_sum", "per_q_head"):
+            d8 = decoder(args.retention, k, mode, c=c8)
+            ms8, _, _ = time_steps(noop, d8, args.steps, args.warmup, flush)
+            extra[f"gqa8_{mode}_us"] = ms8 * 1e3
+        del c8, d8
         # the reference's per-layer call pattern: 28 sequential (select, attend) pairs in one HIP graph
         per_layer = [decoder(args.retention, k, args.select,
                              c={key: t[l] for key, t in cache.items()}) for l in range(L)]
