@@ -206,8 +206,13 @@ def put_heads(dst, src, axis: int, H_kv: int, nrep: int, off: int, size: int):
 
 def wants_head_chunks(H_q: int, H_kv: int, D: int, page_size: int) -> bool:
     """5 to 8 query heads per KV head on the matrix-core layout (head_dim 128,
-    64-token pages): chunked; other shapes take the general kernels whole."""
-    return H_q % H_kv == 0 and 4 < H_q // H_kv <= 8 and D == 128 and page_size == 64
+    64-token pages), and more than 8 on any layout (the library's kernels take
+    at most 8: one selection bit per query head of a group): chunked.  Other
+    shapes take their kernels whole."""
+    if H_kv < 1 or H_q % H_kv:
+        return False
+    nrep = H_q // H_kv
+    return nrep > 8 or (nrep > 4 and D == 128 and page_size == 64)
 
 
 def attend_in_head_chunks(Q, H_kv: int, per_head, call, return_lse: bool):

@@ -151,7 +151,7 @@ def quest_decode_int4(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if nrep > 4 and D == 128 and page_size == 64 and _rotation is None:
+    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None:
         return _chunked_decode(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), H_kv, nrep, out,
                                     dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                          k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
@@ -250,6 +250,9 @@ def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
                 _ops.put_heads(mask, res[2], head_axis, H_kv, nrep, off, size)
         O_out = O
     else:
+        if nrep > 8:
+            raise NotImplementedError(f"per_kv_head_sum selects from one mask bit per query head of a KV group: "
+                                      f"at most 8 query heads per KV head, got {nrep} (per_q_head takes any ratio)")
         if kw.get("K_tail") is not None and kw["K_tail"].shape[-2] > 0 and kw["return_selection"]:
             raise ValueError("return_selection is not available together with a fused tail")
         Q3 = Q[..., 0, :]
@@ -400,7 +403,7 @@ def quest_decode_int8(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if nrep > 4 and D == 128 and page_size == 64:
+    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size):
         return _chunked_decode(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), H_kv, nrep, None,
                                dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                     k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
@@ -495,7 +498,7 @@ def quest_decode_turbo(
         raise AssertionError("K_scale_raw / K_mn_raw must be bf16")
     H_kv = K_msb.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if nrep > 4 and D == 128 and page_size == 64:
+    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size):
         return _chunked_decode(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), H_kv, nrep, None,
                                dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                     k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,

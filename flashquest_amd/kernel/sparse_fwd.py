@@ -55,7 +55,7 @@ def flash_attn_sparse_fwd(
     num_pages = K_scale.shape[2]
     assert selection_mask.shape == (B, H_q, 1, num_pages)
     assert selection_mask.dtype == torch.bool
-    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # 5-8 query heads per KV head
+    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # more than 4 query heads per KV head
         return _ops.attend_in_head_chunks(
             Q, H_kv, selection_mask,
             lambda q, m: flash_attn_sparse_fwd(q, K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn, selection_mask=m,

@@ -40,7 +40,7 @@ def flash_attn_sparse_int4_fwd_compact(
     Bs, H_qs, bucket = sel.shape
     assert Bs == B and H_qs == H_q
     L.require_device(sel)
-    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # 5-8 query heads per KV head
+    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # more than 4 query heads per KV head
         return _ops.attend_in_head_chunks(
             Q, H_kv, sel,
             lambda q, ids: flash_attn_sparse_int4_fwd_compact(q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn,

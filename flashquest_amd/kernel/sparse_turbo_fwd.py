@@ -47,7 +47,7 @@ def flash_attn_sparse_turbo_fwd(
     assert selection_mask.shape == (B, H_q, 1, num_pages)
     assert selection_mask.dtype == torch.bool
     assert K_scale_turbo.dtype == torch.bfloat16 and V_scale_turbo.dtype == torch.bfloat16
-    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # 5-8 query heads per KV head
+    if _ops.wants_head_chunks(H_q, H_kv, D, page_size):      # more than 4 query heads per KV head
         return _ops.attend_in_head_chunks(
             Q, H_kv, selection_mask,
             lambda q, m: flash_attn_sparse_turbo_fwd(q, K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo,
