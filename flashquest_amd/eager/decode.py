@@ -210,15 +210,17 @@ def quest_decode_int4(
 
 def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
     """quest_decode_int4 / quest_decode_int8 / quest_decode_turbo (bits 4 / 8
-    / 3; raw: TurboQuant's (K_scale_raw, K_mn_raw)) for 5 to 8 query heads per
-    KV head (the reference's kernels take any ratio, sparse_int4_fwd.py:54-55,
-    sparse_turbo_fwd.py): the group's query heads
-    in chunks of at most 4, each on the matrix-core kernels.  per_q_head
-    selects every head on its own, so each chunk is an ordinary step over its
-    heads.  per_kv_head_sum selects once per KV group from all of its heads
-    (one selection pass over the whole query, its mask kept), then each chunk
-    attends the group's pages through the mask entry.  A partial-page tail is
-    merged as the reference does (llama_persistent_patch.py:232-245)."""
+    / 3; raw: TurboQuant's (K_scale_raw, K_mn_raw)) for more than 4 query
+    heads per KV head (the reference's kernels take any ratio,
+    sparse_int4_fwd.py:54-55, sparse_turbo_fwd.py): the group's query heads in
+    chunks of at most 4, each on the matrix-core kernels where the layout
+    allows (head_dim 128, 64-token pages).  per_q_head selects every head on
+    its own, so each chunk is an ordinary step over its heads (any ratio).
+    per_kv_head_sum selects once per KV group from all of its heads (one
+    selection pass over the whole query, its mask kept; at most 8 heads, one
+    mask bit each), then each chunk attends the group's pages through the
+    mask entry.  A partial-page tail is merged as the reference does
+    (llama_persistent_patch.py:232-245)."""
     head_axis = Q.dim() - 3
     # pages: K_scale (..., P, D) for INT4 / INT8; TurboQuant's planes are per
     # token, its page count is the raw K metadata's (..., P, D)
