@@ -136,10 +136,14 @@ FQ_DEV void load_page(PageBuf& b, const SliceRsrc& r, int koff, int voff, int mo
 // FUSED (8 waves only): the workgroup scores and selects its group's pages
 // itself (a.sel) and attends split `split` of the list; otherwise the pages
 // come from the workspace lists.
-template <typename MT, int G, int NREP, int NW, bool FUSED>
+//
+// HCH (FUSED only): head chunks, sel.head_chunks virtual KV heads per cache
+// KV head (a separate instantiation, so the other kernels are unchanged).
+template <typename MT, int G, int NREP, int NW, bool FUSED, bool HCH = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int4_mfma_kernel(MfmaParams a) {
     static_assert(!FUSED || NW == 8, "in-kernel selection runs in the 8-wave kernel");
+    static_assert(!HCH || FUSED, "head chunks run in the fused kernel");
     constexpr int D = 128;
     constexpr int NT = 64 * NW;
     constexpr int NSLOT = FUSED ? NW + 1 : NW;      // the fused kernel's extra slot: the partial-page tail
@@ -157,6 +161,15 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     const int g = (gridDim.x == 1 && GY % 8 == 0) ? (gy % 8) * (GY / 8) + gy / 8 : gy;
     const int split = blockIdx.x;
     const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
+    // Head chunks (FUSED, sel.head_chunks = HC > 1): the launch sees HC
+    // virtual KV heads per KV head of the cache, each with NREP of its query
+    // heads (virtual head h = cache head hk * HC + chunk); q, the outputs and
+    // the retention follow h, the cache pages follow hk.  per_kv_head_sum
+    // (chunk_sum) then scores the summed query of all HC * NREP heads of the
+    // cache head, so every chunk selects the same pages.
+    const int HC = HCH ? a.sel.head_chunks : 1;
+    const int hk = HCH ? h / HC : h;
+    const bool chunk_sum = HCH && a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM;
     const int L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
     const int n16 = L & 15, lg = L >> 4;
     WaveLds& W = s_wave[w];
@@ -169,10 +182,15 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // pages and wave 0 selects them.
     constexpr int kEntPer = kMaxWgPages / NT;
     static_assert(kMaxWgPages % NT == 0 && NREP * D <= 2 * NT, "prologue sizes");
+    static_assert(!FUSED || 2 * NREP * D <= 2 * NT, "chunk_sum prologue sizes");
     __shared__ float s_q[NREP][D];
     const int tid = threadIdx.x;
-    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
-    const int i0 = min(tid, NREP * D - 1), i1 = min(tid + NT, NREP * D - 1);
+    // chunk_sum: the prologue loads all 2 NREP heads of the cache head (rows
+    // chunk * NREP .. are this workgroup's own)
+    const int q_rows = chunk_sum ? 2 * NREP : NREP;
+    const int q_row0 = chunk_sum ? (h - hk * HC) * NREP : 0;
+    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)(chunk_sum ? hk * 2 * NREP : h * NREP) * q.q_s[2];
+    const int i0 = min(tid, q_rows * D - 1), i1 = min(tid + NT, q_rows * D - 1);
     // q (raw bits) and the retention go out first, then, in the fused decode,
     // the group's K metadata loads for scoring: loads complete in order, so q
     // can be used while the metadata is still in flight.
@@ -199,7 +217,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     // Needs 16-bit q with unit channel stride and 16-byte aligned rows; other
     // layouts (q_fast false: an empty buffer, the loads read 0) go through LDS.
     uint4 qsr[NREP];
-    const bool q_fast = FUSED && !q32 && !q.rot && q.q_s[3] == 1 && (q.q_s[2] & 7) == 0 &&
+    const bool q_fast = FUSED && !chunk_sum && !q32 && !q.rot && q.q_s[3] == 1 && (q.q_s[2] & 7) == 0 &&
                         (((uintptr_t)q.q + 2 * (uint64_t)qb) & 15) == 0;
     if constexpr (FUSED) {
         const auto rq = make_rsrc((const char*)q.q + 2 * qb, q_fast ? 2 * ((int64_t)(NREP - 1) * q.q_s[2] + D) : 0);
@@ -230,10 +248,13 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     uint4 tkr[2], tvr[2];
     const int tail_T = FUSED && a.tail.in_kernel && split == 0 ? a.tail.len : 0;   // split 0 of a group attends it
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
+        if (chunk_sum)      // uniform: the k of the summed row is the cache head's largest retention
+            ret_l = wave_max(a.sel.retention[l * q.ret_ls + hk * 2 * NREP + min(L, 2 * NREP - 1)]);
+        else
+            ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         const TailArgs& t = a.tail;
-        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + h * t.ks[2]) : nullptr;
-        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + h * t.vs[2]) : nullptr;
+        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + hk * t.ks[2]) : nullptr;
+        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + hk * t.vs[2]) : nullptr;
         const auto rk = make_rsrc(tkb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.ks[3] + 2 * D : 0);
         const auto rv = make_rsrc(tvb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.vs[3] + 2 * D : 0);
 #pragma unroll
@@ -243,7 +264,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
         }
         if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
-        else score_group_load<MT, NT>(sr, c, tid, l, b, h);
+        else score_group_load<MT, NT>(sr, c, tid, l, b, hk);
     }
     const bool qbf = q.q_dtype == FQ_BF16;
     auto q_float = [&](uint32_t u) {
@@ -253,12 +274,12 @@ void attn_int4_mfma_kernel(MfmaParams a) {
     const float v0 = q_float((l0 & ~hi_mask) | ((h0 << 16) & hi_mask));
     const float v1 = q_float((l1 & ~hi_mask) | ((h1 << 16) & hi_mask));
 
-    const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2];
-    const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2];
-    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2];
-    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2];
-    const uint16_t* vsc = (const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2];
-    const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2];
+    const uint8_t* kb = c.kp + l * c.kp_s[0] + b * c.kp_s[1] + hk * c.kp_s[2];
+    const uint8_t* vb = c.vp + l * c.vp_s[0] + b * c.vp_s[1] + hk * c.vp_s[2];
+    const MT* ksc = (const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + hk * c.ksc_s[2];
+    const MT* kmn = (const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + hk * c.kmn_s[2];
+    const uint16_t* vsc = (const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + hk * c.vsc_s[2];
+    const uint16_t* vmn = (const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + hk * c.vmn_s[2];
 
     // A-operand slot of this lane for the q.k digits: k-step qs_s, k-group qs_kg,
     // operand dword qs_jd; channels ch_base + 2b + par (b = 0..3); heads r0, r0+1.
@@ -291,17 +312,27 @@ void attn_int4_mfma_kernel(MfmaParams a) {
         // (the arithmetic of score_kernel), keep the scores in LDS, select.
         // The forced pages (always selected, first in the entry list) are
         // loaded while the selection runs.
-        __shared__ float s_qraw[NREP][D];
+        __shared__ float s_qraw[HCH ? 2 * NREP : NREP][D];      // chunk_sum: every head of the cache head
         __shared__ uint32_t s_key[NREP * 64 * kSelC];
         __shared__ BlockSelectLds s_bsel;
         e0 = 0;
         {
-            if (tid < NREP * D) {
-                s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+            if (tid < q_rows * D) {
+                if constexpr (HCH) {
+                    const int r = (i0 >> 7) - q_row0;
+                    if ((unsigned)r < (unsigned)NREP) s_q[r][i0 & 127] = v0 * q.qk_scale;
+                } else {
+                    s_q[i0 >> 7][i0 & 127] = v0 * q.qk_scale;
+                }
                 s_qraw[i0 >> 7][i0 & 127] = v0;
             }
-            if (tid + NT < NREP * D) {
-                s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+            if (tid + NT < q_rows * D) {
+                if constexpr (HCH) {
+                    const int r = (i1 >> 7) - q_row0;
+                    if ((unsigned)r < (unsigned)NREP) s_q[r][i1 & 127] = v1 * q.qk_scale;
+                } else {
+                    s_q[i1 >> 7][i1 & 127] = v1 * q.qk_scale;
+                }
                 s_qraw[i1 >> 7][i1 & 127] = v1;
             }
 #pragma unroll
@@ -342,7 +373,10 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                     }
                     __syncthreads();
                 }
-                if (sum) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+                if constexpr (HCH) {
+                    if (chunk_sum) score_group_regs<MT, 2 * NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+                    else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
+                } else if (sum) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
                 else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
             }
             const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
@@ -705,7 +739,11 @@ hipError_t launch_mfma_nrep(const MfmaParams& a, dim3 grid, hipStream_t st) {
 #define FQ_CASE(N)                                                                                     \
     case N:                                                                                            \
         timer_before_launch(st);                                                                       \
-        hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
+        if (FUSED && (N == 3 || N == 4) && a.sel.head_chunks > 1)                                      \
+            hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED, FUSED && N >= 3>), grid,       \
+                               dim3(64 * NW), 0, st, a);                                               \
+        else                                                                                           \
+            hipLaunchKernelGGL((attn_int4_mfma_kernel<MT, G, N, NW, FUSED>), grid, dim3(64 * NW), 0, st, a); \
         timer_after_launch(st);                                                                        \
         if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                     \
             launch_split_merge<N, false>(a.q, a.ws, a.c.Hkv, a.c.B, grid.y, a.splits,                  \
@@ -770,6 +808,14 @@ bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLau
            attention_splits_request() <= 0;
 }
 
+bool mfma_tail_in_kernel(const TailArgs& t) {
+    const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
+    auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
+    return t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 && t.vs[3] >= 128 &&
+           ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
+           2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
+}
+
 hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const Workspace& ws, const AttnLaunch& al,
                                  hipStream_t st, const SelectArgs* sel, const TailArgs* tail) {
     MfmaParams a{};
@@ -786,12 +832,11 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
         // least D apart): with one workgroup per group no merge launch follows,
         // with several, split 0 folds it into its partial and the merge has no
         // tail work left
-        const TailArgs& t = a.tail;
-        const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
-        auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
-        a.tail.in_kernel = t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 &&
-                           t.vs[3] >= 128 && ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
-                           2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
+        a.tail.in_kernel = mfma_tail_in_kernel(a.tail);
+        // head chunks: each chunk a workgroup of its own, never a split step
+        if (a.sel.head_chunks > 1 && (a.splits != 1 || a.sel.enabled != kScoreSelect ||
+                                      (a.tail.len > 0 && !a.tail.in_kernel)))
+            return hipErrorInvalidValue;
     }
     dim3 grid(a.splits, groups);
 #define FQ_W(MT_, G_)                                                                       \

@@ -415,8 +415,12 @@ static int quest_bound(const Int4Cache& c, const QueryArgs& q, int num_sinks, in
 // The fused decode's attention kernel scores and selects its own pages when it
 // takes a whole KV group per workgroup; fq_quest_select_int4 then launches
 // nothing unless the caller asks for the scores or the mask.
-static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, int num_sinks, int window_pages,
+static int int4_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
+                            int s_max, const TailArgs* tail);
+
+static bool decode_selects_in_attention(Int4Cache c, QueryArgs q, int num_sinks, int window_pages,
                                         int k_max, int select_mode, const Workspace& ws) {
+    int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, nullptr);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
     return attn_selects_in_kernel(c, q, al);
@@ -428,6 +432,29 @@ static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, 
 // each re-scoring the group's pages.  INT4 and INT8, unrotated.
 static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q, int bound) {
     return c.L * c.B * c.Hkv < 192 && !q.rot && bound > kFusedSmallPages;
+}
+
+// 6 or 8 query heads per KV head on the INT4 matrix-core decode, whose
+// workgroups take at most 4: when the step is one launch of whole-group
+// workgroups, every KV head of the cache becomes 2 virtual KV heads of 3 or 4
+// query heads, one workgroup each, both reading the same cache head (the
+// kernel maps them back; per_kv_head_sum scores the summed query of all the
+// head's queries in each, so both take the same pages).  Rewrites c / q to
+// the virtual heads and returns the chunk count, or 1 with c / q untouched.
+static int int4_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
+                            int s_max, const TailArgs* tail) {
+    if (c.bits != 4 || q.rot || (q.nrep != 6 && q.nrep != 8)) return 1;
+    if (tail && tail->len > 0 && !mfma_tail_in_kernel(*tail)) return 1;
+    Int4Cache c2 = c;
+    QueryArgs q2 = q;
+    c2.Hkv *= 2;
+    q2.nrep /= 2;
+    const int bound = quest_bound(c2, q2, num_sinks, window_pages, k_max, select_mode);
+    const AttnLaunch al = choose_split(c2.L * c2.B * c2.Hkv, bound, s_max);
+    if (!attn_selects_in_kernel(c2, q2, al) || attend_from_scores(c2, q2, al.max_entries)) return 1;
+    c = c2;
+    q = q2;
+    return 2;
 }
 
 static int quest_select(const fq_int4_cache* cache, const fq_query* query, const float* retention,
@@ -487,6 +514,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     if (num_sinks < 0) num_sinks = 0;
     if (window_pages < 0) window_pages = 0;
     if (k_max > c.P) k_max = c.P;
+    const int chunks = int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, tail);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
     if (tail && tail->len > 0 && !(bits == 8 ? int8_mfma_supported(c, q, al) : mfma_supported(c, q, al)))
@@ -498,6 +526,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.mask_out = mask_out;
         sel.enabled = attend_from_scores(c, q, al.max_entries) ? kSelectOnly : kScoreSelect;
+        sel.head_chunks = chunks;
     }
     return hip_status(launch_attn_int4(c, q, ws, al, (hipStream_t)stream, &sel, tail),
                       bits == 8 ? "sparse int8 attention" : "sparse int4 attention");
@@ -567,6 +596,7 @@ int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32
     if (num_sinks < 0) num_sinks = 0;
     if (window_pages < 0) window_pages = 0;
     if (k_max > c.P) k_max = c.P;
+    int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, s_max_for(c.P), nullptr);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max, select_mode),
                                        s_max_for(c.P));
     return attn_selects_in_kernel(c, q, al) ? 1 : 0;

@@ -235,6 +235,7 @@ struct SelectArgs {
     int num_sinks, window, k_max, mode;
     int enabled;
     uint8_t* mask_out;      // fused kernels: the selection as (L, B, H_q, P) bool rows, or null
+    int head_chunks;        // INT4 fused kernel: virtual KV heads per cache KV head (0 or 1: none)
 };
 
 struct AttnLaunch {
@@ -315,6 +316,9 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
                                  hipStream_t st, const SelectArgs* sel, const TailArgs* tail = nullptr);
 bool mfma_supported(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
 bool mfma_select_in_kernel(const Int4Cache& c, const QueryArgs& q, const AttnLaunch& al);
+// The fused INT4 kernel attends a 16-bit partial-page tail itself (16-byte
+// aligned rows at least D apart).
+bool mfma_tail_in_kernel(const TailArgs& t);
 // Page summary scores over the INT8 cache (summary.hip).
 struct SummaryArgs {
     const uint8_t* codes; int64_t c_s[4];          // (B, H_kv, S, D) bytes

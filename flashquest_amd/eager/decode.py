@@ -151,7 +151,9 @@ def quest_decode_int4(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None:
+    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None
+            and not _int4_one_launch(Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), nrep, page_size,
+                                     select_mode, num_sinks, window_pages, k_max_static)):
         return _chunked_decode(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), H_kv, nrep, out,
                                     dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                          k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
@@ -206,6 +208,21 @@ def quest_decode_int4(
     if return_selection:
         return O, lse_out, mask
     return O, lse_out
+
+
+def _int4_one_launch(Q, planes, nrep, page_size, select_mode, num_sinks, window_pages, k_max_static):
+    """True when fq_quest_decode_int4 takes a step of 6 or 8 query heads per
+    KV head as one launch itself: with enough KV groups the library runs every
+    KV head as two virtual heads of 3 or 4 query heads, one workgroup each."""
+    if nrep not in (6, 8):
+        return False
+    cache, keep = _ops.int4_cache(*planes, page_size)
+    Q3 = Q[..., 0, :]
+    probe = _ops.query(Q3, Q3, None, None)
+    P = planes[1].shape[-2]
+    k_max = -1 if k_max_static is None else min(int(k_max_static), P)
+    return L.lib().fq_quest_fused_int4(cache, probe, int(num_sinks), int(window_pages), k_max,
+                                       L.SELECT_MODES[select_mode]) == 1
 
 
 def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
@@ -546,8 +563,10 @@ class QuestDecoder:
     ``attend()`` are the two halves of fq_quest_decode_int4, ``__call__`` runs
     both.
     Every launch goes to torch's current stream, so the calls can be captured
-    in a HIP graph after one eager call has sized the workspace.  With 5 to 8
-    query heads per KV head the step is quest_decode_int4's chunked one.
+    in a HIP graph after one eager call has sized the workspace.  With more
+    than 4 query heads per KV head the step is quest_decode_int4's chunked
+    one, unless the library takes it as one launch (6 or 8 query heads per KV
+    head, enough KV groups to fill the GPU).
     """
 
     def __init__(self, Q, K_packed, K_scale, K_mn, V_packed, V_scale, V_mn, *, retention, num_sinks=4,
@@ -560,14 +579,20 @@ class QuestDecoder:
         self.O3 = torch.empty_like(self.Q3) if out is None else out[..., 0, :]
         self.lse = lse
         self.device = Q.device
-        # 5-8 query heads per KV head: the step is quest_decode_int4's chunked
-        # one (its tensors come from the graph's pool when captured; the
-        # retention is moved to the device here, not during a capture)
+        # more than 4 query heads per KV head, not one launch in the library:
+        # the step is quest_decode_int4's chunked one (its tensors come from
+        # the graph's pool when captured; the retention is moved to the device
+        # here, not during a capture)
         self._chunked = None
-        if (_ops.wants_head_chunks(Q.shape[-3], K_scale.shape[-3], Q.shape[-1], page_size)
-                and rotation_signs is None and mask_out is None):
+        H_kv = K_scale.shape[-3]
+        nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
+        planes = (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn)
+        if (_ops.wants_head_chunks(Q.shape[-3], H_kv, Q.shape[-1], page_size)
+                and rotation_signs is None and mask_out is None
+                and not _int4_one_launch(Q, planes, nrep, page_size, select_mode, num_sinks, window_pages,
+                                         k_max_static)):
             ret = retention.to(device=Q.device, dtype=torch.float32) if torch.is_tensor(retention) else retention
-            self._chunked = (Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn),
+            self._chunked = (Q, planes,
                              dict(retention=ret, num_sinks=num_sinks, window_pages=window_pages,
                                   k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
                                   sm_scale=sm_scale, return_lse=lse is not None, K_tail=K_tail, V_tail=V_tail,

@@ -122,6 +122,8 @@ def fp64_selection_check(q, K_scale, K_mn, got_rows, retention, mode, num_sinks=
     got = np.asarray(got_rows)[0].reshape(Hkv, rep, P)
     if mode == "per_kv_head_sum":
         s, a, got = s.sum(1, keepdims=True), a.sum(1, keepdims=True), got[:, :1]
+        if not np.isscalar(retention):      # a KV head's k: the largest retention of its query heads
+            retention = np.asarray(retention, np.float32).reshape(Hkv, rep).max(1)
     s, a, got = s.reshape(-1, P), a.reshape(-1, P), got.reshape(-1, P)
     tau = (D + 16) * 2.0 ** -24 * a
     nrow = s.shape[0]

@@ -85,7 +85,9 @@ def _oracle_mask(q, planes, retention, mode):
     rep = Hq // Hkv
     if mode == "per_q_head":
         return O.select_pages_vectorized(scores[:, :, None, :], retention, 4, 2)[:, :, 0, :]
-    m = O.select_pages_vectorized(scores[:, :, None, :], retention, 4, 2)[:, :, 0, :]
+    # one row per KV head: its k from the largest retention of its query heads
+    r_kv = retention if np.isscalar(retention) else np.asarray(retention, np.float32).reshape(Hkv, rep).max(1)
+    m = O.select_pages_vectorized(scores[:, :, None, :], r_kv, 4, 2)[:, :, 0, :]
     return np.repeat(m, rep, axis=1)
 
 
@@ -176,6 +178,37 @@ def test_config1_retention_per_head(cfg1):
     r = np.array([0.25, 0.1, 0.4] * 8, np.float32)
     _, rec = _check_step(cfg1, r, "per_q_head", sample=[(3, 0)], mask_sample=[(l, 0) for l in range(0, LAYERS, 3)])
     _report("config1 per-head retention", **rec)
+
+
+@pytest.fixture(scope="module", params=[64, 48], ids=["gqa8", "gqa6"])
+def cfg1_wide(request):
+    """Config 1's caches with 8 or 6 query heads per KV head (64 / 48 heads)."""
+    return bench.make_cache(LAYERS, 1, Hq=request.param, P=P, dev=torch.device("cuda:0"))
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_config1_geometry_wide_gqa_one_launch(cfg1_wide, mode):
+    """6 and 8 query heads per KV head at config 1's geometry take one launch:
+    every KV head runs as two virtual heads of 3 or 4 query heads, one
+    workgroup each reading the same cache head; per_kv_head_sum scores the
+    sum of all the head's queries in both, so both select the same pages."""
+    mask, rec = _check_step(cfg1_wide, 0.25, mode, sample=[(0, 0), (27, 0)],
+                            mask_sample=[(0, 0), (13, 0), (27, 0)])
+    _report(f"config1 geometry, {cfg1_wide['Q'].shape[2]} query heads, {mode}", **rec)
+    nrep = cfg1_wide["Q"].shape[2] // 8
+    per_head = mask.view(LAYERS, 1, 8, nrep, P).sum(-1)
+    assert int(per_head.min()) >= 128 and int(per_head.max()) <= 134
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_config1_geometry_wide_gqa_retention_per_head(cfg1_wide, mode):
+    """Per-head retentions whose largest value falls in either half of a KV
+    head's query heads: per_kv_head_sum takes k from the largest retention of
+    all the head's queries, not of its own virtual head's."""
+    Hq = cfg1_wide["Q"].shape[2]
+    r = np.random.default_rng(Hq).uniform(0.05, 0.3, Hq).astype(np.float32)
+    _, rec = _check_step(cfg1_wide, r, mode, sample=[(2, 0)], mask_sample=[(l, 0) for l in range(0, LAYERS, 7)])
+    _report(f"config1 geometry, {Hq} query heads, per-head retention, {mode}", **rec)
 
 
 def test_config3_rotated_step():
