@@ -129,6 +129,7 @@ SIGNATURES = {
     "fq_quest_decode_int8_tail": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), ctypes.POINTER(Tail),
                                                  _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "fq_quest_fused_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
+    "fq_quest_fused_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
     "fq_quest_attend_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, ctypes.c_size_t, _P]),
     "fq_merge_attn": (ctypes.c_int, [_P, _P, _P, _P, _I, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, _P,

@@ -101,11 +101,18 @@ FQ_DEV void load_half(HalfBuf& b, const Int8Rsrc& r, int p, int hp, int n16, int
     b.km = ld64(r.km, p * 256 + 8 * (L & 31));
 }
 
-template <typename MT, int NREP, bool FUSED>
+// HCH (FUSED only): head chunks, sel.head_chunks virtual KV heads per cache KV
+// head (virtual head h = cache head hk * HC + chunk, NREP query heads each; q,
+// outputs and retention follow h, the cache pages hk).  per_kv_head_sum then
+// scores the summed query of all 2 NREP heads of the cache head, so every
+// chunk selects the same pages.  The chunks of a cache head are mapped to one
+// XCD so that the second one's page reads hit that XCD's L2.
+template <typename MT, int NREP, bool FUSED, bool HCH = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_int8_mfma_kernel(Int8Params a) {
     constexpr int D = 128, NW = 8, NT = 512;
     static_assert(NREP <= 4, "query heads per KV head");
+    static_assert(!HCH || FUSED, "head chunks run in the fused kernel");
     constexpr int NSLOT = FUSED ? NW + 1 : NW;      // the fused kernel's extra slot: the partial-page tail
     constexpr int TTOK = FUSED ? kTailMax : 1;
     __shared__ SplitLds<D, NREP, NSLOT> s_split;
@@ -115,8 +122,14 @@ void attn_int8_mfma_kernel(Int8Params a) {
 
     const Int4Cache& c = a.c;
     const QueryArgs& q = a.q;
-    const int g = blockIdx.y, split = blockIdx.x;
+    const int gy = blockIdx.y, GY = gridDim.y, split = blockIdx.x;
+    // head chunks: workgroup index i takes group (i % 8) * (G / 8) + i / 8, so
+    // consecutive groups (the chunks of one cache head) share an XCD
+    const int g = (HCH && gridDim.x == 1 && GY % 8 == 0) ? (gy % 8) * (GY / 8) + gy / 8 : gy;
     const int h = g % c.Hkv, b = (g / c.Hkv) % c.B, l = g / (c.Hkv * c.B);
+    const int HC = HCH ? a.sel.head_chunks : 1;
+    const int hk = HCH ? h / HC : h;
+    const bool chunk_sum = HCH && a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM;
     const int tid = threadIdx.x, L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
     const int n16 = L & 15, lg = L >> 4;
     WaveLds8& W = s_wave[w];
@@ -124,17 +137,27 @@ void attn_int8_mfma_kernel(Int8Params a) {
 
     // q: element tid of the group's heads, two branch-free 16-bit loads (the
     // high one used only for fp32 q), issued before the metadata loads
-    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
-    const int qi = min(tid, NREP * D - 1);
+    // chunk_sum: all 2 NREP heads of the cache head (two elements per
+    // thread; rows chunk * NREP .. are this workgroup's own)
+    const int q_rows = chunk_sum ? 2 * NREP : NREP;
+    const int q_row0 = chunk_sum ? (h - hk * HC) * NREP : 0;
+    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)(chunk_sum ? hk * 2 * NREP : h * NREP) * q.q_s[2];
+    const int qi = min(tid, q_rows * D - 1);
+    const int qi1 = min(tid + NT, q_rows * D - 1);
     const bool q32 = q.q_dtype == FQ_F32;
     const int esz = q32 ? 4 : 2;
     uint32_t hi_mask = (0u - (uint32_t)q32) & 0xFFFF0000u;
     asm volatile("" : "+s"(hi_mask));
-    uint32_t ql, qh;
+    uint32_t ql, qh, ql1 = 0u, qh1 = 0u;
     {
         const char* qc = (const char*)q.q + (qb + (qi >> 7) * q.q_s[2] + (qi & 127) * q.q_s[3]) * esz;
         ql = *(const uint16_t*)qc;
         qh = *(const uint16_t*)(qc + esz - 2);
+        if constexpr (HCH) {
+            const char* qc1 = (const char*)q.q + (qb + (qi1 >> 7) * q.q_s[2] + (qi1 & 127) * q.q_s[3]) * esz;
+            ql1 = *(const uint16_t*)qc1;
+            qh1 = *(const uint16_t*)(qc1 + esz - 2);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     float ret_l = 0.f;
@@ -150,10 +173,13 @@ void attn_int8_mfma_kernel(Int8Params a) {
     uint4 tkr[2], tvr[2];
     const int tail_T = FUSED && a.tail.in_kernel && split == 0 ? a.tail.len : 0;
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
+        if (chunk_sum)      // uniform: the k of the summed row is the cache head's largest retention
+            ret_l = wave_max(a.sel.retention[l * q.ret_ls + hk * 2 * NREP + min(L, 2 * NREP - 1)]);
+        else
+            ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         const TailArgs& t = a.tail;
-        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + h * t.ks[2]) : nullptr;
-        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + h * t.vs[2]) : nullptr;
+        const char* tkb = tail_T > 0 ? (const char*)t.k + 2 * (l * t.ks[0] + b * t.ks[1] + hk * t.ks[2]) : nullptr;
+        const char* tvb = tail_T > 0 ? (const char*)t.v + 2 * (l * t.vs[0] + b * t.vs[1] + hk * t.vs[2]) : nullptr;
         const auto rk = make_rsrc(tkb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.ks[3] + 2 * D : 0);
         const auto rv = make_rsrc(tvb, tail_T > 0 ? 2 * (int64_t)(tail_T - 1) * t.vs[3] + 2 * D : 0);
 #pragma unroll
@@ -163,22 +189,22 @@ void attn_int8_mfma_kernel(Int8Params a) {
             tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
         }
         if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
-        else score_group_load<MT, NT>(sr, c, tid, l, b, h);
+        else score_group_load<MT, NT>(sr, c, tid, l, b, hk);
     }
-    float qv_raw;
-    {
-        const uint32_t u = (ql & ~hi_mask) | ((qh << 16) & hi_mask);
+    auto q_value = [&](uint32_t lo, uint32_t hi) {
+        const uint32_t u = (lo & ~hi_mask) | ((hi << 16) & hi_mask);
         const float fh = f16_bits_to_f(u), fb = bf16_bits_to_f(u);
-        qv_raw = q32 ? __uint_as_float(u) : (q.q_dtype == FQ_BF16 ? fb : fh);
-    }
+        return q32 ? __uint_as_float(u) : (q.q_dtype == FQ_BF16 ? fb : fh);
+    };
+    const float qv_raw = q_value(ql, qh);
 
     Int8Rsrc rs;
-    rs.k = make_rsrc(c.kp + l * c.kp_s[0] + b * c.kp_s[1] + h * c.kp_s[2], (int64_t)S * 128);
-    rs.v = make_rsrc(c.vp + l * c.vp_s[0] + b * c.vp_s[1] + h * c.vp_s[2], (int64_t)S * 128);
-    rs.vs = make_rsrc((const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + h * c.vsc_s[2], (int64_t)S * 2);
-    rs.vm = make_rsrc((const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + h * c.vmn_s[2], (int64_t)S * 2);
-    rs.ks = make_rsrc((const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + h * c.ksc_s[2], (int64_t)c.P * 256);
-    rs.km = make_rsrc((const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + h * c.kmn_s[2], (int64_t)c.P * 256);
+    rs.k = make_rsrc(c.kp + l * c.kp_s[0] + b * c.kp_s[1] + hk * c.kp_s[2], (int64_t)S * 128);
+    rs.v = make_rsrc(c.vp + l * c.vp_s[0] + b * c.vp_s[1] + hk * c.vp_s[2], (int64_t)S * 128);
+    rs.vs = make_rsrc((const uint16_t*)c.vsc + l * c.vsc_s[0] + b * c.vsc_s[1] + hk * c.vsc_s[2], (int64_t)S * 2);
+    rs.vm = make_rsrc((const uint16_t*)c.vmn + l * c.vmn_s[0] + b * c.vmn_s[1] + hk * c.vmn_s[2], (int64_t)S * 2);
+    rs.ks = make_rsrc((const MT*)c.ksc + l * c.ksc_s[0] + b * c.ksc_s[1] + hk * c.ksc_s[2], (int64_t)c.P * 256);
+    rs.km = make_rsrc((const MT*)c.kmn + l * c.kmn_s[0] + b * c.kmn_s[1] + hk * c.kmn_s[2], (int64_t)c.P * 256);
     auto issue_half = [&](HalfBuf& bf, int p, int hp) {
         __builtin_amdgcn_sched_barrier(0);
         load_half(bf, rs, p, hp, n16, lg, L);
@@ -189,10 +215,22 @@ void attn_int8_mfma_kernel(Int8Params a) {
 
     int e0, e1;
     if constexpr (FUSED) {
-        __shared__ float s_qraw[NREP][D];
+        __shared__ float s_qraw[HCH ? 2 * NREP : NREP][D];      // chunk_sum: every head of the cache head
         __shared__ uint32_t s_key[NREP * 64 * kSelC];
         __shared__ BlockSelectLds s_bsel;
-        if (tid < NREP * D) {
+        if constexpr (HCH) {
+            const float qv1 = q_value(ql1, qh1);
+            if (tid < q_rows * D) {
+                const int r = (qi >> 7) - q_row0;
+                if ((unsigned)r < (unsigned)NREP) s_q[r][qi & 127] = qv_raw * q.qk_scale;
+                s_qraw[qi >> 7][qi & 127] = qv_raw;
+            }
+            if (tid + NT < q_rows * D) {
+                const int r = (qi1 >> 7) - q_row0;
+                if ((unsigned)r < (unsigned)NREP) s_q[r][qi1 & 127] = qv1 * q.qk_scale;
+                s_qraw[qi1 >> 7][qi1 & 127] = qv1;
+            }
+        } else if (tid < NREP * D) {
             s_q[qi >> 7][qi & 127] = qv_raw * q.qk_scale;
             s_qraw[qi >> 7][qi & 127] = qv_raw;
         }
@@ -205,6 +243,8 @@ void attn_int8_mfma_kernel(Int8Params a) {
         __syncthreads();
         if (from_scores)     // uniform: a scoring launch wrote the group's scores
             scores_to_keys<NREP, NT>(srow, s_key, score_rows, c.P, tid);
+        else if (chunk_sum)
+            score_group_regs<MT, HCH ? 2 * NREP : NREP, NT, true>(sr, s_qraw, s_key, tid, c.P, 255.0f);
         else if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM)
             score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P, 255.0f);
         else
@@ -476,7 +516,11 @@ hipError_t launch_int8_nrep(const Int8Params& a, dim3 grid, hipStream_t st) {
 #define FQ_CASE(N)                                                                                      \
     case N:                                                                                             \
         timer_before_launch(st);                                                                        \
-        hipLaunchKernelGGL((attn_int8_mfma_kernel<MT, N, FUSED>), grid, dim3(512), 0, st, a);           \
+        if (FUSED && (N == 3 || N == 4) && a.sel.head_chunks > 1)                                       \
+            hipLaunchKernelGGL((attn_int8_mfma_kernel<MT, N, FUSED, FUSED && N >= 3>), grid, dim3(512), 0, \
+                               st, a);                                                                  \
+        else                                                                                            \
+            hipLaunchKernelGGL((attn_int8_mfma_kernel<MT, N, FUSED>), grid, dim3(512), 0, st, a);       \
         timer_after_launch(st);                                                                         \
         if (a.splits > 1 || (a.tail.len > 0 && !a.tail.in_kernel))                                      \
             launch_split_merge<N, false>(a.q, a.ws, a.c.Hkv, a.c.B, grid.y, a.splits,                   \
@@ -530,12 +574,11 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
         a.sel = *sel;
         // split 0 of each group attends a 16-bit tail itself (16-byte aligned
         // rows, at least D apart); other tails are attended in the split merge
-        const TailArgs& t = a.tail;
-        const bool t16 = t.dtype == FQ_BF16 || t.dtype == FQ_F16;
-        auto al16 = [](const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[3] % 8 == 0; };
-        a.tail.in_kernel = t.len > 0 && t16 && al16(t.ks) && al16(t.vs) && t.ks[3] >= 128 && t.vs[3] >= 128 &&
-                           ((uintptr_t)t.k & 15) == 0 && ((uintptr_t)t.v & 15) == 0 &&
-                           2 * (int64_t)t.len * std::max(t.ks[3], t.vs[3]) < INT32_MAX;
+        a.tail.in_kernel = mfma_tail_in_kernel(a.tail);
+        // head chunks: each chunk a workgroup of its own, never a split step
+        if (a.sel.head_chunks > 1 && (a.splits != 1 || a.sel.enabled != kScoreSelect ||
+                                      (a.tail.len > 0 && !a.tail.in_kernel)))
+            return hipErrorInvalidValue;
     }
     if (c.meta_dtype == FQ_BF16)
         return fused ? launch_int8_nrep<bf16, true>(a, grid, st) : launch_int8_nrep<bf16, false>(a, grid, st);

@@ -415,12 +415,12 @@ static int quest_bound(const Int4Cache& c, const QueryArgs& q, int num_sinks, in
 // The fused decode's attention kernel scores and selects its own pages when it
 // takes a whole KV group per workgroup; fq_quest_select_int4 then launches
 // nothing unless the caller asks for the scores or the mask.
-static int int4_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
+static int mfma_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
                             int s_max, const TailArgs* tail);
 
 static bool decode_selects_in_attention(Int4Cache c, QueryArgs q, int num_sinks, int window_pages,
                                         int k_max, int select_mode, const Workspace& ws) {
-    int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, nullptr);
+    mfma_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, nullptr);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
     return attn_selects_in_kernel(c, q, al);
@@ -434,16 +434,16 @@ static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q, int bound
     return c.L * c.B * c.Hkv < 192 && !q.rot && bound > kFusedSmallPages;
 }
 
-// 6 or 8 query heads per KV head on the INT4 matrix-core decode, whose
-// workgroups take at most 4: when the step is one launch of whole-group
+// 6 or 8 query heads per KV head on the INT4 / INT8 matrix-core decode,
+// whose workgroups take at most 4: when the step is one launch of whole-group
 // workgroups, every KV head of the cache becomes 2 virtual KV heads of 3 or 4
 // query heads, one workgroup each, both reading the same cache head (the
 // kernel maps them back; per_kv_head_sum scores the summed query of all the
 // head's queries in each, so both take the same pages).  Rewrites c / q to
 // the virtual heads and returns the chunk count, or 1 with c / q untouched.
-static int int4_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
+static int mfma_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
                             int s_max, const TailArgs* tail) {
-    if (c.bits != 4 || q.rot || (q.nrep != 6 && q.nrep != 8)) return 1;
+    if ((c.bits != 4 && c.bits != 8) || q.rot || (q.nrep != 6 && q.nrep != 8)) return 1;
     if (tail && tail->len > 0 && !mfma_tail_in_kernel(*tail)) return 1;
     Int4Cache c2 = c;
     QueryArgs q2 = q;
@@ -514,7 +514,7 @@ static int quest_attend(const fq_int4_cache* cache, const fq_query* query, const
     if (num_sinks < 0) num_sinks = 0;
     if (window_pages < 0) window_pages = 0;
     if (k_max > c.P) k_max = c.P;
-    const int chunks = int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, tail);
+    const int chunks = mfma_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, tail);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
     if (tail && tail->len > 0 && !(bits == 8 ? int8_mfma_supported(c, q, al) : mfma_supported(c, q, al)))
@@ -583,11 +583,11 @@ int fq_quest_decode_int8_tail(const fq_int8_cache* cache, const fq_query* query,
                             workspace_bytes_, stream, 8);
 }
 
-int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,
-                        int32_t k_max, int32_t select_mode) {
+static int quest_fused(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,
+                       int32_t k_max, int32_t select_mode, int bits) {
     Int4Cache c{};
     QueryArgs q{};
-    int st = check_cache(cache, &c);
+    int st = check_cache(cache, &c, bits);
     if (st) return -st;
     st = check_query(query, c.D, c.Hkv, &q);
     if (st) return -st;
@@ -596,10 +596,20 @@ int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32
     if (num_sinks < 0) num_sinks = 0;
     if (window_pages < 0) window_pages = 0;
     if (k_max > c.P) k_max = c.P;
-    int4_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, s_max_for(c.P), nullptr);
+    mfma_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, s_max_for(c.P), nullptr);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max, select_mode),
                                        s_max_for(c.P));
     return attn_selects_in_kernel(c, q, al) ? 1 : 0;
+}
+
+int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,
+                        int32_t k_max, int32_t select_mode) {
+    return quest_fused(cache, query, num_sinks, window_pages, k_max, select_mode, 4);
+}
+
+int fq_quest_fused_int8(const fq_int8_cache* cache, const fq_query* query, int32_t num_sinks, int32_t window_pages,
+                        int32_t k_max, int32_t select_mode) {
+    return quest_fused(cache, query, num_sinks, window_pages, k_max, select_mode, 8);
 }
 
 int fq_quest_decode_int4(const fq_int4_cache* cache, const fq_query* query, const float* retention,

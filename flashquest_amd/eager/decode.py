@@ -152,8 +152,8 @@ def quest_decode_int4(
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
     if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None
-            and not _int4_one_launch(Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), nrep, page_size,
-                                     select_mode, num_sinks, window_pages, k_max_static)):
+            and not _one_launch(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), nrep, page_size,
+                                select_mode, num_sinks, window_pages, k_max_static)):
         return _chunked_decode(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), H_kv, nrep, out,
                                     dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                          k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
@@ -210,19 +210,20 @@ def quest_decode_int4(
     return O, lse_out
 
 
-def _int4_one_launch(Q, planes, nrep, page_size, select_mode, num_sinks, window_pages, k_max_static):
-    """True when fq_quest_decode_int4 takes a step of 6 or 8 query heads per
-    KV head as one launch itself: with enough KV groups the library runs every
-    KV head as two virtual heads of 3 or 4 query heads, one workgroup each."""
+def _one_launch(bits, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages, k_max_static):
+    """True when fq_quest_decode_int4 (bits 4) / fq_quest_decode_int8 (bits
+    8) takes a step of 6 or 8 query heads per KV head as one launch itself:
+    with enough KV groups the library runs every KV head as two virtual heads
+    of 3 or 4 query heads, one workgroup each."""
     if nrep not in (6, 8):
         return False
-    cache, keep = _ops.int4_cache(*planes, page_size)
+    cache, keep = (_ops.int4_cache if bits == 4 else _ops.int8_cache)(*planes, page_size)
     Q3 = Q[..., 0, :]
     probe = _ops.query(Q3, Q3, None, None)
     P = planes[1].shape[-2]
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
-    return L.lib().fq_quest_fused_int4(cache, probe, int(num_sinks), int(window_pages), k_max,
-                                       L.SELECT_MODES[select_mode]) == 1
+    fused = L.lib().fq_quest_fused_int4 if bits == 4 else L.lib().fq_quest_fused_int8
+    return fused(cache, probe, int(num_sinks), int(window_pages), k_max, L.SELECT_MODES[select_mode]) == 1
 
 
 def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
@@ -422,7 +423,9 @@ def quest_decode_int8(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size):
+    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
+            and not _one_launch(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), nrep, page_size,
+                                select_mode, num_sinks, window_pages, k_max_static)):
         return _chunked_decode(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), H_kv, nrep, None,
                                dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                     k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
@@ -589,8 +592,8 @@ class QuestDecoder:
         planes = (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn)
         if (_ops.wants_head_chunks(Q.shape[-3], H_kv, Q.shape[-1], page_size)
                 and rotation_signs is None and mask_out is None
-                and not _int4_one_launch(Q, planes, nrep, page_size, select_mode, num_sinks, window_pages,
-                                         k_max_static)):
+                and not _one_launch(4, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages,
+                                    k_max_static)):
             ret = retention.to(device=Q.device, dtype=torch.float32) if torch.is_tensor(retention) else retention
             self._chunked = (Q, planes,
                              dict(retention=ret, num_sinks=num_sinks, window_pages=window_pages,

@@ -306,6 +306,11 @@ int fq_quest_decode_int8_tail(const fq_int8_cache* cache, const fq_query* query,
  * kernels one decode step runs. */
 int fq_quest_fused_int4(const fq_int4_cache* cache, const fq_query* query,
                         int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode);
+/* The same for fq_quest_decode_int8 over the INT8 cache: 1 when the step is one
+ * attention launch that scores and selects its own pages.  No reference
+ * counterpart. */
+int fq_quest_fused_int8(const fq_int8_cache* cache, const fq_query* query,
+                        int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode);
 
 /* _merge_two_attentions (src/flashquest/eager/llama_persistent_patch.py:50-61).
  * O_a/O_b/out (N, D) rows with row strides; lse (N,) fp32.  out dtype = O_a dtype. */
