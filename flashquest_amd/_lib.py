@@ -130,6 +130,7 @@ SIGNATURES = {
                                                  _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P]),
     "fq_quest_fused_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
     "fq_quest_fused_int8": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _I, _I, _I, _I]),
+    "fq_quest_fused_turbo": (ctypes.c_int, [ctypes.POINTER(TurboCache), ctypes.POINTER(Query)]),
     "fq_quest_attend_int4": (ctypes.c_int, [ctypes.POINTER(Int4Cache), ctypes.POINTER(Query), _P, _I, _I, _I, _I,
                                             _P, ctypes.c_size_t, _P]),
     "fq_merge_attn": (ctypes.c_int, [_P, _P, _P, _P, _I, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, _P,

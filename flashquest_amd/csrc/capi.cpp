@@ -984,6 +984,21 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
 
 // The TurboQuant step (select_only false) or its selection half alone (true:
 // scores and the selection, mask_out written when given, no attention).
+// Whether the TurboQuant decode is one launch that scores and selects its own
+// pages: 0 no, 1 yes, 2 yes with head chunks (6 or 8 query heads per KV head
+// as two virtual KV heads of 3 or 4, like the INT4 / INT8 decode).
+static int turbo_one_launch(const fq_turbo_cache& cache, const QueryArgs& q) {
+    const int G = cache.L * cache.B * cache.H_kv;
+    if (q.rot || cache.P > 64 * 8 || attention_splits_request() > 0) return 0;      // in-kernel selection: 512 pages
+    if (turbo_fused_supported(cache, q)) return G >= 192 ? 1 : 0;
+    if ((q.nrep != 6 && q.nrep != 8) || 2 * G < 192) return 0;
+    fq_turbo_cache vc = cache;
+    vc.H_kv *= 2;
+    QueryArgs vq = q;
+    vq.nrep /= 2;
+    return turbo_fused_supported(vc, vq) ? 2 : 0;
+}
+
 static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
                        const void* k_mn_raw, const int64_t kmr_strides[5], const fq_query* query,
                        const float* retention, int32_t num_sinks, int32_t window_pages, int32_t k_max,
@@ -1024,11 +1039,23 @@ static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, con
     hipStream_t s = (hipStream_t)stream;
     const int bound = quest_bound(c, q, num_sinks, window_pages, k_max, select_mode);
     const bool fusable = turbo_fused_supported(*cache, q);
-    if (!select_only && fusable && G >= 192 && c.P <= 64 * 8 && attention_splits_request() <= 0) {
+    const int one = select_only ? 0 : turbo_one_launch(*cache, q);
+    if (one) {
         SelectArgs sel{};
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kScoreSelect; sel.mask_out = mask_out;
-        return hip_status(launch_attn_turbo_fused(*cache, &c, q, ws, bound, &sel, s), "quest turbo decode");
+        if (one == 1) return hip_status(launch_attn_turbo_fused(*cache, &c, q, ws, bound, &sel, s), "quest turbo decode");
+        fq_turbo_cache vc = *cache;      // head chunks: the virtual KV heads
+        vc.H_kv *= 2;
+        QueryArgs vq = q;
+        vq.nrep /= 2;
+        Int4Cache vr = c;
+        vr.Hkv *= 2;
+        sel.head_chunks = 2;
+        return hip_status(launch_attn_turbo_fused(vc, &vr, vq, ws, quest_bound(vr, vq, num_sinks, window_pages, k_max,
+                                                                                select_mode),
+                                                  &sel, s),
+                          "quest turbo decode");
     }
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};
@@ -1051,6 +1078,15 @@ static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, con
     if (fusable) return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, nullptr, s), "quest turbo decode");
     const AttnLaunch al = choose_split(G, bound, ws.s_max);
     return hip_status(launch_attn_turbo(*cache, q, ws, al, s), "quest turbo decode");
+}
+
+int fq_quest_fused_turbo(const fq_turbo_cache* cache, const fq_query* query) {
+    int st = check_turbo_cache(cache);
+    if (st) return -st;
+    QueryArgs q{};
+    st = check_query(query, cache->D, cache->H_kv, &q);
+    if (st) return -st;
+    return turbo_one_launch(*cache, q) ? 1 : 0;
 }
 
 int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],

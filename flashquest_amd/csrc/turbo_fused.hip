@@ -112,24 +112,36 @@ FQ_DEV void split_f16(float x, _Float16& hi, _Float16& lo) {
 // c_lo), added at the end: each product p * V_scale * codebook to 2^-22
 // relative, fp32-level like the reference's fp32 p * v.  Column n16 of
 // channel tile j is channel 8 n16 + j.
-template <int NREP, bool FUSED>
+//
+// HCH (FUSED only): head chunks, sel.head_chunks virtual KV heads per cache KV
+// head (virtual head h = cache head hk * HC + chunk, NREP query heads each; q,
+// outputs and retention follow h, the cache pages and raw metadata hk).
+// per_kv_head_sum then scores the summed query of all 2 NREP heads of the
+// cache head, so every chunk selects the same pages; the chunks of a cache
+// head are mapped to one XCD.
+template <int NREP, bool FUSED, bool HCH = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_turbo_fused_kernel(TurboFusedParams a) {
     constexpr int D = 128, NW = 8, NT = 512;
     static_assert(NREP <= 4, "query heads per KV head");
+    static_assert(!HCH || FUSED, "head chunks run in the fused kernel");
     __shared__ SplitLds<D, NREP, NW> s_split;
     __shared__ int s_ent[kMaxWgPages];
     // q.k codebook table: entry e (lsb byte of 4 channels | their msb nibble << 8)
     // holds the fp16 hi parts of the 4 channels' codebook values, then the lo parts
     __shared__ uint4 s_lut[4096];
-    __shared__ float s_qraw[NREP][D];
+    __shared__ float s_qraw[HCH ? 2 * NREP : NREP][D];      // chunk_sum: every head of the cache head
     __shared__ float s_qrot[NREP][D];
     __shared__ uint8_t s_apv[NW][2][16][4][16];     // p.v A operands per wave: [step][row][k-group, swizzled][16 bytes]
 
     const fq_turbo_cache& c = a.c;
     const QueryArgs& q = a.q;
-    const int g = blockIdx.y, split = blockIdx.x;
+    const int gy = blockIdx.y, GY = gridDim.y, split = blockIdx.x;
+    const int g = (HCH && gridDim.x == 1 && GY % 8 == 0) ? (gy % 8) * (GY / 8) + gy / 8 : gy;
     const int h = g % c.H_kv, b = (g / c.H_kv) % c.B, l = g / (c.H_kv * c.B);
+    const int HC = HCH ? a.sel.head_chunks : 1;
+    const int hk = HCH ? h / HC : h;
+    const bool chunk_sum = HCH && a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM;
     const int tid = threadIdx.x, L = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
     const int n16 = L & 15, lg = L >> 4;
     const int S = c.S;
@@ -137,17 +149,27 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     // q (raw basis): element tid of the group's NREP heads.  Branch-free (two
     // 16-bit loads, the high one masked off for 16-bit q types), so the
     // metadata loads below go out before the first wait.
-    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)h * NREP * q.q_s[2];
-    const int qi = min(tid, NREP * D - 1);
+    // chunk_sum: all 2 NREP heads of the cache head (two elements per
+    // thread; rows chunk * NREP .. are this workgroup's own)
+    const int q_rows = chunk_sum ? 2 * NREP : NREP;
+    const int q_row0 = chunk_sum ? (h - hk * HC) * NREP : 0;
+    const int64_t qb = l * q.q_s[0] + b * q.q_s[1] + (int64_t)(chunk_sum ? hk * 2 * NREP : h * NREP) * q.q_s[2];
+    const int qi = min(tid, q_rows * D - 1);
+    const int qi1 = min(tid + NT, q_rows * D - 1);
     const bool q32 = q.q_dtype == FQ_F32;
     const int esz = q32 ? 4 : 2;
     uint32_t hi_mask = (0u - (uint32_t)q32) & 0xFFFF0000u;
     asm volatile("" : "+s"(hi_mask));
-    uint32_t ql, qh;
+    uint32_t ql, qh, ql1 = 0u, qh1 = 0u;
     {
         const char* qc = (const char*)q.q + (qb + (qi >> 7) * q.q_s[2] + (qi & 127) * q.q_s[3]) * esz;
         ql = *(const uint16_t*)qc;
         qh = *(const uint16_t*)(qc + esz - 2);
+        if constexpr (HCH) {
+            const char* qc1 = (const char*)q.q + (qb + (qi1 >> 7) * q.q_s[2] + (qi1 & 127) * q.q_s[3]) * esz;
+            ql1 = *(const uint16_t*)qc1;
+            qh1 = *(const uint16_t*)(qc1 + esz - 2);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     float ret_l = 0.f;
@@ -156,16 +178,19 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     const bool from_scores = FUSED && a.sel.enabled == kSelectOnly;
     const int score_rows = a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM ? 1 : NREP;
     if constexpr (FUSED) {
-        ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
+        if (chunk_sum)      // uniform: the k of the summed row is the cache head's largest retention
+            ret_l = wave_max(a.sel.retention[l * q.ret_ls + hk * 2 * NREP + min(L, 2 * NREP - 1)]);
+        else
+            ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
         if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
-        else score_group_load<bf16, NT>(sr, a.raw, tid, l, b, h);
+        else score_group_load<bf16, NT>(sr, a.raw, tid, l, b, hk);
     }
-    float qv_raw;
-    {
-        const uint32_t u = (ql & ~hi_mask) | ((qh << 16) & hi_mask);
+    auto q_value = [&](uint32_t lo, uint32_t hi) {
+        const uint32_t u = (lo & ~hi_mask) | ((hi << 16) & hi_mask);
         const float fh = f16_bits_to_f(u), fb = bf16_bits_to_f(u);
-        qv_raw = q32 ? __uint_as_float(u) : (q.q_dtype == FQ_BF16 ? fb : fh);
-    }
+        return q32 ? __uint_as_float(u) : (q.q_dtype == FQ_BF16 ? fb : fh);
+    };
+    const float qv_raw = q_value(ql, qh);
     {
         // byte tables of the codebook's fp16 parts for v_perm: [part][low / high byte][codes 0-3 / 4-7]
         uint32_t tb[2][2][2] = {};
@@ -195,12 +220,17 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             s_lut[e] = make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
-    if (tid < NREP * D) s_qraw[qi >> 7][qi & 127] = qv_raw;
+    if constexpr (HCH) {
+        if (tid < q_rows * D) s_qraw[qi >> 7][qi & 127] = qv_raw;
+        if (tid + NT < q_rows * D) s_qraw[qi1 >> 7][qi1 & 127] = q_value(ql1, qh1);
+    } else if (tid < NREP * D) {
+        s_qraw[qi >> 7][qi & 127] = qv_raw;
+    }
     __syncthreads();
     // q_rot = WHT(q) / sqrt(D) (Sylvester order), pre-scaled by sm_scale * log2(e);
-    // wave r rotates head r
+    // wave r rotates head r (row q_row0 + r of s_qraw)
     if (w < NREP) {
-        float v0 = s_qraw[w][L], v1 = s_qraw[w][L + 64];
+        float v0 = s_qraw[q_row0 + w][L], v1 = s_qraw[q_row0 + w][L + 64];
         wave_hadamard128(v0, v1);
         const float sc = q.qk_scale / sqrtf((float)D);
         s_qrot[w][L] = v0 * sc;
@@ -210,12 +240,12 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
     TurboRsrc rs;
     {
         const int64_t bl = l;
-        const uint8_t* km = c.k_msb + bl * c.kmsb_strides[0] + b * c.kmsb_strides[1] + h * c.kmsb_strides[2];
-        const uint8_t* kl = c.k_lsb + bl * c.klsb_strides[0] + b * c.klsb_strides[1] + h * c.klsb_strides[2];
-        const uint8_t* vm = c.v_msb + bl * c.vmsb_strides[0] + b * c.vmsb_strides[1] + h * c.vmsb_strides[2];
-        const uint8_t* vl = c.v_lsb + bl * c.vlsb_strides[0] + b * c.vlsb_strides[1] + h * c.vlsb_strides[2];
-        const uint16_t* ks = (const uint16_t*)c.k_scale + bl * c.kst_strides[0] + b * c.kst_strides[1] + h * c.kst_strides[2];
-        const uint16_t* vs = (const uint16_t*)c.v_scale + bl * c.vst_strides[0] + b * c.vst_strides[1] + h * c.vst_strides[2];
+        const uint8_t* km = c.k_msb + bl * c.kmsb_strides[0] + b * c.kmsb_strides[1] + hk * c.kmsb_strides[2];
+        const uint8_t* kl = c.k_lsb + bl * c.klsb_strides[0] + b * c.klsb_strides[1] + hk * c.klsb_strides[2];
+        const uint8_t* vm = c.v_msb + bl * c.vmsb_strides[0] + b * c.vmsb_strides[1] + hk * c.vmsb_strides[2];
+        const uint8_t* vl = c.v_lsb + bl * c.vlsb_strides[0] + b * c.vlsb_strides[1] + hk * c.vlsb_strides[2];
+        const uint16_t* ks = (const uint16_t*)c.k_scale + bl * c.kst_strides[0] + b * c.kst_strides[1] + hk * c.kst_strides[2];
+        const uint16_t* vs = (const uint16_t*)c.v_scale + bl * c.vst_strides[0] + b * c.vst_strides[1] + hk * c.vst_strides[2];
         rs.km_t = (int)c.kmsb_strides[3]; rs.kl_t = (int)c.klsb_strides[3];
         rs.vm_t = (int)c.vmsb_strides[3]; rs.vl_t = (int)c.vlsb_strides[3];
         rs.km = make_rsrc(km, (int64_t)S * rs.km_t);
@@ -249,6 +279,7 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
         __shared__ uint32_t s_key[NREP * 64 * kSelC];
         __shared__ BlockSelectLds s_bsel;
         if (from_scores) scores_to_keys<NREP, NT>(srow, s_key, score_rows, c.P, tid);
+        else if (chunk_sum) score_group_regs<bf16, HCH ? 2 * NREP : NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
         else if (a.sel.mode == FQ_SELECT_PER_KV_HEAD_SUM) score_group_regs<bf16, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
         else score_group_regs<bf16, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
         const ForcedPages fp = forced_pages(c.P, a.sel.num_sinks, a.sel.window);
@@ -523,7 +554,10 @@ hipError_t launch_turbo_fused_nrep(const TurboFusedParams& a, dim3 grid, hipStre
 #define FQ_CASE(N)                                                                                          \
     case N:                                                                                                 \
         timer_before_launch(st);                                                                            \
-        hipLaunchKernelGGL((attn_turbo_fused_kernel<N, FUSED>), grid, dim3(512), 0, st, a);                 \
+        if (FUSED && (N == 3 || N == 4) && a.sel.head_chunks > 1)                                           \
+            hipLaunchKernelGGL((attn_turbo_fused_kernel<N, FUSED, FUSED && N >= 3>), grid, dim3(512), 0, st, a); \
+        else                                                                                                \
+            hipLaunchKernelGGL((attn_turbo_fused_kernel<N, FUSED>), grid, dim3(512), 0, st, a);             \
         timer_after_launch(st);                                                                             \
         if (a.splits > 1)                                                                                   \
             launch_split_merge<N, true>(a.q, a.ws, a.c.H_kv, a.c.B, grid.y, a.splits, TailArgs{}, st);         \
@@ -571,6 +605,7 @@ hipError_t launch_attn_turbo_fused(const fq_turbo_cache& c, const Int4Cache* raw
         a.splits = 1;
         return launch_turbo_fused_nrep<true>(a, dim3(1, groups), st);
     }
+    if (sel && sel->head_chunks > 1) return hipErrorInvalidValue;      // head chunks: the single launch only
     if (sel && sel->enabled == kSelectOnly) {
         if (c.P > 64 * kSelC) return hipErrorInvalidValue;
         a.sel = *sel;

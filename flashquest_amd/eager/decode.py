@@ -210,16 +210,20 @@ def quest_decode_int4(
     return O, lse_out
 
 
-def _one_launch(bits, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages, k_max_static):
-    """True when fq_quest_decode_int4 (bits 4) / fq_quest_decode_int8 (bits
-    8) takes a step of 6 or 8 query heads per KV head as one launch itself:
-    with enough KV groups the library runs every KV head as two virtual heads
-    of 3 or 4 query heads, one workgroup each."""
+def _one_launch(bits, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages, k_max_static, raw=None):
+    """True when fq_quest_decode_int4 / _int8 / _turbo (bits 4 / 8 / 3; raw:
+    TurboQuant's (K_scale_raw, K_mn_raw)) takes a step of 6 or 8 query heads
+    per KV head as one launch itself: with enough KV groups the library runs
+    every KV head as two virtual heads of 3 or 4 query heads, one workgroup
+    each."""
     if nrep not in (6, 8):
         return False
-    cache, keep = (_ops.int4_cache if bits == 4 else _ops.int8_cache)(*planes, page_size)
     Q3 = Q[..., 0, :]
     probe = _ops.query(Q3, Q3, None, None)
+    if bits == 3:
+        cache, keep = _ops.turbo_cache(*planes, raw[0].shape[-2], page_size)
+        return L.lib().fq_quest_fused_turbo(cache, probe) == 1
+    cache, keep = (_ops.int4_cache if bits == 4 else _ops.int8_cache)(*planes, page_size)
     P = planes[1].shape[-2]
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     fused = L.lib().fq_quest_fused_int4 if bits == 4 else L.lib().fq_quest_fused_int8
@@ -520,7 +524,9 @@ def quest_decode_turbo(
         raise AssertionError("K_scale_raw / K_mn_raw must be bf16")
     H_kv = K_msb.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size):
+    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
+            and not _one_launch(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), nrep, page_size,
+                                select_mode, num_sinks, window_pages, k_max_static, raw=(K_scale_raw, K_mn_raw))):
         return _chunked_decode(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), H_kv, nrep, None,
                                dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
                                     k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,

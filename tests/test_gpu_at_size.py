@@ -469,6 +469,60 @@ def test_turbo_fused_step_at_size(turbo_cfg1, mode, qdtype):
             max_abs_O=f"{err_max:.3e}", fused_vs_split=f"{d:.3e}")
 
 
+@pytest.fixture(scope="module", params=[64, 48], ids=["gqa8", "gqa6"])
+def turbo_wide(request):
+    """The TurboQuant caches of config 1's geometry with 8 or 6 query heads per KV head."""
+    return bench.make_turbo_cache(LAYERS, Hq=request.param, P=P, dev=torch.device("cuda:0"))
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_turbo_wide_gqa_one_launch(turbo_wide, mode):
+    """6 and 8 query heads per KV head over the TurboQuant cache at config 1's
+    geometry: one launch (two virtual heads of 3 or 4 query heads per KV
+    head), selection equal to the oracle's and to the split path's, O within
+    the bar on sampled layers."""
+    from flashquest_amd.eager.decode import _one_launch, quest_decode_turbo
+    tc = turbo_wide
+    Q = tc["Q"]
+    Hq = Q.shape[-3]
+    keys = ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")
+    raw = (tc["K_scale_raw"], tc["K_mn_raw"])
+    assert _one_launch(3, Q, [tc[k] for k in keys], Hq // 8, 64, mode, 4, 2, 128, raw=raw)
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, k_max_static=128, select_mode=mode)
+    args = [Q] + [tc[k] for k in keys] + list(raw)
+    o, lse, mask = quest_decode_turbo(*args, return_selection=True, **kw)
+    o2, lse2 = quest_decode_turbo(*args, **kw)
+    with L.attention_splits(4):
+        os_, lses, masks = quest_decode_turbo(*args, return_selection=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(mask, masks)
+    m_host = mask.cpu().numpy()
+    rows = amb = amb_diff = 0
+    err_max = 0.0
+    for l in (0, 9, 27):
+        q = Q[l:l + 1, :, 0].float().cpu().numpy()
+        ksr, kmr = _host4(tc, ("K_scale_raw", "K_mn_raw"), l)
+        scores = O.page_scores_fixed(q, ksr, kmr, mode)
+        ref_mask = O.select_pages_vectorized(scores[:, :, None, :], 0.25, 4, 2, 128)[:, :, 0, :]
+        if mode == "per_kv_head_sum":
+            ref_mask = np.repeat(ref_mask, Hq // 8, axis=1)
+        assert np.array_equal(m_host[l:l + 1], ref_mask), l
+        n, a, mis, ad = fp64_selection_check(q, ksr, kmr, m_host[l:l + 1], 0.25, mode)
+        assert mis == 0, l
+        rows, amb, amb_diff = rows + n, amb + a, amb_diff + ad
+        if l in (0, 27):
+            ref_o, ref_l = O.sparse_turbo_attention(q, *_host4(tc, keys, l), ref_mask, 64)
+            err = float(np.abs(o[l:l + 1, :, 0].float().cpu().numpy() - ref_o).max())
+            err_max = max(err_max, err)
+            assert err <= _qtol("bf16", ref_o), (l, err)
+            assert np.abs(lse[l:l + 1, :, 0].cpu().numpy() - ref_l).max() <= TOL_LSE
+    d = (o.float() - os_.float()).abs().max().item()
+    assert d <= 2 * _qtol("bf16", np.array([2.0]))
+    _report(f"turbo {Hq} query heads {mode}", rows=rows, ambiguous_rows=amb, ambiguous_resolved_differently=amb_diff,
+            max_abs_O=f"{err_max:.3e}", fused_vs_split=f"{d:.3e}")
+
+
 def test_read_only_pass_runs_on_config1(cfg1):
     """The bench's ceiling probe (fq_read_decode_pages) takes config 1's cache
     and the decode's own selection mask and completes."""
