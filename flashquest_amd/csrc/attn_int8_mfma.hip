@@ -188,7 +188,9 @@ void attn_int8_mfma_kernel(Int8Params a) {
             tkr[u] = ld128(rk, (int)(2 * tt * t.ks[3]) + 16 * j);
             tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
         }
-        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        if (from_scores)      // per_kv_head_sum with head chunks: the cache head's one summed row
+            scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)(chunk_sum ? g - (h - hk * HC) : g) * NREP * c.P,
+                                  score_rows, c.P, tid);
         else score_group_load<MT, NT>(sr, c, tid, l, b, hk);
     }
     auto q_value = [&](uint32_t lo, uint32_t hi) {
@@ -575,10 +577,9 @@ hipError_t launch_attn_int8_mfma(const Int4Cache& c, const QueryArgs& q, const W
         // split 0 of each group attends a 16-bit tail itself (16-byte aligned
         // rows, at least D apart); other tails are attended in the split merge
         a.tail.in_kernel = mfma_tail_in_kernel(a.tail);
-        // head chunks: each chunk a workgroup of its own, never a split step
-        if (a.sel.head_chunks > 1 && (a.splits != 1 || a.sel.enabled != kScoreSelect ||
-                                      (a.tail.len > 0 && !a.tail.in_kernel)))
-            return hipErrorInvalidValue;
+        // head chunks: a tail only inside the kernel (the split merge's tail
+        // work indexes the cache by the virtual heads)
+        if (a.sel.head_chunks > 1 && a.tail.len > 0 && !a.tail.in_kernel) return hipErrorInvalidValue;
     }
     if (c.meta_dtype == FQ_BF16)
         return fused ? launch_int8_nrep<bf16, true>(a, grid, st) : launch_int8_nrep<bf16, false>(a, grid, st);

@@ -263,7 +263,9 @@ void attn_int4_mfma_kernel(MfmaParams a) {
             tkr[u] = ld128(rk, (int)(2 * tt * t.ks[3]) + 16 * j);
             tvr[u] = ld128(rv, (int)(2 * tt * t.vs[3]) + 16 * j);
         }
-        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        if (from_scores)      // per_kv_head_sum with head chunks: the cache head's one summed row
+            scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)(chunk_sum ? g - (h - hk * HC) : g) * NREP * c.P,
+                                  score_rows, c.P, tid);
         else score_group_load<MT, NT>(sr, c, tid, l, b, hk);
     }
     const bool qbf = q.q_dtype == FQ_BF16;
@@ -833,10 +835,9 @@ hipError_t launch_attn_int4_mfma(const Int4Cache& c, const QueryArgs& q, const W
         // with several, split 0 folds it into its partial and the merge has no
         // tail work left
         a.tail.in_kernel = mfma_tail_in_kernel(a.tail);
-        // head chunks: each chunk a workgroup of its own, never a split step
-        if (a.sel.head_chunks > 1 && (a.splits != 1 || a.sel.enabled != kScoreSelect ||
-                                      (a.tail.len > 0 && !a.tail.in_kernel)))
-            return hipErrorInvalidValue;
+        // head chunks: a tail only inside the kernel (the split merge's tail
+        // work indexes the cache by the virtual heads)
+        if (a.sel.head_chunks > 1 && a.tail.len > 0 && !a.tail.in_kernel) return hipErrorInvalidValue;
     }
     dim3 grid(a.splits, groups);
 #define FQ_W(MT_, G_)                                                                       \

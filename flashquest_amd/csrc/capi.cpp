@@ -418,9 +418,8 @@ static int quest_bound(const Int4Cache& c, const QueryArgs& q, int num_sinks, in
 static int mfma_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
                             int s_max, const TailArgs* tail);
 
-static bool decode_selects_in_attention(Int4Cache c, QueryArgs q, int num_sinks, int window_pages,
+static bool decode_selects_in_attention(const Int4Cache& c, const QueryArgs& q, int num_sinks, int window_pages,
                                         int k_max, int select_mode, const Workspace& ws) {
-    mfma_head_chunks(c, q, num_sinks, window_pages, k_max, select_mode, ws.s_max, nullptr);
     const AttnLaunch al = choose_split(c.L * c.B * c.Hkv, quest_bound(c, q, num_sinks, window_pages, k_max,
                                                                       select_mode), ws.s_max);
     return attn_selects_in_kernel(c, q, al);
@@ -435,12 +434,14 @@ static bool attend_from_scores(const Int4Cache& c, const QueryArgs& q, int bound
 }
 
 // 6 or 8 query heads per KV head on the INT4 / INT8 matrix-core decode,
-// whose workgroups take at most 4: when the step is one launch of whole-group
-// workgroups, every KV head of the cache becomes 2 virtual KV heads of 3 or 4
-// query heads, one workgroup each, both reading the same cache head (the
-// kernel maps them back; per_kv_head_sum scores the summed query of all the
-// head's queries in each, so both take the same pages).  Rewrites c / q to
-// the virtual heads and returns the chunk count, or 1 with c / q untouched.
+// whose workgroups take at most 4: when the attention kernel selects for
+// itself, every KV head of the cache becomes 2 virtual KV heads of 3 or 4
+// query heads, each its own workgroup(s), all reading the same cache head
+// (the kernel maps them back; per_kv_head_sum selects from the summed query
+// of all the head's queries in each, so every chunk takes the same pages).
+// Split steps select from the scores of a scoring launch over the real KV
+// heads.  Rewrites c / q to the virtual heads and returns the chunk count,
+// or 1 with c / q untouched.
 static int mfma_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int window_pages, int k_max, int select_mode,
                             int s_max, const TailArgs* tail) {
     if ((c.bits != 4 && c.bits != 8) || q.rot || (q.nrep != 6 && q.nrep != 8)) return 1;
@@ -451,7 +452,7 @@ static int mfma_head_chunks(Int4Cache& c, QueryArgs& q, int num_sinks, int windo
     q2.nrep /= 2;
     const int bound = quest_bound(c2, q2, num_sinks, window_pages, k_max, select_mode);
     const AttnLaunch al = choose_split(c2.L * c2.B * c2.Hkv, bound, s_max);
-    if (!attn_selects_in_kernel(c2, q2, al) || attend_from_scores(c2, q2, al.max_entries)) return 1;
+    if (!attn_selects_in_kernel(c2, q2, al)) return 1;
     c = c2;
     q = q2;
     return 2;
@@ -476,10 +477,15 @@ static int quest_select(const fq_int4_cache* cache, const fq_query* query, const
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};   // (L*B, H_q, 1, P) contiguous
     float* sc_user = (scores_out && select_mode == FQ_SELECT_PER_Q_HEAD) ? scores_out : nullptr;
     // the fused attention kernel selects for itself (and, when the whole step
-    // is one call, writes the mask too)
+    // is one call, writes the mask too); vc / vq: the heads it runs (virtual
+    // heads with 6 or 8 query heads per KV head), the scoring launch takes the
+    // real ones
+    Int4Cache vc = c;
+    QueryArgs vq = q;
+    mfma_head_chunks(vc, vq, num_sinks, window_pages, k_max, select_mode, ws.s_max, nullptr);
     if ((!mask_out || mask_from_attention) && !sc_user &&
-        decode_selects_in_attention(c, q, num_sinks, window_pages, k_max, select_mode, ws)) {
-        if (!attend_from_scores(c, q, quest_bound(c, q, num_sinks, window_pages, k_max, select_mode)))
+        decode_selects_in_attention(vc, vq, num_sinks, window_pages, k_max, select_mode, ws)) {
+        if (!attend_from_scores(vc, vq, quest_bound(vc, vq, num_sinks, window_pages, k_max, select_mode)))
             return FQ_OK;      // the attention kernel scores too
         return hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks,
                                        window_pages, k_max, nullptr, (hipStream_t)stream, false),

@@ -1,0 +1,120 @@
+"""6 and 8 query heads per KV head in single-layer decode steps (the
+reference's per-layer call pattern, llama_persistent_patch.py:196-245).
+
+The matrix-core kernels take at most 4 query heads per workgroup.  For 6 or 8
+the library runs every KV head as two virtual KV heads of 3 or 4 query heads:
+a single layer's 8 KV heads are too few to fill the GPU, so the step is the
+split form (a scoring launch over the real KV heads, attention workgroups
+that each select from those scores and attend a slice of the list, the split
+merge).  per_kv_head_sum selects from the summed query of all the head's
+queries in every virtual head.  Checked against the oracle (selection bit for
+bit, O and lse within the decode bar), with and without a partial-page tail,
+and replayed from a HIP graph.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fq_oracle as O
+from tests.cases import Int4Case, Int8Case, decode_tol, max_err, to_dev_half
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("Hq", [64, 48])
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+@pytest.mark.parametrize("P", [200, 512])
+def test_single_layer_step_virtual_heads(bits, Hq, mode, P):
+    from flashquest_amd.eager.decode import _one_launch, quest_decode_int4, quest_decode_int8
+    S = 64 * (P - 1) + 29
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, k_max_static=None, select_mode=mode)
+    ref_kw = dict(retention=0.25, num_sinks=4, window_pages=2, k_max_static=None, mode=mode)
+    print(f"[virtual heads] bits={bits} Hq={Hq} mode={mode} P={P}", flush=True)
+    if bits == 4:
+        c = Int4Case(seed=900 + Hq + P, B=1, Hq=Hq, Hkv=8, S=S, D=128, dtype="f16", meta="f16", vgroup=32)
+        dev = c.device()
+        planes = [dev[k] for k in ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")]
+        assert _one_launch(4, c.q_dev(), planes, Hq // 8, 64, mode, 4, 2, None)
+        o, lse, mask = quest_decode_int4(c.q_dev(), *planes, return_selection=True, **kw)
+        ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, **ref_kw)
+        tol = decode_tol(ref["O"], "f16")
+    else:
+        c = Int8Case(seed=950 + Hq + P, B=1, Hq=Hq, Hkv=8, S=S, D=128)
+        dev = c.device()
+        planes = [dev[k] for k in ("K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")]
+        assert _one_launch(8, c.q_dev(), planes, Hq // 8, 64, mode, 4, 2, None)
+        o, lse, mask = quest_decode_int8(c.q_dev(), *planes, return_selection=True, **kw)
+        ref = O.decode_step(c.Q, c.ku, c.ks, c.km, c.vu, c.vs, c.vm, bits=8, **ref_kw)
+        tol = decode_tol(ref["O"], "bf16")
+    torch.cuda.synchronize()
+    assert np.array_equal(mask.cpu().numpy(), ref["mask"])
+    assert max_err(o[:, :, 0], ref["O"]) <= tol
+    assert max_err(lse[:, :, 0], ref["lse"]) <= 1e-4
+
+
+@pytest.mark.parametrize("Hq", [64, 48])
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_single_layer_step_virtual_heads_with_tail(Hq, mode):
+    """The partial page attended inside the attention workgroups of every
+    virtual head (split 0 of each), then merged with the pages."""
+    from flashquest_amd.eager.decode import quest_decode_int4
+    P, T = 300, 37
+    c = Int4Case(seed=990 + Hq, B=1, Hq=Hq, Hkv=8, S=64 * P, D=128, dtype="f16", meta="f16", vgroup=32)
+    rng = np.random.default_rng(Hq)
+    kt = O.round_bf16(rng.standard_normal((1, 8, T, 128)).astype(np.float32))
+    vt = O.round_bf16(rng.standard_normal((1, 8, T, 128)).astype(np.float32))
+    o, lse = quest_decode_int4(c.q_dev(), **c.device(), retention=0.25, num_sinks=4, window_pages=2,
+                               select_mode=mode, K_tail=to_dev_half(kt, "bf16"), V_tail=to_dev_half(vt, "bf16"))
+    torch.cuda.synchronize()
+    ref = O.decode_step(c.Q, c.kp, c.ks, c.km, c.vp, c.vs, c.vm, retention=0.25, num_sinks=4, window_pages=2,
+                        mode=mode)
+    ot, lt = O.dense_attn_with_lse(c.Q, kt, vt)
+    ro = O.merge_two_attentions(ref["O"], ref["lse"], ot, lt)
+    m = np.maximum(ref["lse"], lt)
+    rl = m + np.log(np.exp(ref["lse"] - m) + np.exp(lt - m))
+    assert max_err(o[:, :, 0], ro) <= decode_tol(ro, "f16")
+    assert max_err(lse[:, :, 0], rl) <= 1e-4
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_per_layer_graph_virtual_heads(mode):
+    """Four single-layer steps (64 query / 8 KV heads, 256 pages) captured in
+    one HIP graph: every replay, with new queries written in place between
+    them, equals the same steps run eagerly bit for bit."""
+    from flashquest_amd.eager.decode import QuestDecoder
+    layers, P = 4, 256
+    cases = [Int4Case(seed=1400 + i, B=1, Hq=64, Hkv=8, S=64 * P, D=128, dtype="f16", meta="f16", vgroup=32)
+             for i in range(layers)]
+    keys = ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")
+    devs = [c.device() for c in cases]
+    Qs = [c.q_dev() for c in cases]
+    decs = [QuestDecoder(Qs[l], *[devs[l][k] for k in keys], retention=0.25, num_sinks=4, window_pages=2,
+                         k_max_static=64, select_mode=mode) for l in range(layers)]
+    assert all(d._chunked is None for d in decs), "the library takes these steps itself"
+    for d in decs:
+        d()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for d in decs:
+            d()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for d in decs:
+                d()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for q in Qs:
+            q.copy_(torch.randn(q.shape, device=q.device).to(q.dtype))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [d.O3.clone() for d in decs]
+        for d in decs:
+            d()
+        torch.cuda.synchronize()
+        for l, d in enumerate(decs):
+            assert torch.equal(got[l], d.O3), (rep, l)
+        assert bool(torch.isfinite(got[0]).all())
