@@ -990,19 +990,25 @@ int fq_sparse_turbo_fwd_mask(const fq_turbo_cache* cache, const fq_query* query,
 
 // The TurboQuant step (select_only false) or its selection half alone (true:
 // scores and the selection, mask_out written when given, no attention).
-// Whether the TurboQuant decode is one launch that scores and selects its own
-// pages: 0 no, 1 yes, 2 yes with head chunks (6 or 8 query heads per KV head
-// as two virtual KV heads of 3 or 4, like the INT4 / INT8 decode).
-static int turbo_one_launch(const fq_turbo_cache& cache, const QueryArgs& q) {
-    const int G = cache.L * cache.B * cache.H_kv;
-    if (q.rot || cache.P > 64 * 8 || attention_splits_request() > 0) return 0;      // in-kernel selection: 512 pages
-    if (turbo_fused_supported(cache, q)) return G >= 192 ? 1 : 0;
-    if ((q.nrep != 6 && q.nrep != 8) || 2 * G < 192) return 0;
+// 6 or 8 query heads per KV head on the matrix-core TurboQuant kernel (at
+// most 4 per workgroup): every KV head as two virtual KV heads of 3 or 4
+// query heads, like the INT4 / INT8 decode.  Whether that layout applies.
+static bool turbo_head_chunks(const fq_turbo_cache& cache, const QueryArgs& q) {
+    if (q.rot || (q.nrep != 6 && q.nrep != 8) || cache.P > 64 * 8 || attention_splits_request() > 0) return false;
     fq_turbo_cache vc = cache;
     vc.H_kv *= 2;
     QueryArgs vq = q;
     vq.nrep /= 2;
-    return turbo_fused_supported(vc, vq) ? 2 : 0;
+    return turbo_fused_supported(vc, vq);
+}
+
+// Whether the TurboQuant decode is one launch that scores and selects its own
+// pages: 0 no, 1 yes, 2 yes with head chunks.
+static int turbo_one_launch(const fq_turbo_cache& cache, const QueryArgs& q) {
+    const int G = cache.L * cache.B * cache.H_kv;
+    if (q.rot || cache.P > 64 * 8 || attention_splits_request() > 0) return 0;      // in-kernel selection: 512 pages
+    if (turbo_fused_supported(cache, q)) return G >= 192 ? 1 : 0;
+    return 2 * G >= 192 && turbo_head_chunks(cache, q) ? 2 : 0;
 }
 
 static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],
@@ -1065,9 +1071,11 @@ static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, con
     }
     const int64_t q4[4] = {q.q_s[1], q.q_s[2], 0, q.q_s[3]};
     int64_t sc4[4] = {(int64_t)q.Hq * c.P, c.P, c.P, 1};
-    if (!select_only && fusable && c.P <= 64 * 8 && attention_splits_request() <= 0) {   // in-kernel selection: 512 pages
+    const bool chunks = !select_only && !fusable && turbo_head_chunks(*cache, q);
+    if (!select_only && (fusable || chunks) && c.P <= 64 * 8 && attention_splits_request() <= 0) {
         // few groups (a single layer's step): the scoring launch writes the
-        // scores, the attention workgroups of each group select from them
+        // scores of the real KV heads, the attention workgroups of each group
+        // (virtual heads with 6 or 8 query heads per KV head) select from them
         st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                      k_max, nullptr, s, false),
                         "page scores");
@@ -1075,7 +1083,18 @@ static int quest_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, con
         SelectArgs sel{};
         sel.retention = retention; sel.num_sinks = num_sinks; sel.window = window_pages;
         sel.k_max = k_max; sel.mode = select_mode; sel.enabled = kSelectOnly; sel.mask_out = mask_out;
-        return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, &sel, s), "quest turbo decode");
+        if (!chunks) return hip_status(launch_attn_turbo_fused(*cache, nullptr, q, ws, bound, &sel, s), "quest turbo decode");
+        fq_turbo_cache vc = *cache;
+        vc.H_kv *= 2;
+        QueryArgs vq = q;
+        vq.nrep /= 2;
+        Int4Cache vr = c;
+        vr.Hkv *= 2;
+        sel.head_chunks = 2;
+        return hip_status(launch_attn_turbo_fused(vc, nullptr, vq, ws,
+                                                  quest_bound(vr, vq, num_sinks, window_pages, k_max, select_mode), &sel,
+                                                  s),
+                          "quest turbo decode");
     }
     st = hip_status(launch_score(c, q, 1, q4, nullptr, sc4, &ws, select_mode, retention, num_sinks, window_pages,
                                  k_max, mask_out, s),
@@ -1092,7 +1111,7 @@ int fq_quest_fused_turbo(const fq_turbo_cache* cache, const fq_query* query) {
     QueryArgs q{};
     st = check_query(query, cache->D, cache->H_kv, &q);
     if (st) return -st;
-    return turbo_one_launch(*cache, q) ? 1 : 0;
+    return turbo_one_launch(*cache, q) || turbo_head_chunks(*cache, q) ? 1 : 0;
 }
 
 int fq_quest_decode_turbo(const fq_turbo_cache* cache, const void* k_scale_raw, const int64_t ksr_strides[5],

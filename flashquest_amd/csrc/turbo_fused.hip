@@ -182,7 +182,9 @@ void attn_turbo_fused_kernel(TurboFusedParams a) {
             ret_l = wave_max(a.sel.retention[l * q.ret_ls + hk * 2 * NREP + min(L, 2 * NREP - 1)]);
         else
             ret_l = a.sel.retention[l * q.ret_ls + h * NREP + min(L, NREP - 1)];
-        if (from_scores) scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)g * NREP * c.P, score_rows, c.P, tid);
+        if (from_scores)      // per_kv_head_sum with head chunks: the cache head's one summed row
+            scores_load<NREP, NT>(srow, a.ws.scores + (int64_t)(chunk_sum ? g - (h - hk * HC) : g) * NREP * c.P,
+                                  score_rows, c.P, tid);
         else score_group_load<bf16, NT>(sr, a.raw, tid, l, b, hk);
     }
     auto q_value = [&](uint32_t lo, uint32_t hi) {
@@ -605,7 +607,6 @@ hipError_t launch_attn_turbo_fused(const fq_turbo_cache& c, const Int4Cache* raw
         a.splits = 1;
         return launch_turbo_fused_nrep<true>(a, dim3(1, groups), st);
     }
-    if (sel && sel->head_chunks > 1) return hipErrorInvalidValue;      // head chunks: the single launch only
     if (sel && sel->enabled == kSelectOnly) {
         if (c.P > 64 * kSelC) return hipErrorInvalidValue;
         a.sel = *sel;

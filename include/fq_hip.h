@@ -391,11 +391,12 @@ int fq_quest_decode_turbo(const fq_turbo_cache* cache,
                           int32_t num_sinks, int32_t window_pages, int32_t k_max, int32_t select_mode,
                           uint8_t* mask_out, void* workspace, size_t workspace_bytes, fq_stream_t stream);
 
-/* Whether fq_quest_decode_turbo runs these arguments as one attention launch
- * that scores and selects its own pages (1) or not (0; with 6 or 8 query heads
- * per KV head the caller may then attend them in chunks).  Negative: an
- * FQ_ERR_* code.  No reference counterpart: it tells a caller which kernels
- * one decode step runs. */
+/* Whether fq_quest_decode_turbo selects the pages inside its matrix-core
+ * attention kernel for these arguments (1: one launch with enough KV groups,
+ * else a scoring launch and the attention; with 6 or 8 query heads per KV
+ * head included) or not (0; the caller may then attend a KV group's query
+ * heads in chunks).  Negative: an FQ_ERR_* code.  No reference counterpart:
+ * it tells a caller which kernels one decode step runs. */
 int fq_quest_fused_turbo(const fq_turbo_cache* cache, const fq_query* query);
 
 /* The selection half of fq_quest_decode_turbo (the page scores and

@@ -118,3 +118,32 @@ def test_per_layer_graph_virtual_heads(mode):
         for l, d in enumerate(decs):
             assert torch.equal(got[l], d.O3), (rep, l)
         assert bool(torch.isfinite(got[0]).all())
+
+
+@pytest.mark.parametrize("Hq", [64, 48])
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_turbo_single_layer_step_virtual_heads(Hq, mode):
+    """The same over the TurboQuant cache (scores from the raw K page metadata,
+    codebook attention), one layer of the bench's synthetic TurboQuant cache."""
+    import bench
+    from flashquest_amd.eager.decode import _one_launch, quest_decode_turbo
+    P = 300
+    tc = bench.make_turbo_cache(1, Hq=Hq, P=P, dev=torch.device("cuda:0"))
+    keys = ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")
+    raw = (tc["K_scale_raw"], tc["K_mn_raw"])
+    Q = tc["Q"]
+    assert _one_launch(3, Q, [tc[k] for k in keys], Hq // 8, 64, mode, 4, 2, None, raw=raw)
+    o, lse, mask = quest_decode_turbo(Q, *[tc[k] for k in keys], *raw, retention=0.25, num_sinks=4,
+                                      window_pages=2, select_mode=mode, return_selection=True)
+    torch.cuda.synchronize()
+    q = Q[:, :, 0].float().cpu().numpy()
+    host = {k: (tc[k].cpu().numpy() if tc[k].dtype == torch.uint8 else tc[k].float().cpu().numpy())
+            for k in keys + ("K_scale_raw", "K_mn_raw")}
+    scores = O.page_scores_fixed(q, host["K_scale_raw"], host["K_mn_raw"], mode)
+    ref_mask = O.select_pages_vectorized(scores[:, :, None, :], 0.25, 4, 2)[:, :, 0, :]
+    if mode == "per_kv_head_sum":
+        ref_mask = np.repeat(ref_mask, Hq // 8, axis=1)
+    assert np.array_equal(mask.cpu().numpy(), ref_mask)
+    ref_o, ref_l = O.sparse_turbo_attention(q, *[host[k] for k in keys], ref_mask, 64)
+    assert max_err(o[:, :, 0], ref_o) <= decode_tol(ref_o, "bf16")
+    assert max_err(lse[:, :, 0], ref_l) <= 1e-4
