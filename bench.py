@@ -65,6 +65,9 @@ def parse():
                          "in one HIP graph), 5 flushed replays only")
     ap.add_argument("--profile-turbo", action="store_true",
                     help="for rocprofv3 runs: 10 flushed fused TurboQuant decode steps (--select mode) only")
+    ap.add_argument("--profile-gqa8", action="store_true",
+                    help="for rocprofv3 runs: config 1 with 64 query heads (8 per KV head, two virtual KV heads "
+                         "per KV head): a 256 MiB device copy (calibration), then 5 flushed steps (--select mode)")
     return ap.parse_args()
 
 
@@ -498,6 +501,19 @@ def main():
         per_layer_graph_ms(per_layer, 5, 1, flush)
         torch.cuda.synchronize()
         print(json.dumps({"profile_per_layer": "done", "select": args.select}))
+        return
+
+    if args.profile_gqa8:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)                      # FETCH = WRITE = 256 MiB of HBM traffic
+        c8 = make_cache(L, B, Hq=64, P=P, dev=dev)
+        dec = decoder(args.retention, k, args.select, c=c8)
+        for _ in range(5):
+            flush()
+            dec()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_gqa8": "done", "select": args.select, "copy_bytes": src.numel()}))
         return
 
     if args.profile_kernels:
