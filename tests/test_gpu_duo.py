@@ -30,9 +30,12 @@ def _retention_rows(pattern, r, nrep):
 
 @pytest.mark.parametrize("mode", ["per_q_head", "per_kv_head_sum"])
 @pytest.mark.parametrize("splits", [None, 4])
-def test_layer_patterns_in_one_multilayer_call(mode, splits):
+@pytest.mark.parametrize("Hq", [24, 64])
+def test_layer_patterns_in_one_multilayer_call(mode, splits, Hq):
+    """Hq = 64: 8 query heads per KV head, two virtual KV heads per KV head in
+    the single launch, each reading its layer's retention row."""
     from flashquest_amd.eager.decode import quest_decode_int4
-    Lyr, Hq, Hkv, P = 24, 24, 8, 40          # 192 groups: the single-launch kernel unless splits are pinned
+    Lyr, Hkv, P = 24, 8, 40          # 192 groups: the single-launch kernel unless splits are pinned
     rng = np.random.default_rng(123)
     cases = [Int4Case(seed=500 + i, B=1, Hq=Hq, Hkv=Hkv, S=64 * P, D=128, meta="f16", vgroup=32, dtype="f16")
              for i in range(Lyr)]
