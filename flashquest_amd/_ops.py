@@ -177,8 +177,10 @@ def retention_tensor(retention, H: int, device) -> torch.Tensor:
 
 
 # ---- GQA ratios above 4 on the matrix-core kernels ---------------------------
-# Those kernels take at most 4 query heads per KV head; a group of 5 to 8 is
-# attended in chunks of its query heads, each chunk reading the group's pages.
+# Those kernels take at most 4 query heads per KV head.  The fused decode
+# entries run 6 or 8 as virtual KV heads themselves where the attention kernel
+# selects its own pages; every other group of more than 4 is attended here in
+# chunks of its query heads, each chunk reading the group's pages.
 
 def head_chunks(nrep: int):
     """(offset, size) chunks of a KV group's query heads, each of at most 4
@@ -207,8 +209,9 @@ def put_heads(dst, src, axis: int, H_kv: int, nrep: int, off: int, size: int):
 def wants_head_chunks(H_q: int, H_kv: int, D: int, page_size: int) -> bool:
     """5 to 8 query heads per KV head on the matrix-core layout (head_dim 128,
     64-token pages), and more than 8 on any layout (the library's kernels take
-    at most 8: one selection bit per query head of a group): chunked.  Other
-    shapes take their kernels whole."""
+    at most 8: one selection bit per query head of a group): chunked, unless
+    the decode entry takes 6 or 8 on virtual KV heads itself (the callers ask
+    the library).  Other shapes take their kernels whole."""
     if H_kv < 1 or H_q % H_kv:
         return False
     nrep = H_q // H_kv
