@@ -154,12 +154,12 @@ def quest_decode_int4(
     if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None
             and not _one_launch(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static)):
-        return _chunked_decode(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), H_kv, nrep, out,
-                                    dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
-                                         k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
-                                         sm_scale=sm_scale, return_lse=return_lse,
-                                         return_selection=return_selection, K_tail=K_tail, V_tail=V_tail,
-                                         head_pattern=head_pattern))
+        planes = (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn)
+        kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
+                  page_size=page_size, select_mode=select_mode, sm_scale=sm_scale, return_lse=return_lse,
+                  return_selection=return_selection, K_tail=K_tail, V_tail=V_tail, head_pattern=head_pattern)
+        res = _padded_decode(4, Q, planes, H_kv, nrep, out, kw) if nrep in (5, 7) else None
+        return res if res is not None else _chunked_decode(4, Q, planes, H_kv, nrep, out, kw)
     layered = Q.dim() == 5
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
@@ -228,6 +228,61 @@ def _one_launch(bits, Q, planes, nrep, page_size, select_mode, num_sinks, window
     k_max = -1 if k_max_static is None else min(int(k_max_static), P)
     fused = L.lib().fq_quest_fused_int4 if bits == 4 else L.lib().fq_quest_fused_int8
     return fused(cache, probe, int(num_sinks), int(window_pages), k_max, L.SELECT_MODES[select_mode]) == 1
+
+
+def _pad_heads(x, axis: int, H_kv: int, nrep: int, fill: float = 0.0):
+    """x with one more head per KV group on its (group-major) head axis `axis`,
+    the new last head of every group filled with `fill`."""
+    g = x.unflatten(axis, (H_kv, nrep))
+    shape = list(g.shape)
+    shape[axis + 1] = 1
+    return torch.cat([g, torch.full(shape, fill, dtype=x.dtype, device=x.device)], dim=axis + 1).flatten(axis, axis + 1)
+
+
+def _real_heads(x, axis: int, H_kv: int, nrep: int, grouped: bool = False):
+    """The nrep real heads of every group of a tensor padded by _pad_heads: a
+    view with the heads as (H_kv, nrep) when `grouped` (writable in place),
+    else flattened back to H_kv * nrep heads (a copy)."""
+    g = x.unflatten(axis, (H_kv, nrep + 1)).narrow(axis + 1, 0, nrep)
+    return g if grouped else g.flatten(axis, axis + 1)
+
+
+def _padded_retention(retention, H_q: int, H_kv: int, nrep: int, device):
+    """The per-head retention of a padded step: the real heads' values, 0 for
+    the extra head of every group (it then selects only the forced pages)."""
+    return _pad_heads(_ops.retention_tensor(retention, H_q, device), 0, H_kv, nrep)
+
+
+def _padded_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
+    """quest_decode_int4 / _int8 / _turbo (bits 4 / 8 / 3) for 5 or 7 query
+    heads per KV head as one step of 6 or 8: a zero query head is added to
+    every KV group, with retention 0, so the library runs each KV head as two
+    virtual heads of 3 or 4 query heads.  The extra head changes nothing the
+    real heads see: its selection is the forced pages, which every head holds
+    already; a per_kv_head_sum row adds 0 to the summed query (exact in fp32)
+    and its k comes from the largest retention, never 0's; its own output is
+    dropped.  Returns None when the library would not take the padded step in
+    its matrix-core kernels (the caller then attends in chunks)."""
+    head_axis = Q.dim() - 3
+    Qp = _pad_heads(Q, head_axis, H_kv, nrep)
+    if not _one_launch(bits, Qp, planes, nrep + 1, kw["page_size"], kw["select_mode"], kw["num_sinks"],
+                       kw["window_pages"], kw["k_max_static"], raw=raw):
+        return None
+    sub = dict(kw, retention=_padded_retention(kw["retention"], Q.shape[-3], H_kv, nrep, Q.device))
+    if bits == 3:
+        res = quest_decode_turbo(Qp, *planes, *raw, **sub)
+    else:
+        res = (quest_decode_int4 if bits == 4 else quest_decode_int8)(Qp, *planes, **sub)
+    O = _real_heads(res[0], head_axis, H_kv, nrep)
+    if out is not None:
+        out.copy_(O)
+        O = out
+    else:
+        O = O.contiguous()
+    lse = None if res[1] is None else _real_heads(res[1], res[1].dim() - 2, H_kv, nrep).contiguous()
+    if kw["return_selection"]:
+        return O, lse, _real_heads(res[2], res[2].dim() - 2, H_kv, nrep).contiguous()
+    return O, lse
 
 
 def _chunked_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
@@ -430,11 +485,12 @@ def quest_decode_int8(
     if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
             and not _one_launch(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static)):
-        return _chunked_decode(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), H_kv, nrep, None,
-                               dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
-                                    k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
-                                    sm_scale=sm_scale, return_lse=return_lse, return_selection=return_selection,
-                                    K_tail=K_tail, V_tail=V_tail, head_pattern=head_pattern))
+        planes = (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn)
+        kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
+                  page_size=page_size, select_mode=select_mode, sm_scale=sm_scale, return_lse=return_lse,
+                  return_selection=return_selection, K_tail=K_tail, V_tail=V_tail, head_pattern=head_pattern)
+        res = _padded_decode(8, Q, planes, H_kv, nrep, None, kw) if nrep in (5, 7) else None
+        return res if res is not None else _chunked_decode(8, Q, planes, H_kv, nrep, None, kw)
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
     P = K_scale.shape[-2]
@@ -527,11 +583,13 @@ def quest_decode_turbo(
     if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
             and not _one_launch(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static, raw=(K_scale_raw, K_mn_raw))):
-        return _chunked_decode(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), H_kv, nrep, None,
-                               dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages,
-                                    k_max_static=k_max_static, page_size=page_size, select_mode=select_mode,
-                                    sm_scale=sm_scale, return_lse=return_lse, return_selection=return_selection,
-                                    head_pattern=head_pattern), raw=(K_scale_raw, K_mn_raw))
+        planes = (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo)
+        kw = dict(retention=retention, num_sinks=num_sinks, window_pages=window_pages, k_max_static=k_max_static,
+                  page_size=page_size, select_mode=select_mode, sm_scale=sm_scale, return_lse=return_lse,
+                  return_selection=return_selection, head_pattern=head_pattern)
+        raw = (K_scale_raw, K_mn_raw)
+        res = _padded_decode(3, Q, planes, H_kv, nrep, None, kw, raw=raw) if nrep in (5, 7) else None
+        return res if res is not None else _chunked_decode(3, Q, planes, H_kv, nrep, None, kw, raw=raw)
     Q3 = Q[..., 0, :]
     H_q = Q3.shape[-2]
     P = K_scale_raw.shape[-2]
@@ -588,18 +646,45 @@ class QuestDecoder:
         self.O3 = torch.empty_like(self.Q3) if out is None else out[..., 0, :]
         self.lse = lse
         self.device = Q.device
+        self.tail = None
         # more than 4 query heads per KV head, not one launch in the library:
         # the step is quest_decode_int4's chunked one (its tensors come from
         # the graph's pool when captured; the retention is moved to the device
         # here, not during a capture)
         self._chunked = None
+        self._padded = None
         H_kv = K_scale.shape[-3]
         nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
         planes = (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn)
-        if (_ops.wants_head_chunks(Q.shape[-3], H_kv, Q.shape[-1], page_size)
-                and rotation_signs is None and mask_out is None
-                and not _one_launch(4, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages,
-                                    k_max_static)):
+        wants = (_ops.wants_head_chunks(Q.shape[-3], H_kv, Q.shape[-1], page_size)
+                 and rotation_signs is None and mask_out is None
+                 and not _one_launch(4, Q, planes, nrep, page_size, select_mode, num_sinks, window_pages,
+                                     k_max_static))
+        if wants and nrep in (5, 7):
+            # 5 or 7 query heads per KV head: a step of 6 or 8 with a zero query
+            # head per group (quest_decode_int4's padded step) when the library
+            # takes that in its matrix-core kernels; q is copied in and O out
+            axis = Q.dim() - 3
+            Qp = _pad_heads(Q, axis, H_kv, nrep)
+            if _one_launch(4, Qp, planes, nrep + 1, page_size, select_mode, num_sinks, window_pages, k_max_static):
+                self._Op = torch.empty_like(Qp)
+                self._lsep = None if lse is None else torch.empty(Qp.shape[:-2], dtype=torch.float32,
+                                                                  device=Q.device)
+                rp = _padded_retention(retention, Q.shape[-3], H_kv, nrep, Q.device)
+                self._inner = QuestDecoder(Qp, *planes, retention=rp, num_sinks=num_sinks,
+                                           window_pages=window_pages, k_max_static=k_max_static,
+                                           page_size=page_size, select_mode=select_mode, sm_scale=sm_scale,
+                                           out=self._Op, lse=self._lsep, K_tail=K_tail, V_tail=V_tail,
+                                           head_pattern=head_pattern)
+                # in-place views: the real heads of the padded query and output
+                # beside the caller's, both as (H_kv, nrep)
+                self._padded = (Q.unflatten(axis, (H_kv, nrep)), _real_heads(Qp, axis, H_kv, nrep, grouped=True),
+                                _real_heads(self._Op[..., 0, :], axis, H_kv, nrep, grouped=True),
+                                self.O3.unflatten(axis, (H_kv, nrep)),
+                                None if lse is None else _real_heads(self._lsep, axis, H_kv, nrep, grouped=True),
+                                None if lse is None else lse.unflatten(axis, (H_kv, nrep)))
+                return
+        if wants:
             ret = retention.to(device=Q.device, dtype=torch.float32) if torch.is_tensor(retention) else retention
             self._chunked = (Q, planes,
                              dict(retention=ret, num_sinks=num_sinks, window_pages=window_pages,
@@ -633,6 +718,8 @@ class QuestDecoder:
     def fused(self) -> bool:
         """True when attend() is the whole step: one attention kernel that scores
         and selects its own pages (select() then launches nothing)."""
+        if self._padded is not None:
+            return self._inner.fused
         if self._chunked is not None:
             return False
         r = L.lib().fq_quest_fused_int4(self.cache, self.query, self.sinks, self.window, self.k_max, self.mode)
@@ -641,6 +728,12 @@ class QuestDecoder:
         return r == 1
 
     def select(self):
+        if self._padded is not None:       # q into the padded query, then its selection
+            q_src, q_dst = self._padded[0], self._padded[1]
+            q_dst.copy_(q_src)
+            if self._inner.tail is None:
+                self._inner.select()
+            return
         if self._chunked is not None:      # the chunked step selects inside attend()
             return
         L.check(L.lib().fq_quest_select_int4(self.cache, self.query, self.r.data_ptr(), self.sinks, self.window,
@@ -648,6 +741,13 @@ class QuestDecoder:
                                              self.ws.numel(), L.stream_handle(self.device)), "quest select")
 
     def attend(self):
+        if self._padded is not None:       # the padded step, then the real heads' O (and lse) out
+            _, _, o_src, o_dst, l_src, l_dst = self._padded
+            self._inner.attend()
+            o_dst.copy_(o_src)
+            if l_dst is not None:
+                l_dst.copy_(l_src)
+            return
         if self._chunked is not None:
             Q, planes, kw = self._chunked
             _, lse = quest_decode_int4(Q, *planes, out=self.O3.unsqueeze(-2), **kw)
@@ -665,7 +765,7 @@ class QuestDecoder:
                                              L.stream_handle(self.device)), "quest attend")
 
     def __call__(self):
-        if self._chunked is None and self.tail is None:
+        if self._padded is not None or (self._chunked is None and self.tail is None):
             self.select()
         self.attend()
         return self.O3.unsqueeze(-2)

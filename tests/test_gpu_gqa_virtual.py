@@ -147,3 +147,112 @@ def test_turbo_single_layer_step_virtual_heads(Hq, mode):
     ref_o, ref_l = O.sparse_turbo_attention(q, *[host[k] for k in keys], ref_mask, 64)
     assert max_err(o[:, :, 0], ref_o) <= decode_tol(ref_o, "bf16")
     assert max_err(lse[:, :, 0], ref_l) <= 1e-4
+
+
+@pytest.mark.parametrize("bits", [4, 8, 3])
+@pytest.mark.parametrize("Hq", [56, 40])
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+@pytest.mark.parametrize("layers", [1, 12])
+def test_padded_step_five_and_seven_heads(bits, Hq, mode, layers):
+    """5 and 7 query heads per KV head as a step of 6 or 8 with a zero query
+    head per group (retention 0: it selects only the forced pages); the real
+    heads' selection, O and lse against the oracle.  12 layers x 8 KV heads:
+    one launch; one layer: the split form."""
+    import bench
+    from flashquest_amd.eager.decode import _one_launch, _pad_heads, quest_decode_int4, quest_decode_int8, \
+        quest_decode_turbo
+    P, nrep = 160, Hq // 8
+    dev = torch.device("cuda:0")
+    print(f"[padded] bits={bits} Hq={Hq} mode={mode} layers={layers}", flush=True)
+    kw = dict(retention=0.25, num_sinks=4, window_pages=2, select_mode=mode, return_selection=True)
+    if bits == 4:
+        c = bench.make_cache(layers, 1, Hq=Hq, P=P, dev=dev)
+        keys = ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")
+        Q = c["Q"]
+        Qp = _pad_heads(Q, Q.dim() - 3, 8, nrep)
+        assert _one_launch(4, Qp, [c[k] for k in keys], nrep + 1, 64, mode, 4, 2, None)
+        o, lse, mask = quest_decode_int4(Q, *[c[k] for k in keys], **kw)
+        host = lambda l: [c[k][l, 0:1].cpu().numpy() if c[k].dtype == torch.uint8 else c[k][l, 0:1].float().cpu().numpy()
+                          for k in keys]
+        q_of = lambda l: Q[l, 0:1, :, 0].float().cpu().numpy()
+        pick = lambda t, l: t[l]
+    elif bits == 8:
+        c = bench.make_int8_cache(layers, Hq=Hq, P=P, dev=dev)
+        keys = ("K_uint8", "K_scale", "K_mn", "V_uint8", "V_scale", "V_mn")
+        Q = c["Q"]
+        o, lse, mask = quest_decode_int8(Q, *[c[k] for k in keys], **kw)
+        host = lambda l: [c[k][l:l + 1].cpu().numpy() if c[k].dtype == torch.uint8 else c[k][l:l + 1].float().cpu().numpy()
+                          for k in keys]
+        q_of = lambda l: Q[l:l + 1, :, 0].float().cpu().numpy()
+        pick = lambda t, l: t[l:l + 1]
+    else:
+        c = bench.make_turbo_cache(layers, Hq=Hq, P=P, dev=dev)
+        keys = ("K_msb", "K_lsb", "K_scale_turbo", "V_msb", "V_lsb", "V_scale_turbo")
+        Q = c["Q"]
+        o, lse, mask = quest_decode_turbo(Q, *[c[k] for k in keys], c["K_scale_raw"], c["K_mn_raw"], **kw)
+        host = lambda l: [c[k][l:l + 1].cpu().numpy() if c[k].dtype == torch.uint8 else c[k][l:l + 1].float().cpu().numpy()
+                          for k in keys + ("K_scale_raw", "K_mn_raw")]
+        q_of = lambda l: Q[l:l + 1, :, 0].float().cpu().numpy()
+        pick = lambda t, l: t[l:l + 1]
+    torch.cuda.synchronize()
+    assert o.shape == Q.shape and mask.shape[-2] == Hq
+    for l in sorted({0, layers - 1}):
+        q, pl = q_of(l), host(l)
+        if bits == 3:
+            scores = O.page_scores_fixed(q, pl[6], pl[7], mode)
+        else:
+            scores = O.page_scores_fixed(q, pl[1], pl[2], mode, 255.0 if bits == 8 else 15.0)
+        ref_mask = O.select_pages_vectorized(scores[:, :, None, :], 0.25, 4, 2)[:, :, 0, :]
+        if mode == "per_kv_head_sum":
+            ref_mask = np.repeat(ref_mask, nrep, axis=1)
+        got_mask = pick(mask, l).cpu().numpy().reshape(ref_mask.shape)
+        assert np.array_equal(got_mask, ref_mask), l
+        if bits == 3:
+            ref_o, ref_l = O.sparse_turbo_attention(q, *pl[:6], ref_mask, 64)
+        elif bits == 8:
+            ref_o, ref_l = O.sparse_int8_attention(q, *pl, ref_mask, 64)
+        else:
+            ref_o, ref_l = O.sparse_int4_attention(q, *pl, ref_mask, 64)
+        got_o = pick(o, l)[..., 0, :].reshape(ref_o.shape)
+        got_l = pick(lse, l)[..., 0].reshape(ref_l.shape)
+        assert max_err(got_o, ref_o) <= decode_tol(ref_o, "f16" if bits == 4 else "bf16"), l
+        assert max_err(got_l, ref_l) <= 1e-4, l
+
+
+@pytest.mark.parametrize("mode", ["per_kv_head_sum", "per_q_head"])
+def test_padded_decoder_graph(mode):
+    """QuestDecoder with 7 query heads per KV head (the padded step: q copied
+    into the padded query, O copied out) captured in a HIP graph: every
+    replay equals the eager step bit for bit, and the eager step the
+    functional operator."""
+    import bench
+    from flashquest_amd.eager.decode import QuestDecoder, quest_decode_int4
+    c = bench.make_cache(12, 1, Hq=56, P=96, dev=torch.device("cuda:0"))
+    keys = ("K_packed", "K_scale", "K_mn", "V_packed", "V_scale", "V_mn")
+    Q = c["Q"]
+    d = QuestDecoder(Q, *[c[k] for k in keys], retention=0.25, num_sinks=4, window_pages=2, k_max_static=24,
+                     select_mode=mode)
+    assert d._padded is not None and d.fused
+    d()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        d()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            d()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        Q.copy_(torch.randn(Q.shape, device=Q.device).to(Q.dtype))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = d.O3.clone()
+        d()
+        torch.cuda.synchronize()
+        assert torch.equal(got, d.O3), rep
+    want, _ = quest_decode_int4(Q, *[c[k] for k in keys], retention=0.25, num_sinks=4, window_pages=2,
+                                k_max_static=24, select_mode=mode)
+    torch.cuda.synchronize()
+    assert torch.equal(want[..., 0, :], d.O3)
