@@ -376,7 +376,7 @@ void attn_int4_mfma_kernel(MfmaParams a) {
                     __syncthreads();
                 }
                 if constexpr (HCH) {
-                    if (chunk_sum) score_group_regs<MT, 2 * NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
+                    if (chunk_sum) score_group_sum_lds<MT, 2 * NREP, NT>(sr, s_qraw, s_key, tid, c.P);
                     else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);
                 } else if (sum) score_group_regs<MT, NREP, NT, true>(sr, s_qraw, s_key, tid, c.P);
                 else score_group_regs<MT, NREP, NT, false>(sr, s_qraw, s_key, tid, c.P);

@@ -99,12 +99,32 @@ FQ_DEV void scores_to_keys(const ScoreRowRegs<NREP, NT>& sr, uint32_t* s_key, in
     }
 }
 
+// The page loop of the in-kernel scoring: NR rows of query values (qr) and
+// their relu (qp), channels 8 * (tid & 15) .. + 7, against every page's
+// metadata in registers; keys to s_key[r * 64 kSelC + p].
+template <typename MT, int NR, int NT>
+FQ_DEV void score_group_pages(const ScoreRegs<NT>& sr, const float (&qr)[NR][8], const float (&qp)[NR][8],
+                              uint32_t* s_key, int tid, int P, float levels) {
+    constexpr int PPP = NT / 16;
+    const int lip = tid & 15, pip = tid >> 4;
+#pragma unroll
+    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
+        const int p = u * PPP + pip;
+        if (u * PPP < P) {            // uniform
+            score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
+                if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
+            }, levels);
+        } else if (lip == 0) {        // a pass past the group's pages: their keys are 0
+#pragma unroll
+            for (int r = 0; r < NR; ++r) s_key[r * 64 * kSelC + p] = 0u;
+        }
+    }
+}
+
 // qin[r][j]: query head r's raw value at channel 8 * (tid & 15) + j.
 template <typename MT, int NREP, int NT, bool SUM>
 FQ_DEV void score_group_regs_q(const ScoreRegs<NT>& sr, const float (&qin)[NREP][8], uint32_t* s_key, int tid, int P,
                                float levels = 15.0f) {
-    constexpr int PPP = NT / 16;
-    const int lip = tid & 15, pip = tid >> 4;
     // per_kv_head_sum scores the group's summed query, (q_0 + q_1) + ... with
     // relu applied per head before the sum; per_q_head scores every head
     constexpr int NR = SUM ? 1 : NREP;
@@ -130,18 +150,34 @@ FQ_DEV void score_group_regs_q(const ScoreRegs<NT>& sr, const float (&qin)[NREP]
             }
         }
     }
+    score_group_pages<MT, NR, NT>(sr, qr, qp, s_key, tid, P, levels);
+}
+
+// per_kv_head_sum over ROWS query heads read from LDS one row at a time
+// (s_qraw[r][channel]): the summed query and the summed relu in
+// score_group_regs_q's fp32 order, without every row's values live at once
+// (the scoring registers hold the group's metadata loads meanwhile).
+template <typename MT, int ROWS, int NT>
+FQ_DEV void score_group_sum_lds(const ScoreRegs<NT>& sr, const float (*s_qraw)[128], uint32_t* s_key, int tid, int P,
+                                float levels = 15.0f) {
+    const int lip = tid & 15;
+    float qr[1][8], qp[1][8];
 #pragma unroll
-    for (int u = 0; u < ScoreRegs<NT>::kPass; ++u) {
-        const int p = u * PPP + pip;
-        if (u * PPP < P) {            // uniform
-            score_page_regs<NR, MT>(sr.sv[u], sr.mv[u], qr, qp, [&](int r, float sc) {
-                if (lip == 0) s_key[r * 64 * kSelC + p] = p < P ? sortable_key(sc) : 0u;
-            }, levels);
-        } else if (lip == 0) {        // a pass past the group's pages: their keys are 0
+    for (int j = 0; j < 8; ++j) {
+        const float v = s_qraw[0][lip * 8 + j];
+        qr[0][j] = v;
+        qp[0][j] = v > 0.f ? v : 0.f;
+    }
+#pragma unroll 1
+    for (int r = 1; r < ROWS; ++r) {
 #pragma unroll
-            for (int r = 0; r < NR; ++r) s_key[r * 64 * kSelC + p] = 0u;
+        for (int j = 0; j < 8; ++j) {
+            const float v = s_qraw[r][lip * 8 + j];
+            qr[0][j] = __fadd_rn(qr[0][j], v);
+            qp[0][j] = __fadd_rn(qp[0][j], v > 0.f ? v : 0.f);
         }
     }
+    score_group_pages<MT, 1, NT>(sr, qr, qp, s_key, tid, P, levels);
 }
 
 template <typename MT, int NREP, int NT, bool SUM>
