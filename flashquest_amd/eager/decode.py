@@ -112,6 +112,7 @@ def quest_decode_int4(
     head_pattern: torch.Tensor | None = None,
     rotation_signs: torch.Tensor | None = None,
     _rotation: torch.Tensor | None = None,
+    _direct: bool = False,
 ):
     """Fused score -> select -> sparse attention over completed pages.
 
@@ -151,7 +152,7 @@ def quest_decode_int4(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None
+    if (not _direct and _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size) and _rotation is None
             and not _one_launch(4, Q, (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static)):
         planes = (K_packed, K_scale, K_mn, V_packed, V_scale, V_mn)
@@ -247,10 +248,27 @@ def _real_heads(x, axis: int, H_kv: int, nrep: int, grouped: bool = False):
     return g if grouped else g.flatten(axis, axis + 1)
 
 
+_padded_scalar = {}
+
+
 def _padded_retention(retention, H_q: int, H_kv: int, nrep: int, device):
     """The per-head retention of a padded step: the real heads' values, 0 for
-    the extra head of every group (it then selects only the forced pages)."""
-    return _pad_heads(_ops.retention_tensor(retention, H_q, device), 0, H_kv, nrep)
+    the extra head of every group (it then selects only the forced pages).
+    Scalar retentions are kept per (value, shape, device) outside graph
+    capture, like _ops.retention_tensor's vectors."""
+    if torch.is_tensor(retention):
+        return _pad_heads(_ops.retention_tensor(retention, H_q, device), 0, H_kv, nrep)
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    key = (float(retention), H_q, H_kv, nrep, device.type, device.index)
+    r = _padded_scalar.get(key)
+    if r is None:
+        r = _pad_heads(_ops.retention_tensor(retention, H_q, device), 0, H_kv, nrep)
+        capturing = device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+        if not capturing and len(_padded_scalar) < 64:
+            _padded_scalar[key] = r
+    return r
 
 
 def _padded_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
@@ -268,7 +286,8 @@ def _padded_decode(bits, Q, planes, H_kv, nrep, out, kw, raw=None):
     if not _one_launch(bits, Qp, planes, nrep + 1, kw["page_size"], kw["select_mode"], kw["num_sinks"],
                        kw["window_pages"], kw["k_max_static"], raw=raw):
         return None
-    sub = dict(kw, retention=_padded_retention(kw["retention"], Q.shape[-3], H_kv, nrep, Q.device))
+    # _direct: the library takes the padded step (just checked), no second check
+    sub = dict(kw, retention=_padded_retention(kw["retention"], Q.shape[-3], H_kv, nrep, Q.device), _direct=True)
     if bits == 3:
         res = quest_decode_turbo(Qp, *planes, *raw, **sub)
     else:
@@ -463,6 +482,7 @@ def quest_decode_int8(
     head_pattern: torch.Tensor | None = None,
     K_tail: torch.Tensor | None = None,
     V_tail: torch.Tensor | None = None,
+    _direct: bool = False,
 ):
     """The INT8 decode step (llama_persistent_patch.py:143-160 with the
     selection of 196-245): page_scores_int8_fast -> select_pages_vectorized ->
@@ -482,7 +502,7 @@ def quest_decode_int8(
         raise NotImplementedError(f"head_dim={D} not in (64, 128)")
     H_kv = K_scale.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
+    if (not _direct and _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
             and not _one_launch(8, Q, (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static)):
         planes = (K_uint8, K_scale, K_mn, V_uint8, V_scale, V_mn)
@@ -558,6 +578,7 @@ def quest_decode_turbo(
     return_lse: bool = True,
     return_selection: bool = False,
     head_pattern: torch.Tensor | None = None,
+    _direct: bool = False,
 ):
     """The reference's TurboQuant decode over completed pages, fused: page scores
     from the un-rotated K page metadata (criticality.py:128-163), selection
@@ -580,7 +601,7 @@ def quest_decode_turbo(
         raise AssertionError("K_scale_raw / K_mn_raw must be bf16")
     H_kv = K_msb.shape[-3]
     nrep = Q.shape[-3] // H_kv if Q.shape[-3] % H_kv == 0 else 0
-    if (_ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
+    if (not _direct and _ops.wants_head_chunks(Q.shape[-3], H_kv, D, page_size)
             and not _one_launch(3, Q, (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo), nrep, page_size,
                                 select_mode, num_sinks, window_pages, k_max_static, raw=(K_scale_raw, K_mn_raw))):
         planes = (K_msb, K_lsb, K_scale_turbo, V_msb, V_lsb, V_scale_turbo)
