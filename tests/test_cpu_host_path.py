@@ -148,3 +148,28 @@ def test_strided_per_head_retention_is_made_contiguous():
     r = torch.linspace(0, 1, 48)[::2]
     t = _ops.retention_tensor(r, 24, "cpu")
     assert t.is_contiguous() and torch.equal(t, r)
+
+
+@pytest.mark.parametrize("nrep", [5, 7])
+def test_padded_heads_round_trip_and_retention(nrep):
+    """The padded step of 5 or 7 query heads per KV head: every group gains
+    one zero head at its end, the real heads come back unchanged (as a copy,
+    or in place through the grouped view), and the padded retention keeps the
+    real heads' values with 0 for the extra head (scalar and per-head)."""
+    from flashquest_amd.eager.decode import _pad_heads, _padded_retention, _real_heads
+    H_kv, D = 3, 8
+    Q = torch.randn(2, 4, H_kv * nrep, 1, D)
+    Qp = _pad_heads(Q, 2, H_kv, nrep)
+    assert Qp.shape == (2, 4, H_kv * (nrep + 1), 1, D)
+    g = Qp.unflatten(2, (H_kv, nrep + 1))
+    assert torch.equal(g[:, :, :, nrep], torch.zeros_like(g[:, :, :, nrep]))
+    assert torch.equal(_real_heads(Qp, 2, H_kv, nrep), Q)
+    Q2 = torch.randn_like(Q)
+    _real_heads(Qp, 2, H_kv, nrep, grouped=True).copy_(Q2.unflatten(2, (H_kv, nrep)))
+    assert torch.equal(_real_heads(Qp, 2, H_kv, nrep), Q2)       # written in place
+    r = _padded_retention(0.3, H_kv * nrep, H_kv, nrep, "cpu")
+    want = torch.tensor(([0.3] * nrep + [0.0]) * H_kv, dtype=torch.float32)
+    assert torch.equal(r, want)
+    per_head = torch.arange(H_kv * nrep, dtype=torch.float32) / 100
+    rp = _padded_retention(per_head, H_kv * nrep, H_kv, nrep, "cpu").unflatten(0, (H_kv, nrep + 1))
+    assert torch.equal(rp[:, :nrep].flatten(), per_head) and not rp[:, nrep].any()
