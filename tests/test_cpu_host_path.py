@@ -173,3 +173,27 @@ def test_padded_heads_round_trip_and_retention(nrep):
     per_head = torch.arange(H_kv * nrep, dtype=torch.float32) / 100
     rp = _padded_retention(per_head, H_kv * nrep, H_kv, nrep, "cpu").unflatten(0, (H_kv, nrep + 1))
     assert torch.equal(rp[:, :nrep].flatten(), per_head) and not rp[:, nrep].any()
+
+
+def test_library_takes_six_and_eight_heads_per_kv_head_itself():
+    """fq_quest_fused_int4 (host logic only, no launch): 6 and 8 query heads
+    per KV head run on virtual KV heads in the library whether the step is
+    one launch (28 layers) or the split form (one layer); 7 does not (the
+    Python layer pads it to 8); above 8 the entry refuses the query."""
+    Hkv, P, D = 8, 64, 128
+    S = P * 64
+    for layers in (28, 1):
+        planes = (torch.zeros(layers, 1, Hkv, S, D // 2, dtype=torch.uint8),
+                  torch.zeros(layers, 1, Hkv, P, D, dtype=torch.float16),
+                  torch.zeros(layers, 1, Hkv, P, D, dtype=torch.float16),
+                  torch.zeros(layers, 1, Hkv, S, D // 2, dtype=torch.uint8),
+                  torch.zeros(layers, 1, Hkv, S, 4, dtype=torch.float16),
+                  torch.zeros(layers, 1, Hkv, S, 4, dtype=torch.float16))
+        cache, keep = _ops.int4_cache(*planes, 64)
+        for Hq, want in ((24, 1), (48, 1), (64, 1), (56, 0)):
+            Q3 = torch.zeros(layers, 1, Hq, D, dtype=torch.float16)
+            q = _ops.query(Q3, Q3, None, None)
+            for mode in (0, 1):
+                assert L.lib().fq_quest_fused_int4(cache, q, 4, 2, 16, mode) == want, (layers, Hq, mode)
+        Q3 = torch.zeros(layers, 1, 72, D, dtype=torch.float16)
+        assert L.lib().fq_quest_fused_int4(cache, _ops.query(Q3, Q3, None, None), 4, 2, 16, 0) < 0
